@@ -1,0 +1,885 @@
+// q4hip.hip -- HIP kernels and the C ABI (include/q4hip.h) of the Qwen2 Q4_0 token loop.
+//
+// One pass over M tokens (decode: M = 1) is the reference's forward_pass
+// (h2-own-inference-engine/engine/kernels.c:306-415) as a sequence of kernels on the
+// context's stream; its barriers become kernel boundaries.  The M = 1 step is captured once
+// into a hipGraph that reads the position from device memory, so decode replays it with no
+// host work per token.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+#include "q4hip.h"
+
+using namespace q4;
+
+// ================================================================ kernels
+
+// GGUF Q4_0 rows [rows][nb][18 B] -> tiled layout (see kernels.h), rows row0.. of the matrix.
+__global__ void k_repack_q4(const uint8_t* __restrict__ raw, int64_t rows, int nb, int nb8, int row0,
+                            uint32_t* __restrict__ qs, uint16_t* __restrict__ dsc) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * nb) return;
+  const int64_t r = idx / nb;
+  const int b = (int)(idx - r * nb);
+  const int64_t R = row0 + r;
+  const int64_t tile = R >> 6;
+  const int rr = (int)(R & 63);
+  const uint8_t* s = raw + idx * 18;
+  dsc[((tile * nb8 + (b >> 3)) * 64 + rr) * 8 + (b & 7)] = (uint16_t)(s[0] | (s[1] << 8));
+  const uint8_t* q = s + 2;
+  uint32_t* o = qs + ((tile * nb + b) * 64 + rr) * 4;
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    o[j] = (uint32_t)q[2 * j] | ((uint32_t)q[2 * j + 1] << 8) | ((uint32_t)q[8 + 2 * j] << 16) |
+           ((uint32_t)q[9 + 2 * j] << 24);
+}
+
+// Embedding rows (kernels.c:312-322): x[m][32b+j] = ((q&15)-8)*d, x[m][32b+16+j] = ((q>>4)-8)*d.
+// The table stays in GGUF layout [vocab][D/32][18 B]; one token reads 18*D/32 bytes.
+__global__ void k_embed(const uint8_t* __restrict__ emb, int D, const int* __restrict__ tokens,
+                        const State* __restrict__ st, float* __restrict__ x) {
+  const int m = blockIdx.x;
+  const int t = tokens[st->pos0 + m];
+  const uint8_t* row = emb + (size_t)t * (D / 32) * 18;
+  float* xr = x + (size_t)m * D;
+  for (int idx = threadIdx.x; idx < D / 2; idx += blockDim.x) {
+    const int blk = idx >> 4, j = idx & 15;
+    const uint8_t* bp = row + blk * 18;
+    const float d = half_bits_to_float((uint32_t)bp[0] | ((uint32_t)bp[1] << 8));
+    const int q = bp[2 + j];
+    xr[32 * blk + j] = (float)((q & 15) - 8) * d;
+    xr[32 * blk + 16 + j] = (float)((q >> 4) - 8) * d;
+  }
+}
+
+// Quantize rows m_first .. m_first+gridDim.x-1 of `in` into xq rows 0.. (kernels.c:328-331,
+// 379, 385-388, 393-397, 405-407).
+template <int MODE>
+__global__ __launch_bounds__(256) void k_quant(const float* __restrict__ in, int ld_in, int n,
+                                               const float* __restrict__ w, float eps,
+                                               uint4* __restrict__ xq, int xstride, int m_first) {
+  __shared__ float red[8];
+  const float* xr = in + (size_t)(m_first + blockIdx.x) * ld_in;
+  float rs = 0.0f;
+  if (MODE == QM_NORM) rs = rms_scale(xr, n, eps, red);
+  quantize_row_dev<MODE>(xr, n, w, rs, xq + (size_t)blockIdx.x * xstride * 4, threadIdx.x, blockDim.x);
+}
+
+enum { OP_STORE = 0, OP_BIAS = 1, OP_ADD = 2 };   // put() of kernels.c:190-194
+
+// y[m][n] (op)= W[n] . x[m] for M tokens (matmul_q4, kernels.c:200-273).  One wave = 16 rows;
+// lane (r, j) owns accumulator j of row r and walks the blocks in order:
+//   acc_j = acc_j + f32(p_j) * (dw * dx)           (kernels.c:217-218, 137)
+// then ((acc_0 + acc_1) + acc_2) + acc_3 across the four lanes (hsum, kernels.c:116-118).
+template <int MT, int OP>
+__global__ __launch_bounds__(64) void k_matvec(const uint32_t* __restrict__ qs, const uint4* __restrict__ dsc,
+                                               int nb, int nb8, const uint4* __restrict__ xq, int xstride,
+                                               int M, float* __restrict__ y, int ldy, int N,
+                                               const float* __restrict__ bias) {
+  const int lane = threadIdx.x, r = lane >> 2, j = lane & 3;
+  const int wv = blockIdx.x, tile = wv >> 2, rr = ((wv & 3) << 4) + r;
+  const int row = (tile << 6) + rr;
+  float acc[MT];
+#pragma unroll
+  for (int m = 0; m < MT; m++) acc[m] = 0.0f;
+  const uint32_t* wp = qs + ((size_t)tile * nb * 64 + rr) * 4 + j;
+  const uint4* dp = dsc + ((size_t)tile * nb8 * 64 + rr);
+  for (int b8 = 0; b8 < nb8; b8++) {
+    const uint4 dv = dp[(size_t)b8 * 64];
+    const uint32_t dh[4] = {dv.x, dv.y, dv.z, dv.w};
+    uint32_t w8[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int b = b8 * 8 + k;
+      w8[k] = b < nb ? wp[(size_t)b * 256] : 0u;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int b = b8 * 8 + k;
+      if (b < nb) {
+        const float dw = half_bits_to_float((k & 1) ? (dh[k >> 1] >> 16) : (dh[k >> 1] & 0xffffu));
+        const uint32_t lo = w8[k] & 0x0F0F0F0Fu, hi = (w8[k] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+          if (m < M) {
+            const uint4 xv = xq[((size_t)m * xstride + b) * 4 + j];
+            int p = sdot4(lo, xv.x, (int)xv.z);
+            p = sdot4(hi, xv.y, p);
+            const float sc = dw * __uint_as_float(xv.w);
+            acc[m] = acc[m] + (float)p * sc;
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MT; m++) {
+    if (m < M) {
+      const float a0 = acc[m];
+      const float a1 = __shfl_down(a0, 1, 4), a2 = __shfl_down(a0, 2, 4), a3 = __shfl_down(a0, 3, 4);
+      if (j == 0 && row < N) {
+        const float v = a0 + a1 + a2 + a3;
+        float* o = y + (size_t)m * ldy + row;
+        if (OP == OP_ADD) *o = *o + v;
+        else if (OP == OP_BIAS) *o = v + bias[row];
+        else *o = v;
+      }
+    }
+  }
+}
+
+// RoPE on the q and k heads, then K (roped) and V appended to the fp32 cache at pos
+// (kernels.c:337-352).  Grid (heads + kv_heads, M), HD/2 threads: thread i owns pair (i, i+HD/2).
+__global__ void k_rope_kv(float* __restrict__ qkv, int QKV, int D, int H, int KVH, int HD,
+                          const float* __restrict__ rope, float* __restrict__ kc, float* __restrict__ vc,
+                          int ctx, int layer, const State* __restrict__ st) {
+  const int h = blockIdx.x, m = blockIdx.y, i = threadIdx.x, half = HD / 2;
+  const int pos = st->pos0 + m;
+  float* v = qkv + (size_t)m * QKV + h * HD;
+  const float* cs = rope + (size_t)pos * HD;
+  const float c = cs[2 * i], s = cs[2 * i + 1], x0 = v[i], x1 = v[i + half];
+  const float y0 = x0 * c - x1 * s, y1 = x1 * c + x0 * s;
+  v[i] = y0;
+  v[i + half] = y1;
+  if (h >= H) {
+    const int kh = h - H;
+    const size_t off = (((size_t)layer * KVH + kh) * ctx + pos) * HD;
+    const float* vs = qkv + (size_t)m * QKV + D + KVH * HD + kh * HD;
+    kc[off + i] = y0;
+    kc[off + i + half] = y1;
+    vc[off + i] = vs[i];
+    vc[off + i + half] = vs[i + half];
+  }
+}
+
+// Attention for one (head, token) over T = pos0+m+1 cached positions (kernels.c:355-377), in the
+// reference's order: scores as four lane sums, max, fast_exp and a running sum in t order, then
+// out_i = sum over t in order of (e_t/sum)*v_t[i].  Grid (H, M), 64 threads, shared: HD + T floats.
+__global__ __launch_bounds__(64) void k_attn(const float* __restrict__ qkv, int QKV, int D, int H, int KVH,
+                                             int HD, const float* __restrict__ kc, const float* __restrict__ vc,
+                                             int ctx, int layer, float* __restrict__ att,
+                                             const State* __restrict__ st) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  __shared__ float red[64];
+  const int h = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
+  const int T = st->pos0 + m + 1, kh = h / (H / KVH);
+  const float* q = qkv + (size_t)m * QKV + h * HD;
+  const float* kb = kc + ((size_t)layer * KVH + kh) * ctx * HD;
+  const float* vb = vc + ((size_t)layer * KVH + kh) * ctx * HD;
+  float* sq = sm;
+  float* sc = sm + HD;
+  for (int i = tid; i < HD; i += 64) sq[i] = q[i];
+  __syncthreads();
+  const float scale = 1.0f / __builtin_sqrtf((float)HD);
+  float lmax = -1e30f;
+  for (int t = tid; t < T; t += 64) {
+    const float4* kr = reinterpret_cast<const float4*>(kb + (size_t)t * HD);
+    const float4* qr = reinterpret_cast<const float4*>(sq);
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    for (int i4 = 0; i4 < HD / 4; i4++) {
+      const float4 kv = kr[i4], qv = qr[i4];
+      s0 = s0 + qv.x * kv.x;
+      s1 = s1 + qv.y * kv.y;
+      s2 = s2 + qv.z * kv.z;
+      s3 = s3 + qv.w * kv.w;
+    }
+    const float v = (s0 + s1 + s2 + s3) * scale;
+    sc[t] = v;
+    lmax = __builtin_fmaxf(lmax, v);
+  }
+  red[tid] = lmax;
+  __syncthreads();
+  if (tid == 0) {
+    float mx = red[0];
+    for (int i = 1; i < 64; i++) mx = __builtin_fmaxf(mx, red[i]);
+    red[0] = mx;
+  }
+  __syncthreads();
+  const float mx = red[0];
+  for (int t = tid; t < T; t += 64) sc[t] = fast_exp(sc[t] - mx);
+  __syncthreads();
+  if (tid == 0) {
+    float sum = 0.0f;
+    for (int t = 0; t < T; t++) sum = sum + sc[t];
+    red[1] = sum;
+  }
+  __syncthreads();
+  const float sum = red[1];
+  for (int t = tid; t < T; t += 64) sc[t] = sc[t] / sum;
+  __syncthreads();
+  for (int i = tid; i < HD; i += 64) {
+    float acc = 0.0f;
+    const float* vp = vb + i;
+    int t = 0;
+    for (; t + 4 <= T; t += 4) {
+      const float v0 = vp[(size_t)t * HD], v1 = vp[(size_t)(t + 1) * HD];
+      const float v2 = vp[(size_t)(t + 2) * HD], v3 = vp[(size_t)(t + 3) * HD];
+      acc = acc + sc[t] * v0;
+      acc = acc + sc[t + 1] * v1;
+      acc = acc + sc[t + 2] * v2;
+      acc = acc + sc[t + 3] * v3;
+    }
+    for (; t < T; t++) acc = acc + sc[t] * vp[(size_t)t * HD];
+    att[(size_t)m * D + h * HD + i] = acc;
+  }
+}
+
+// Greedy sample, stage 1: (max, first index) per 4096-entry slice (cpu-worker.js:156-157).
+__device__ __forceinline__ void amax_merge(float& bv, int& bi, float v, int i) {
+  if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) { bv = v; bi = i; }
+}
+
+__global__ __launch_bounds__(256) void k_argmax1(const float* __restrict__ lg, int V, float* __restrict__ pv,
+                                                 int* __restrict__ pi) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const int tid = threadIdx.x;
+  const int lo = blockIdx.x * 4096, hi = min(V, lo + 4096);
+  float bv = 0.0f;
+  int bi = -1;
+  for (int i = lo + tid; i < hi; i += 256) amax_merge(bv, bi, lg[i], i);
+  sv[tid] = bv;
+  si[tid] = bi;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) {
+      float v = sv[tid];
+      int i = si[tid];
+      amax_merge(v, i, sv[tid + s], si[tid + s]);
+      sv[tid] = v;
+      si[tid] = i;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) { pv[blockIdx.x] = sv[0]; pi[blockIdx.x] = si[0]; }
+}
+
+// Stage 2: reduce the slices, write tokens[pos0+M] = next and advance pos0 by M, so the next
+// replay of the decode graph runs the sampled token.
+__global__ __launch_bounds__(256) void k_argmax2(const float* __restrict__ pv, const int* __restrict__ pi, int P,
+                                                 int* __restrict__ tokens, State* __restrict__ st, int M) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const int tid = threadIdx.x;
+  float bv = 0.0f;
+  int bi = -1;
+  for (int i = tid; i < P; i += 256) amax_merge(bv, bi, pv[i], pi[i]);
+  sv[tid] = bv;
+  si[tid] = bi;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) {
+      float v = sv[tid];
+      int i = si[tid];
+      amax_merge(v, i, sv[tid + s], si[tid + s]);
+      sv[tid] = v;
+      si[tid] = i;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const int next = si[0] < 0 ? 0 : si[0];
+    const int p = st->pos0 + M;
+    tokens[p] = next;
+    st->next = next;
+    st->pos0 = p;
+  }
+}
+
+__global__ void k_set_pos(State* st, int pos0) {
+  if (threadIdx.x == 0) st->pos0 = pos0;
+}
+
+// ================================================================ host side
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIPCHK(call)                                                                   \
+  do {                                                                                 \
+    hipError_t e_ = (call);                                                            \
+    if (e_ != hipSuccess) return fail(Q4HIP_EHIP, "%s: %s", #call, hipGetErrorString(e_)); \
+  } while (0)
+
+struct Mat {
+  uint32_t* qs = nullptr;
+  uint16_t* d = nullptr;
+  int N = 0, K = 0, nb = 0, nb8 = 0, Np = 0;
+  int64_t loaded = 0;
+};
+
+int mat_alloc(Mat& m, int N, int K) {
+  m.N = N;
+  m.K = K;
+  m.nb = K / 32;
+  m.nb8 = (m.nb + 7) / 8;
+  m.Np = (N + kRowTile - 1) / kRowTile * kRowTile;
+  const size_t qbytes = (size_t)m.Np * m.nb * 16, dbytes = (size_t)m.Np * m.nb8 * 16;
+  HIPCHK(hipMalloc(&m.qs, qbytes));
+  HIPCHK(hipMalloc(&m.d, dbytes));
+  HIPCHK(hipMemset(m.qs, 0, qbytes));
+  HIPCHK(hipMemset(m.d, 0, dbytes));
+  return Q4HIP_OK;
+}
+
+void mat_free(Mat& m) {
+  if (m.qs) (void)hipFree(m.qs);
+  if (m.d) (void)hipFree(m.d);
+  m.qs = nullptr;
+  m.d = nullptr;
+}
+
+// Upload GGUF Q4_0 rows [row0, row0+rows) of m through a device staging buffer.
+int mat_upload(Mat& m, int row0, int64_t rows, const void* data, hipStream_t s) {
+  if (row0 < 0 || rows <= 0 || row0 + rows > m.N) return fail(Q4HIP_EINVAL, "rows %d..%lld outside 0..%d", row0, (long long)(row0 + rows), m.N);
+  const size_t bytes = (size_t)rows * m.nb * 18;
+  uint8_t* raw = nullptr;
+  HIPCHK(hipMalloc(&raw, bytes));
+  hipError_t e = hipMemcpyAsync(raw, data, bytes, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) {
+    const int64_t n = rows * m.nb;
+    k_repack_q4<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(raw, rows, m.nb, m.nb8, row0, m.qs, m.d);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  (void)hipFree(raw);
+  if (e != hipSuccess) return fail(Q4HIP_EHIP, "Q4_0 upload: %s", hipGetErrorString(e));
+  m.loaded += rows;
+  return Q4HIP_OK;
+}
+
+struct Layer {
+  Mat qkv, o, gu, down;
+  float *attn_norm = nullptr, *ffn_norm = nullptr, *bqkv = nullptr;
+  int64_t n_attn_norm = 0, n_ffn_norm = 0, n_bqkv = 0;
+};
+
+}  // namespace
+
+struct q4hip {
+  int D, NL, F, H, KVH, HD, QKV, V, ctx, MT, device;
+  float eps;
+  hipStream_t stream = nullptr;
+  std::vector<Layer> L;
+  Mat head;
+  uint8_t* embd = nullptr;
+  int64_t embd_loaded = 0;
+  float* out_norm = nullptr;
+  int64_t n_out_norm = 0;
+  float* rope = nullptr;
+  bool rope_set = false;
+  float *x = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *logits = nullptr;
+  float *kc = nullptr, *vc = nullptr;
+  uint4* xq = nullptr;
+  int xstride = 0;   // activation blocks per token row of xq
+  float* am_v = nullptr;
+  int* am_i = nullptr;
+  int am_parts = 0;
+  int* tokens = nullptr;
+  State* st = nullptr;
+  int* pin_ids = nullptr;     // pinned staging: token ids in, ids out
+  int* pin_next = nullptr;
+  hipGraphExec_t graph = nullptr;
+  bool graph_failed = false;
+  // profiling: events recorded around each launch of an eager step
+  std::vector<std::pair<int, hipEvent_t>>* prof = nullptr;
+};
+
+namespace {
+
+void prof_mark(q4hip* h, int cls) {
+  if (!h->prof) return;
+  hipEvent_t e;
+  if (hipEventCreate(&e) != hipSuccess) return;
+  (void)hipEventRecord(e, h->stream);
+  h->prof->push_back({cls, e});
+}
+
+int check_ready(q4hip* h) {
+  for (int l = 0; l < h->NL; l++) {
+    const Layer& y = h->L[l];
+    if (y.qkv.loaded < y.qkv.N || y.o.loaded < y.o.N || y.gu.loaded < y.gu.N || y.down.loaded < y.down.N)
+      return fail(Q4HIP_ESTATE, "layer %d: weights not fully loaded", l);
+    if (y.n_attn_norm < h->D || y.n_ffn_norm < h->D || y.n_bqkv < h->QKV)
+      return fail(Q4HIP_ESTATE, "layer %d: norms or bias not loaded", l);
+  }
+  if (h->embd_loaded < h->V) return fail(Q4HIP_ESTATE, "token embedding not loaded");
+  if (h->head.loaded < h->head.N) return fail(Q4HIP_ESTATE, "output head not loaded");
+  if (h->n_out_norm < h->D) return fail(Q4HIP_ESTATE, "output norm not loaded");
+  if (!h->rope_set) return fail(Q4HIP_ESTATE, "RoPE table not set");
+  return Q4HIP_OK;
+}
+
+template <int OP>
+void launch_matvec(q4hip* h, const Mat& W, int M, float* y, int ldy, const float* bias) {
+  const unsigned grid = (unsigned)(W.Np / 16);
+  if (M == 1)
+    k_matvec<1, OP><<<grid, 64, 0, h->stream>>>(W.qs, (const uint4*)W.d, W.nb, W.nb8, h->xq, h->xstride, 1, y, ldy, W.N, bias);
+  else
+    k_matvec<kMaxChunk, OP><<<grid, 64, 0, h->stream>>>(W.qs, (const uint4*)W.d, W.nb, W.nb8, h->xq, h->xstride, M, y, ldy, W.N, bias);
+}
+
+// One pass over M <= MT tokens at device position st->pos0 (forward_pass, kernels.c:306-415).
+void enqueue_pass(q4hip* h, int M, bool want_logits) {
+  const int D = h->D, F = h->F, HD = h->HD, QKV = h->QKV;
+  hipStream_t s = h->stream;
+  prof_mark(h, Q4HIP_PROF_EMBED);
+  k_embed<<<M, 256, 0, s>>>(h->embd, D, h->tokens, h->st, h->x);
+  const size_t attn_lds = (size_t)(HD + h->ctx) * sizeof(float);
+  for (int l = 0; l < h->NL; l++) {
+    Layer& y = h->L[l];
+    prof_mark(h, Q4HIP_PROF_NORM_Q);
+    k_quant<QM_NORM><<<M, 256, 0, s>>>(h->x, D, D, y.attn_norm, h->eps, h->xq, h->xstride, 0);
+    prof_mark(h, Q4HIP_PROF_QKV);
+    launch_matvec<OP_BIAS>(h, y.qkv, M, h->qkv, QKV, y.bqkv);
+    prof_mark(h, Q4HIP_PROF_ROPE);
+    k_rope_kv<<<dim3(h->H + h->KVH, M), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, h->kc, h->vc, h->ctx, l, h->st);
+    prof_mark(h, Q4HIP_PROF_ATTN);
+    k_attn<<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->kc, h->vc, h->ctx, l, h->att, h->st);
+    prof_mark(h, Q4HIP_PROF_QUANT);
+    k_quant<QM_PLAIN><<<M, 256, 0, s>>>(h->att, D, D, nullptr, 0.0f, h->xq, h->xstride, 0);
+    prof_mark(h, Q4HIP_PROF_O);
+    launch_matvec<OP_ADD>(h, y.o, M, h->x, D, nullptr);
+    prof_mark(h, Q4HIP_PROF_NORM_Q);
+    k_quant<QM_NORM><<<M, 256, 0, s>>>(h->x, D, D, y.ffn_norm, h->eps, h->xq, h->xstride, 0);
+    prof_mark(h, Q4HIP_PROF_GU);
+    launch_matvec<OP_STORE>(h, y.gu, M, h->gu, 2 * F, nullptr);
+    prof_mark(h, Q4HIP_PROF_SWIGLU);
+    k_quant<QM_SWIGLU><<<M, 256, 0, s>>>(h->gu, 2 * F, F, nullptr, 0.0f, h->xq, h->xstride, 0);
+    prof_mark(h, Q4HIP_PROF_DOWN);
+    launch_matvec<OP_ADD>(h, y.down, M, h->x, D, nullptr);
+  }
+  if (want_logits) {
+    prof_mark(h, Q4HIP_PROF_OUT);
+    k_quant<QM_NORM><<<1, 256, 0, s>>>(h->x, D, D, h->out_norm, h->eps, h->xq, h->xstride, M - 1);
+    launch_matvec<OP_STORE>(h, h->head, 1, h->logits, h->V, nullptr);
+    prof_mark(h, Q4HIP_PROF_SAMPLE);
+    k_argmax1<<<h->am_parts, 256, 0, s>>>(h->logits, h->V, h->am_v, h->am_i);
+    k_argmax2<<<1, 256, 0, s>>>(h->am_v, h->am_i, h->am_parts, h->tokens, h->st, M);
+  }
+  prof_mark(h, -1);
+}
+
+int build_graph(q4hip* h) {
+  if (h->graph || h->graph_failed) return Q4HIP_OK;
+  hipGraph_t g = nullptr;
+  if (hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+    h->graph_failed = true;
+    (void)hipGetLastError();
+    return Q4HIP_OK;
+  }
+  enqueue_pass(h, 1, true);
+  hipError_t e = hipStreamEndCapture(h->stream, &g);
+  if (e == hipSuccess) e = hipGraphInstantiate(&h->graph, g, nullptr, nullptr, 0);
+  if (g) (void)hipGraphDestroy(g);
+  if (e != hipSuccess) {
+    h->graph = nullptr;
+    h->graph_failed = true;
+    (void)hipGetLastError();
+  }
+  return Q4HIP_OK;
+}
+
+void decode_step(q4hip* h) {
+  if (h->graph) (void)hipGraphLaunch(h->graph, h->stream);
+  else enqueue_pass(h, 1, true);
+}
+
+}  // namespace
+
+// ================================================================ C ABI
+
+extern "C" {
+
+const char* q4hip_last_error(void) { return g_err.c_str(); }
+
+int q4hip_device_count(int* count) {
+  if (!count) return fail(Q4HIP_EINVAL, "null argument");
+  HIPCHK(hipGetDeviceCount(count));
+  return Q4HIP_OK;
+}
+
+void q4hip_destroy(q4hip* h) {
+  if (!h) return;
+  (void)hipSetDevice(h->device);
+  if (h->stream) (void)hipStreamSynchronize(h->stream);
+  if (h->graph) (void)hipGraphExecDestroy(h->graph);
+  for (Layer& y : h->L) {
+    mat_free(y.qkv); mat_free(y.o); mat_free(y.gu); mat_free(y.down);
+    if (y.attn_norm) (void)hipFree(y.attn_norm);
+    if (y.ffn_norm) (void)hipFree(y.ffn_norm);
+    if (y.bqkv) (void)hipFree(y.bqkv);
+  }
+  mat_free(h->head);
+  void* bufs[] = {h->embd, h->out_norm, h->rope, h->x, h->qkv, h->att, h->gu, h->logits, h->kc, h->vc,
+                  h->xq, h->am_v, h->am_i, h->tokens, h->st};
+  for (void* p : bufs) if (p) (void)hipFree(p);
+  if (h->pin_ids) (void)hipHostFree(h->pin_ids);
+  if (h->pin_next) (void)hipHostFree(h->pin_next);
+  if (h->stream) (void)hipStreamDestroy(h->stream);
+  delete h;
+}
+
+int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_heads, int vocab, int ctx,
+                 int mt, float eps, int device) {
+  if (!out) return fail(Q4HIP_EINVAL, "null argument");
+  *out = nullptr;
+  if (dim <= 0 || layers <= 0 || ffn <= 0 || heads <= 0 || kv_heads <= 0 || vocab <= 0 || ctx <= 1)
+    return fail(Q4HIP_EINVAL, "bad configuration");
+  if (dim % 32 || ffn % 32 || dim % heads || heads % kv_heads)
+    return fail(Q4HIP_EINVAL, "dim and ffn must be multiples of 32, heads a multiple of kv_heads");
+  const int HD = dim / heads;
+  if (HD % 4 || HD > 256) return fail(Q4HIP_EINVAL, "head_dim %d unsupported", HD);
+  if ((size_t)(HD + ctx) * 4 > 65536) return fail(Q4HIP_EINVAL, "ctx %d too large for the attention kernel", ctx);
+  if (mt <= 0 || mt > kMaxChunk) mt = kMaxChunk;
+  int ndev = 0;
+  HIPCHK(hipGetDeviceCount(&ndev));
+  if (device < 0 || device >= ndev) return fail(Q4HIP_EINVAL, "device %d of %d", device, ndev);
+  HIPCHK(hipSetDevice(device));
+
+  q4hip* h = new q4hip();
+  h->D = dim; h->NL = layers; h->F = ffn; h->H = heads; h->KVH = kv_heads; h->HD = HD;
+  h->QKV = dim + 2 * kv_heads * HD; h->V = vocab; h->ctx = ctx; h->MT = mt; h->device = device; h->eps = eps;
+  int rc = Q4HIP_OK;
+#define TRY(x) do { rc = (x); if (rc != Q4HIP_OK) { q4hip_destroy(h); return rc; } } while (0)
+#define TRYHIP(call) do { hipError_t e_ = (call); if (e_ != hipSuccess) { rc = fail(Q4HIP_EHIP, "%s: %s", #call, hipGetErrorString(e_)); q4hip_destroy(h); return rc; } } while (0)
+  TRYHIP(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+  h->L.resize(layers);
+  for (int l = 0; l < layers; l++) {
+    Layer& y = h->L[l];
+    TRY(mat_alloc(y.qkv, h->QKV, dim));
+    TRY(mat_alloc(y.o, dim, dim));
+    TRY(mat_alloc(y.gu, 2 * ffn, dim));
+    TRY(mat_alloc(y.down, dim, ffn));
+    TRYHIP(hipMalloc(&y.attn_norm, (size_t)dim * 4));
+    TRYHIP(hipMalloc(&y.ffn_norm, (size_t)dim * 4));
+    TRYHIP(hipMalloc(&y.bqkv, (size_t)h->QKV * 4));
+  }
+  TRY(mat_alloc(h->head, vocab, dim));
+  TRYHIP(hipMalloc(&h->embd, (size_t)vocab * (dim / 32) * 18));
+  TRYHIP(hipMalloc(&h->out_norm, (size_t)dim * 4));
+  TRYHIP(hipMalloc(&h->rope, (size_t)ctx * HD * 4));
+  const int M = mt;
+  h->xstride = std::max(dim, ffn) / 32;
+  TRYHIP(hipMalloc(&h->x, (size_t)M * dim * 4));
+  TRYHIP(hipMalloc(&h->qkv, (size_t)M * h->QKV * 4));
+  TRYHIP(hipMalloc(&h->att, (size_t)M * dim * 4));
+  TRYHIP(hipMalloc(&h->gu, (size_t)M * 2 * ffn * 4));
+  TRYHIP(hipMalloc(&h->logits, (size_t)vocab * 4));
+  const size_t kvbytes = (size_t)layers * kv_heads * ctx * HD * 4;
+  TRYHIP(hipMalloc(&h->kc, kvbytes));
+  TRYHIP(hipMalloc(&h->vc, kvbytes));
+  TRYHIP(hipMemset(h->kc, 0, kvbytes));
+  TRYHIP(hipMemset(h->vc, 0, kvbytes));
+  TRYHIP(hipMalloc(&h->xq, (size_t)M * h->xstride * 64));
+  h->am_parts = (vocab + 4095) / 4096;
+  TRYHIP(hipMalloc(&h->am_v, (size_t)h->am_parts * 4));
+  TRYHIP(hipMalloc(&h->am_i, (size_t)h->am_parts * 4));
+  TRYHIP(hipMalloc(&h->tokens, (size_t)(ctx + 1) * 4));
+  TRYHIP(hipMemset(h->tokens, 0, (size_t)(ctx + 1) * 4));
+  TRYHIP(hipMalloc(&h->st, sizeof(State)));
+  TRYHIP(hipMemset(h->st, 0, sizeof(State)));
+  TRYHIP(hipHostMalloc(&h->pin_ids, (size_t)(ctx + 1) * 4, hipHostMallocDefault));
+  TRYHIP(hipHostMalloc(&h->pin_next, 64, hipHostMallocDefault));
+#undef TRY
+#undef TRYHIP
+  *out = h;
+  return Q4HIP_OK;
+}
+
+int q4hip_set_tensor(q4hip* h, int kind, int layer, int row0, int type, const void* data, int64_t rows,
+                     size_t nbytes) {
+  if (!h || !data) return fail(Q4HIP_EINVAL, "null argument");
+  if (rows <= 0) return fail(Q4HIP_EINVAL, "no rows");
+  {
+    // bytes per row of this kind and type
+    const int64_t K = (kind == 3) ? h->F : h->D;
+    int64_t per = 0;
+    if (type == Q4HIP_TYPE_F32) per = 4;
+    else if (type == Q4HIP_TYPE_Q4_0) per = K / 32 * 18;
+    else if (type == Q4HIP_TYPE_Q8_0) per = K / 32 * 34;
+    if (per > 0 && (uint64_t)rows * (uint64_t)per > (uint64_t)nbytes)
+      return fail(Q4HIP_EINVAL, "kind %d: %zu bytes given, %lld rows need %lld", kind, nbytes, (long long)rows,
+                  (long long)(rows * per));
+  }
+  HIPCHK(hipSetDevice(h->device));
+  const bool per_layer = kind >= 0 && kind <= 6;
+  if (per_layer && (layer < 0 || layer >= h->NL)) return fail(Q4HIP_EINVAL, "layer %d of %d", layer, h->NL);
+  if (kind >= 0 && kind <= 3) {
+    if (type != Q4HIP_TYPE_Q4_0) return fail(Q4HIP_ETYPE, "kind %d: expected Q4_0", kind);
+    Layer& y = h->L[layer];
+    Mat* m = kind == 0 ? &y.qkv : kind == 1 ? &y.o : kind == 2 ? &y.gu : &y.down;
+    return mat_upload(*m, row0, rows, data, h->stream);
+  }
+  if (kind == 4 || kind == 5 || kind == 6 || kind == 9) {
+    if (type != Q4HIP_TYPE_F32) return fail(Q4HIP_ETYPE, "kind %d: expected F32", kind);
+    float* dst;
+    int64_t cap, *cnt;
+    if (kind == 4) { dst = h->L[layer].attn_norm; cap = h->D; cnt = &h->L[layer].n_attn_norm; }
+    else if (kind == 5) { dst = h->L[layer].ffn_norm; cap = h->D; cnt = &h->L[layer].n_ffn_norm; }
+    else if (kind == 6) { dst = h->L[layer].bqkv; cap = h->QKV; cnt = &h->L[layer].n_bqkv; }
+    else { dst = h->out_norm; cap = h->D; cnt = &h->n_out_norm; }
+    if (row0 < 0 || rows <= 0 || row0 + rows > cap) return fail(Q4HIP_EINVAL, "kind %d: values %d..%lld outside 0..%lld", kind, row0, (long long)(row0 + rows), (long long)cap);
+    HIPCHK(hipMemcpy(dst + row0, data, (size_t)rows * 4, hipMemcpyHostToDevice));
+    *cnt += rows;
+    return Q4HIP_OK;
+  }
+  if (kind == 7) {
+    if (type != Q4HIP_TYPE_Q4_0) return fail(Q4HIP_ETYPE, "kind 7: expected Q4_0");
+    if (row0 < 0 || rows <= 0 || row0 + rows > h->V) return fail(Q4HIP_EINVAL, "embedding rows outside 0..%d", h->V);
+    const size_t rb = (size_t)(h->D / 32) * 18;
+    HIPCHK(hipMemcpy(h->embd + (size_t)row0 * rb, data, (size_t)rows * rb, hipMemcpyHostToDevice));
+    h->embd_loaded += rows;
+    return Q4HIP_OK;
+  }
+  if (kind == 8) {
+    if (type != Q4HIP_TYPE_Q4_0) return fail(Q4HIP_ETYPE, "kind 8: expected Q4_0");
+    return mat_upload(h->head, row0, rows, data, h->stream);
+  }
+  return fail(Q4HIP_EINVAL, "unknown tensor kind %d", kind);
+}
+
+int q4hip_set_rope(q4hip* h, const float* table, int n_pos) {
+  if (!h || !table) return fail(Q4HIP_EINVAL, "null argument");
+  if (n_pos < h->ctx) return fail(Q4HIP_EINVAL, "RoPE table has %d positions, ctx is %d", n_pos, h->ctx);
+  HIPCHK(hipSetDevice(h->device));
+  HIPCHK(hipMemcpy(h->rope, table, (size_t)h->ctx * h->HD * 4, hipMemcpyHostToDevice));
+  h->rope_set = true;
+  return Q4HIP_OK;
+}
+
+static int check_ids(q4hip* h, const int* ids, int n) {
+  for (int i = 0; i < n; i++)
+    if (ids[i] < 0 || ids[i] >= h->V) return fail(Q4HIP_EINVAL, "token id %d out of range 0..%d", ids[i], h->V - 1);
+  return Q4HIP_OK;
+}
+
+int q4hip_forward(q4hip* h, const int* ids, int n, int pos, int* next) {
+  if (!h || !ids || !next) return fail(Q4HIP_EINVAL, "null argument");
+  if (n <= 0) return fail(Q4HIP_EINVAL, "no tokens");
+  if (pos < 0 || (int64_t)pos + n >= h->ctx) return fail(Q4HIP_ECONTEXT, "context full");
+  int rc = check_ready(h);
+  if (rc) return rc;
+  rc = check_ids(h, ids, n);
+  if (rc) return rc;
+  HIPCHK(hipSetDevice(h->device));
+  if (n == 1) build_graph(h);
+  memcpy(h->pin_ids, ids, (size_t)n * 4);
+  HIPCHK(hipMemcpyAsync(h->tokens + pos, h->pin_ids, (size_t)n * 4, hipMemcpyHostToDevice, h->stream));
+  for (int c = 0; c < n; c += h->MT) {
+    const int k = std::min(h->MT, n - c);
+    const bool last = c + k >= n;
+    k_set_pos<<<1, 64, 0, h->stream>>>(h->st, pos + c);
+    if (k == 1 && last && h->graph) HIPCHK(hipGraphLaunch(h->graph, h->stream));
+    else enqueue_pass(h, k, last);
+  }
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(h->pin_next, &h->st->next, 4, hipMemcpyDeviceToHost, h->stream));
+  HIPCHK(hipStreamSynchronize(h->stream));
+  *next = h->pin_next[0];
+  return Q4HIP_OK;
+}
+
+int q4hip_read_logits(q4hip* h, float* out, int n) {
+  if (!h || !out) return fail(Q4HIP_EINVAL, "null argument");
+  if (n < h->V) return fail(Q4HIP_EINVAL, "buffer of %d floats, vocab is %d", n, h->V);
+  HIPCHK(hipSetDevice(h->device));
+  HIPCHK(hipStreamSynchronize(h->stream));
+  HIPCHK(hipMemcpy(out, h->logits, (size_t)h->V * 4, hipMemcpyDeviceToHost));
+  return Q4HIP_OK;
+}
+
+static int run_generate(q4hip* h, int first, int pos, int steps, int* out, float* ms) {
+  if (!h || (steps > 0 && !out)) return fail(Q4HIP_EINVAL, "null argument");
+  if (steps <= 0) return fail(Q4HIP_EINVAL, "steps must be positive");
+  if (pos < 0 || (int64_t)pos + steps >= h->ctx) return fail(Q4HIP_ECONTEXT, "context full");
+  int rc = check_ready(h);
+  if (rc) return rc;
+  rc = check_ids(h, &first, 1);
+  if (rc) return rc;
+  HIPCHK(hipSetDevice(h->device));
+  build_graph(h);
+  h->pin_ids[0] = first;
+  HIPCHK(hipMemcpyAsync(h->tokens + pos, h->pin_ids, 4, hipMemcpyHostToDevice, h->stream));
+  k_set_pos<<<1, 64, 0, h->stream>>>(h->st, pos);
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (ms) {
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    HIPCHK(hipEventRecord(e0, h->stream));
+  }
+  for (int i = 0; i < steps; i++) decode_step(h);
+  if (ms) HIPCHK(hipEventRecord(e1, h->stream));
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(h->pin_ids, h->tokens + pos + 1, (size_t)steps * 4, hipMemcpyDeviceToHost, h->stream));
+  HIPCHK(hipStreamSynchronize(h->stream));
+  memcpy(out, h->pin_ids, (size_t)steps * 4);
+  if (ms) {
+    HIPCHK(hipEventElapsedTime(ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+  }
+  return Q4HIP_OK;
+}
+
+int q4hip_generate(q4hip* h, int first, int pos, int steps, int* out) {
+  return run_generate(h, first, pos, steps, out, nullptr);
+}
+
+int q4hip_time_generate(q4hip* h, int first, int pos, int steps, int* out, float* ms) {
+  if (!ms) return fail(Q4HIP_EINVAL, "null argument");
+  return run_generate(h, first, pos, steps, out, ms);
+}
+
+int q4hip_profile(q4hip* h, int token, int pos, float* us, int n) {
+  if (!h || !us) return fail(Q4HIP_EINVAL, "null argument");
+  if (n < Q4HIP_PROF_N) return fail(Q4HIP_EINVAL, "need %d entries", Q4HIP_PROF_N);
+  if (pos < 0 || pos + 1 >= h->ctx) return fail(Q4HIP_ECONTEXT, "context full");
+  int rc = check_ready(h);
+  if (rc) return rc;
+  rc = check_ids(h, &token, 1);
+  if (rc) return rc;
+  HIPCHK(hipSetDevice(h->device));
+  h->pin_ids[0] = token;
+  HIPCHK(hipMemcpyAsync(h->tokens + pos, h->pin_ids, 4, hipMemcpyHostToDevice, h->stream));
+  k_set_pos<<<1, 64, 0, h->stream>>>(h->st, pos);
+  std::vector<std::pair<int, hipEvent_t>> marks;
+  h->prof = &marks;
+  enqueue_pass(h, 1, true);
+  h->prof = nullptr;
+  hipError_t e = hipStreamSynchronize(h->stream);
+  for (int i = 0; i < Q4HIP_PROF_N; i++) us[i] = 0.0f;
+  for (size_t i = 0; i + 1 < marks.size(); i++) {
+    float ms = 0.0f;
+    if (e == hipSuccess && hipEventElapsedTime(&ms, marks[i].second, marks[i + 1].second) == hipSuccess &&
+        marks[i].first >= 0)
+      us[marks[i].first] += ms * 1000.0f;
+  }
+  for (auto& p : marks) (void)hipEventDestroy(p.second);
+  if (e != hipSuccess) return fail(Q4HIP_EHIP, "profile: %s", hipGetErrorString(e));
+  return Q4HIP_OK;
+}
+
+int q4hip_time_head(q4hip* h, int iters, float* us_per_launch) {
+  if (!h || !us_per_launch || iters <= 0) return fail(Q4HIP_EINVAL, "bad argument");
+  int rc = check_ready(h);
+  if (rc) return rc;
+  HIPCHK(hipSetDevice(h->device));
+  hipEvent_t e0, e1;
+  HIPCHK(hipEventCreate(&e0));
+  HIPCHK(hipEventCreate(&e1));
+  HIPCHK(hipEventRecord(e0, h->stream));
+  for (int i = 0; i < iters; i++) launch_matvec<OP_STORE>(h, h->head, 1, h->logits, h->V, nullptr);
+  HIPCHK(hipEventRecord(e1, h->stream));
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipEventSynchronize(e1));
+  float ms = 0.0f;
+  HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *us_per_launch = ms * 1000.0f / iters;
+  return Q4HIP_OK;
+}
+
+// ---------------------------------------------------------------- isolated matvec
+
+struct q4hip_mv {
+  int device;
+  hipStream_t stream;
+  Mat W;
+  float *x, *y;
+  uint4* xq;
+};
+
+void q4hip_mv_destroy(q4hip_mv* m) {
+  if (!m) return;
+  (void)hipSetDevice(m->device);
+  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  mat_free(m->W);
+  if (m->x) (void)hipFree(m->x);
+  if (m->y) (void)hipFree(m->y);
+  if (m->xq) (void)hipFree(m->xq);
+  if (m->stream) (void)hipStreamDestroy(m->stream);
+  delete m;
+}
+
+int q4hip_mv_create(q4hip_mv** out, int N, int K, const void* w, int device) {
+  if (!out || !w) return fail(Q4HIP_EINVAL, "null argument");
+  *out = nullptr;
+  if (N <= 0 || K <= 0 || K % 32) return fail(Q4HIP_EINVAL, "bad shape %d x %d", N, K);
+  int ndev = 0;
+  HIPCHK(hipGetDeviceCount(&ndev));
+  if (device < 0 || device >= ndev) return fail(Q4HIP_EINVAL, "device %d of %d", device, ndev);
+  HIPCHK(hipSetDevice(device));
+  q4hip_mv* m = new q4hip_mv();
+  m->device = device;
+  m->stream = nullptr; m->x = nullptr; m->y = nullptr; m->xq = nullptr;
+  int rc = Q4HIP_OK;
+  hipError_t e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipMalloc(&m->x, (size_t)K * 4);
+  if (e == hipSuccess) e = hipMalloc(&m->y, (size_t)N * 4);
+  if (e == hipSuccess) e = hipMalloc(&m->xq, (size_t)(K / 32) * 64);
+  if (e != hipSuccess) { rc = fail(Q4HIP_EHIP, "matvec alloc: %s", hipGetErrorString(e)); q4hip_mv_destroy(m); return rc; }
+  rc = mat_alloc(m->W, N, K);
+  if (rc == Q4HIP_OK) rc = mat_upload(m->W, 0, N, w, m->stream);
+  if (rc != Q4HIP_OK) { q4hip_mv_destroy(m); return rc; }
+  *out = m;
+  return Q4HIP_OK;
+}
+
+static void mv_launch(q4hip_mv* m) {
+  k_matvec<1, OP_STORE><<<(unsigned)(m->W.Np / 16), 64, 0, m->stream>>>(
+      m->W.qs, (const uint4*)m->W.d, m->W.nb, m->W.nb8, m->xq, m->W.nb, 1, m->y, m->W.N, m->W.N, nullptr);
+}
+
+int q4hip_mv_run(q4hip_mv* m, const float* x, float* y) {
+  if (!m || !x || !y) return fail(Q4HIP_EINVAL, "null argument");
+  HIPCHK(hipSetDevice(m->device));
+  const int K = m->W.K;
+  HIPCHK(hipMemcpyAsync(m->x, x, (size_t)K * 4, hipMemcpyHostToDevice, m->stream));
+  k_quant<QM_PLAIN><<<1, 256, 0, m->stream>>>(m->x, K, K, nullptr, 0.0f, m->xq, K / 32, 0);
+  mv_launch(m);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(y, m->y, (size_t)m->W.N * 4, hipMemcpyDeviceToHost, m->stream));
+  HIPCHK(hipStreamSynchronize(m->stream));
+  return Q4HIP_OK;
+}
+
+int q4hip_mv_time(q4hip_mv* m, int iters, float* us) {
+  if (!m || !us || iters <= 0) return fail(Q4HIP_EINVAL, "bad argument");
+  HIPCHK(hipSetDevice(m->device));
+  hipEvent_t e0, e1;
+  HIPCHK(hipEventCreate(&e0));
+  HIPCHK(hipEventCreate(&e1));
+  HIPCHK(hipEventRecord(e0, m->stream));
+  for (int i = 0; i < iters; i++) mv_launch(m);
+  HIPCHK(hipEventRecord(e1, m->stream));
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipEventSynchronize(e1));
+  float ms = 0.0f;
+  HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *us = ms * 1000.0f / iters;
+  return Q4HIP_OK;
+}
+
+}  // extern "C"

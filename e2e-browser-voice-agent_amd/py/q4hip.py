@@ -1,0 +1,202 @@
+"""ctypes binding of the q4hip C ABI (include/q4hip.h) for Python callers: the tests and bench.py.
+
+The JavaScript backend (engine/hip.js) is the product's host; this module exposes the same C ABI
+to Python.  It loads the in-tree libq4hip.so and fails loudly when it is missing: there is no
+CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+import synth
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libq4hip.so")
+
+OK, EINVAL, ECONTEXT, ETYPE, EHIP, ESTATE = 0, 1, 2, 3, 4, 5
+PROF_NAMES = ["embed", "norm+quantize", "matvec qkv", "rope+kv", "attention", "quantize", "matvec o",
+              "matvec gate+up", "swiglu+quantize", "matvec down", "matvec output", "sample"]
+
+EXPORTS = [
+    "q4hip_last_error", "q4hip_device_count", "q4hip_create", "q4hip_set_tensor", "q4hip_set_rope",
+    "q4hip_forward", "q4hip_read_logits", "q4hip_generate", "q4hip_profile", "q4hip_time_generate",
+    "q4hip_time_head", "q4hip_destroy", "q4hip_mv_create", "q4hip_mv_run", "q4hip_mv_time",
+    "q4hip_mv_destroy",
+]
+
+_lib = None
+
+
+class Q4Error(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build() first")
+    L = ctypes.CDLL(LIB_PATH)
+    P, I, I64, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+    sig = {
+        "q4hip_last_error": (ctypes.c_char_p, []),
+        "q4hip_device_count": (I, [ctypes.POINTER(I)]),
+        "q4hip_create": (I, [ctypes.POINTER(P), I, I, I, I, I, I, I, I, F, I]),
+        "q4hip_set_tensor": (I, [P, I, I, I, I, P, I64, ctypes.c_size_t]),
+        "q4hip_set_rope": (I, [P, P, I]),
+        "q4hip_forward": (I, [P, P, I, I, ctypes.POINTER(I)]),
+        "q4hip_read_logits": (I, [P, P, I]),
+        "q4hip_generate": (I, [P, I, I, I, P]),
+        "q4hip_profile": (I, [P, I, I, P, I]),
+        "q4hip_time_generate": (I, [P, I, I, I, P, ctypes.POINTER(F)]),
+        "q4hip_time_head": (I, [P, I, ctypes.POINTER(F)]),
+        "q4hip_destroy": (None, [P]),
+        "q4hip_mv_create": (I, [ctypes.POINTER(P), I, I, P, I]),
+        "q4hip_mv_run": (I, [P, P, P]),
+        "q4hip_mv_time": (I, [P, I, ctypes.POINTER(F)]),
+        "q4hip_mv_destroy": (None, [P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != OK:
+        raise Q4Error(rc, lib().q4hip_last_error().decode())
+
+
+def _ptr(a: np.ndarray) -> ctypes.c_void_p:
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    _check(lib().q4hip_device_count(ctypes.byref(n)))
+    return n.value
+
+
+class Model:
+    """One loaded model on one GPU: the backend object's C side."""
+
+    def __init__(self, shape: synth.Shape, ctx: int = 2048, mt: int = 16, device: int = 0):
+        self.shape, self.ctx = shape, ctx
+        h = ctypes.c_void_p()
+        _check(lib().q4hip_create(ctypes.byref(h), shape.dim, shape.layers, shape.ffn, shape.heads,
+                                  shape.kv_heads, shape.vocab, ctx, mt, ctypes.c_float(shape.eps), device))
+        self.h = h
+
+    def close(self) -> None:
+        if self.h:
+            lib().q4hip_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_tensor(self, kind: int, layer: int, row0: int, t: synth.Tensor) -> None:
+        data = np.ascontiguousarray(t.data)
+        rows = t.rows if t.type != synth.GGML_F32 else data.size
+        _check(lib().q4hip_set_tensor(self.h, kind, layer, row0, t.type, _ptr(data), rows, data.nbytes))
+
+    def load(self, tensors: dict, rope: np.ndarray | None = None) -> None:
+        """Upload a model dict from synth.make_model, fusing q|k|v and gate|up as
+        engine/cpu-worker.js:106-128 does."""
+        s = self.shape
+        D, F, KV = s.dim, s.ffn, s.kv_heads * s.head_dim
+        for layer in range(s.layers):
+            p = f"blk.{layer}."
+            for kind, names, offs in [(0, ["attn_q", "attn_k", "attn_v"], [0, D, D + KV]), (1, ["attn_output"], [0]),
+                                      (2, ["ffn_gate", "ffn_up"], [0, F]), (3, ["ffn_down"], [0])]:
+                for n, o in zip(names, offs):
+                    self.set_tensor(kind, layer, o, tensors[p + n + ".weight"])
+            self.set_tensor(4, layer, 0, tensors[p + "attn_norm.weight"])
+            self.set_tensor(5, layer, 0, tensors[p + "ffn_norm.weight"])
+            for n, o in zip(["attn_q", "attn_k", "attn_v"], [0, D, D + KV]):
+                self.set_tensor(6, layer, o, tensors[p + n + ".bias"])
+        self.set_tensor(7, 0, 0, tensors["token_embd.weight"])
+        self.set_tensor(8, 0, 0, tensors["output.weight"])
+        self.set_tensor(9, 0, 0, tensors["output_norm.weight"])
+        if rope is None:
+            rope = synth.rope_table(self.ctx, s.head_dim, s.rope_theta)
+        rope = np.ascontiguousarray(rope, dtype=np.float32)
+        _check(lib().q4hip_set_rope(self.h, _ptr(rope), rope.shape[0]))
+
+    def forward(self, ids, pos: int) -> int:
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        nxt = ctypes.c_int(0)
+        _check(lib().q4hip_forward(self.h, _ptr(a), a.size, pos, ctypes.byref(nxt)))
+        return nxt.value
+
+    def read_logits(self) -> np.ndarray:
+        out = np.empty(self.shape.vocab, dtype=np.float32)
+        _check(lib().q4hip_read_logits(self.h, _ptr(out), out.size))
+        return out
+
+    def generate(self, first: int, pos: int, steps: int) -> list:
+        out = np.empty(steps, dtype=np.int32)
+        _check(lib().q4hip_generate(self.h, first, pos, steps, _ptr(out)))
+        return out.tolist()
+
+    def time_generate(self, first: int, pos: int, steps: int) -> tuple:
+        out = np.empty(steps, dtype=np.int32)
+        ms = ctypes.c_float(0)
+        _check(lib().q4hip_time_generate(self.h, first, pos, steps, _ptr(out), ctypes.byref(ms)))
+        return out.tolist(), ms.value
+
+    def profile(self, token: int, pos: int) -> dict:
+        us = np.zeros(len(PROF_NAMES), dtype=np.float32)
+        _check(lib().q4hip_profile(self.h, token, pos, _ptr(us), us.size))
+        return dict(zip(PROF_NAMES, us.tolist()))
+
+    def time_head(self, iters: int) -> float:
+        us = ctypes.c_float(0)
+        _check(lib().q4hip_time_head(self.h, iters, ctypes.byref(us)))
+        return us.value
+
+
+class Matvec:
+    """Isolated Q4_0 matvec y = W x (N x K, W in GGUF Q4_0 blocks)."""
+
+    def __init__(self, raw_q4: np.ndarray, N: int, K: int, device: int = 0):
+        self.N, self.K = N, K
+        data = np.ascontiguousarray(raw_q4, dtype=np.uint8)
+        assert data.size == N * (K // 32) * 18
+        h = ctypes.c_void_p()
+        _check(lib().q4hip_mv_create(ctypes.byref(h), N, K, _ptr(data), device))
+        self.h = h
+
+    def run(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        assert x.size == self.K
+        y = np.empty(self.N, dtype=np.float32)
+        _check(lib().q4hip_mv_run(self.h, _ptr(x), _ptr(y)))
+        return y
+
+    def time(self, iters: int) -> float:
+        us = ctypes.c_float(0)
+        _check(lib().q4hip_mv_time(self.h, iters, ctypes.byref(us)))
+        return us.value
+
+    def close(self) -> None:
+        if self.h:
+            lib().q4hip_mv_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,134 @@
+/*
+ * q4hip.h -- C ABI of the MI355X Qwen2 Q4_0 token loop.
+ *
+ * One opaque context per loaded model, bound to one GPU and one HIP stream.
+ * Calls on a context are serialized by the caller (one job at a time, as the
+ * reference backend's single `pending` slot does, engine/cpu.js:215-232);
+ * contexts are independent.  Every entry point returns Q4HIP_OK (0) or an
+ * error code; q4hip_last_error() gives the message of the calling thread's
+ * last failure ("context full", "kind 0: expected Q4_0", a HIP error ...).
+ *
+ * Reference paths below are relative to h2-own-inference-engine/.
+ */
+#ifndef Q4HIP_H
+#define Q4HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q4HIP_OK 0
+#define Q4HIP_EINVAL 1      /* bad argument or configuration                         */
+#define Q4HIP_ECONTEXT 2    /* pos + n >= ctx: "context full" (engine/cpu-worker.js:173) */
+#define Q4HIP_ETYPE 3       /* tensor of an unsupported GGML type for its kind        */
+#define Q4HIP_EHIP 4        /* HIP runtime failure (message names the call)           */
+#define Q4HIP_ESTATE 5      /* model not fully loaded, or context destroyed          */
+
+/* GGML tensor types accepted by q4hip_set_tensor (engine/gguf.js:6) */
+#define Q4HIP_TYPE_F32 0
+#define Q4HIP_TYPE_Q4_0 2
+#define Q4HIP_TYPE_Q8_0 8
+
+/* Tensor kinds, numbered as the reference's set_tensor (engine/kernels.c:422):
+ * 0 qkv, 1 o, 2 gate+up, 3 down (Q4_0); 4 attn_norm, 5 ffn_norm, 6 qkv bias (F32);
+ * 7 token embedding (Q4_0); 8 output head (Q4_0 or Q8_0); 9 output_norm (F32). */
+#define Q4HIP_KIND_QKV 0
+#define Q4HIP_KIND_O 1
+#define Q4HIP_KIND_GU 2
+#define Q4HIP_KIND_DOWN 3
+#define Q4HIP_KIND_ATTN_NORM 4
+#define Q4HIP_KIND_FFN_NORM 5
+#define Q4HIP_KIND_BQKV 6
+#define Q4HIP_KIND_EMBD 7
+#define Q4HIP_KIND_OUTPUT 8
+#define Q4HIP_KIND_OUTPUT_NORM 9
+
+typedef struct q4hip q4hip;
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* q4hip_last_error(void);
+
+/* Number of visible HIP devices. */
+int q4hip_device_count(int* count);
+
+/* Create a context: replaces set_config (engine/kernels.c:418-421) and the memory plan of
+ * engine/cpu-worker.js:52-88.  Allocates weights, activations for chunks of up to `mt` tokens,
+ * the fp32 KV cache for `ctx` positions and the token array on `device`.  head_dim = dim/heads. */
+int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_heads, int vocab,
+                 int ctx, int mt, float eps, int device);
+
+/* Upload one GGUF tensor (or a part of a fused one): replaces set_tensor (engine/kernels.c:423-431)
+ * together with copyBlocks (engine/cpu-worker.js:97-124).  `data` holds `rows` rows in GGUF
+ * layout (Q4_0 18-byte / Q8_0 34-byte blocks, or F32 values).  `row0` is the first row of the
+ * fused tensor they fill: q at 0, k at dim, v at dim + kv_heads*head_dim (kind 0 and its bias 6);
+ * gate at 0, up at ffn (kind 2).  For F32 kinds a "row" is one value.  `nbytes` is the size of
+ * `data`; a buffer shorter than `rows` rows is rejected. */
+int q4hip_set_tensor(q4hip* h, int kind, int layer, int row0, int ggml_type, const void* data,
+                     int64_t rows, size_t nbytes);
+
+/* Upload the RoPE table: fp32 [n_pos][head_dim/2][2] = cos, sin of pos/theta^(2i/head_dim),
+ * computed in double by the host as engine/cpu-worker.js:130-135 does.  n_pos >= ctx. */
+int q4hip_set_rope(q4hip* h, const float* table, int n_pos);
+
+/* Run tokens ids[0..n) at positions pos..pos+n-1 and return the greedy next token (first
+ * maximum wins): replaces forward() of engine/cpu-worker.js:169-182 with temperature 0, i.e.
+ * the chunk loop over run() (engine/kernels.c:454-465) plus sample() (cpu-worker.js:154-158).
+ * K/V of those positions are (over)written; logits of the last token stay on the device. */
+int q4hip_forward(q4hip* h, const int* ids, int n, int pos, int* next);
+
+/* Copy the last forward's logits (vocab floats) to host memory: readLogits (engine/cpu.js:242). */
+int q4hip_read_logits(q4hip* h, float* out, int n);
+
+/* Greedy continuation on the device: token `first` at position `pos`, then `steps` decode steps,
+ * each feeding back its own argmax; out[i] = token at position pos+1+i.  The same tokens as
+ * `steps` calls of forward([t], pos+i) (engine/llm.js:86-97) without a host round trip per step. */
+int q4hip_generate(q4hip* h, int first, int pos, int steps, int* out);
+
+/* Per-operation GPU time of one decode step (forward([token], pos)), in microseconds, summed
+ * over layers: profile (engine/cpu-worker.js:31-37, engine/kernels.c:481-483).  us[] receives
+ * Q4HIP_PROF_N entries in the order of the Q4HIP_PROF_* indices. */
+#define Q4HIP_PROF_EMBED 0
+#define Q4HIP_PROF_NORM_Q 1
+#define Q4HIP_PROF_QKV 2
+#define Q4HIP_PROF_ROPE 3
+#define Q4HIP_PROF_ATTN 4
+#define Q4HIP_PROF_QUANT 5
+#define Q4HIP_PROF_O 6
+#define Q4HIP_PROF_GU 7
+#define Q4HIP_PROF_SWIGLU 8
+#define Q4HIP_PROF_DOWN 9
+#define Q4HIP_PROF_OUT 10
+#define Q4HIP_PROF_SAMPLE 11
+#define Q4HIP_PROF_N 12
+int q4hip_profile(q4hip* h, int token, int pos, float* us, int n);
+
+/* Time `steps` greedy decode steps (as q4hip_generate) with HIP events on the context's stream;
+ * *ms = elapsed device time of the whole loop. */
+int q4hip_time_generate(q4hip* h, int first, int pos, int steps, int* out, float* ms);
+
+/* Launch the output-head matvec alone `iters` times back to back on the context's stream, on the
+ * activations of the last forward, and report its mean duration from HIP events. */
+int q4hip_time_head(q4hip* h, int iters, float* us_per_launch);
+
+/* Release all device memory of the context. */
+void q4hip_destroy(q4hip* h);
+
+/* ---- isolated Q4_0 matvec (the kernel of every projection) ---------------------------------
+ * y[n] = W[n] . x for an N x K Q4_0 matrix given in GGUF layout, with x quantized to int8 per
+ * 32-block exactly as quantize_row (engine/kernels.c:90-114) and each output accumulated as
+ * matmul_q4 does (engine/kernels.c:200-229).  Used by the matvec sweep and its parity tests.
+ * A matvec handle owns its device copy of W, x and y. */
+typedef struct q4hip_mv q4hip_mv;
+int q4hip_mv_create(q4hip_mv** out, int N, int K, const void* gguf_q4_0, int device);
+/* Set x (K floats, host), quantize on the device, run once, copy y (N floats) back. */
+int q4hip_mv_run(q4hip_mv* m, const float* x, float* y);
+/* Run `iters` matvecs on the resident x; *us = mean HIP-event duration per launch. */
+int q4hip_mv_time(q4hip_mv* m, int iters, float* us);
+void q4hip_mv_destroy(q4hip_mv* m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,151 @@
+"""End-to-end token loop on the GPU against the oracle (kernels.c forward_pass + cpu-worker.js
+forward/sample) on seeded synthetic Qwen2 Q4_0 models.
+
+Bar: identical greedy token sequences and bit-identical logits (the north-star tolerance is
+max-abs <= 1e-3; the kernels reproduce the reference's operation order, so both are checked and
+bit equality is what is asserted).
+"""
+import numpy as np
+import pytest
+
+import oracle
+import synth
+
+pytestmark = pytest.mark.gpu
+
+_cache = {}
+
+
+def _model(name, seed):
+    key = (name, seed)
+    if key not in _cache:
+        _cache[key] = synth.make_model(synth.SHAPES[name], seed)
+    return _cache[key]
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _pair(name, seed, ctx, mt=16, threads=8):
+    import q4hip
+    shape = synth.SHAPES[name]
+    t = _model(name, seed)
+    g = q4hip.Model(shape, ctx=ctx, mt=mt)
+    g.load(t)
+    o = oracle.Model(shape, t, ctx=ctx, mt=mt, threads=threads)
+    return shape, g, o
+
+
+def _compare_logits(g, o, what):
+    lg, lo = g.read_logits(), o.logits()
+    diff = float(np.max(np.abs(lg - lo)))
+    assert diff <= 1e-3, f"{what}: max-abs logit error {diff}"
+    bad = np.flatnonzero(_bits(lg) != _bits(lo))
+    assert bad.size == 0, f"{what}: {bad.size} logits differ (max-abs {diff}), first {bad[:5]}"
+
+
+@pytest.mark.parametrize("name,seed,n_prompt", [("tiny", 3, 20), ("tiny", 4, 1), ("small", 5, 37)])
+def test_forward_steps_match(name, seed, n_prompt):
+    """forward(ids, pos) then forward([next], pos) per step: tokens and logits of every step."""
+    print(f"model {name} seed {seed} prompt {n_prompt}", flush=True)
+    shape, g, o = _pair(name, seed, ctx=128)
+    try:
+        ids = synth.prompt_ids(seed, n_prompt, shape.vocab)
+        ng, no = g.forward(ids, 0), o.forward(ids, 0)
+        assert ng == no
+        _compare_logits(g, o, "prefill")
+        pos = n_prompt
+        for step in range(12):
+            ng, no = g.forward([ng], pos), o.forward([no], pos)
+            assert ng == no, f"step {step}"
+            _compare_logits(g, o, f"step {step}")
+            pos += 1
+    finally:
+        g.close()
+        o.close()
+
+
+def test_generate_matches_forward_loop():
+    """The device-side greedy loop (hipGraph replays) gives the tokens of the per-call loop."""
+    shape, g, o = _pair("small", 11, ctx=256)
+    try:
+        ids = synth.prompt_ids(11, 30, shape.vocab)
+        first = g.forward(ids, 0)
+        dev = g.generate(first, len(ids), 40)
+        ref = o.generate(ids, 41)
+        assert [first] + dev == ref
+    finally:
+        g.close()
+        o.close()
+
+
+def test_chunking_and_prefix_reuse():
+    """Results do not depend on prompt chunking (wiki/04-cpu-webassembly.md:75-77); a later
+    forward at a smaller pos overwrites the cache, which is how KV-prefix reuse works
+    (engine/llm.js:45-54)."""
+    import q4hip
+    shape = synth.SHAPES["tiny"]
+    t = _model("tiny", 21)
+    ids = synth.prompt_ids(21, 45, shape.vocab)
+    outs = []
+    for mt in (16, 5, 1):
+        g = q4hip.Model(shape, ctx=128, mt=mt)
+        g.load(t)
+        n = g.forward(ids, 0)
+        outs.append((n, g.read_logits()))
+        g.close()
+    for n, lg in outs[1:]:
+        assert n == outs[0][0] and np.array_equal(_bits(lg), _bits(outs[0][1]))
+    g = q4hip.Model(shape, ctx=128)
+    g.load(t)
+    try:
+        g.forward(synth.prompt_ids(99, 30, shape.vocab), 0)   # different history
+        n = g.forward(ids, 0)                                  # overwrite from pos 0
+        assert n == outs[0][0] and np.array_equal(_bits(g.read_logits()), _bits(outs[0][1]))
+    finally:
+        g.close()
+
+
+def test_context_full_and_bad_ids():
+    import q4hip
+    shape, g, o = _pair("tiny", 2, ctx=32)
+    try:
+        with pytest.raises(q4hip.Q4Error, match="context full"):
+            g.forward(list(range(32)), 0)
+        with pytest.raises(q4hip.Q4Error, match="context full"):
+            g.forward([1], 31)
+        with pytest.raises(q4hip.Q4Error, match="out of range"):
+            g.forward([shape.vocab], 0)
+        assert g.forward([1, 2, 3], 0) == o.forward([1, 2, 3], 0)
+    finally:
+        g.close()
+        o.close()
+
+
+@pytest.mark.slow
+def test_qwen05b_prompt64_greedy64():
+    """The headline workload: 0.5B shape, 64-token seeded prompt, 64 greedy steps."""
+    print("qwen2.5-0.5b prompt 64 + 64 steps", flush=True)
+    shape, g, o = _pair("qwen2.5-0.5b", 1, ctx=256, threads=16)
+    try:
+        ids = synth.prompt_ids(1, 64, shape.vocab)
+        ng, no = g.forward(ids, 0), o.forward(ids, 0)
+        assert ng == no
+        _compare_logits(g, o, "prefill")
+        toks_g, toks_o = [ng], [no]
+        pos = 64
+        for step in range(63):
+            ng, no = g.forward([ng], pos), o.forward([no], pos)
+            toks_g.append(ng)
+            toks_o.append(no)
+            assert ng == no, f"step {step}"
+            if step % 8 == 0 or step == 62:
+                _compare_logits(g, o, f"step {step}")
+            pos += 1
+        assert toks_g == toks_o
+        dev = g.generate(toks_g[0], 64, 63)
+        assert [toks_g[0]] + dev == toks_o
+    finally:
+        g.close()
+        o.close()
