@@ -1,0 +1,175 @@
+"""Decode throughput of the Qwen2 Q4_0 token loop on one MI355X.
+
+Workload (the headline configuration): Qwen2.5-0.5B shape (hidden 896, 24 layers, 14/2 heads,
+head_dim 64, FFN 4864, vocab 151936), random-init N(0,0.02) weights in GGUF Q4_0, batch 1,
+a 64-token seeded prompt, then greedy decode.  One step = one decode token.  W warmup steps run
+from position 64; then K timed steps run again from position 64 (same tokens, K/V overwritten),
+bracketed by device synchronisation.  value = K / elapsed seconds.
+
+Also reported: algorithmic HBM bytes per token / time per token (achieved GB/s), the roofline of
+the kernel that takes the most time per step (HIP events around each launch of one eager step,
+averaged over several steps), and the oracle timed on the host cores as the CPU baseline.
+
+Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 8]
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "e2e-browser-voice-agent_amd", "py"))
+
+HBM_PEAK_GBPS = 8000.0
+PROMPT = 64
+SEED = 1
+
+
+def algorithmic_bytes(shape, T):
+    """HBM bytes one decode step must move at context length T: GGUF Q4_0 weights (18 B per 32),
+    fp32 norms and bias, one embedding row, the logits write and the fp32 K/V read."""
+    D, F, L, V, QKV = shape.dim, shape.ffn, shape.layers, shape.vocab, shape.qkv
+    q4 = lambda n, k: n * k // 32 * 18  # noqa: E731
+    layers = L * (q4(QKV, D) + q4(D, D) + q4(2 * F, D) + q4(D, F))
+    head = q4(V, D)
+    norms = (2 * L + 1) * D * 4
+    bias = L * QKV * 4
+    emb = D // 32 * 18
+    logits = V * 4
+    kv = L * shape.kv_heads * shape.head_dim * 4 * 2 * T
+    return {"layers": layers, "head": head, "other": norms + bias + emb + logits, "kv": kv,
+            "total": layers + head + norms + bias + emb + logits + kv}
+
+
+def kernel_bytes(shape):
+    """Algorithmic bytes per launch of each per-step kernel class (weights + input + output)."""
+    D, F, V, QKV = shape.dim, shape.ffn, shape.vocab, shape.qkv
+    q4 = lambda n, k: n * k // 32 * 18  # noqa: E731
+    return {
+        "matvec qkv": q4(QKV, D) + D + QKV * 4 * 2,
+        "matvec o": q4(D, D) + D + D * 4 * 2,
+        "matvec gate+up": q4(2 * F, D) + D + 2 * F * 4,
+        "matvec down": q4(D, F) + F + D * 4 * 2,
+        "matvec output": q4(V, D) + D * 4 + V * 4,
+    }
+
+
+def cpu_baseline(shape, tensors, ids, first_tokens):
+    """The oracle on the host cores: prompt with every logical core, decode with ceil(cores/2)
+    threads (the reference's policy, engine/cpu.js:203-205); median ms per decode token."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = min(cores, 16)
+    decode_threads = max(1, math.ceil(cores / 2))
+    o = oracle.Model(shape, tensors, ctx=256, threads=cores)
+    nxt = o.forward(ids, 0)
+    o.set_threads(decode_threads)
+    times, toks = [], [nxt]
+    pos = len(ids)
+    budget = time.time() + 20.0
+    while len(times) < 32 and time.time() < budget:
+        t0 = time.perf_counter()
+        nxt = o.forward([nxt], pos)
+        times.append(time.perf_counter() - t0)
+        toks.append(nxt)
+        pos += 1
+    o.close()
+    agree = toks[:len(first_tokens)] == first_tokens[:len(toks)]
+    med = statistics.median(times)
+    return {"value": round(1.0 / med, 3), "unit": "tokens/s", "cores": decode_threads, "kind": "port",
+            "sample": f"oracle (C restatement of kernels.c) decode of {len(times)} greedy tokens after the same "
+                      f"64-token prompt, median ms/token {med * 1e3:.1f}, {decode_threads} of {cores} threads",
+            "tokens_agree_with_gpu": bool(agree)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the batch-1 decode loop runs on a single device "
+              "(multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        sys.exit("--steps must be >= 1 and --warmup >= 0")
+
+    import q4hip
+    import synth
+
+    shape = synth.SHAPES["qwen2.5-0.5b"]
+    ctx = max(256, PROMPT + max(args.steps, args.warmup) + 2)
+    t0 = time.time()
+    tensors = synth.make_model(shape, SEED)
+    t_gen = time.time() - t0
+    m = q4hip.Model(shape, ctx=ctx)
+    m.load(tensors)
+    ids = synth.prompt_ids(SEED, PROMPT, shape.vocab)
+
+    t0 = time.perf_counter()
+    first = m.forward(ids, 0)                      # prefill (not timed for the metric)
+    prefill_ms = (time.perf_counter() - t0) * 1e3
+
+    if args.warmup:
+        m.generate(first, PROMPT, args.warmup)
+    # timed region: K greedy steps from position 64, device synchronised on both sides
+    t0 = time.perf_counter()
+    toks, dev_ms = m.time_generate(first, PROMPT, args.steps)
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ms_per_step = dev_ms / args.steps
+    value = args.steps / (dev_ms / 1e3)
+
+    # algorithmic bytes over the timed steps (T = 65 .. 64+K)
+    tot = sum(algorithmic_bytes(shape, PROMPT + i + 1)["total"] for i in range(args.steps))
+    achieved_gbps = tot / (dev_ms / 1e3) / 1e9
+
+    # per-kernel time of real decode steps (eager, HIP events around each launch)
+    prof = {k: 0.0 for k in q4hip.PROF_NAMES}
+    nprof = 8
+    tok = first
+    for i in range(nprof):
+        p = m.profile(tok, PROMPT + i)
+        for k, v in p.items():
+            prof[k] += v / nprof
+        tok = toks[i]
+    launches = {"matvec qkv": shape.layers, "matvec o": shape.layers, "matvec gate+up": shape.layers,
+                "matvec down": shape.layers, "matvec output": 1}
+    kb = kernel_bytes(shape)
+    dom = max(launches, key=lambda k: prof[k])
+    avg_us = prof[dom] / launches[dom]
+    ach = kb[dom] / (avg_us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None,
+                "bytes_per_launch": kb[dom], "avg_launch_us": round(avg_us, 3)}
+
+    out = {
+        "metric": "decode tokens/s at batch 1 (Qwen2.5-0.5B Q4_0 shape); achieved HBM GB/s",
+        "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8xq4->fp32", "data": "synthetic",
+        "config": {"workload": "qwen2.5-0.5b-shape Q4_0 greedy decode, batch 1, 64-token prompt",
+                   "global_batch": 1, "seq_len": PROMPT + args.steps, "prompt": PROMPT,
+                   "parallelism": "single-gpu"},
+        "achieved_gbps": round(achieved_gbps, 1),
+        "hbm_roofline_frac": round(achieved_gbps / HBM_PEAK_GBPS, 4),
+        "algorithmic_mb_per_token": round(tot / args.steps / 1e6, 2),
+        "wall_ms_timed": round(wall_ms, 2),
+        "prefill64_ms": round(prefill_ms, 2),
+        "profile_us_per_step": {k: round(v, 2) for k, v in prof.items()},
+        "roofline": roofline,
+        "model_gen_s": round(t_gen, 1),
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(shape, tensors, ids, [first] + toks)
+    m.close()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -71,6 +71,18 @@ __device__ __forceinline__ int quant_one(float v) {
   return (int)r;
 }
 
+// Stage a row of n floats into shared memory "by lane": value i goes to xl[(i & 3) * st + (i >> 2)],
+// st = n/4 + 1, so reference lane j (the values i = j mod 4, kernels.c:81-82) is one contiguous run
+// and the four runs start in different banks.
+__device__ __forceinline__ void stage_row_by_lane(const float* __restrict__ x, int n, float* xl, int st,
+                                                  int tid, int nthreads) {
+  for (int i = tid; i < n; i += nthreads) xl[(i & 3) * st + (i >> 2)] = x[i];
+}
+
+__device__ __forceinline__ float lane_staged(const float* xl, int st, int i) {
+  return xl[(i & 3) * st + (i >> 2)];
+}
+
 // ---------------------------------------------------------------- quantization
 
 enum QuantMode { QM_PLAIN = 0, QM_NORM = 1, QM_SWIGLU = 2 };
@@ -79,8 +91,10 @@ enum QuantMode { QM_PLAIN = 0, QM_NORM = 1, QM_SWIGLU = 2 };
 // with the value transform of the caller fused in: plain, RMSNorm (x*r)*w (kernels.c:85), or
 // SwiGLU g/(1+e^-g)*u (kernels.c:395).  Work item t = (block b, lane j); the four lanes of a
 // block sit in consecutive threads of one wave and exchange the block maximum by shuffles.
+// QM_NORM reads x from the row staged by lane (xl, st); the others read xr (SwiGLU: gate at xr[i],
+// up at xr[n + i]).
 template <int MODE>
-__device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, int n,
+__device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, const float* xl, int st, int n,
                                                  const float* __restrict__ w, float rs,
                                                  uint4* __restrict__ out, int tid, int nthreads) {
   const int nb = n >> 5;
@@ -93,7 +107,7 @@ __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, i
     for (int k = 0; k < 8; k++) {
       const int i = e[k];
       if (MODE == QM_NORM) {
-        v[k] = (xr[i] * rs) * w[i];
+        v[k] = (lane_staged(xl, st, i) * rs) * w[i];
       } else if (MODE == QM_SWIGLU) {
         const float g = xr[i];
         v[k] = g / (1.0f + fast_exp(-g)) * xr[n + i];
@@ -118,13 +132,23 @@ __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, i
 }
 
 // 1 / sqrt(mean(x^2) + eps) with the reference's four lane sums (lane j takes i = j mod 4, in
-// order) and ((l0+l1)+l2)+l3 (kernels.c:81-84).  Threads 0..3 of the block run the lanes;
-// the result is broadcast through `red` (>= 5 floats of shared memory).
-__device__ __forceinline__ float rms_scale(const float* __restrict__ x, int n, float eps, float* red) {
+// order) and ((l0+l1)+l2)+l3 (kernels.c:81-84), over a row staged by stage_row_by_lane.  Threads
+// 0..3 run the four lanes from shared memory; the result is broadcast through `red` (>= 5 floats).
+__device__ __forceinline__ float rms_scale_staged(const float* xl, int n, int st, float eps, float* red) {
   const int tid = threadIdx.x;
   if (tid < 4) {
+    const float* p = xl + tid * st;
+    const int cnt = n >> 2;
     float s = 0.0f;
-    for (int i = tid; i < n; i += 4) { const float v = x[i]; s = s + v * v; }
+    int k = 0;
+    for (; k + 8 <= cnt; k += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = p[k + u];
+#pragma unroll
+      for (int u = 0; u < 8; u++) s = s + v[u] * v[u];
+    }
+    for (; k < cnt; k++) { const float v = p[k]; s = s + v * v; }
     red[tid] = s;
   }
   __syncthreads();
@@ -134,6 +158,88 @@ __device__ __forceinline__ float rms_scale(const float* __restrict__ x, int n, f
   }
   __syncthreads();
   return red[4];
+}
+
+// ---------------------------------------------------------------- Q4_0 matvec
+
+// Device view of one Q4 matrix in the tiled layout:
+//   qs: uint4 [N/64][ng][64 rows][4 lanes j]  -- word j of blocks 4g..4g+3 of that row
+//   d : uint4 [N/64][nb8][64 rows]            -- 8 fp16 scales (blocks 8c..8c+7) of that row
+struct Q4Mat {
+  const uint4* qs;
+  const uint4* d;
+  int N, nb, ng, nb8, Np;
+};
+
+// Accumulate, for the 16 rows of one wave, lane (r, j)'s partial sums of MT tokens in the
+// reference's block order: acc[m] = acc[m] + f32(p_j) * (dw * dx) for b = 0 .. nb-1
+// (kernels.c:137, 217-218).  Weights are read 16 bytes per lane (4 blocks of word j), a chunk of
+// 32 blocks ahead of the arithmetic.  Activation blocks come from `xs` (shared or global memory),
+// token m at xs + m * xstride4 (uint4 units), block b lane j at [b*4 + j].
+template <int MT>
+__device__ __forceinline__ void matvec_rows16(const Q4Mat& W, int tile, int rr, int j,
+                                              const uint4* __restrict__ xs, int xstride4, int M,
+                                              float (&acc)[MT]) {
+  constexpr int CG = 8;    // groups of 4 blocks per chunk
+  const uint4* wq = W.qs + ((size_t)tile * W.ng * 64 + rr) * 4 + j;
+  const uint4* wd = W.d + (size_t)tile * W.nb8 * 64 + rr;
+  const int nch = (W.ng + CG - 1) / CG;
+  uint4 w[CG], sc[CG / 2];
+#pragma unroll
+  for (int g = 0; g < CG; g++) w[g] = g < W.ng ? wq[(size_t)g * 256] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int c = 0; c < CG / 2; c++) sc[c] = c < W.nb8 ? wd[(size_t)c * 64] : make_uint4(0, 0, 0, 0);
+  for (int ch = 0; ch < nch; ch++) {
+    uint4 wn[CG], sn[CG / 2];
+    const int g0 = (ch + 1) * CG;
+    if (ch + 1 < nch) {
+#pragma unroll
+      for (int g = 0; g < CG; g++) wn[g] = g0 + g < W.ng ? wq[(size_t)(g0 + g) * 256] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int c = 0; c < CG / 2; c++) {
+        const int c8 = g0 / 2 + c;
+        sn[c] = c8 < W.nb8 ? wd[(size_t)c8 * 64] : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < CG; g++) {
+      const uint32_t ww[4] = {w[g].x, w[g].y, w[g].z, w[g].w};
+      const uint4 sv = sc[g >> 1];
+      const uint32_t sh[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int b = (ch * CG + g) * 4 + k;
+        if (b < W.nb) {
+          const int hb = ((g & 1) << 2) + k;            // half index within the 8 scales
+          const uint32_t hbits = (hb & 1) ? (sh[hb >> 1] >> 16) : (sh[hb >> 1] & 0xffffu);
+          const float dw = half_bits_to_float(hbits);
+          const uint32_t lo = ww[k] & 0x0F0F0F0Fu, hi = (ww[k] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+          for (int m = 0; m < MT; m++) {
+            if (m < M) {
+              const uint4 xv = xs[(size_t)m * xstride4 + b * 4 + j];
+              int p = sdot4(lo, xv.x, (int)xv.z);
+              p = sdot4(hi, xv.y, p);
+              acc[m] = acc[m] + (float)p * (dw * __uint_as_float(xv.w));
+            }
+          }
+        }
+      }
+    }
+    if (ch + 1 < nch) {
+#pragma unroll
+      for (int g = 0; g < CG; g++) w[g] = wn[g];
+#pragma unroll
+      for (int c = 0; c < CG / 2; c++) sc[c] = sn[c];
+    }
+  }
+}
+
+// ((acc_0 + acc_1) + acc_2) + acc_3 over the four lanes of a row (hsum, kernels.c:116-118);
+// valid in lane j == 0.
+__device__ __forceinline__ float hsum4(float a0) {
+  const float a1 = __shfl_down(a0, 1, 4), a2 = __shfl_down(a0, 2, 4), a3 = __shfl_down(a0, 3, 4);
+  return a0 + a1 + a2 + a3;
 }
 
 }  // namespace q4

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -21,8 +22,9 @@ using namespace q4;
 
 // ================================================================ kernels
 
-// GGUF Q4_0 rows [rows][nb][18 B] -> tiled layout (see kernels.h), rows row0.. of the matrix.
-__global__ void k_repack_q4(const uint8_t* __restrict__ raw, int64_t rows, int nb, int nb8, int row0,
+// GGUF Q4_0 rows [rows][nb][18 B] -> tiled layout (kernels.h, Q4Mat), rows row0.. of the matrix.
+// Word j of a block = its value bytes {2j, 2j+1, 8+2j, 9+2j}: the elements of reference lane j.
+__global__ void k_repack_q4(const uint8_t* __restrict__ raw, int64_t rows, int nb, int ng, int nb8, int row0,
                             uint32_t* __restrict__ qs, uint16_t* __restrict__ dsc) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= rows * nb) return;
@@ -34,11 +36,11 @@ __global__ void k_repack_q4(const uint8_t* __restrict__ raw, int64_t rows, int n
   const uint8_t* s = raw + idx * 18;
   dsc[((tile * nb8 + (b >> 3)) * 64 + rr) * 8 + (b & 7)] = (uint16_t)(s[0] | (s[1] << 8));
   const uint8_t* q = s + 2;
-  uint32_t* o = qs + ((tile * nb + b) * 64 + rr) * 4;
+  uint32_t* o = qs + (((tile * ng + (b >> 2)) * 64 + rr) * 4) * 4 + (b & 3);
 #pragma unroll
   for (int j = 0; j < 4; j++)
-    o[j] = (uint32_t)q[2 * j] | ((uint32_t)q[2 * j + 1] << 8) | ((uint32_t)q[8 + 2 * j] << 16) |
-           ((uint32_t)q[9 + 2 * j] << 24);
+    o[j * 4] = (uint32_t)q[2 * j] | ((uint32_t)q[2 * j + 1] << 8) | ((uint32_t)q[8 + 2 * j] << 16) |
+               ((uint32_t)q[9 + 2 * j] << 24);
 }
 
 // Embedding rows (kernels.c:312-322): x[m][32b+j] = ((q&15)-8)*d, x[m][32b+16+j] = ((q>>4)-8)*d.
@@ -60,72 +62,53 @@ __global__ void k_embed(const uint8_t* __restrict__ emb, int D, const int* __res
 }
 
 // Quantize rows m_first .. m_first+gridDim.x-1 of `in` into xq rows 0.. (kernels.c:328-331,
-// 379, 385-388, 393-397, 405-407).
+// 379, 385-388, 393-397, 405-407).  QM_NORM stages the row in shared memory ((n/4+1)*4 floats of
+// dynamic shared memory) for the serial sum of squares.
 template <int MODE>
 __global__ __launch_bounds__(256) void k_quant(const float* __restrict__ in, int ld_in, int n,
                                                const float* __restrict__ w, float eps,
                                                uint4* __restrict__ xq, int xstride, int m_first) {
+  extern __shared__ float xl[];
   __shared__ float red[8];
   const float* xr = in + (size_t)(m_first + blockIdx.x) * ld_in;
+  const int st = (n >> 2) + 1;
   float rs = 0.0f;
-  if (MODE == QM_NORM) rs = rms_scale(xr, n, eps, red);
-  quantize_row_dev<MODE>(xr, n, w, rs, xq + (size_t)blockIdx.x * xstride * 4, threadIdx.x, blockDim.x);
+  if (MODE == QM_NORM) {
+    stage_row_by_lane(xr, n, xl, st, threadIdx.x, blockDim.x);
+    __syncthreads();
+    rs = rms_scale_staged(xl, n, st, eps, red);
+  }
+  quantize_row_dev<MODE>(xr, xl, st, n, w, rs, xq + (size_t)blockIdx.x * xstride * 4, threadIdx.x, blockDim.x);
 }
 
 enum { OP_STORE = 0, OP_BIAS = 1, OP_ADD = 2 };   // put() of kernels.c:190-194
 
 // y[m][n] (op)= W[n] . x[m] for M tokens (matmul_q4, kernels.c:200-273).  One wave = 16 rows;
-// lane (r, j) owns accumulator j of row r and walks the blocks in order:
-//   acc_j = acc_j + f32(p_j) * (dw * dx)           (kernels.c:217-218, 137)
-// then ((acc_0 + acc_1) + acc_2) + acc_3 across the four lanes (hsum, kernels.c:116-118).
+// lane (r, j) owns accumulator j of row r (matvec_rows16), then hsum4 and the epilogue of
+// put() (kernels.c:190-194).  For one token the activation blocks are staged in shared memory
+// (nb*64 bytes of dynamic shared memory); for a prefill chunk they are read from global memory.
 template <int MT, int OP>
-__global__ __launch_bounds__(64) void k_matvec(const uint32_t* __restrict__ qs, const uint4* __restrict__ dsc,
-                                               int nb, int nb8, const uint4* __restrict__ xq, int xstride,
-                                               int M, float* __restrict__ y, int ldy, int N,
-                                               const float* __restrict__ bias) {
+__global__ __launch_bounds__(64) void k_matvec(Q4Mat W, const uint4* __restrict__ xq, int xstride, int M,
+                                               float* __restrict__ y, int ldy, const float* __restrict__ bias) {
+  extern __shared__ uint4 xs[];
   const int lane = threadIdx.x, r = lane >> 2, j = lane & 3;
   const int wv = blockIdx.x, tile = wv >> 2, rr = ((wv & 3) << 4) + r;
   const int row = (tile << 6) + rr;
+  const uint4* src = xq;
+  if (MT == 1) {
+    for (int i = lane; i < W.nb * 4; i += 64) xs[i] = xq[i];
+    __syncthreads();
+    src = xs;
+  }
   float acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; m++) acc[m] = 0.0f;
-  const uint32_t* wp = qs + ((size_t)tile * nb * 64 + rr) * 4 + j;
-  const uint4* dp = dsc + ((size_t)tile * nb8 * 64 + rr);
-  for (int b8 = 0; b8 < nb8; b8++) {
-    const uint4 dv = dp[(size_t)b8 * 64];
-    const uint32_t dh[4] = {dv.x, dv.y, dv.z, dv.w};
-    uint32_t w8[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int b = b8 * 8 + k;
-      w8[k] = b < nb ? wp[(size_t)b * 256] : 0u;
-    }
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int b = b8 * 8 + k;
-      if (b < nb) {
-        const float dw = half_bits_to_float((k & 1) ? (dh[k >> 1] >> 16) : (dh[k >> 1] & 0xffffu));
-        const uint32_t lo = w8[k] & 0x0F0F0F0Fu, hi = (w8[k] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-        for (int m = 0; m < MT; m++) {
-          if (m < M) {
-            const uint4 xv = xq[((size_t)m * xstride + b) * 4 + j];
-            int p = sdot4(lo, xv.x, (int)xv.z);
-            p = sdot4(hi, xv.y, p);
-            const float sc = dw * __uint_as_float(xv.w);
-            acc[m] = acc[m] + (float)p * sc;
-          }
-        }
-      }
-    }
-  }
+  matvec_rows16<MT>(W, tile, rr, j, src, xstride * 4, M, acc);
 #pragma unroll
   for (int m = 0; m < MT; m++) {
     if (m < M) {
-      const float a0 = acc[m];
-      const float a1 = __shfl_down(a0, 1, 4), a2 = __shfl_down(a0, 2, 4), a3 = __shfl_down(a0, 3, 4);
-      if (j == 0 && row < N) {
-        const float v = a0 + a1 + a2 + a3;
+      const float v = hsum4(acc[m]);
+      if (j == 0 && row < W.N) {
         float* o = y + (size_t)m * ldy + row;
         if (OP == OP_ADD) *o = *o + v;
         else if (OP == OP_BIAS) *o = v + bias[row];
@@ -160,14 +143,17 @@ __global__ void k_rope_kv(float* __restrict__ qkv, int QKV, int D, int H, int KV
 }
 
 // Attention for one (head, token) over T = pos0+m+1 cached positions (kernels.c:355-377), in the
-// reference's order: scores as four lane sums, max, fast_exp and a running sum in t order, then
-// out_i = sum over t in order of (e_t/sum)*v_t[i].  Grid (H, M), 64 threads, shared: HD + T floats.
+// reference's order: scores as four lane sums over i = j mod 4, max, fast_exp and a running sum in
+// t order, then out_i = sum over t in order of (e_t/sum)*v_t[i].  Grid (H, M), one wave; thread t
+// scores position t (its K row loaded whole), thread i accumulates output element(s) i over t with
+// V loaded 32 positions ahead.  Shared: HD + T floats.
+template <int HD>
 __global__ __launch_bounds__(64) void k_attn(const float* __restrict__ qkv, int QKV, int D, int H, int KVH,
-                                             int HD, const float* __restrict__ kc, const float* __restrict__ vc,
+                                             const float* __restrict__ kc, const float* __restrict__ vc,
                                              int ctx, int layer, float* __restrict__ att,
                                              const State* __restrict__ st) {
   extern __shared__ __attribute__((aligned(16))) float sm[];
-  __shared__ float red[64];
+  __shared__ float red[2];
   const int h = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
   const int T = st->pos0 + m + 1, kh = h / (H / KVH);
   const float* q = qkv + (size_t)m * QKV + h * HD;
@@ -179,56 +165,83 @@ __global__ __launch_bounds__(64) void k_attn(const float* __restrict__ qkv, int 
   __syncthreads();
   const float scale = 1.0f / __builtin_sqrtf((float)HD);
   float lmax = -1e30f;
+  const float4* qr = reinterpret_cast<const float4*>(sq);
   for (int t = tid; t < T; t += 64) {
     const float4* kr = reinterpret_cast<const float4*>(kb + (size_t)t * HD);
-    const float4* qr = reinterpret_cast<const float4*>(sq);
+    float4 kv[HD / 4];
+#pragma unroll
+    for (int i4 = 0; i4 < HD / 4; i4++) kv[i4] = kr[i4];
     float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
     for (int i4 = 0; i4 < HD / 4; i4++) {
-      const float4 kv = kr[i4], qv = qr[i4];
-      s0 = s0 + qv.x * kv.x;
-      s1 = s1 + qv.y * kv.y;
-      s2 = s2 + qv.z * kv.z;
-      s3 = s3 + qv.w * kv.w;
+      const float4 qv = qr[i4];
+      s0 = s0 + qv.x * kv[i4].x;
+      s1 = s1 + qv.y * kv[i4].y;
+      s2 = s2 + qv.z * kv[i4].z;
+      s3 = s3 + qv.w * kv[i4].w;
     }
     const float v = (s0 + s1 + s2 + s3) * scale;
     sc[t] = v;
     lmax = __builtin_fmaxf(lmax, v);
   }
-  red[tid] = lmax;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) lmax = __builtin_fmaxf(lmax, __shfl_xor(lmax, o));
   __syncthreads();
-  if (tid == 0) {
-    float mx = red[0];
-    for (int i = 1; i < 64; i++) mx = __builtin_fmaxf(mx, red[i]);
-    red[0] = mx;
-  }
-  __syncthreads();
-  const float mx = red[0];
-  for (int t = tid; t < T; t += 64) sc[t] = fast_exp(sc[t] - mx);
+  for (int t = tid; t < T; t += 64) sc[t] = fast_exp(sc[t] - lmax);
   __syncthreads();
   if (tid == 0) {
     float sum = 0.0f;
-    for (int t = 0; t < T; t++) sum = sum + sc[t];
-    red[1] = sum;
+    int t = 0;
+    for (; t + 8 <= T; t += 8) {
+      float e[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) e[u] = sc[t + u];
+#pragma unroll
+      for (int u = 0; u < 8; u++) sum = sum + e[u];
+    }
+    for (; t < T; t++) sum = sum + sc[t];
+    red[0] = sum;
   }
   __syncthreads();
-  const float sum = red[1];
+  const float sum = red[0];
   for (int t = tid; t < T; t += 64) sc[t] = sc[t] / sum;
   __syncthreads();
-  for (int i = tid; i < HD; i += 64) {
-    float acc = 0.0f;
-    const float* vp = vb + i;
-    int t = 0;
-    for (; t + 4 <= T; t += 4) {
-      const float v0 = vp[(size_t)t * HD], v1 = vp[(size_t)(t + 1) * HD];
-      const float v2 = vp[(size_t)(t + 2) * HD], v3 = vp[(size_t)(t + 3) * HD];
-      acc = acc + sc[t] * v0;
-      acc = acc + sc[t + 1] * v1;
-      acc = acc + sc[t + 2] * v2;
-      acc = acc + sc[t + 3] * v3;
+  constexpr int E = HD / 64;     // output elements per thread
+  constexpr int TB = 32;         // positions per V batch
+  float acc[E];
+#pragma unroll
+  for (int e = 0; e < E; e++) acc[e] = 0.0f;
+  float vcur[TB][E];
+#pragma unroll
+  for (int u = 0; u < TB; u++)
+#pragma unroll
+    for (int e = 0; e < E; e++) vcur[u][e] = u < T ? vb[(size_t)u * HD + tid + 64 * e] : 0.0f;
+  for (int t0 = 0; t0 < T; t0 += TB) {
+    float vnext[TB][E];
+    const int t1 = t0 + TB;
+    if (t1 < T) {
+#pragma unroll
+      for (int u = 0; u < TB; u++)
+#pragma unroll
+        for (int e = 0; e < E; e++) vnext[u][e] = t1 + u < T ? vb[(size_t)(t1 + u) * HD + tid + 64 * e] : 0.0f;
     }
-    for (; t < T; t++) acc = acc + sc[t] * vp[(size_t)t * HD];
-    att[(size_t)m * D + h * HD + i] = acc;
+#pragma unroll
+    for (int u = 0; u < TB; u++) {
+      if (t0 + u < T) {
+        const float p = sc[t0 + u];
+#pragma unroll
+        for (int e = 0; e < E; e++) acc[e] = acc[e] + p * vcur[u][e];
+      }
+    }
+    if (t1 < T) {
+#pragma unroll
+      for (int u = 0; u < TB; u++)
+#pragma unroll
+        for (int e = 0; e < E; e++) vcur[u][e] = vnext[u][e];
+    }
   }
+#pragma unroll
+  for (int e = 0; e < E; e++) att[(size_t)m * D + h * HD + tid + 64 * e] = acc[e];
 }
 
 // Greedy sample, stage 1: (max, first index) per 4096-entry slice (cpu-worker.js:156-157).
@@ -322,17 +335,19 @@ int fail(int code, const char* fmt, ...) {
 struct Mat {
   uint32_t* qs = nullptr;
   uint16_t* d = nullptr;
-  int N = 0, K = 0, nb = 0, nb8 = 0, Np = 0;
+  int N = 0, K = 0, nb = 0, ng = 0, nb8 = 0, Np = 0;
   int64_t loaded = 0;
+  Q4Mat view() const { return Q4Mat{(const uint4*)qs, (const uint4*)d, N, nb, ng, nb8, Np}; }
 };
 
 int mat_alloc(Mat& m, int N, int K) {
   m.N = N;
   m.K = K;
   m.nb = K / 32;
+  m.ng = (m.nb + 3) / 4;
   m.nb8 = (m.nb + 7) / 8;
   m.Np = (N + kRowTile - 1) / kRowTile * kRowTile;
-  const size_t qbytes = (size_t)m.Np * m.nb * 16, dbytes = (size_t)m.Np * m.nb8 * 16;
+  const size_t qbytes = (size_t)m.Np * m.ng * 64, dbytes = (size_t)m.Np * m.nb8 * 16;
   HIPCHK(hipMalloc(&m.qs, qbytes));
   HIPCHK(hipMalloc(&m.d, dbytes));
   HIPCHK(hipMemset(m.qs, 0, qbytes));
@@ -356,7 +371,7 @@ int mat_upload(Mat& m, int row0, int64_t rows, const void* data, hipStream_t s) 
   hipError_t e = hipMemcpyAsync(raw, data, bytes, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) {
     const int64_t n = rows * m.nb;
-    k_repack_q4<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(raw, rows, m.nb, m.nb8, row0, m.qs, m.d);
+    k_repack_q4<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(raw, rows, m.nb, m.ng, m.nb8, row0, m.qs, m.d);
     e = hipGetLastError();
   }
   if (e == hipSuccess) e = hipStreamSynchronize(s);
@@ -429,12 +444,20 @@ int check_ready(q4hip* h) {
 }
 
 template <int OP>
-void launch_matvec(q4hip* h, const Mat& W, int M, float* y, int ldy, const float* bias) {
+void launch_matvec(hipStream_t s, const Mat& W, const uint4* xq, int xstride, int M, float* y, int ldy,
+                   const float* bias) {
   const unsigned grid = (unsigned)(W.Np / 16);
   if (M == 1)
-    k_matvec<1, OP><<<grid, 64, 0, h->stream>>>(W.qs, (const uint4*)W.d, W.nb, W.nb8, h->xq, h->xstride, 1, y, ldy, W.N, bias);
+    k_matvec<1, OP><<<grid, 64, (size_t)W.nb * 64, s>>>(W.view(), xq, xstride, 1, y, ldy, bias);
   else
-    k_matvec<kMaxChunk, OP><<<grid, 64, 0, h->stream>>>(W.qs, (const uint4*)W.d, W.nb, W.nb8, h->xq, h->xstride, M, y, ldy, W.N, bias);
+    k_matvec<kMaxChunk, OP><<<grid, 64, 0, s>>>(W.view(), xq, xstride, M, y, ldy, bias);
+}
+
+template <int MODE>
+void launch_quant(hipStream_t s, int rows, const float* in, int ld_in, int n, const float* w, float eps,
+                  uint4* xq, int xstride, int m_first) {
+  const size_t lds = MODE == QM_NORM ? (size_t)((n >> 2) + 1) * 4 * sizeof(float) : 0;
+  k_quant<MODE><<<rows, 256, lds, s>>>(in, ld_in, n, w, eps, xq, xstride, m_first);
 }
 
 // One pass over M <= MT tokens at device position st->pos0 (forward_pass, kernels.c:306-415).
@@ -447,30 +470,34 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
   for (int l = 0; l < h->NL; l++) {
     Layer& y = h->L[l];
     prof_mark(h, Q4HIP_PROF_NORM_Q);
-    k_quant<QM_NORM><<<M, 256, 0, s>>>(h->x, D, D, y.attn_norm, h->eps, h->xq, h->xstride, 0);
+    launch_quant<QM_NORM>(s, M, h->x, D, D, y.attn_norm, h->eps, h->xq, h->xstride, 0);
     prof_mark(h, Q4HIP_PROF_QKV);
-    launch_matvec<OP_BIAS>(h, y.qkv, M, h->qkv, QKV, y.bqkv);
+    launch_matvec<OP_BIAS>(s, y.qkv, h->xq, h->xstride, M, h->qkv, QKV, y.bqkv);
     prof_mark(h, Q4HIP_PROF_ROPE);
     k_rope_kv<<<dim3(h->H + h->KVH, M), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, h->kc, h->vc, h->ctx, l, h->st);
     prof_mark(h, Q4HIP_PROF_ATTN);
-    k_attn<<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->kc, h->vc, h->ctx, l, h->att, h->st);
+    if (HD == 64)
+      k_attn<64><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, h->st);
+    else
+      k_attn<128><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, h->st);
     prof_mark(h, Q4HIP_PROF_QUANT);
-    k_quant<QM_PLAIN><<<M, 256, 0, s>>>(h->att, D, D, nullptr, 0.0f, h->xq, h->xstride, 0);
+    launch_quant<QM_PLAIN>(s, M, h->att, D, D, nullptr, 0.0f, h->xq, h->xstride, 0);
     prof_mark(h, Q4HIP_PROF_O);
-    launch_matvec<OP_ADD>(h, y.o, M, h->x, D, nullptr);
+    launch_matvec<OP_ADD>(s, y.o, h->xq, h->xstride, M, h->x, D, nullptr);
     prof_mark(h, Q4HIP_PROF_NORM_Q);
-    k_quant<QM_NORM><<<M, 256, 0, s>>>(h->x, D, D, y.ffn_norm, h->eps, h->xq, h->xstride, 0);
+    launch_quant<QM_NORM>(s, M, h->x, D, D, y.ffn_norm, h->eps, h->xq, h->xstride, 0);
     prof_mark(h, Q4HIP_PROF_GU);
-    launch_matvec<OP_STORE>(h, y.gu, M, h->gu, 2 * F, nullptr);
+    launch_matvec<OP_STORE>(s, y.gu, h->xq, h->xstride, M, h->gu, 2 * F, nullptr);
     prof_mark(h, Q4HIP_PROF_SWIGLU);
-    k_quant<QM_SWIGLU><<<M, 256, 0, s>>>(h->gu, 2 * F, F, nullptr, 0.0f, h->xq, h->xstride, 0);
+    launch_quant<QM_SWIGLU>(s, M, h->gu, 2 * F, F, nullptr, 0.0f, h->xq, h->xstride, 0);
     prof_mark(h, Q4HIP_PROF_DOWN);
-    launch_matvec<OP_ADD>(h, y.down, M, h->x, D, nullptr);
+    launch_matvec<OP_ADD>(s, y.down, h->xq, h->xstride, M, h->x, D, nullptr);
   }
   if (want_logits) {
+    prof_mark(h, Q4HIP_PROF_NORM_Q);
+    launch_quant<QM_NORM>(s, 1, h->x, D, D, h->out_norm, h->eps, h->xq, h->xstride, M - 1);
     prof_mark(h, Q4HIP_PROF_OUT);
-    k_quant<QM_NORM><<<1, 256, 0, s>>>(h->x, D, D, h->out_norm, h->eps, h->xq, h->xstride, M - 1);
-    launch_matvec<OP_STORE>(h, h->head, 1, h->logits, h->V, nullptr);
+    launch_matvec<OP_STORE>(s, h->head, h->xq, h->xstride, 1, h->logits, h->V, nullptr);
     prof_mark(h, Q4HIP_PROF_SAMPLE);
     k_argmax1<<<h->am_parts, 256, 0, s>>>(h->logits, h->V, h->am_v, h->am_i);
     k_argmax2<<<1, 256, 0, s>>>(h->am_v, h->am_i, h->am_parts, h->tokens, h->st, M);
@@ -480,6 +507,11 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
 
 int build_graph(q4hip* h) {
   if (h->graph || h->graph_failed) return Q4HIP_OK;
+  const char* env = getenv("Q4HIP_GRAPH");
+  if (env && env[0] == '0') {   // eager launches, e.g. under a tracer that cannot follow graphs
+    h->graph_failed = true;
+    return Q4HIP_OK;
+  }
   hipGraph_t g = nullptr;
   if (hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
     h->graph_failed = true;
@@ -547,7 +579,7 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
   if (dim % 32 || ffn % 32 || dim % heads || heads % kv_heads)
     return fail(Q4HIP_EINVAL, "dim and ffn must be multiples of 32, heads a multiple of kv_heads");
   const int HD = dim / heads;
-  if (HD % 4 || HD > 256) return fail(Q4HIP_EINVAL, "head_dim %d unsupported", HD);
+  if (HD != 64 && HD != 128) return fail(Q4HIP_EINVAL, "head_dim %d unsupported (64 or 128)", HD);
   if ((size_t)(HD + ctx) * 4 > 65536) return fail(Q4HIP_EINVAL, "ctx %d too large for the attention kernel", ctx);
   if (mt <= 0 || mt > kMaxChunk) mt = kMaxChunk;
   int ndev = 0;
@@ -787,7 +819,7 @@ int q4hip_time_head(q4hip* h, int iters, float* us_per_launch) {
   HIPCHK(hipEventCreate(&e0));
   HIPCHK(hipEventCreate(&e1));
   HIPCHK(hipEventRecord(e0, h->stream));
-  for (int i = 0; i < iters; i++) launch_matvec<OP_STORE>(h, h->head, 1, h->logits, h->V, nullptr);
+  for (int i = 0; i < iters; i++) launch_matvec<OP_STORE>(h->stream, h->head, h->xq, h->xstride, 1, h->logits, h->V, nullptr);
   HIPCHK(hipEventRecord(e1, h->stream));
   HIPCHK(hipGetLastError());
   HIPCHK(hipEventSynchronize(e1));
@@ -846,8 +878,7 @@ int q4hip_mv_create(q4hip_mv** out, int N, int K, const void* w, int device) {
 }
 
 static void mv_launch(q4hip_mv* m) {
-  k_matvec<1, OP_STORE><<<(unsigned)(m->W.Np / 16), 64, 0, m->stream>>>(
-      m->W.qs, (const uint4*)m->W.d, m->W.nb, m->W.nb8, m->xq, m->W.nb, 1, m->y, m->W.N, m->W.N, nullptr);
+  launch_matvec<OP_STORE>(m->stream, m->W, m->xq, m->W.nb, 1, m->y, m->W.N, nullptr);
 }
 
 int q4hip_mv_run(q4hip_mv* m, const float* x, float* y) {
@@ -855,7 +886,7 @@ int q4hip_mv_run(q4hip_mv* m, const float* x, float* y) {
   HIPCHK(hipSetDevice(m->device));
   const int K = m->W.K;
   HIPCHK(hipMemcpyAsync(m->x, x, (size_t)K * 4, hipMemcpyHostToDevice, m->stream));
-  k_quant<QM_PLAIN><<<1, 256, 0, m->stream>>>(m->x, K, K, nullptr, 0.0f, m->xq, K / 32, 0);
+  launch_quant<QM_PLAIN>(m->stream, 1, m->x, K, K, nullptr, 0.0f, m->xq, K / 32, 0);
   mv_launch(m);
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(y, m->y, (size_t)m->W.N * 4, hipMemcpyDeviceToHost, m->stream));

@@ -47,9 +47,10 @@ SHAPES = {
     "qwen2.5-0.5b": Shape(896, 24, 4864, 14, 2, 151936),
     # Qwen2.5-1.5B: hidden 1536, 28 layers, 12 q-heads / 2 kv-heads, head_dim 128, FFN 8960
     "qwen2.5-1.5b": Shape(1536, 28, 8960, 12, 2, 151936),
-    # small shapes for fast tests (same head layout families)
-    "tiny": Shape(128, 2, 256, 4, 2, 512),
+    # small shapes for fast tests, same head_dim families (64 and 128)
+    "tiny": Shape(128, 2, 256, 2, 1, 512),
     "small": Shape(256, 3, 512, 4, 1, 4096),
+    "small128": Shape(256, 2, 512, 2, 1, 1024),
 }
 
 

@@ -45,7 +45,7 @@ def _compare_logits(g, o, what):
     assert bad.size == 0, f"{what}: {bad.size} logits differ (max-abs {diff}), first {bad[:5]}"
 
 
-@pytest.mark.parametrize("name,seed,n_prompt", [("tiny", 3, 20), ("tiny", 4, 1), ("small", 5, 37)])
+@pytest.mark.parametrize("name,seed,n_prompt", [("tiny", 3, 20), ("tiny", 4, 1), ("small", 5, 37), ("small128", 6, 70)])
 def test_forward_steps_match(name, seed, n_prompt):
     """forward(ids, pos) then forward([next], pos) per step: tokens and logits of every step."""
     print(f"model {name} seed {seed} prompt {n_prompt}", flush=True)
