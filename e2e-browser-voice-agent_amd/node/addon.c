@@ -255,15 +255,15 @@ static napi_value js_device_count(napi_env env, napi_callback_info info) {
 
 static napi_value init(napi_env env, napi_value exports) {
   napi_property_descriptor p[] = {
-      {"create", NULL, js_create, NULL, NULL, NULL, napi_default, NULL},
-      {"destroy", NULL, js_destroy, NULL, NULL, NULL, napi_default, NULL},
-      {"setTensor", NULL, js_set_tensor, NULL, NULL, NULL, napi_default, NULL},
-      {"setRope", NULL, js_set_rope, NULL, NULL, NULL, napi_default, NULL},
-      {"forward", NULL, js_forward, NULL, NULL, NULL, napi_default, NULL},
-      {"readLogits", NULL, js_read_logits, NULL, NULL, NULL, napi_default, NULL},
-      {"generate", NULL, js_generate, NULL, NULL, NULL, napi_default, NULL},
-      {"profile", NULL, js_profile, NULL, NULL, NULL, napi_default, NULL},
-      {"deviceCount", NULL, js_device_count, NULL, NULL, NULL, napi_default, NULL},
+      {"create", NULL, js_create, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"destroy", NULL, js_destroy, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"setTensor", NULL, js_set_tensor, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"setRope", NULL, js_set_rope, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"forward", NULL, js_forward, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"readLogits", NULL, js_read_logits, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"generate", NULL, js_generate, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"profile", NULL, js_profile, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"deviceCount", NULL, js_device_count, NULL, NULL, NULL, napi_enumerable, NULL},
   };
   NAPI_CALL(env, napi_define_properties(env, exports, sizeof p / sizeof p[0], p));
   return exports;

@@ -202,6 +202,15 @@ int orc_argmax(const float* lg, int n) {
   return best;
 }
 
+/* kernels.c:312-322 for one row */
+void orc_embed_row(float* xr, const uint8_t* q, const float* d, int D) {
+  for (int blk = 0; blk < D / 32; blk++)
+    for (int j = 0; j < 16; j++) {
+      xr[32 * blk + j] = (float)((q[16 * blk + j] & 15) - 8) * d[blk];
+      xr[32 * blk + 16 + j] = (float)((q[16 * blk + j] >> 4) - 8) * d[blk];
+    }
+}
+
 /* ------------------------------------------------------------------ host-side steps */
 
 /* cpu-worker.js:93-96: exact IEEE half -> binary32 */
@@ -318,14 +327,7 @@ void orc_run(orc_model* g, int pos0, int M, int want_logits) {
   /* embedding rows, Q4_0 (kernels.c:312-322) */
   for (int m = 0; m < M; m++) {
     int t = g->tokens[pos0 + m];
-    const uint8_t* q = g->embd.qs + (size_t)t * (D / 32) * 16;
-    const float* d = g->embd.d + (size_t)t * (D / 32);
-    float* xr = g->x + (size_t)m * D;
-    for (int blk = 0; blk < D / 32; blk++)
-      for (int j = 0; j < 16; j++) {
-        xr[32 * blk + j] = (float)((q[16 * blk + j] & 15) - 8) * d[blk];
-        xr[32 * blk + 16 + j] = (float)((q[16 * blk + j] >> 4) - 8) * d[blk];
-      }
+    orc_embed_row(g->x + (size_t)m * D, g->embd.qs + (size_t)t * (D / 32) * 16, g->embd.d + (size_t)t * (D / 32), D);
   }
 
   for (int l = 0; l < g->layers; l++) {

@@ -45,6 +45,8 @@ void orc_rope_head(float* v, const float* cs, int hd);
 void orc_swiglu(float* act, const float* gate, const float* up, int n);
 /* greedy argmax, first maximum wins (cpu-worker.js:156-157) */
 int orc_argmax(const float* logits, int n);
+/* one embedding row: dequantize Q4_0 (qs 16 B + fp32 d per block) to dim floats (kernels.c:312-322) */
+void orc_embed_row(float* out, const uint8_t* qs, const float* d, int dim);
 
 /* --- host-side steps (cpu-worker.js) ------------------------------------ */
 float orc_f16_to_f32(uint16_t h);                                     /* cpu-worker.js:93-96 */

@@ -45,6 +45,7 @@ def lib() -> ctypes.CDLL:
         "orc_rope_head": (None, [P, P, I]),
         "orc_swiglu": (None, [P, P, P, I]),
         "orc_argmax": (I, [P, I]),
+        "orc_embed_row": (None, [P, P, P, I]),
         "orc_f16_to_f32": (F, [ctypes.c_uint16]),
         "orc_copy_blocks": (None, [P, ctypes.c_int64, I, P, P]),
         "orc_rope_table": (None, [P, I, I, D]),
@@ -144,6 +145,13 @@ def swiglu(gate, up) -> np.ndarray:
 def argmax(x: np.ndarray) -> int:
     x = np.ascontiguousarray(x, np.float32)
     return lib().orc_argmax(ptr(x), x.size)
+
+
+def embed_row(qs: np.ndarray, d: np.ndarray) -> np.ndarray:
+    qs = np.ascontiguousarray(qs, np.uint8); d = np.ascontiguousarray(d, np.float32)
+    out = np.empty(d.size * 32, np.float32)
+    lib().orc_embed_row(ptr(out), ptr(qs), ptr(d), out.size)
+    return out
 
 
 def f16_to_f32(h: int) -> float:
