@@ -1,0 +1,55 @@
+"use strict";
+// Test driver for the Node.js host (engine/*.js): one command per run, JSON on stdout.
+//   parse <gguf>                                   -> {cfg, tensors}
+//   load <gguf> <ctx>                              -> {ok} or {error, code}
+//   generate <gguf> <ctx> <ids.json> <steps> <logits.f32>
+//        -> {tokens (per-step forward loop), device (device loop), stats}; last logits written raw
+//   sample <logits.f32> <temperature> <seed>      -> {id}
+const fs = require("fs");
+const path = require("path");
+const engine = path.join(__dirname, "..", "..", "e2e-browser-voice-agent_amd", "engine");
+const { parseGGUF, qwen2Config, readModel } = require(path.join(engine, "gguf.js"));
+const { LLM } = require(path.join(engine, "llm.js"));
+const { sample } = require(path.join(engine, "hip.js"));
+
+async function main() {
+  const [cmd, ...args] = process.argv.slice(2);
+  if (cmd === "parse") {
+    const g = parseGGUF(readModel(args[0]));
+    const tensors = {};
+    for (const [n, t] of Object.entries(g.tensors)) tensors[n] = [t.type, t.shape, t.start, t.bytes];
+    return { cfg: qwen2Config(g.meta), version: g.version, dataStart: g.dataStart, tensors };
+  }
+  if (cmd === "load") {
+    try {
+      const llm = await LLM.load({ path: args[0], ctx: Number(args[1]) });
+      llm.destroy();
+      return { ok: true };
+    } catch (e) {
+      return { error: String(e.message), code: e.code === undefined ? null : e.code };
+    }
+  }
+  if (cmd === "generate") {
+    const ids = JSON.parse(fs.readFileSync(args[2], "utf8"));
+    const steps = Number(args[3]);
+    const llm = await LLM.load({ path: args[0], ctx: Number(args[1]) });
+    const tokens = await llm.generateIds(ids, steps);
+    const stats = llm.stats;
+    const lg = await llm.be.readLogits();
+    fs.writeFileSync(args[4], Buffer.from(lg.buffer));
+    const device = await llm.generateIdsDevice(ids, steps);
+    let ctxError = null;
+    try { await llm.be.forward([1], llm.be.ctx - 1); } catch (e) { ctxError = e.message; }
+    llm.destroy();
+    return { tokens, device, stats, deviceStats: llm.stats, ctxError };
+  }
+  if (cmd === "sample") {
+    const b = fs.readFileSync(args[0]);
+    const lg = new Float32Array(b.buffer, b.byteOffset, b.length / 4);
+    return { id: sample(lg, Number(args[1]), Number(args[2]) >>> 0) };
+  }
+  throw new Error(`unknown command ${cmd}`);
+}
+
+main().then((r) => { process.stdout.write(JSON.stringify(r) + "\n"); },
+  (e) => { process.stderr.write(String(e && e.stack || e) + "\n"); process.exit(1); });
