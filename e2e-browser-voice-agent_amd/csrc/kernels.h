@@ -30,11 +30,16 @@ constexpr int kRowTile = 64;        // rows per weight tile
 constexpr int kMaxChunk = 16;       // tokens per prefill pass (the reference's MT default, engine/cpu.js:228)
 
 // Device-resident step state: pos0 of the current pass, last sampled token.  Kernels read
-// pos0 from here so one captured graph replays every decode step.
+// pos0 from here so one captured graph replays every decode step.  The persistent decode kernel
+// also keeps its exchange epoch here (so consecutive launches never reuse an epoch) and an abort
+// flag that any workgroup raises when a bounded wait runs out.
 struct State {
   int pos0;
   int next;
-  int pad[2];
+  unsigned epoch;
+  int abort;
+  int fail_phase;
+  int pad[3];
 };
 
 // ---------------------------------------------------------------- arithmetic helpers

@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "kernels.h"
+#include "persistent.h"
 #include "q4hip.h"
 
 using namespace q4;
@@ -414,6 +415,16 @@ struct q4hip {
   int* pin_next = nullptr;
   hipGraphExec_t graph = nullptr;
   bool graph_failed = false;
+  int last_mode = 0;
+  // persistent decode (one launch per forward/generate call)
+  int mode = Q4HIP_DECODE_AUTO;
+  bool pers_ok = false;        // shape and device admit the persistent kernel
+  bool pers_broken = false;    // a launch failed or timed out: use the graph from then on
+  LayerView* d_layers = nullptr;
+  uint64_t* ll = nullptr;
+  int pers_grid = 0;
+  size_t pers_lds = 0;
+  const void* pers_fn = nullptr;
   // profiling: events recorded around each launch of an eager step
   std::vector<std::pair<int, hipEvent_t>>* prof = nullptr;
 };
@@ -505,6 +516,95 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
   prof_mark(h, -1);
 }
 
+int wave_groups(int ng) { return (((ng + 3) >> 2) + 1) & ~1; }
+
+// Decide once whether this model and device admit the persistent decode kernel, and set it up.
+void setup_persistent(q4hip* h) {
+  if (h->pers_ok || h->pers_broken || h->mode == Q4HIP_DECODE_GRAPH) return;
+  h->pers_broken = true;   // until proven otherwise
+  const int D = h->D, F = h->F;
+  if (h->HD != kHD || D % 64 || F % 32) return;
+  const Layer& y0 = h->L[0];
+  const int ngD = y0.qkv.ng, perO = wave_groups(y0.o.ng), perDn = wave_groups(y0.down.ng);
+  if (ngD <= 7 && perO <= 2 && perDn <= 10) h->pers_fn = (const void*)k_decode_persistent<7, 2, 10>;
+  else if (ngD <= 8 && perO <= 4 && perDn <= 18) h->pers_fn = (const void*)k_decode_persistent<8, 4, 18>;
+  else return;
+  const int nbm = std::max(D, F) / 32;
+  if (h->ctx > 64 * nbm) return;
+  h->pers_lds = psmem_bytes(D, F);
+  if (h->pers_lds > 65536) return;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device) != hipSuccess) return;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, h->pers_fn, kPThreads, h->pers_lds) != hipSuccess || per_cu < 1) {
+    (void)hipGetLastError();
+    return;
+  }
+  // One workgroup per CU: all of them fit on the device at once, which the waits between them
+  // rely on (a workgroup that could not start would only make the others time out and abort).
+  const int need = D / 16 + h->H + F / 32;
+  const int G = cus;
+  if (need > G || G > 256) return;   // the head argmax exchange gives one entry per thread of a WG
+  std::vector<LayerView> lv(h->NL);
+  for (int l = 0; l < h->NL; l++) {
+    const Layer& y = h->L[l];
+    lv[l] = LayerView{y.qkv.view(), y.o.view(), y.gu.view(), y.down.view(), y.attn_norm, y.ffn_norm, y.bqkv};
+  }
+  const size_t ll_entries = (size_t)3 * D + (size_t)(F / 32) * 9 + 2 * (size_t)G;
+  if (hipMalloc(&h->d_layers, lv.size() * sizeof(LayerView)) != hipSuccess ||
+      hipMemcpy(h->d_layers, lv.data(), lv.size() * sizeof(LayerView), hipMemcpyHostToDevice) != hipSuccess ||
+      hipMalloc(&h->ll, ll_entries * 8) != hipSuccess || hipMemset(h->ll, 0, ll_entries * 8) != hipSuccess) {
+    (void)hipGetLastError();
+    return;
+  }
+  h->pers_grid = G;
+  h->pers_ok = true;
+  h->pers_broken = false;
+}
+
+bool use_persistent(q4hip* h) {
+  if (h->mode == Q4HIP_DECODE_GRAPH) return false;
+  setup_persistent(h);
+  return h->pers_ok && !h->pers_broken;
+}
+
+hipError_t launch_persistent(q4hip* h, int steps, unsigned long long* prof = nullptr) {
+  PArgs a;
+  a.D = h->D; a.F = h->F; a.H = h->H; a.KVH = h->KVH; a.QKV = h->QKV; a.V = h->V; a.NL = h->NL; a.ctx = h->ctx;
+  a.eps = h->eps;
+  a.embd = h->embd;
+  a.out_norm = h->out_norm;
+  a.head = h->head.view();
+  a.layers = h->d_layers;
+  a.rope = h->rope;
+  a.kc = h->kc;
+  a.vc = h->vc;
+  a.logits = h->logits;
+  a.tokens = h->tokens;
+  a.st = h->st;
+  a.ll = h->ll;
+  a.steps = steps;
+  a.nOD = h->D / 16;
+  a.nA = h->H;
+  a.nGU = h->F / 32;
+  a.prof = prof;
+  void* args[] = {&a};
+  return hipLaunchKernel(h->pers_fn, dim3(h->pers_grid), dim3(kPThreads), args, h->pers_lds, h->stream);
+}
+
+// After a synchronised persistent launch: a raised abort flag means a bounded wait ran out (for
+// example because another process held CUs so not every workgroup could start).  Clears the flag,
+// switches this context to the graph path and returns true: the caller reruns the call, which
+// overwrites everything the aborted launch wrote (K/V from pos on, tokens after pos).
+bool aborted(q4hip* h) {
+  State hs;
+  if (hipMemcpy(&hs, h->st, sizeof(State), hipMemcpyDeviceToHost) != hipSuccess) return false;
+  if (!hs.abort) return false;
+  h->pers_broken = true;
+  hs.abort = 0;
+  (void)hipMemcpy(h->st, &hs, sizeof(State), hipMemcpyHostToDevice);
+  return true;
+}
+
 int build_graph(q4hip* h) {
   if (h->graph || h->graph_failed) return Q4HIP_OK;
   const char* env = getenv("Q4HIP_GRAPH");
@@ -562,7 +662,7 @@ void q4hip_destroy(q4hip* h) {
   }
   mat_free(h->head);
   void* bufs[] = {h->embd, h->out_norm, h->rope, h->x, h->qkv, h->att, h->gu, h->logits, h->kc, h->vc,
-                  h->xq, h->am_v, h->am_i, h->tokens, h->st};
+                  h->xq, h->am_v, h->am_i, h->tokens, h->st, h->d_layers, h->ll};
   for (void* p : bufs) if (p) (void)hipFree(p);
   if (h->pin_ids) (void)hipHostFree(h->pin_ids);
   if (h->pin_next) (void)hipHostFree(h->pin_next);
@@ -713,20 +813,55 @@ int q4hip_forward(q4hip* h, const int* ids, int n, int pos, int* next) {
   rc = check_ids(h, ids, n);
   if (rc) return rc;
   HIPCHK(hipSetDevice(h->device));
-  if (n == 1) build_graph(h);
+  const bool pers = n == 1 && use_persistent(h);
+  if (n == 1 && !pers) build_graph(h);
   memcpy(h->pin_ids, ids, (size_t)n * 4);
   HIPCHK(hipMemcpyAsync(h->tokens + pos, h->pin_ids, (size_t)n * 4, hipMemcpyHostToDevice, h->stream));
   for (int c = 0; c < n; c += h->MT) {
     const int k = std::min(h->MT, n - c);
     const bool last = c + k >= n;
     k_set_pos<<<1, 64, 0, h->stream>>>(h->st, pos + c);
-    if (k == 1 && last && h->graph) HIPCHK(hipGraphLaunch(h->graph, h->stream));
-    else enqueue_pass(h, k, last);
+    if (k == 1 && last && pers) {
+      HIPCHK(launch_persistent(h, 1));
+      h->last_mode = Q4HIP_DECODE_PERSISTENT;
+    } else if (k == 1 && last && h->graph) {
+      HIPCHK(hipGraphLaunch(h->graph, h->stream));
+      h->last_mode = Q4HIP_DECODE_GRAPH;
+    } else {
+      enqueue_pass(h, k, last);
+      if (k == 1) h->last_mode = Q4HIP_DECODE_GRAPH;
+    }
   }
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(h->pin_next, &h->st->next, 4, hipMemcpyDeviceToHost, h->stream));
   HIPCHK(hipStreamSynchronize(h->stream));
+  if (pers && aborted(h)) return q4hip_forward(h, ids, n, pos, next);
   *next = h->pin_next[0];
+  return Q4HIP_OK;
+}
+
+int q4hip_set_decode_mode(q4hip* h, int mode) {
+  if (!h) return fail(Q4HIP_EINVAL, "null argument");
+  if (mode != Q4HIP_DECODE_AUTO && mode != Q4HIP_DECODE_GRAPH && mode != Q4HIP_DECODE_PERSISTENT)
+    return fail(Q4HIP_EINVAL, "unknown decode mode %d", mode);
+  HIPCHK(hipSetDevice(h->device));
+  h->mode = mode;
+  if (mode == Q4HIP_DECODE_PERSISTENT) {
+    int rc = check_ready(h);
+    if (rc) return rc;
+    h->pers_broken = false;
+    setup_persistent(h);
+    if (!h->pers_ok || h->pers_broken) {
+      h->mode = Q4HIP_DECODE_AUTO;
+      return fail(Q4HIP_EINVAL, "the persistent decode kernel does not support this model or device");
+    }
+  }
+  return Q4HIP_OK;
+}
+
+int q4hip_decode_mode_used(q4hip* h, int* mode) {
+  if (!h || !mode) return fail(Q4HIP_EINVAL, "null argument");
+  *mode = h->last_mode;
   return Q4HIP_OK;
 }
 
@@ -748,7 +883,8 @@ static int run_generate(q4hip* h, int first, int pos, int steps, int* out, float
   rc = check_ids(h, &first, 1);
   if (rc) return rc;
   HIPCHK(hipSetDevice(h->device));
-  build_graph(h);
+  const bool pers = use_persistent(h);
+  if (!pers) build_graph(h);
   h->pin_ids[0] = first;
   HIPCHK(hipMemcpyAsync(h->tokens + pos, h->pin_ids, 4, hipMemcpyHostToDevice, h->stream));
   k_set_pos<<<1, 64, 0, h->stream>>>(h->st, pos);
@@ -758,11 +894,18 @@ static int run_generate(q4hip* h, int first, int pos, int steps, int* out, float
     HIPCHK(hipEventCreate(&e1));
     HIPCHK(hipEventRecord(e0, h->stream));
   }
-  for (int i = 0; i < steps; i++) decode_step(h);
+  if (pers) {
+    HIPCHK(launch_persistent(h, steps));
+    h->last_mode = Q4HIP_DECODE_PERSISTENT;
+  } else {
+    for (int i = 0; i < steps; i++) decode_step(h);
+    h->last_mode = Q4HIP_DECODE_GRAPH;
+  }
   if (ms) HIPCHK(hipEventRecord(e1, h->stream));
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(h->pin_ids, h->tokens + pos + 1, (size_t)steps * 4, hipMemcpyDeviceToHost, h->stream));
   HIPCHK(hipStreamSynchronize(h->stream));
+  if (pers && aborted(h)) return run_generate(h, first, pos, steps, out, ms);
   memcpy(out, h->pin_ids, (size_t)steps * 4);
   if (ms) {
     HIPCHK(hipEventElapsedTime(ms, e0, e1));
@@ -807,6 +950,37 @@ int q4hip_profile(q4hip* h, int token, int pos, float* us, int n) {
   }
   for (auto& p : marks) (void)hipEventDestroy(p.second);
   if (e != hipSuccess) return fail(Q4HIP_EHIP, "profile: %s", hipGetErrorString(e));
+  return Q4HIP_OK;
+}
+
+int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n) {
+  if (!h || !us) return fail(Q4HIP_EINVAL, "null argument");
+  if (n < (h->NL + 1) * 16) return fail(Q4HIP_EINVAL, "need %d entries", (h->NL + 1) * 16);
+  if (pos < 0 || pos + 1 >= h->ctx) return fail(Q4HIP_ECONTEXT, "context full");
+  int rc = check_ready(h);
+  if (rc) return rc;
+  rc = check_ids(h, &token, 1);
+  if (rc) return rc;
+  HIPCHK(hipSetDevice(h->device));
+  if (!use_persistent(h)) return fail(Q4HIP_EINVAL, "the persistent decode kernel is not in use");
+  const int cnt = (h->NL + 1) * 16;
+  unsigned long long* d = nullptr;
+  HIPCHK(hipMalloc(&d, (size_t)cnt * 8));
+  std::vector<unsigned long long> t(cnt, 0);
+  hipError_t e = hipMemset(d, 0, (size_t)cnt * 8);
+  h->pin_ids[0] = token;
+  if (e == hipSuccess) e = hipMemcpyAsync(h->tokens + pos, h->pin_ids, 4, hipMemcpyHostToDevice, h->stream);
+  if (e == hipSuccess) {
+    k_set_pos<<<1, 64, 0, h->stream>>>(h->st, pos);
+    e = launch_persistent(h, 1, d);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+  if (e == hipSuccess) e = hipMemcpy(t.data(), d, (size_t)cnt * 8, hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) return fail(Q4HIP_EHIP, "persistent profile: %s", hipGetErrorString(e));
+  if (aborted(h)) return fail(Q4HIP_EHIP, "persistent profile: a bounded wait timed out");
+  const unsigned long long t0 = t[h->NL * 16 + 3];
+  for (int i = 0; i < cnt; i++) us[i] = t[i] ? (float)((double)(long long)(t[i] - t0) * 0.01) : -1.0f;
   return Q4HIP_OK;
 }
 

@@ -17,6 +17,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libq4hip.so")
 
 OK, EINVAL, ECONTEXT, ETYPE, EHIP, ESTATE = 0, 1, 2, 3, 4, 5
+DECODE_AUTO, DECODE_GRAPH, DECODE_PERSISTENT = 0, 1, 2
 PROF_NAMES = ["embed", "norm+quantize", "matvec qkv", "rope+kv", "attention", "quantize", "matvec o",
               "matvec gate+up", "swiglu+quantize", "matvec down", "matvec output", "sample"]
 
@@ -24,7 +25,7 @@ EXPORTS = [
     "q4hip_last_error", "q4hip_device_count", "q4hip_create", "q4hip_set_tensor", "q4hip_set_rope",
     "q4hip_forward", "q4hip_read_logits", "q4hip_generate", "q4hip_profile", "q4hip_time_generate",
     "q4hip_time_head", "q4hip_destroy", "q4hip_mv_create", "q4hip_mv_run", "q4hip_mv_time",
-    "q4hip_mv_destroy",
+    "q4hip_mv_destroy", "q4hip_set_decode_mode", "q4hip_decode_mode_used", "q4hip_profile_persistent",
 ]
 
 _lib = None
@@ -61,6 +62,9 @@ def lib() -> ctypes.CDLL:
         "q4hip_mv_run": (I, [P, P, P]),
         "q4hip_mv_time": (I, [P, I, ctypes.POINTER(F)]),
         "q4hip_mv_destroy": (None, [P]),
+        "q4hip_set_decode_mode": (I, [P, I]),
+        "q4hip_decode_mode_used": (I, [P, ctypes.POINTER(I)]),
+        "q4hip_profile_persistent": (I, [P, I, I, P, I]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -134,6 +138,14 @@ class Model:
         rope = np.ascontiguousarray(rope, dtype=np.float32)
         _check(lib().q4hip_set_rope(self.h, _ptr(rope), rope.shape[0]))
 
+    def set_decode_mode(self, mode: int) -> None:
+        _check(lib().q4hip_set_decode_mode(self.h, mode))
+
+    def decode_mode_used(self) -> int:
+        m = ctypes.c_int(0)
+        _check(lib().q4hip_decode_mode_used(self.h, ctypes.byref(m)))
+        return m.value
+
     def forward(self, ids, pos: int) -> int:
         a = np.ascontiguousarray(ids, dtype=np.int32)
         nxt = ctypes.c_int(0)
@@ -160,6 +172,14 @@ class Model:
         us = np.zeros(len(PROF_NAMES), dtype=np.float32)
         _check(lib().q4hip_profile(self.h, token, pos, _ptr(us), us.size))
         return dict(zip(PROF_NAMES, us.tolist()))
+
+    def profile_persistent(self, token: int, pos: int) -> np.ndarray:
+        """Timeline of one persistent decode step, microseconds from kernel start,
+        shape (layers + 1, 16); see q4hip_profile_persistent in include/q4hip.h."""
+        n = (self.shape.layers + 1) * 16
+        us = np.zeros(n, dtype=np.float32)
+        _check(lib().q4hip_profile_persistent(self.h, token, pos, _ptr(us), n))
+        return us.reshape(self.shape.layers + 1, 16)
 
     def time_head(self, iters: int) -> float:
         us = ctypes.c_float(0)

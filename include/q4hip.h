@@ -78,6 +78,20 @@ int q4hip_set_rope(q4hip* h, const float* table, int n_pos);
  * K/V of those positions are (over)written; logits of the last token stay on the device. */
 int q4hip_forward(q4hip* h, const int* ids, int n, int pos, int* next);
 
+/* How single-token decode steps run (forward with n == 1, generate):
+ *   AUTO       the persistent kernel when the model and device admit it, else the graph (default)
+ *   GRAPH      a captured hipGraph of one launch per operation
+ *   PERSISTENT one launch per call that runs all of the call's steps; fails with
+ *              Q4HIP_EINVAL if the model (head_dim 64, D <= 1024, ...) or device does not admit it.
+ * Both give bit-identical results.  The reference picks among its kernel builds the same way
+ * (engine/cpu.js:199-206); this has no other counterpart there. */
+#define Q4HIP_DECODE_AUTO 0
+#define Q4HIP_DECODE_GRAPH 1
+#define Q4HIP_DECODE_PERSISTENT 2
+int q4hip_set_decode_mode(q4hip* h, int mode);
+/* The path the last decode step took (Q4HIP_DECODE_GRAPH or Q4HIP_DECODE_PERSISTENT; 0 before any). */
+int q4hip_decode_mode_used(q4hip* h, int* mode);
+
 /* Copy the last forward's logits (vocab floats) to host memory: readLogits (engine/cpu.js:242). */
 int q4hip_read_logits(q4hip* h, float* out, int n);
 
@@ -103,6 +117,14 @@ int q4hip_generate(q4hip* h, int first, int pos, int steps, int* out);
 #define Q4HIP_PROF_SAMPLE 11
 #define Q4HIP_PROF_N 12
 int q4hip_profile(q4hip* h, int token, int pos, float* us, int n);
+
+/* Timeline of one persistent decode step (forward([token], pos)), in microseconds from the
+ * kernel's start, for (layers + 1) * 16 slots; -1 where nothing was recorded.  Per layer l, slot
+ * 16l + k: 0 att received, 1 x after o sent, 2 act received, 3 x after down sent (first o/down
+ * workgroup); 4 x received, 5 q/k/v done, 6 att sent (head 0); 7 x received, 8 act sent (first
+ * gate/up workgroup).  Slots 16L + 0..2: head x received, (value, index) sent, token known.
+ * Measured with the device's constant 100 MHz clock. */
+int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n);
 
 /* Time `steps` greedy decode steps (as q4hip_generate) with HIP events on the context's stream;
  * *ms = elapsed device time of the whole loop. */

@@ -27,12 +27,16 @@ def _bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-def _pair(name, seed, ctx, mt=16, threads=8):
+MODES = ["graph", "persistent"]
+
+
+def _pair(name, seed, ctx, mt=16, threads=8, mode="graph"):
     import q4hip
     shape = synth.SHAPES[name]
     t = _model(name, seed)
     g = q4hip.Model(shape, ctx=ctx, mt=mt)
     g.load(t)
+    g.set_decode_mode(q4hip.DECODE_PERSISTENT if mode == "persistent" else q4hip.DECODE_GRAPH)
     o = oracle.Model(shape, t, ctx=ctx, mt=mt, threads=threads)
     return shape, g, o
 
@@ -45,11 +49,14 @@ def _compare_logits(g, o, what):
     assert bad.size == 0, f"{what}: {bad.size} logits differ (max-abs {diff}), first {bad[:5]}"
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("name,seed,n_prompt", [("tiny", 3, 20), ("tiny", 4, 1), ("small", 5, 37), ("small128", 6, 70)])
-def test_forward_steps_match(name, seed, n_prompt):
+def test_forward_steps_match(name, seed, n_prompt, mode):
     """forward(ids, pos) then forward([next], pos) per step: tokens and logits of every step."""
-    print(f"model {name} seed {seed} prompt {n_prompt}", flush=True)
-    shape, g, o = _pair(name, seed, ctx=128)
+    if mode == "persistent" and synth.SHAPES[name].head_dim != 64:
+        pytest.skip("the persistent decode kernel is specialised for head_dim 64")
+    print(f"model {name} seed {seed} prompt {n_prompt} mode {mode}", flush=True)
+    shape, g, o = _pair(name, seed, ctx=128, mode=mode)
     try:
         ids = synth.prompt_ids(seed, n_prompt, shape.vocab)
         ng, no = g.forward(ids, 0), o.forward(ids, 0)
@@ -61,14 +68,18 @@ def test_forward_steps_match(name, seed, n_prompt):
             assert ng == no, f"step {step}"
             _compare_logits(g, o, f"step {step}")
             pos += 1
+        assert g.decode_mode_used() == (2 if mode == "persistent" else 1)
     finally:
         g.close()
         o.close()
 
 
-def test_generate_matches_forward_loop():
-    """The device-side greedy loop (hipGraph replays) gives the tokens of the per-call loop."""
-    shape, g, o = _pair("small", 11, ctx=256)
+@pytest.mark.parametrize("mode", MODES)
+def test_generate_matches_forward_loop(mode):
+    """The device-side greedy loop (graph replays, or one persistent launch for all steps) gives
+    the tokens of the per-call loop."""
+    print(f"generate small mode {mode}", flush=True)
+    shape, g, o = _pair("small", 11, ctx=256, mode=mode)
     try:
         ids = synth.prompt_ids(11, 30, shape.vocab)
         first = g.forward(ids, 0)
@@ -124,10 +135,11 @@ def test_context_full_and_bad_ids():
 
 
 @pytest.mark.slow
-def test_qwen05b_prompt64_greedy64():
+@pytest.mark.parametrize("mode", MODES)
+def test_qwen05b_prompt64_greedy64(mode):
     """The headline workload: 0.5B shape, 64-token seeded prompt, 64 greedy steps."""
-    print("qwen2.5-0.5b prompt 64 + 64 steps", flush=True)
-    shape, g, o = _pair("qwen2.5-0.5b", 1, ctx=256, threads=16)
+    print(f"qwen2.5-0.5b prompt 64 + 64 steps mode {mode}", flush=True)
+    shape, g, o = _pair("qwen2.5-0.5b", 1, ctx=256, threads=16, mode=mode)
     try:
         ids = synth.prompt_ids(1, 64, shape.vocab)
         ng, no = g.forward(ids, 0), o.forward(ids, 0)
@@ -146,6 +158,26 @@ def test_qwen05b_prompt64_greedy64():
         assert toks_g == toks_o
         dev = g.generate(toks_g[0], 64, 63)
         assert [toks_g[0]] + dev == toks_o
+    finally:
+        g.close()
+        o.close()
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_decode_rewrites_positions(mode):
+    """Decoding again over positions that an earlier launch filled with other tokens gives the
+    oracle's tokens: no K/V written by a previous launch is read stale."""
+    print(f"rewrite positions mode {mode}", flush=True)
+    shape, g, o = _pair("small", 13, ctx=256, mode=mode)
+    try:
+        ids = synth.prompt_ids(13, 30, shape.vocab)
+        first = g.forward(ids, 0)
+        g.generate((first + 1) % shape.vocab, 30, 20)
+        dev = g.generate(first, 30, 20)
+        assert [first] + dev == o.generate(ids, 21)
+        for step in range(3):                       # and single steps over the same positions
+            nxt = g.forward([dev[step] if step else first], 30 + step)
+            assert nxt == dev[step]
     finally:
         g.close()
         o.close()
