@@ -4,15 +4,16 @@
 // (one per CU) stays resident and takes one role for the whole launch:
 //   OD  (D/16 WGs)   rows 16w..16w+15 of o and down; owns those rows of the residual x
 //   A   (heads WGs)  one attention head: its q rows and its kv group's k, v rows (the k/v rows are
-//                    recomputed by the 7 heads of a group instead of exchanged), RoPE, K/V append,
+//                    recomputed by the heads of a group instead of exchanged), RoPE, K/V append,
 //                    attention
 //   GU  (F/32 WGs)   gate and up rows of one 32-value block of the SwiGLU activation, quantized
 //   all              the output head (rows round-robin), then the greedy argmax
 // Four exchanges per layer (att -> OD, x after o -> GU, act -> OD, x after down -> A) and one per
 // step (argmax).  Each exchanged value is stored together with the epoch of the phase that wrote it
 // in one 8-byte agent-scope store ("LL" store): a reader polls the data itself, so a hand-off is
-// one hop.  Every role issues the loads of its next weights before it waits, so weight traffic
-// overlaps the waits.  Waits are bounded: a timeout raises State::abort and every workgroup exits.
+// one hop, and a thread's entries are all in flight at once.  Every role issues the loads of its
+// next weights (and the attention role its past K/V rows) before it waits, so that traffic overlaps
+// the waits.  Waits are bounded: a timeout raises State::abort and every workgroup exits.
 //
 // Arithmetic per output is the one of kernels.h (the reference's lane order), so results are
 // bit-identical to the kernel-per-operation path.
@@ -44,12 +45,40 @@ struct PArgs {
   uint64_t* ll;   // exchange area: X1[D] X2[D] ATT[D] ACT[F/32*9] ARG[2G] (value, index pairs)
   int steps;
   int nOD, nA, nGU;
+  int kv_tile;    // past positions of K and V the attention role stages in shared memory
   unsigned long long* prof;   // optional: phase timestamps of step 0, [(NL + 1) * 16]
 };
 
 constexpr int kPThreads = 256;
 constexpr int kSpinLimit = 1 << 21;
 constexpr int kHD = 64;           // head_dim of the persistent path
+constexpr int kKVRow = 68;        // floats per staged K/V row (64 + 4: conflict-free row-per-thread reads)
+constexpr int kRecvD = 4;         // LL entries per thread for D-vectors (D <= 1024)
+constexpr int kRecvAct = 6;       // LL entries per thread for the quantized activation (9 * F/32 <= 1536)
+
+// ---------------------------------------------------------------- memory helpers
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4 GlobalU32x4;
+typedef __attribute__((address_space(1))) const f32x4 GlobalF32x4;
+typedef __attribute__((address_space(1))) const float GlobalF32;
+
+// Weights and the K/V cache live in global memory; pointers read from the device layer table are
+// generic, so load through explicit global-address-space pointers (global_load, not flat_load).
+__device__ __forceinline__ uint4 gld(const uint4* p) {
+  const u32x4 v = *(GlobalU32x4*)(const void*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 gld4f(const float* p) {
+  const f32x4 v = *(GlobalF32x4*)(const void*)p;
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float gldf(const float* p) { return *(GlobalF32*)(const void*)p; }
+
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // ---------------------------------------------------------------- LL exchange
 
@@ -63,7 +92,8 @@ __device__ __forceinline__ uint64_t ll_peek(const uint64_t* p) {
 
 // Wait for entries base[tid + 256k] (k < K, index < n) to carry epoch ep.  All K loads are in
 // flight together and only the entries still missing are polled again, so a hand-off costs one
-// memory round trip however many entries a thread receives.
+// memory round trip however many entries a thread receives.  Bounded: after kSpinLimit polls the
+// thread raises st->abort; a raised flag makes every waiter give up (`bad`).
 template <int K>
 __device__ __forceinline__ void ll_recv(const uint64_t* base, int n, uint32_t ep, State* st, bool& bad,
                                         uint32_t (&out)[K]) {
@@ -96,28 +126,7 @@ __device__ __forceinline__ void ll_recv(const uint64_t* base, int n, uint32_t ep
   for (int k = 0; k < K; k++) out[k] = (uint32_t)w[k];
 }
 
-__device__ __forceinline__ void st_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // ---------------------------------------------------------------- register-resident weights
-
-// Weights live in global memory; pointers read from the device layer table are generic, so load
-// through an explicit global-address-space pointer (global_load rather than flat_load).
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(1))) const f32x4 GlobalF32x4;
-typedef __attribute__((address_space(1))) const float GlobalF32;
-__device__ __forceinline__ float4 gld4f(const float* p) {
-  const f32x4 v = *(GlobalF32x4*)(const void*)p;
-  return make_float4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ float gldf(const float* p) { return *(GlobalF32*)(const void*)p; }
-typedef __attribute__((address_space(1))) const u32x4 GlobalU32x4;
-__device__ __forceinline__ uint4 gld(const uint4* p) {
-  const u32x4 v = *(GlobalU32x4*)(const void*)p;
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
 
 // Groups [g0, g0+ng) (g0 even) of one 16-row group, lane (r, j): word j of 4 blocks per group and
 // the fp16 scales of 8 blocks per uint4.
@@ -140,64 +149,115 @@ __device__ __forceinline__ void rg_load(const Q4Mat& W, int rg16, int r, int j, 
     R.s[c] = 2 * c < ng ? gld(wd + (size_t)(g0 / 2 + c) * 64) : make_uint4(0, 0, 0, 0);
 }
 
-// One block's term f32(p_j) * (dw * dx) (kernels.c:137).
+// One block's term f32(p_j) * (dw * dx) (kernels.c:137); xv = {A_j, B_j, c_j, dx}.
 template <int NG>
-__device__ __forceinline__ float rg_term(const RG<NG>& R, int g, int k, int b, const uint4* xs, int j) {
+__device__ __forceinline__ float rg_term(const RG<NG>& R, int g, int k, uint4 xv) {
   const uint32_t wv = k == 0 ? R.w[g].x : k == 1 ? R.w[g].y : k == 2 ? R.w[g].z : R.w[g].w;
   const uint4 sv = R.s[g >> 1];
   const int hb = ((g & 1) << 2) + k;
   const uint32_t sw = (hb >> 1) == 0 ? sv.x : (hb >> 1) == 1 ? sv.y : (hb >> 1) == 2 ? sv.z : sv.w;
   const float dw = half_bits_to_float((hb & 1) ? (sw >> 16) : (sw & 0xffffu));
-  const uint4 xv = xs[b * 4 + j];
   int p = sdot4(wv & 0x0F0F0F0Fu, xv.x, (int)xv.z);
   p = sdot4((wv >> 4) & 0x0F0F0F0Fu, xv.y, p);
   return (float)p * (dw * __uint_as_float(xv.w));
 }
 
-// acc = acc + term, blocks of groups [g0, g0+ng) in order (kernels.c:217-218).
-template <int NG>
-__device__ __forceinline__ float rg_dot(const RG<NG>& R, int g0, int ng, int nb, const uint4* xs, int j, float acc) {
+// The four activation blocks of group g for lane j (zero past nb).
+__device__ __forceinline__ void xg_load(const uint4* xs, int g, int nb, int j, uint4 (&xv)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int b = g * 4 + k;
+    xv[k] = b < nb ? xs[b * 4 + j] : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// acc_i = acc_i + term for N row groups sharing each activation read, blocks of groups
+// [g0, g0+ng) in order (kernels.c:217-218); the next group's activation blocks are read ahead.
+template <int NG, int N>
+__device__ __forceinline__ void rg_dot(const RG<NG> (&R)[N], int g0, int ng, int nb, const uint4* xs, int j,
+                                       float (&acc)[N]) {
+  uint4 xa[4], xb[4];
+  if (ng > 0) xg_load(xs, g0, nb, j, xa);
 #pragma unroll
   for (int g = 0; g < NG; g++) {
     if (g < ng) {
+      if (g + 1 < ng) xg_load(xs, g0 + g + 1, nb, j, xb);
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        const int b = (g0 + g) * 4 + k;
-        if (b < nb) acc = acc + rg_term(R, g, k, b, xs, j);
+        if ((g0 + g) * 4 + k < nb) {
+#pragma unroll
+          for (int n = 0; n < N; n++) acc[n] = acc[n] + rg_term(R[n], g, k, xa[k]);
+        }
       }
+#pragma unroll
+      for (int k = 0; k < 4; k++) xa[k] = xb[k];
     }
   }
-  return acc;
 }
 
 // The same terms written to shared memory, terms[b * 64 + lane], for a serial pass by one wave.
 template <int NG>
 __device__ __forceinline__ void rg_terms(const RG<NG>& R, int g0, int ng, int nb, const uint4* xs, int j,
                                          float* terms, int lane) {
+  uint4 xa[4], xb[4];
+  if (ng > 0) xg_load(xs, g0, nb, j, xa);
 #pragma unroll
   for (int g = 0; g < NG; g++) {
     if (g < ng) {
+      if (g + 1 < ng) xg_load(xs, g0 + g + 1, nb, j, xb);
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         const int b = (g0 + g) * 4 + k;
-        if (b < nb) terms[b * 64 + lane] = rg_term(R, g, k, b, xs, j);
+        if (b < nb) terms[b * 64 + lane] = rg_term(R, g, k, xa[k]);
       }
+#pragma unroll
+      for (int k = 0; k < 4; k++) xa[k] = xb[k];
     }
   }
 }
 
-// ((0 + t_0) + t_1) + ... over the blocks, the accumulation order of one reference lane.
+// ((0 + t_0) + t_1) + ... over the blocks, the accumulation order of one reference lane; loads run
+// 8 blocks ahead of the additions.
 __device__ __forceinline__ float serial_sum(const float* terms, int nb, int lane) {
   float acc = 0.0f;
-  int b = 0;
-  for (; b + 8 <= nb; b += 8) {
-    float t[8];
+  float cur[8], nxt[8];
 #pragma unroll
-    for (int u = 0; u < 8; u++) t[u] = terms[(b + u) * 64 + lane];
+  for (int u = 0; u < 8; u++) cur[u] = u < nb ? terms[u * 64 + lane] : 0.0f;
+  for (int b = 0; b < nb; b += 8) {
 #pragma unroll
-    for (int u = 0; u < 8; u++) acc = acc + t[u];
+    for (int u = 0; u < 8; u++) nxt[u] = b + 8 + u < nb ? terms[(b + 8 + u) * 64 + lane] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      if (b + u < nb) acc = acc + cur[u];
+#pragma unroll
+    for (int u = 0; u < 8; u++) cur[u] = nxt[u];
   }
-  for (; b < nb; b++) acc = acc + terms[b * 64 + lane];
+  return acc;
+}
+
+// Sum of x[0..n) in index order (n a multiple of 4, x 16-byte aligned), 16 values loaded ahead.
+__device__ __forceinline__ float serial_sum_vec(const float* x, int n) {
+  const float4* p = reinterpret_cast<const float4*>(x);
+  const int n4 = n >> 2;
+  float acc = 0.0f;
+  float4 cur[4], nxt[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) cur[u] = u < n4 ? p[u] : make_float4(0, 0, 0, 0);
+  for (int b = 0; b < n4; b += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) nxt[u] = b + 4 + u < n4 ? p[b + 4 + u] : make_float4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      if (b + u < n4) {
+        acc = acc + cur[u].x;
+        acc = acc + cur[u].y;
+        acc = acc + cur[u].z;
+        acc = acc + cur[u].w;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) cur[u] = nxt[u];
+  }
   return acc;
 }
 
@@ -220,26 +280,30 @@ __device__ __forceinline__ float embed_value(const uint8_t* emb, int D, int t, i
 // ---------------------------------------------------------------- shared memory plan
 
 struct PSmem {
-  float* xl;      // (D/4 + 1) * 4 floats: a row staged by lane, or plain
+  float* xl;      // (D + 16) floats: a row staged by lane (run stride D/4 + 4), or plain
   uint4* xq;      // activation blocks, max(nbD, nbF) * 4
-  float* terms;   // 64 * max(nbD, nbF) floats; attention scores
+  float* terms;   // 64 * max(nbD, nbF) floats; attention scores; raw exchange entries
+  uint4* tq;      // 4 (GU quantized block)
   float* red;     // 16
   float* qv;      // 3 * 64: q, k, v of one head
   float* own;     // 16 residual rows (OD)
   float* gu;      // 64: gate, up (GU)
-  uint4* tq;      // 4 (GU quantized block)
   float* argv;    // 256
   int* argi;      // 256
+  float* kvt;     // kv_tile * 2 * kKVRow: staged past K and V rows (A)
 };
 
-__host__ __device__ inline size_t psmem_bytes(int D, int F) {
+__host__ __device__ inline size_t psmem_base_bytes(int D, int F) {
   const int nbm = (D > F ? D : F) / 32;
-  size_t b = (size_t)(D + 4) * 4;
-  b = (b + 15) & ~(size_t)15;
+  size_t b = (size_t)(D + 16) * 4;
   b += (size_t)nbm * 64;
   b += (size_t)64 * nbm * 4;
-  b += (16 + 192 + 16 + 64 + 16 + 256 + 256) * 4;
+  b += (16 + 16 + 192 + 16 + 64 + 256 + 256) * 4;
   return b;
+}
+
+__host__ __device__ inline size_t psmem_bytes(int D, int F, int kv_tile) {
+  return psmem_base_bytes(D, F) + (size_t)kv_tile * 2 * kKVRow * 4;
 }
 
 __device__ __forceinline__ PSmem psmem(unsigned char* base, int D, int F) {
@@ -247,8 +311,7 @@ __device__ __forceinline__ PSmem psmem(unsigned char* base, int D, int F) {
   PSmem m;
   size_t off = 0;
   m.xl = (float*)(base + off);
-  off += (size_t)(D + 4) * 4;
-  off = (off + 15) & ~(size_t)15;
+  off += (size_t)(D + 16) * 4;
   m.xq = (uint4*)(base + off);
   off += (size_t)nbm * 64;
   m.terms = (float*)(base + off);
@@ -266,6 +329,8 @@ __device__ __forceinline__ PSmem psmem(unsigned char* base, int D, int F) {
   m.argv = (float*)(base + off);
   off += 256 * 4;
   m.argi = (int*)(base + off);
+  off += 256 * 4;
+  m.kvt = (float*)(base + off);
   return m;
 }
 
@@ -273,12 +338,11 @@ __device__ __forceinline__ uint32_t phase_epoch(uint32_t ep0, int s, int E, int 
   return ep0 + (uint32_t)(s * E + code) + 1u;
 }
 
-constexpr int kRecvD = 4;    // entries per thread for D-vectors (D <= 1024)
-constexpr int kRecvAct = 6;  // entries per thread for the quantized activation (9 * F/32 <= 1536)
+__device__ __forceinline__ int run_stride(int D) { return D / 4 + 4; }
 
-// Wait for the D-vector `src` (epoch ep) and stage it by lane into xl (st = D/4 + 1).
+// Wait for the D-vector `src` (epoch ep) and stage it by lane into xl.
 __device__ __forceinline__ void recv_x(const uint64_t* src, int D, uint32_t ep, State* st, float* xl, bool& bad) {
-  const int stv = D / 4 + 1;
+  const int stv = run_stride(D);
   uint32_t v[kRecvD];
   ll_recv<kRecvD>(src, D, ep, st, bad, v);
 #pragma unroll
@@ -288,15 +352,41 @@ __device__ __forceinline__ void recv_x(const uint64_t* src, int D, uint32_t ep, 
   }
 }
 
-__device__ __forceinline__ void prof_mark(const PArgs a, int s, int slot) {
-  if (a.prof && s == 0 && threadIdx.x == 0) a.prof[slot] = wall_clock64();
-}
-
-// RMSNorm + quantize the staged row into m.xq (kernels.c:328-331).
+// RMSNorm + quantize the staged row into m.xq (kernels.c:80-86, 328-331).  Threads 0..3 run the
+// four lane sums of x*x, each over its contiguous run, 16 values loaded ahead.
 __device__ __forceinline__ void norm_quant(const PSmem m, int D, const float* w, float eps) {
-  const int stv = D / 4 + 1;
-  const float rs = rms_scale_staged(m.xl, D, stv, eps, m.red);
-  quantize_row_dev<QM_NORM>(nullptr, m.xl, stv, D, w, rs, m.xq, threadIdx.x, kPThreads);
+  const int stv = run_stride(D), tid = threadIdx.x;
+  if (tid < 4) {
+    const float4* p = reinterpret_cast<const float4*>(m.xl + tid * stv);
+    const int n4 = D >> 4;
+    float s = 0.0f;
+    float4 cur[4], nxt[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) cur[u] = u < n4 ? p[u] : make_float4(0, 0, 0, 0);
+    for (int b = 0; b < n4; b += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; u++) nxt[u] = b + 4 + u < n4 ? p[b + 4 + u] : make_float4(0, 0, 0, 0);
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        if (b + u < n4) {
+          s = s + cur[u].x * cur[u].x;
+          s = s + cur[u].y * cur[u].y;
+          s = s + cur[u].z * cur[u].z;
+          s = s + cur[u].w * cur[u].w;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) cur[u] = nxt[u];
+    }
+    m.red[tid] = s;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const float ss = m.red[0] + m.red[1] + m.red[2] + m.red[3];
+    m.red[4] = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+  }
+  __syncthreads();
+  quantize_row_dev<QM_NORM>(nullptr, m.xl, stv, D, w, m.red[4], m.xq, tid, kPThreads);
   __syncthreads();
 }
 
@@ -305,10 +395,28 @@ __device__ __forceinline__ void arg_merge(float& bv, int& bi, float v, int i) {
   if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) { bv = v; bi = i; }
 }
 
+__device__ __forceinline__ void prof_mark(const PArgs a, int s, int slot) {
+  if (a.prof && s == 0 && threadIdx.x == 0) a.prof[slot] = wall_clock64();
+}
+
 // ---------------------------------------------------------------- the output head + argmax
 
 template <int NGD>
-__device__ __forceinline__ int head_phase(const PArgs a, const PSmem m, int s, int pos, uint32_t ep0, int E, bool& bad) {
+__device__ __forceinline__ void head_rows(const PArgs a, const PSmem m, const RG<NGD> (&R)[1], int rg, int ngD,
+                                          int nbD, int r, int j, float& bv, int& bi) {
+  float acc[1] = {0.0f};
+  rg_dot<NGD, 1>(R, 0, ngD, nbD, m.xq, j, acc);
+  const float v = hsum4(acc[0]);
+  const int row = rg * 16 + r;
+  if (j == 0 && row < a.V) {
+    a.logits[row] = v;
+    arg_merge(bv, bi, v, row);
+  }
+}
+
+template <int NGD>
+__device__ __forceinline__ int head_phase(const PArgs a, const PSmem m, int s, int pos, uint32_t ep0, int E,
+                                          bool& bad) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane >> 2, j = lane & 3;
   const int G = gridDim.x, wg = blockIdx.x, D = a.D, nbD = D / 32;
   const Q4Mat& W = a.head;
@@ -319,10 +427,12 @@ __device__ __forceinline__ int head_phase(const PArgs a, const PSmem m, int s, i
   const uint32_t epx = phase_epoch(ep0, s, E, 4 * (a.NL - 1) + 3);
   const uint32_t eph = phase_epoch(ep0, s, E, 4 * a.NL);
 
-  // first row group's weights before waiting for x
+  // the first two row groups' weights are in flight before waiting for x
+  const int stride = 4 * G;
   int rgi = wg + G * wave;
-  RG<NGD> cur, nxt;
-  if (rgi < nRG) rg_load<NGD>(W, rgi, r, j, 0, ngD, cur);
+  RG<NGD> R0[1], R1[1], R2[1];
+  if (rgi < nRG) rg_load<NGD>(W, rgi, r, j, 0, ngD, R0[0]);
+  if (rgi + stride < nRG) rg_load<NGD>(W, rgi + stride, r, j, 0, ngD, R1[0]);
   recv_x(LX2, D, epx, a.st, m.xl, bad);
   if (__syncthreads_or(bad)) return -1;
   prof_mark(a, s, a.NL * 16 + 0);
@@ -330,17 +440,19 @@ __device__ __forceinline__ int head_phase(const PArgs a, const PSmem m, int s, i
 
   float bv = 0.0f;
   int bi = -1;
+  // three rotating buffers: two row groups in flight while one is computed
   while (rgi < nRG) {
-    const int nx = rgi + 4 * G;
-    if (nx < nRG) rg_load<NGD>(W, nx, r, j, 0, ngD, nxt);
-    const float v = hsum4(rg_dot<NGD>(cur, 0, ngD, nbD, m.xq, j, 0.0f));
-    const int row = rgi * 16 + r;
-    if (j == 0 && row < a.V) {
-      a.logits[row] = v;
-      arg_merge(bv, bi, v, row);
-    }
-    if (nx < nRG) cur = nxt;
-    rgi = nx;
+    if (rgi + 2 * stride < nRG) rg_load<NGD>(W, rgi + 2 * stride, r, j, 0, ngD, R2[0]);
+    head_rows<NGD>(a, m, R0, rgi, ngD, nbD, r, j, bv, bi);
+    rgi += stride;
+    if (rgi >= nRG) break;
+    if (rgi + 2 * stride < nRG) rg_load<NGD>(W, rgi + 2 * stride, r, j, 0, ngD, R0[0]);
+    head_rows<NGD>(a, m, R1, rgi, ngD, nbD, r, j, bv, bi);
+    rgi += stride;
+    if (rgi >= nRG) break;
+    if (rgi + 2 * stride < nRG) rg_load<NGD>(W, rgi + 2 * stride, r, j, 0, ngD, R1[0]);
+    head_rows<NGD>(a, m, R2, rgi, ngD, nbD, r, j, bv, bi);
+    rgi += stride;
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -368,13 +480,13 @@ __device__ __forceinline__ int head_phase(const PArgs a, const PSmem m, int s, i
   bv = 0.0f;
   bi = -1;
   for (int g = tid; g < G; g += kPThreads) arg_merge(bv, bi, __uint_as_float(raw[2 * g]), (int)raw[2 * g + 1]);
-  if (__syncthreads_or(bad)) return -1;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o);
     const int oi = __shfl_xor(bi, o);
     arg_merge(bv, bi, ov, oi);
   }
+  __syncthreads();
   if (lane == 0) { m.argv[wave] = bv; m.argi[wave] = bi; }
   __syncthreads();
   bv = m.argv[0];
@@ -384,6 +496,7 @@ __device__ __forceinline__ int head_phase(const PArgs a, const PSmem m, int s, i
   const int next = bi < 0 ? 0 : bi;
   if (wg == 0 && tid == 0) a.tokens[pos + 1] = next;
   prof_mark(a, s, a.NL * 16 + 2);
+  if (a.prof && s == 0 && wg == 0 && tid == 0) a.prof[a.NL * 16 + 5] = clock64();
   return next;
 }
 
@@ -441,6 +554,7 @@ __device__ __forceinline__ void role_od(const PArgs a, const PSmem m, uint32_t e
         uint32_t v[kRecvAct];
         uint32_t* raw = (uint32_t*)m.terms;
         ll_recv<kRecvAct>(LACT, nbF * 9, ep_act, a.st, bad, v);
+        __syncthreads();   // wave 0's serial pass over m.terms has finished
 #pragma unroll
         for (int k = 0; k < kRecvAct; k++)
           if (tid + 256 * k < nbF * 9) raw[tid + 256 * k] = v[k];
@@ -482,7 +596,8 @@ __device__ __forceinline__ void role_od(const PArgs a, const PSmem m, uint32_t e
 }
 
 // One attention head h: q rows of h and k, v rows of its kv group, RoPE, K/V append (first head of
-// the group), attention over the cache (kernels.c:333-377).
+// the group), attention over the cache (kernels.c:333-377).  Past K/V rows (up to kv_tile of them)
+// are staged in shared memory while the role waits for x.
 template <int NGD>
 __device__ __forceinline__ void role_attn(const PArgs a, const PSmem m, uint32_t ep0, int pos, int tok) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane >> 2, j = lane & 3;
@@ -496,17 +611,28 @@ __device__ __forceinline__ void role_attn(const PArgs a, const PSmem m, uint32_t
   float* kv = m.qv + 64;
   float* vv = m.qv + 128;
   float* sc = m.terms;
+  float* kt = m.kvt;                              // [kv_tile][kKVRow] K
+  float* vt = m.kvt + (size_t)a.kv_tile * kKVRow;  // [kv_tile][kKVRow] V
   bool bad = false;
   for (int s = 0; s < a.steps; s++, pos++) {
+    const int nt = pos < a.kv_tile ? pos : a.kv_tile;    // staged past positions
     for (int l = 0; l < a.NL; l++) {
       const LayerView L = a.layers[l];
       const int ng = L.qkv.ng;
-      RG<NGD> wq, wk, wvv;
-      rg_load<NGD>(L.qkv, rq, r, j, 0, ng, wq);
-      rg_load<NGD>(L.qkv, rk, r, j, 0, ng, wk);
-      rg_load<NGD>(L.qkv, rv, r, j, 0, ng, wvv);
-      const int stv = D / 4 + 1;
+      RG<NGD> w3[3];
+      rg_load<NGD>(L.qkv, rq, r, j, 0, ng, w3[0]);
+      rg_load<NGD>(L.qkv, rk, r, j, 0, ng, w3[1]);
+      rg_load<NGD>(L.qkv, rv, r, j, 0, ng, w3[2]);
+      const size_t cbase = ((size_t)l * a.KVH + kh) * a.ctx * kHD;
+      // stage K and V of positions [0, nt) (written by earlier steps or launches)
+      for (int idx = tid; idx < nt * 32; idx += kPThreads) {
+        const int which = idx >= nt * 16, rem = idx - which * nt * 16, t = rem >> 4, c4 = (rem & 15) * 4;
+        const float4 v4 = gld4f((which ? a.vc : a.kc) + cbase + (size_t)t * kHD + c4);
+        float* dst = (which ? vt : kt) + t * kKVRow + c4;
+        *reinterpret_cast<float4*>(dst) = v4;
+      }
       if (l == 0) {
+        const int stv = run_stride(D);
         for (int i = tid; i < D; i += kPThreads) m.xl[(i & 3) * stv + (i >> 2)] = embed_value(a.embd, D, tok, i);
       } else {
         recv_x(LX2, D, phase_epoch(ep0, s, E, 4 * (l - 1) + 3), a.st, m.xl, bad);
@@ -514,9 +640,9 @@ __device__ __forceinline__ void role_attn(const PArgs a, const PSmem m, uint32_t
       if (__syncthreads_or(bad)) return;
       if (h == 0) prof_mark(a, s, l * 16 + 4);
       norm_quant(m, D, L.attn_norm, a.eps);
-      const float q = hsum4(rg_dot<NGD>(wq, 0, ng, nbD, m.xq, j, 0.0f));
-      const float k = hsum4(rg_dot<NGD>(wk, 0, ng, nbD, m.xq, j, 0.0f));
-      const float v = hsum4(rg_dot<NGD>(wvv, 0, ng, nbD, m.xq, j, 0.0f));
+      float acc[3] = {0.0f, 0.0f, 0.0f};
+      rg_dot<NGD, 3>(w3, 0, ng, nbD, m.xq, j, acc);
+      const float q = hsum4(acc[0]), k = hsum4(acc[1]), v = hsum4(acc[2]);
       if (j == 0) {
         qv[16 * wave + r] = q + L.bqkv[rq * 16 + r];
         kv[16 * wave + r] = k + L.bqkv[rk * 16 + r];
@@ -534,37 +660,34 @@ __device__ __forceinline__ void role_attn(const PArgs a, const PSmem m, uint32_t
         x[i + 32] = x1 * c + x0 * sn;
       }
       __syncthreads();
-      const size_t cbase = ((size_t)l * a.KVH + kh) * a.ctx * kHD;
       if (writer && tid < 64) {
         st_coherent(a.kc + cbase + (size_t)pos * kHD + tid, kv[tid]);
         st_coherent(a.vc + cbase + (size_t)pos * kHD + tid, vv[tid]);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
       }
       // scores: four lane sums over i = j mod 4, hsum, scale (kernels.c:362-366)
       const int T = pos + 1;
       const float scale = 1.0f / __builtin_sqrtf((float)kHD);
       float lmax = -1e30f;
       for (int t = tid; t < T; t += kPThreads) {
-        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+        float4 kk[kHD / 4];
         if (t == pos) {
-          for (int i = 0; i < kHD; i += 4) {
-            s0 = s0 + qv[i] * kv[i];
-            s1 = s1 + qv[i + 1] * kv[i + 1];
-            s2 = s2 + qv[i + 2] * kv[i + 2];
-            s3 = s3 + qv[i + 3] * kv[i + 3];
-          }
+#pragma unroll
+          for (int i = 0; i < kHD / 4; i++) kk[i] = reinterpret_cast<const float4*>(kv)[i];
+        } else if (t < nt) {
+#pragma unroll
+          for (int i = 0; i < kHD / 4; i++) kk[i] = reinterpret_cast<const float4*>(kt + t * kKVRow)[i];
         } else {
-          const float* kr = a.kc + cbase + (size_t)t * kHD;
-          float4 kk[kHD / 4];
 #pragma unroll
-          for (int i = 0; i < kHD / 4; i++) kk[i] = gld4f(kr + 4 * i);
+          for (int i = 0; i < kHD / 4; i++) kk[i] = gld4f(a.kc + cbase + (size_t)t * kHD + 4 * i);
+        }
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
 #pragma unroll
-          for (int i = 0; i < kHD / 4; i++) {
-            s0 = s0 + qv[4 * i] * kk[i].x;
-            s1 = s1 + qv[4 * i + 1] * kk[i].y;
-            s2 = s2 + qv[4 * i + 2] * kk[i].z;
-            s3 = s3 + qv[4 * i + 3] * kk[i].w;
-          }
+        for (int i = 0; i < kHD / 4; i++) {
+          const float4 q4 = reinterpret_cast<const float4*>(qv)[i];
+          s0 = s0 + q4.x * kk[i].x;
+          s1 = s1 + q4.y * kk[i].y;
+          s2 = s2 + q4.z * kk[i].z;
+          s3 = s3 + q4.w * kk[i].w;
         }
         const float sv = (s0 + s1 + s2 + s3) * scale;
         sc[t] = sv;
@@ -578,48 +701,38 @@ __device__ __forceinline__ void role_attn(const PArgs a, const PSmem m, uint32_t
       for (int t = tid; t < T; t += kPThreads) sc[t] = fast_exp(sc[t] - mx);
       __syncthreads();
       if (tid == 0) {
-        float sum = 0.0f;
-        int t = 0;
-        for (; t + 8 <= T; t += 8) {
-          float e[8];
-#pragma unroll
-          for (int u = 0; u < 8; u++) e[u] = sc[t + u];
-#pragma unroll
-          for (int u = 0; u < 8; u++) sum = sum + e[u];
-        }
-        for (; t < T; t++) sum = sum + sc[t];
+        const int T4 = T & ~3;
+        float sum = serial_sum_vec(sc, T4);
+        for (int t = T4; t < T; t++) sum = sum + sc[t];
         m.red[8] = sum;
       }
       __syncthreads();
       const float sum = m.red[8];
       for (int t = tid; t < T; t += kPThreads) sc[t] = sc[t] / sum;
       __syncthreads();
-      // out_i = sum over t in order of p_t * v_t[i] (kernels.c:372-375); V loaded 32 positions ahead
+      // out_i = sum over t in order of p_t * v_t[i] (kernels.c:372-375)
       if (tid < kHD) {
-        constexpr int TB = 32;
-        const float* vb = a.vc + cbase + tid;
-        float acc = 0.0f;
-        float vcur[TB];
+        float accv = 0.0f;
+        int t = 0;
+        for (; t + 8 <= nt; t += 8) {
+          float vx[8];
 #pragma unroll
-        for (int u = 0; u < TB; u++) vcur[u] = u < pos ? gldf(vb + (size_t)u * kHD) : 0.0f;
-        for (int t0 = 0; t0 < T; t0 += TB) {
-          float vnext[TB];
-          const int t1 = t0 + TB;
-          if (t1 < pos) {
+          for (int u = 0; u < 8; u++) vx[u] = vt[(t + u) * kKVRow + tid];
 #pragma unroll
-            for (int u = 0; u < TB; u++) vnext[u] = t1 + u < pos ? gldf(vb + (size_t)(t1 + u) * kHD) : 0.0f;
-          }
-#pragma unroll
-          for (int u = 0; u < TB; u++) {
-            const int t = t0 + u;
-            if (t < T) acc = acc + sc[t] * (t == pos ? vv[tid] : vcur[u]);
-          }
-          if (t1 < pos) {
-#pragma unroll
-            for (int u = 0; u < TB; u++) vcur[u] = vnext[u];
-          }
+          for (int u = 0; u < 8; u++) accv = accv + sc[t + u] * vx[u];
         }
-        ll_put(LATT + h * kHD + tid, __float_as_uint(acc), phase_epoch(ep0, s, E, 4 * l + 0));
+        for (; t < nt; t++) accv = accv + sc[t] * vt[t * kKVRow + tid];
+        constexpr int TB = 32;     // positions past the staged tile: streamed, 32 loads ahead
+        for (; t < pos; t += TB) {
+          float vx[TB];
+#pragma unroll
+          for (int u = 0; u < TB; u++) vx[u] = t + u < pos ? gldf(a.vc + cbase + (size_t)(t + u) * kHD + tid) : 0.0f;
+#pragma unroll
+          for (int u = 0; u < TB; u++)
+            if (t + u < pos) accv = accv + sc[t + u] * vx[u];
+        }
+        accv = accv + sc[pos] * vv[tid];
+        ll_put(LATT + h * kHD + tid, __float_as_uint(accv), phase_epoch(ep0, s, E, 4 * l + 0));
       }
       if (h == 0) prof_mark(a, s, l * 16 + 6);
       __syncthreads();
@@ -644,13 +757,15 @@ __device__ __forceinline__ void role_gu(const PArgs a, const PSmem m, uint32_t e
     for (int l = 0; l < a.NL; l++) {
       const LayerView L = a.layers[l];
       const int ng = L.gu.ng;
-      RG<NGD> w;
-      rg_load<NGD>(L.gu, rg, r, j, 0, ng, w);
+      RG<NGD> w[1];
+      rg_load<NGD>(L.gu, rg, r, j, 0, ng, w[0]);
       recv_x(LX1, D, phase_epoch(ep0, s, E, 4 * l + 1), a.st, m.xl, bad);
       if (__syncthreads_or(bad)) return;
       if (u == 0) prof_mark(a, s, l * 16 + 7);
       norm_quant(m, D, L.ffn_norm, a.eps);
-      const float v = hsum4(rg_dot<NGD>(w, 0, ng, nbD, m.xq, j, 0.0f));
+      float acc[1] = {0.0f};
+      rg_dot<NGD, 1>(w, 0, ng, nbD, m.xq, j, acc);
+      const float v = hsum4(acc[0]);
       if (j == 0) m.gu[16 * wave + r] = v;
       __syncthreads();
       if (tid < 4) quantize_row_dev<QM_SWIGLU>(m.gu, nullptr, 0, 32, nullptr, 0.0f, m.tq, tid, 4);
@@ -687,6 +802,7 @@ __global__ __launch_bounds__(kPThreads, 1) void k_decode_persistent(PArgs a) {
   const int tok = a.tokens[pos];
   const int wg = blockIdx.x;
   if (wg == 0) prof_mark(a, 0, a.NL * 16 + 3);
+  if (a.prof && wg == 0 && threadIdx.x == 0) a.prof[a.NL * 16 + 4] = clock64();
   if (wg < a.nOD) role_od<NGO, NGDN, NGD>(a, m, ep0, pos, tok);
   else if (wg < a.nOD + a.nA) role_attn<NGD>(a, m, ep0, pos, tok);
   else if (wg < a.nOD + a.nA + a.nGU) role_gu<NGD>(a, m, ep0, pos, tok);

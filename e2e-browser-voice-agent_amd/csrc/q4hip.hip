@@ -423,6 +423,8 @@ struct q4hip {
   LayerView* d_layers = nullptr;
   uint64_t* ll = nullptr;
   int pers_grid = 0;
+  const char* pers_why = "";
+  int pers_kv_tile = 0;
   size_t pers_lds = 0;
   const void* pers_fn = nullptr;
   // profiling: events recorded around each launch of an eager step
@@ -519,31 +521,45 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
 int wave_groups(int ng) { return (((ng + 3) >> 2) + 1) & ~1; }
 
 // Decide once whether this model and device admit the persistent decode kernel, and set it up.
+// On refusal h->pers_why says which requirement failed.
 void setup_persistent(q4hip* h) {
   if (h->pers_ok || h->pers_broken || h->mode == Q4HIP_DECODE_GRAPH) return;
   h->pers_broken = true;   // until proven otherwise
   const int D = h->D, F = h->F;
-  if (h->HD != kHD || D % 64 || F % 32) return;
+  auto no = [h](const char* why) { h->pers_why = why; };
+  if (h->HD != kHD) return no("head_dim is not 64");
+  if (D % 64 || F % 32 || D > 1024 || (F / 32) * 9 > 256 * kRecvAct) return no("dim or ffn out of range");
   const Layer& y0 = h->L[0];
   const int ngD = y0.qkv.ng, perO = wave_groups(y0.o.ng), perDn = wave_groups(y0.down.ng);
   if (ngD <= 7 && perO <= 2 && perDn <= 10) h->pers_fn = (const void*)k_decode_persistent<7, 2, 10>;
   else if (ngD <= 8 && perO <= 4 && perDn <= 18) h->pers_fn = (const void*)k_decode_persistent<8, 4, 18>;
-  else return;
+  else return no("no kernel instance for these block counts");
   const int nbm = std::max(D, F) / 32;
-  if (h->ctx > 64 * nbm) return;
-  h->pers_lds = psmem_bytes(D, F);
-  if (h->pers_lds > 65536) return;
+  if (h->ctx > 64 * nbm) return no("ctx too large for the score buffer");
+  int lds_max = 0;
+  if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, h->device) != hipSuccess)
+    return no("cannot query shared memory size");
+  const size_t base = psmem_base_bytes(D, F), budget = (size_t)lds_max > 4096 ? (size_t)lds_max - 4096 : 0;
+  if (base > budget) return no("shared memory too small");
+  // past K/V rows the attention role stages in shared memory; the rest are streamed
+  h->pers_kv_tile = (int)std::min<size_t>({(size_t)h->ctx, (size_t)192, (budget - base) / (2 * kKVRow * 4)});
+  h->pers_lds = psmem_bytes(D, F, h->pers_kv_tile);
+  if (hipFuncSetAttribute(h->pers_fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)h->pers_lds) != hipSuccess) {
+    (void)hipGetLastError();
+    return no("cannot raise the kernel's shared memory limit");
+  }
   int cus = 0, per_cu = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device) != hipSuccess) return;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device) != hipSuccess)
+    return no("cannot query CU count");
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, h->pers_fn, kPThreads, h->pers_lds) != hipSuccess || per_cu < 1) {
     (void)hipGetLastError();
-    return;
+    return no("the kernel does not fit on a CU");
   }
   // One workgroup per CU: all of them fit on the device at once, which the waits between them
   // rely on (a workgroup that could not start would only make the others time out and abort).
   const int need = D / 16 + h->H + F / 32;
   const int G = cus;
-  if (need > G || G > 256) return;   // the head argmax exchange gives one entry per thread of a WG
+  if (need > G || G > 256) return no("more roles than CUs");   // the argmax exchange gives one entry per thread
   std::vector<LayerView> lv(h->NL);
   for (int l = 0; l < h->NL; l++) {
     const Layer& y = h->L[l];
@@ -554,7 +570,7 @@ void setup_persistent(q4hip* h) {
       hipMemcpy(h->d_layers, lv.data(), lv.size() * sizeof(LayerView), hipMemcpyHostToDevice) != hipSuccess ||
       hipMalloc(&h->ll, ll_entries * 8) != hipSuccess || hipMemset(h->ll, 0, ll_entries * 8) != hipSuccess) {
     (void)hipGetLastError();
-    return;
+    return no("device allocation failed");
   }
   h->pers_grid = G;
   h->pers_ok = true;
@@ -586,6 +602,7 @@ hipError_t launch_persistent(q4hip* h, int steps, unsigned long long* prof = nul
   a.nOD = h->D / 16;
   a.nA = h->H;
   a.nGU = h->F / 32;
+  a.kv_tile = h->pers_kv_tile;
   a.prof = prof;
   void* args[] = {&a};
   return hipLaunchKernel(h->pers_fn, dim3(h->pers_grid), dim3(kPThreads), args, h->pers_lds, h->stream);
@@ -853,7 +870,7 @@ int q4hip_set_decode_mode(q4hip* h, int mode) {
     setup_persistent(h);
     if (!h->pers_ok || h->pers_broken) {
       h->mode = Q4HIP_DECODE_AUTO;
-      return fail(Q4HIP_EINVAL, "the persistent decode kernel does not support this model or device");
+      return fail(Q4HIP_EINVAL, "the persistent decode kernel does not support this model or device: %s", h->pers_why);
     }
   }
   return Q4HIP_OK;
@@ -981,6 +998,11 @@ int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n) {
   if (aborted(h)) return fail(Q4HIP_EHIP, "persistent profile: a bounded wait timed out");
   const unsigned long long t0 = t[h->NL * 16 + 3];
   for (int i = 0; i < cnt; i++) us[i] = t[i] ? (float)((double)(long long)(t[i] - t0) * 0.01) : -1.0f;
+  // slots 16L+4/5 hold the shader clock counter at kernel start / step end: report its MHz
+  const double wall_us = (double)(long long)(t[h->NL * 16 + 2] - t0) * 0.01;
+  const double cycles = (double)(long long)(t[h->NL * 16 + 5] - t[h->NL * 16 + 4]);
+  us[h->NL * 16 + 4] = wall_us > 0 ? (float)(cycles / wall_us) : -1.0f;
+  us[h->NL * 16 + 5] = -1.0f;
   return Q4HIP_OK;
 }
 
