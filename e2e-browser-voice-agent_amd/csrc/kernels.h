@@ -44,15 +44,16 @@ struct State {
 
 // ---------------------------------------------------------------- arithmetic helpers
 
-// e^x of kernels.c:69-78 (Cody-Waite reduction, degree-6 Taylor, exponent add), op for op.
+// e^x of kernels.c:69-78 (Cody-Waite reduction, degree-6 Taylor, exponent add), op for op.  The
+// two range tests are selects rather than branches (the value computed for x < -87 is discarded).
 __device__ __forceinline__ float fast_exp(float x) {
-  if (x < -87.0f) return 0.0f;
-  if (x > 88.0f) x = 88.0f;
-  float n = __builtin_floorf(x * 1.44269504f + 0.5f);
-  float r = x - n * 0.693145752f - n * 1.42860677e-6f;
+  const float xc = x > 88.0f ? 88.0f : x;
+  float n = __builtin_floorf(xc * 1.44269504f + 0.5f);
+  float r = xc - n * 0.693145752f - n * 1.42860677e-6f;
   float p = 1.0f + r * (1.0f + r * (0.5f + r * (0.166666672f + r * (0.0416666679f +
             r * (0.00833333377f + r * 0.00138888892f)))));
-  return __uint_as_float(__float_as_uint(p) + ((uint32_t)(int32_t)n << 23));
+  const float e = __uint_as_float(__float_as_uint(p) + ((uint32_t)(int32_t)n << 23));
+  return x < -87.0f ? 0.0f : e;
 }
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {

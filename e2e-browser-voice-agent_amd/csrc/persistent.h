@@ -3,17 +3,22 @@
 // A kernel-per-operation step is ~245 dependent launches of 2.5-20 us each.  Here every workgroup
 // (one per CU) stays resident and takes one role for the whole launch:
 //   OD  (D/16 WGs)   rows 16w..16w+15 of o and down; owns those rows of the residual x
-//   A   (heads WGs)  one attention head: its q rows and its kv group's k, v rows (the k/v rows are
+//   A   (H WGs)      one attention head: its q rows and its kv group's k, v rows (the k/v rows are
 //                    recomputed by the heads of a group instead of exchanged), RoPE, K/V append,
 //                    attention
 //   GU  (F/32 WGs)   gate and up rows of one 32-value block of the SwiGLU activation, quantized
-//   all              the output head (rows round-robin), then the greedy argmax
+//   all              the output head (row groups round-robin), then the greedy argmax
 // Four exchanges per layer (att -> OD, x after o -> GU, act -> OD, x after down -> A) and one per
 // step (argmax).  Each exchanged value is stored together with the epoch of the phase that wrote it
 // in one 8-byte agent-scope store ("LL" store): a reader polls the data itself, so a hand-off is
 // one hop, and a thread's entries are all in flight at once.  Every role issues the loads of its
-// next weights (and the attention role its past K/V rows) before it waits, so that traffic overlaps
-// the waits.  Waits are bounded: a timeout raises State::abort and every workgroup exits.
+// next weights, norm weights and biases (and the attention role its past K/V rows) before it
+// waits, so that traffic overlaps the waits.  Waits are bounded: a timeout raises State::abort and
+// every workgroup exits.
+//
+// The kernel is compiled for one model shape (PShape): every loop over blocks, groups and rows has
+// a constant trip count and is unrolled into straight-line code with no per-term branches, and the
+// split of o and down over the four waves is fixed per wave.
 //
 // Arithmetic per output is the one of kernels.h (the reference's lane order), so results are
 // bit-identical to the kernel-per-operation path.
@@ -30,7 +35,7 @@ struct LayerView {
 };
 
 struct PArgs {
-  int D, F, H, KVH, QKV, V, NL, ctx;
+  int V, NL, ctx;
   float eps;
   const uint8_t* embd;
   const float* out_norm;
@@ -42,9 +47,8 @@ struct PArgs {
   float* logits;
   int* tokens;
   State* st;
-  uint64_t* ll;   // exchange area: X1[D] X2[D] ATT[D] ACT[F/32*9] ARG[2G] (value, index pairs)
+  uint64_t* ll;   // exchange area, offsets in PShape
   int steps;
-  int nOD, nA, nGU;
   int kv_tile;    // past positions of K and V the attention role stages in shared memory
   unsigned long long* prof;   // optional: phase timestamps of step 0, [(NL + 1) * 16]
 };
@@ -53,15 +57,44 @@ constexpr int kPThreads = 256;
 constexpr int kSpinLimit = 1 << 21;
 constexpr int kHD = 64;           // head_dim of the persistent path
 constexpr int kKVRow = 68;        // floats per staged K/V row (64 + 4: conflict-free row-per-thread reads)
-constexpr int kRecvD = 4;         // LL entries per thread for D-vectors (D <= 1024)
-constexpr int kRecvAct = 6;       // LL entries per thread for the quantized activation (9 * F/32 <= 1536)
+
+// Even-aligned split of ng groups of 4 blocks over the four waves: wave w takes
+// [split_g0, split_g0 + split_cnt).  Even starts keep a wave's fp16 scales in whole uint4 words.
+constexpr int split_per(int ng) { return (((ng + 3) >> 2) + 1) & ~1; }
+constexpr int split_g0(int ng, int w) { return w * split_per(ng); }
+constexpr int split_cnt(int ng, int w) {
+  return ng - split_g0(ng, w) <= 0 ? 0 : (ng - split_g0(ng, w) < split_per(ng) ? ng - split_g0(ng, w) : split_per(ng));
+}
+
+// The model shape a persistent kernel is compiled for (head_dim 64).
+template <int D_, int F_, int H_, int KVH_>
+struct PShape {
+  static constexpr int D = D_, F = F_, H = H_, KVH = KVH_;
+  static constexpr int NBD = D / 32, NBF = F / 32, NBM = NBD > NBF ? NBD : NBF;
+  static constexpr int NGD = (NBD + 3) / 4, NGF = (NBF + 3) / 4;      // groups of 4 blocks
+  static constexpr int NB8D = (NBD + 7) / 8, NB8F = (NBF + 7) / 8;    // uint4 words of 8 scales
+  static constexpr int nOD = D / 16, nA = H, nGU = F / 32, nRoles = nOD + nA + nGU;
+  static constexpr int KD = (D + kPThreads - 1) / kPThreads;           // x entries per thread
+  static constexpr int NACT = 9 * nGU;                                 // act entries
+  static constexpr int KACT = (NACT + kPThreads - 1) / kPThreads;
+  static constexpr int STV = D / 4 + 4;                                // stride of the lane runs
+  // exchange area, in 8-byte entries: x after o, x after down, x into the head, attention
+  // output, quantized activation, then two (value, index) argmax buffers used by step parity
+  static constexpr int oX1 = 0, oX2 = D, oXH = 2 * D, oATT = 3 * D, oACT = 4 * D, oARG = 4 * D + NACT;
+  static constexpr size_t ll_entries(int G) { return (size_t)oARG + 4 * (size_t)G; }
+  static constexpr int RAW = NACT > 2 * kPThreads ? NACT : 2 * kPThreads;   // raw entry words
+  static_assert(D % 64 == 0 && F % 32 == 0 && D == H * kHD && H % KVH == 0, "unsupported shape");
+  static_assert(D <= 4 * kPThreads, "norm_quant gives one block lane per thread");
+};
 
 // ---------------------------------------------------------------- memory helpers
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(1))) const u32x4 GlobalU32x4;
 typedef __attribute__((address_space(1))) const f32x4 GlobalF32x4;
+typedef __attribute__((address_space(1))) const f32x2 GlobalF32x2;
 typedef __attribute__((address_space(1))) const float GlobalF32;
 
 // Weights and the K/V cache live in global memory; pointers read from the device layer table are
@@ -74,11 +107,17 @@ __device__ __forceinline__ float4 gld4f(const float* p) {
   const f32x4 v = *(GlobalF32x4*)(const void*)p;
   return make_float4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ float2 gld2f(const float* p) {
+  const f32x2 v = *(GlobalF32x2*)(const void*)p;
+  return make_float2(v.x, v.y);
+}
 __device__ __forceinline__ float gldf(const float* p) { return *(GlobalF32*)(const void*)p; }
 
 __device__ __forceinline__ void st_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 // ---------------------------------------------------------------- LL exchange
 
@@ -100,7 +139,7 @@ __device__ __forceinline__ void ll_recv(const uint64_t* base, int n, uint32_t ep
   uint64_t w[K];
 #pragma unroll
   for (int k = 0; k < K; k++) {
-    const int i = (int)threadIdx.x + 256 * k;
+    const int i = (int)threadIdx.x + kPThreads * k;
     w[k] = i < n ? ll_peek(base + i) : ((uint64_t)ep << 32);
   }
   int spins = 0;
@@ -112,7 +151,7 @@ __device__ __forceinline__ void ll_recv(const uint64_t* base, int n, uint32_t ep
     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
     for (int k = 0; k < K; k++) {
-      const int i = (int)threadIdx.x + 256 * k;
+      const int i = (int)threadIdx.x + kPThreads * k;
       if (i < n && (uint32_t)(w[k] >> 32) != ep) w[k] = ll_peek(base + i);
     }
     if (++spins > kSpinLimit) {
@@ -128,30 +167,34 @@ __device__ __forceinline__ void ll_recv(const uint64_t* base, int n, uint32_t ep
 
 // ---------------------------------------------------------------- register-resident weights
 
-// Groups [g0, g0+ng) (g0 even) of one 16-row group, lane (r, j): word j of 4 blocks per group and
+// CNT groups of one 16-row group, lane (r = lane/4, j = lane%4): word j of 4 blocks per group and
 // the fp16 scales of 8 blocks per uint4.
-template <int NG>
-struct RG {
-  uint4 w[NG];
-  uint4 s[(NG + 1) / 2];
+template <int CNT>
+struct WR {
+  uint4 w[CNT > 0 ? CNT : 1];
+  uint4 s[CNT > 0 ? (CNT + 1) / 2 : 1];
 };
 
-template <int NG>
-__device__ __forceinline__ void rg_load(const Q4Mat& W, int rg16, int r, int j, int g0, int ng, RG<NG>& R) {
-  const int row = rg16 * 16 + r;
-  const int tile = row >> 6, rr = row & 63;
-  const uint4* wq = W.qs + ((size_t)tile * W.ng * 64 + rr) * 4 + j;
-  const uint4* wd = W.d + (size_t)tile * W.nb8 * 64 + rr;
+// Groups [G0, G0 + CNT) (G0 even) of row group rg16 of a matrix with NG groups and NB8 scale words
+// per row.
+template <int NG, int NB8, int G0, int CNT>
+__device__ __forceinline__ void wr_load(const Q4Mat& W, int rg16, int lane, WR<CNT>& R) {
+  if constexpr (CNT > 0) {
+    const int row = rg16 * 16 + (lane >> 2), j = lane & 3;
+    const int tile = row >> 6, rr = row & 63;
+    const uint4* wq = W.qs + ((size_t)tile * NG * 64 + rr) * 4 + j + (size_t)G0 * 256;
+    const uint4* wd = W.d + ((size_t)tile * NB8 + G0 / 2) * 64 + rr;
 #pragma unroll
-  for (int g = 0; g < NG; g++) R.w[g] = g < ng ? gld(wq + (size_t)(g0 + g) * 256) : make_uint4(0, 0, 0, 0);
+    for (int g = 0; g < CNT; g++) R.w[g] = gld(wq + (size_t)g * 256);
 #pragma unroll
-  for (int c = 0; c < (NG + 1) / 2; c++)
-    R.s[c] = 2 * c < ng ? gld(wd + (size_t)(g0 / 2 + c) * 64) : make_uint4(0, 0, 0, 0);
+    for (int c = 0; c < (CNT + 1) / 2; c++) R.s[c] = gld(wd + (size_t)c * 64);
+  }
 }
 
-// One block's term f32(p_j) * (dw * dx) (kernels.c:137); xv = {A_j, B_j, c_j, dx}.
-template <int NG>
-__device__ __forceinline__ float rg_term(const RG<NG>& R, int g, int k, uint4 xv) {
+// One block's term f32(p_j) * (dw * dx) (kernels.c:137); xv = {A_j, B_j, c_j, dx}.  g, k are
+// constants after unrolling.
+template <int CNT>
+__device__ __forceinline__ float wr_term(const WR<CNT>& R, int g, int k, uint4 xv) {
   const uint32_t wv = k == 0 ? R.w[g].x : k == 1 ? R.w[g].y : k == 2 ? R.w[g].z : R.w[g].w;
   const uint4 sv = R.s[g >> 1];
   const int hb = ((g & 1) << 2) + k;
@@ -162,111 +205,201 @@ __device__ __forceinline__ float rg_term(const RG<NG>& R, int g, int k, uint4 xv
   return (float)p * (dw * __uint_as_float(xv.w));
 }
 
-// The four activation blocks of group g for lane j (zero past nb).
-__device__ __forceinline__ void xg_load(const uint4* xs, int g, int nb, int j, uint4 (&xv)[4]) {
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const int b = g * 4 + k;
-    xv[k] = b < nb ? xs[b * 4 + j] : make_uint4(0, 0, 0, 0);
-  }
-}
+// Mark a value as used here: the loads that produced it complete before this point, and code after
+// it stays after it.  Used to software-pipeline shared-memory reads: the next chunk's loads are
+// issued, then the current chunk is pinned, then computed, so the compiler can neither wait for
+// the newer loads early nor issue them late.
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(float4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+__device__ __forceinline__ void pin(uint4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
 
-// acc_i = acc_i + term for N row groups sharing each activation read, blocks of groups
-// [g0, g0+ng) in order (kernels.c:217-218); the next group's activation blocks are read ahead.
-template <int NG, int N>
-__device__ __forceinline__ void rg_dot(const RG<NG> (&R)[N], int g0, int ng, int nb, const uint4* xs, int j,
-                                       float (&acc)[N]) {
-  uint4 xa[4], xb[4];
-  if (ng > 0) xg_load(xs, g0, nb, j, xa);
+// acc_n = acc_n + term over blocks [4 G0, min(NB, 4 (G0 + CNT))) in order (kernels.c:217-218), for N
+// row groups sharing each activation read; the next group's activation blocks are read ahead.
+template <int NB, int G0, int CNT, int N>
+__device__ __forceinline__ void wr_dot(const WR<CNT> (&R)[N], const uint4* xq, int j, float (&acc)[N]) {
+  if constexpr (CNT > 0) {
+    uint4 xb[2][4];
 #pragma unroll
-  for (int g = 0; g < NG; g++) {
-    if (g < ng) {
-      if (g + 1 < ng) xg_load(xs, g0 + g + 1, nb, j, xb);
+    for (int k = 0; k < 4; k++)
+      if (G0 * 4 + k < NB) xb[0][k] = xq[(G0 * 4 + k) * 4 + j];
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        if ((g0 + g) * 4 + k < nb) {
+    for (int g = 0; g < CNT; g++) {
+      if (g + 1 < CNT) {
 #pragma unroll
-          for (int n = 0; n < N; n++) acc[n] = acc[n] + rg_term(R[n], g, k, xa[k]);
-        }
+        for (int k = 0; k < 4; k++)
+          if ((G0 + g + 1) * 4 + k < NB) xb[(g + 1) & 1][k] = xq[((G0 + g + 1) * 4 + k) * 4 + j];
       }
 #pragma unroll
-      for (int k = 0; k < 4; k++) xa[k] = xb[k];
+      for (int k = 0; k < 4; k++)
+        if ((G0 + g) * 4 + k < NB) pin(xb[g & 1][k]);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        if ((G0 + g) * 4 + k < NB) {
+#pragma unroll
+          for (int n = 0; n < N; n++) acc[n] = acc[n] + wr_term(R[n], g, k, xb[g & 1][k]);
+        }
+      }
     }
   }
 }
 
 // The same terms written to shared memory, terms[b * 64 + lane], for a serial pass by one wave.
-template <int NG>
-__device__ __forceinline__ void rg_terms(const RG<NG>& R, int g0, int ng, int nb, const uint4* xs, int j,
-                                         float* terms, int lane) {
-  uint4 xa[4], xb[4];
-  if (ng > 0) xg_load(xs, g0, nb, j, xa);
+template <int NB, int G0, int CNT>
+__device__ __forceinline__ void wr_terms(const WR<CNT>& R, const uint4* xq, int lane, float* terms) {
+  if constexpr (CNT > 0) {
+    const int j = lane & 3;
+    uint4 xb[2][4];
 #pragma unroll
-  for (int g = 0; g < NG; g++) {
-    if (g < ng) {
-      if (g + 1 < ng) xg_load(xs, g0 + g + 1, nb, j, xb);
+    for (int k = 0; k < 4; k++)
+      if (G0 * 4 + k < NB) xb[0][k] = xq[(G0 * 4 + k) * 4 + j];
+#pragma unroll
+    for (int g = 0; g < CNT; g++) {
+      if (g + 1 < CNT) {
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          if ((G0 + g + 1) * 4 + k < NB) xb[(g + 1) & 1][k] = xq[((G0 + g + 1) * 4 + k) * 4 + j];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+        if ((G0 + g) * 4 + k < NB) pin(xb[g & 1][k]);
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        const int b = (g0 + g) * 4 + k;
-        if (b < nb) terms[b * 64 + lane] = rg_term(R, g, k, xa[k]);
+        const int b = (G0 + g) * 4 + k;
+        if (b < NB) terms[b * 64 + lane] = wr_term(R, g, k, xb[g & 1][k]);
       }
-#pragma unroll
-      for (int k = 0; k < 4; k++) xa[k] = xb[k];
     }
   }
 }
 
-// ((0 + t_0) + t_1) + ... over the blocks, the accumulation order of one reference lane; loads run
-// 8 blocks ahead of the additions.
-__device__ __forceinline__ float serial_sum(const float* terms, int nb, int lane) {
+// ((0 + t_0) + t_1) + ... + t_{NB-1}: the accumulation order of one reference lane, reading
+// terms[b * 64 + lane] 8 blocks ahead of the additions.
+template <int NB>
+__device__ __forceinline__ float serial_sum(const float* terms, int lane) {
+  constexpr int C = 8, NC = (NB + C - 1) / C;
+  float buf[2][C];
   float acc = 0.0f;
-  float cur[8], nxt[8];
 #pragma unroll
-  for (int u = 0; u < 8; u++) cur[u] = u < nb ? terms[u * 64 + lane] : 0.0f;
-  for (int b = 0; b < nb; b += 8) {
+  for (int u = 0; u < C; u++)
+    if (u < NB) buf[0][u] = terms[u * 64 + lane];
 #pragma unroll
-    for (int u = 0; u < 8; u++) nxt[u] = b + 8 + u < nb ? terms[(b + 8 + u) * 64 + lane] : 0.0f;
+  for (int c = 0; c < NC; c++) {
+    if (c + 1 < NC) {
 #pragma unroll
-    for (int u = 0; u < 8; u++)
-      if (b + u < nb) acc = acc + cur[u];
+      for (int u = 0; u < C; u++)
+        if ((c + 1) * C + u < NB) buf[(c + 1) & 1][u] = terms[((c + 1) * C + u) * 64 + lane];
+    }
 #pragma unroll
-    for (int u = 0; u < 8; u++) cur[u] = nxt[u];
+    for (int u = 0; u < C; u++)
+      if (c * C + u < NB) pin(buf[c & 1][u]);
+#pragma unroll
+    for (int u = 0; u < C; u++)
+      if (c * C + u < NB) acc = acc + buf[c & 1][u];
   }
   return acc;
 }
 
-// Sum of x[0..n) in index order (n a multiple of 4, x 16-byte aligned), 16 values loaded ahead.
-__device__ __forceinline__ float serial_sum_vec(const float* x, int n) {
-  const float4* p = reinterpret_cast<const float4*>(x);
-  const int n4 = n >> 2;
-  float acc = 0.0f;
-  float4 cur[4], nxt[4];
+// ((0 + x_0) + x_1) + ... over a contiguous run of N floats (N a multiple of 16, 16-byte
+// aligned), 16 values read ahead of the additions.
+template <int N>
+__device__ __forceinline__ float run_sum(const float* run) {
+  static_assert(N % 16 == 0, "run length");
+  constexpr int NC = N / 16;
+  const float4* p = reinterpret_cast<const float4*>(run);
+  float4 buf[2][4];
+  float s = 0.0f;
 #pragma unroll
-  for (int u = 0; u < 4; u++) cur[u] = u < n4 ? p[u] : make_float4(0, 0, 0, 0);
-  for (int b = 0; b < n4; b += 4) {
+  for (int u = 0; u < 4; u++) buf[0][u] = p[u];
 #pragma unroll
-    for (int u = 0; u < 4; u++) nxt[u] = b + 4 + u < n4 ? p[b + 4 + u] : make_float4(0, 0, 0, 0);
+  for (int c = 0; c < NC; c++) {
+    if (c + 1 < NC) {
+#pragma unroll
+      for (int u = 0; u < 4; u++) buf[(c + 1) & 1][u] = p[(c + 1) * 4 + u];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) pin(buf[c & 1][u]);
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      if (b + u < n4) {
-        acc = acc + cur[u].x;
-        acc = acc + cur[u].y;
-        acc = acc + cur[u].z;
-        acc = acc + cur[u].w;
-      }
+      s = s + buf[c & 1][u].x;
+      s = s + buf[c & 1][u].y;
+      s = s + buf[c & 1][u].z;
+      s = s + buf[c & 1][u].w;
     }
-#pragma unroll
-    for (int u = 0; u < 4; u++) cur[u] = nxt[u];
   }
-  return acc;
+  return s;
 }
 
-// Even-aligned split of ng groups over the 4 waves.
-__device__ __forceinline__ void wave_range(int ng, int wave, int& g0, int& cnt) {
-  const int per = (((ng + 3) >> 2) + 1) & ~1;
-  g0 = wave * per;
-  cnt = ng - g0 < per ? ng - g0 : per;
-  if (cnt < 0) cnt = 0;
+// ((0 + x_0) + x_1) + ... + x_{n-1} for x in shared memory (16-byte aligned): chunks of 16 values
+// with the next chunk read ahead (its index clamped, so every chunk's loads are issued
+// unconditionally), the last n % 16 values read before the loop and added under selects.
+__device__ __forceinline__ float seq_sum(const float* x, int n) {
+  const float4* p = reinterpret_cast<const float4*>(x);
+  const int nc = n >> 4, t0 = nc << 4, last = n > 0 ? n - 1 : 0;
+  float tail[15];
+#pragma unroll
+  for (int i = 0; i < 15; i++) tail[i] = x[t0 + i < last ? t0 + i : last];
+  float s = 0.0f;
+  if (nc > 0) {
+    float4 A[4], B[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) A[u] = p[u];
+    int c = 0;
+    for (;;) {
+      const int nb = c + 1 < nc ? c + 1 : c;
+#pragma unroll
+      for (int u = 0; u < 4; u++) B[u] = p[nb * 4 + u];
+#pragma unroll
+      for (int u = 0; u < 4; u++) pin(A[u]);
+#pragma unroll
+      for (int u = 0; u < 4; u++) { s = s + A[u].x; s = s + A[u].y; s = s + A[u].z; s = s + A[u].w; }
+      if (++c == nc) break;
+      const int na = c + 1 < nc ? c + 1 : c;
+#pragma unroll
+      for (int u = 0; u < 4; u++) A[u] = p[na * 4 + u];
+#pragma unroll
+      for (int u = 0; u < 4; u++) pin(B[u]);
+#pragma unroll
+      for (int u = 0; u < 4; u++) { s = s + B[u].x; s = s + B[u].y; s = s + B[u].z; s = s + B[u].w; }
+      if (++c == nc) break;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 15; i++) {
+    const float t = s + tail[i];
+    s = t0 + i < n ? t : s;
+  }
+  return s;
+}
+
+// acc = ((acc + p_0 * v_0) + p_1 * v_1) + ... over t in [0, n): p_t = pr[t], v_t = vrow[t * stride]
+// in shared memory, chunks of 8 positions with the next chunk read ahead (clamped index).
+__device__ __forceinline__ float seq_dot(float acc, const float* pr, const float* vrow, int stride, int n) {
+  const int nc = n >> 3;
+  if (nc > 0) {
+    float pa[8], va[8], pb[8], vb[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) { pa[u] = pr[u]; va[u] = vrow[u * stride]; }
+    int c = 0;
+    for (;;) {
+      const int nb = (c + 1 < nc ? c + 1 : c) * 8;
+#pragma unroll
+      for (int u = 0; u < 8; u++) { pb[u] = pr[nb + u]; vb[u] = vrow[(nb + u) * stride]; }
+#pragma unroll
+      for (int u = 0; u < 8; u++) { pin(pa[u]); pin(va[u]); }
+#pragma unroll
+      for (int u = 0; u < 8; u++) acc = acc + pa[u] * va[u];
+      if (++c == nc) break;
+      const int na = (c + 1 < nc ? c + 1 : c) * 8;
+#pragma unroll
+      for (int u = 0; u < 8; u++) { pa[u] = pr[na + u]; va[u] = vrow[(na + u) * stride]; }
+#pragma unroll
+      for (int u = 0; u < 8; u++) { pin(pb[u]); pin(vb[u]); }
+#pragma unroll
+      for (int u = 0; u < 8; u++) acc = acc + pb[u] * vb[u];
+      if (++c == nc) break;
+    }
+  }
+  for (int t = nc * 8; t < n; t++) acc = acc + pr[t] * vrow[t * stride];
+  return acc;
 }
 
 __device__ __forceinline__ float embed_value(const uint8_t* emb, int D, int t, int i) {
@@ -277,59 +410,70 @@ __device__ __forceinline__ float embed_value(const uint8_t* emb, int D, int t, i
   return (float)((e < 16 ? (q & 15) : (q >> 4)) - 8) * d;
 }
 
+// Quantize one 32-block lane (quantize_row, kernels.c:90-114): v = the values at elements
+// {2j, 2j+1, 8+2j, 9+2j, 16+2j, 17+2j, 24+2j, 25+2j}; the four lanes of a block are consecutive
+// threads and exchange the block maximum by shuffles.
+__device__ __forceinline__ uint4 quant_lane(const float (&v)[8]) {
+  float am = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; k++) am = __builtin_fmaxf(am, __builtin_fabsf(v[k]));
+  am = __builtin_fmaxf(am, __shfl_xor(am, 1, 4));
+  am = __builtin_fmaxf(am, __shfl_xor(am, 2, 4));
+  const float dd = am / 127.0f;
+  const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+  int q[8];
+  int sum = 0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) { q[k] = quant_one(v[k] * id); sum += q[k]; }
+  return make_uint4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]), (uint32_t)(-8 * sum),
+                    __float_as_uint(dd));
+}
+
+// Element k (0..7) of block lane t = (block t/4, lane t%4).
+__device__ __forceinline__ int lane_elem(int t, int k) {
+  return ((t >> 2) << 5) + ((t & 3) << 1) + ((k >> 1) << 3) + (k & 1);
+}
+
 // ---------------------------------------------------------------- shared memory plan
 
 struct PSmem {
-  float* xl;      // (D + 16) floats: a row staged by lane (run stride D/4 + 4), or plain
-  uint4* xq;      // activation blocks, max(nbD, nbF) * 4
-  float* terms;   // 64 * max(nbD, nbF) floats; attention scores; raw exchange entries
-  uint4* tq;      // 4 (GU quantized block)
+  float* xl;      // 4 * STV floats: x by lane runs (value i at (i & 3) * STV + (i >> 2)), or plain
+  float* sq;      // 4 * STV floats: x*x in the same layout
+  uint4* xq;      // NBM * 4 activation block lanes
+  float* terms;   // 64 * NBM floats: per-block terms; attention scores
+  uint32_t* raw;  // RAW words: exchange entries
+  uint4* tq;      // 4
   float* red;     // 16
   float* qv;      // 3 * 64: q, k, v of one head
   float* own;     // 16 residual rows (OD)
   float* gu;      // 64: gate, up (GU)
-  float* argv;    // 256
-  int* argi;      // 256
+  float* argv;    // 8
+  int* argi;      // 8
   float* kvt;     // kv_tile * 2 * kKVRow: staged past K and V rows (A)
 };
 
-__host__ __device__ inline size_t psmem_base_bytes(int D, int F) {
-  const int nbm = (D > F ? D : F) / 32;
-  size_t b = (size_t)(D + 16) * 4;
-  b += (size_t)nbm * 64;
-  b += (size_t)64 * nbm * 4;
-  b += (16 + 16 + 192 + 16 + 64 + 256 + 256) * 4;
-  return b;
+template <class S>
+constexpr size_t psmem_base_bytes() {
+  return (size_t)8 * S::STV * 4 + (size_t)S::NBM * 64 + (size_t)64 * S::NBM * 4 + (size_t)S::RAW * 4 +
+         (size_t)(16 + 16 + 192 + 16 + 64 + 8 + 8) * 4;
 }
 
-__host__ __device__ inline size_t psmem_bytes(int D, int F, int kv_tile) {
-  return psmem_base_bytes(D, F) + (size_t)kv_tile * 2 * kKVRow * 4;
-}
-
-__device__ __forceinline__ PSmem psmem(unsigned char* base, int D, int F) {
-  const int nbm = (D > F ? D : F) / 32;
+template <class S>
+__device__ __forceinline__ PSmem psmem(unsigned char* base) {
   PSmem m;
   size_t off = 0;
-  m.xl = (float*)(base + off);
-  off += (size_t)(D + 16) * 4;
-  m.xq = (uint4*)(base + off);
-  off += (size_t)nbm * 64;
-  m.terms = (float*)(base + off);
-  off += (size_t)64 * nbm * 4;
-  m.tq = (uint4*)(base + off);
-  off += 16 * 4;
-  m.red = (float*)(base + off);
-  off += 16 * 4;
-  m.qv = (float*)(base + off);
-  off += 192 * 4;
-  m.own = (float*)(base + off);
-  off += 16 * 4;
-  m.gu = (float*)(base + off);
-  off += 64 * 4;
-  m.argv = (float*)(base + off);
-  off += 256 * 4;
-  m.argi = (int*)(base + off);
-  off += 256 * 4;
+  m.xl = (float*)(base + off);      off += (size_t)4 * S::STV * 4;
+  m.sq = (float*)(base + off);      off += (size_t)4 * S::STV * 4;
+  m.xq = (uint4*)(base + off);      off += (size_t)S::NBM * 64;
+  m.terms = (float*)(base + off);   off += (size_t)64 * S::NBM * 4;
+  m.raw = (uint32_t*)(base + off);  off += (size_t)S::RAW * 4;
+  m.tq = (uint4*)(base + off);      off += 16 * 4;
+  m.red = (float*)(base + off);     off += 16 * 4;
+  m.qv = (float*)(base + off);      off += 192 * 4;
+  m.own = (float*)(base + off);     off += 16 * 4;
+  m.gu = (float*)(base + off);      off += 64 * 4;
+  m.argv = (float*)(base + off);    off += 8 * 4;
+  m.argi = (int*)(base + off);      off += 8 * 4;
   m.kvt = (float*)(base + off);
   return m;
 }
@@ -338,55 +482,68 @@ __device__ __forceinline__ uint32_t phase_epoch(uint32_t ep0, int s, int E, int 
   return ep0 + (uint32_t)(s * E + code) + 1u;
 }
 
-__device__ __forceinline__ int run_stride(int D) { return D / 4 + 4; }
+__device__ __forceinline__ void prof_mark(const PArgs& a, int s, int slot) {
+  if (a.prof && s == 0 && threadIdx.x == 0) a.prof[slot] = wall_clock64();
+}
 
-// Wait for the D-vector `src` (epoch ep) and stage it by lane into xl.
-__device__ __forceinline__ void recv_x(const uint64_t* src, int D, uint32_t ep, State* st, float* xl, bool& bad) {
-  const int stv = run_stride(D);
-  uint32_t v[kRecvD];
-  ll_recv<kRecvD>(src, D, ep, st, bad, v);
+// ---------------------------------------------------------------- RMSNorm + quantize
+
+template <class S>
+__device__ __forceinline__ void stage_x(const PSmem& m, int i, float x) {
+  const int o = (i & 3) * S::STV + (i >> 2);
+  m.xl[o] = x;
+  m.sq[o] = x * x;
+}
+
+// Wait for the D-vector at src (epoch ep) and stage it by lane runs, with its squares.
+template <class S>
+__device__ __forceinline__ void recv_x(const uint64_t* src, uint32_t ep, State* st, const PSmem& m, bool& bad) {
+  uint32_t v[S::KD];
+  ll_recv<S::KD>(src, S::D, ep, st, bad, v);
 #pragma unroll
-  for (int k = 0; k < kRecvD; k++) {
-    const int i = (int)threadIdx.x + 256 * k;
-    if (i < D) xl[(i & 3) * stv + (i >> 2)] = __uint_as_float(v[k]);
+  for (int k = 0; k < S::KD; k++) {
+    const int i = (int)threadIdx.x + kPThreads * k;
+    if (i < S::D) stage_x<S>(m, i, __uint_as_float(v[k]));
   }
 }
 
-// RMSNorm + quantize the staged row into m.xq (kernels.c:80-86, 328-331).  Threads 0..3 run the
-// four lane sums of x*x, each over its contiguous run, 16 values loaded ahead.
-__device__ __forceinline__ void norm_quant(const PSmem m, int D, const float* w, float eps) {
-  const int stv = run_stride(D), tid = threadIdx.x;
-  if (tid < 4) {
-    const float4* p = reinterpret_cast<const float4*>(m.xl + tid * stv);
-    const int n4 = D >> 4;
-    float s = 0.0f;
-    float4 cur[4], nxt[4];
+// The 8 norm weights of this thread's block lane, loaded ahead of the wait.
+template <class S>
+__device__ __forceinline__ void normw_load(const float* w, float (&nw)[8]) {
+  const int t = threadIdx.x;
+  if (t < S::NBD * 4) {
 #pragma unroll
-    for (int u = 0; u < 4; u++) cur[u] = u < n4 ? p[u] : make_float4(0, 0, 0, 0);
-    for (int b = 0; b < n4; b += 4) {
-#pragma unroll
-      for (int u = 0; u < 4; u++) nxt[u] = b + 4 + u < n4 ? p[b + 4 + u] : make_float4(0, 0, 0, 0);
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        if (b + u < n4) {
-          s = s + cur[u].x * cur[u].x;
-          s = s + cur[u].y * cur[u].y;
-          s = s + cur[u].z * cur[u].z;
-          s = s + cur[u].w * cur[u].w;
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 4; u++) cur[u] = nxt[u];
+    for (int u = 0; u < 4; u++) {
+      const float2 p = gld2f(w + lane_elem(t, 2 * u));
+      nw[2 * u] = p.x;
+      nw[2 * u + 1] = p.y;
     }
-    m.red[tid] = s;
+  }
+}
+
+// RMSNorm + quantize of the staged x into m.xq (kernels.c:80-86, 328-331): lanes 0..3 of wave 0
+// run the four lane sums of x*x in order, then thread t < NBD*4 quantizes block lane t.
+// The caller has synchronised after staging; returns after a barrier.
+template <class S>
+__device__ __forceinline__ void norm_quant(const PSmem& m, const float (&nw)[8], float eps) {
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    float s = 0.0f;
+    if (tid < 4) s = run_sum<S::D / 4>(m.sq + tid * S::STV);
+    const float s0 = __shfl(s, 0), s1 = __shfl(s, 1), s2 = __shfl(s, 2), s3 = __shfl(s, 3);
+    if (tid == 0) m.red[4] = 1.0f / __builtin_sqrtf((((s0 + s1) + s2) + s3) / (float)S::D + eps);
   }
   __syncthreads();
-  if (tid == 0) {
-    const float ss = m.red[0] + m.red[1] + m.red[2] + m.red[3];
-    m.red[4] = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+  const float rs = m.red[4];
+  if (tid < S::NBD * 4) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int i = lane_elem(tid, k);
+      v[k] = (m.xl[(i & 3) * S::STV + (i >> 2)] * rs) * nw[k];
+    }
+    m.xq[tid] = quant_lane(v);
   }
-  __syncthreads();
-  quantize_row_dev<QM_NORM>(nullptr, m.xl, stv, D, w, m.red[4], m.xq, tid, kPThreads);
   __syncthreads();
 }
 
@@ -395,63 +552,60 @@ __device__ __forceinline__ void arg_merge(float& bv, int& bi, float v, int i) {
   if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) { bv = v; bi = i; }
 }
 
-__device__ __forceinline__ void prof_mark(const PArgs a, int s, int slot) {
-  if (a.prof && s == 0 && threadIdx.x == 0) a.prof[slot] = wall_clock64();
-}
-
 // ---------------------------------------------------------------- the output head + argmax
 
-template <int NGD>
-__device__ __forceinline__ void head_rows(const PArgs a, const PSmem m, const RG<NGD> (&R)[1], int rg, int ngD,
-                                          int nbD, int r, int j, float& bv, int& bi) {
+template <class S>
+__device__ __forceinline__ void head_rows(const PArgs& a, const PSmem& m, const WR<S::NGD> (&R)[1], int rg,
+                                          int lane, float& bv, int& bi) {
   float acc[1] = {0.0f};
-  rg_dot<NGD, 1>(R, 0, ngD, nbD, m.xq, j, acc);
+  wr_dot<S::NBD, 0, S::NGD, 1>(R, m.xq, lane & 3, acc);
   const float v = hsum4(acc[0]);
-  const int row = rg * 16 + r;
-  if (j == 0 && row < a.V) {
+  const int row = rg * 16 + (lane >> 2);
+  if ((lane & 3) == 0 && row < a.V) {
     a.logits[row] = v;
     arg_merge(bv, bi, v, row);
   }
 }
 
-template <int NGD>
-__device__ __forceinline__ int head_phase(const PArgs a, const PSmem m, int s, int pos, uint32_t ep0, int E,
-                                          bool& bad) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane >> 2, j = lane & 3;
-  const int G = gridDim.x, wg = blockIdx.x, D = a.D, nbD = D / 32;
-  const Q4Mat& W = a.head;
-  const int ngD = W.ng;
-  const int nRG = W.Np / 16;
-  uint64_t* LX2 = a.ll + a.D;
-  uint64_t* LARG = a.ll + 3 * a.D + (a.F / 32) * 9;
+// Final RMSNorm, logits of this workgroup's row groups, then every workgroup reduces every
+// workgroup's (value, index): the same token everywhere.  Returns the token, or -1 on abort.
+template <class S>
+__device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int pos, bool& bad) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int G = gridDim.x, wg = blockIdx.x, E = 4 * a.NL + 1;
+  const int nRG = a.head.Np / 16;
+  const uint64_t* LXH = a.ll + S::oXH;
+  uint64_t* LARG = a.ll + S::oARG + (size_t)(s & 1) * 2 * G;
   const uint32_t epx = phase_epoch(ep0, s, E, 4 * (a.NL - 1) + 3);
   const uint32_t eph = phase_epoch(ep0, s, E, 4 * a.NL);
 
-  // the first two row groups' weights are in flight before waiting for x
+  // the first two row groups' weights and the norm weights are in flight before waiting for x
+  float nw[8];
+  normw_load<S>(a.out_norm, nw);
   const int stride = 4 * G;
   int rgi = wg + G * wave;
-  RG<NGD> R0[1], R1[1], R2[1];
-  if (rgi < nRG) rg_load<NGD>(W, rgi, r, j, 0, ngD, R0[0]);
-  if (rgi + stride < nRG) rg_load<NGD>(W, rgi + stride, r, j, 0, ngD, R1[0]);
-  recv_x(LX2, D, epx, a.st, m.xl, bad);
+  WR<S::NGD> R0[1], R1[1], R2[1];
+  if (rgi < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi, lane, R0[0]);
+  if (rgi + stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + stride, lane, R1[0]);
+  recv_x<S>(LXH, epx, a.st, m, bad);
   if (__syncthreads_or(bad)) return -1;
   prof_mark(a, s, a.NL * 16 + 0);
-  norm_quant(m, D, a.out_norm, a.eps);
+  norm_quant<S>(m, nw, a.eps);
 
   float bv = 0.0f;
   int bi = -1;
   // three rotating buffers: two row groups in flight while one is computed
   while (rgi < nRG) {
-    if (rgi + 2 * stride < nRG) rg_load<NGD>(W, rgi + 2 * stride, r, j, 0, ngD, R2[0]);
-    head_rows<NGD>(a, m, R0, rgi, ngD, nbD, r, j, bv, bi);
+    if (rgi + 2 * stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + 2 * stride, lane, R2[0]);
+    head_rows<S>(a, m, R0, rgi, lane, bv, bi);
     rgi += stride;
     if (rgi >= nRG) break;
-    if (rgi + 2 * stride < nRG) rg_load<NGD>(W, rgi + 2 * stride, r, j, 0, ngD, R0[0]);
-    head_rows<NGD>(a, m, R1, rgi, ngD, nbD, r, j, bv, bi);
+    if (rgi + 2 * stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + 2 * stride, lane, R0[0]);
+    head_rows<S>(a, m, R1, rgi, lane, bv, bi);
     rgi += stride;
     if (rgi >= nRG) break;
-    if (rgi + 2 * stride < nRG) rg_load<NGD>(W, rgi + 2 * stride, r, j, 0, ngD, R1[0]);
-    head_rows<NGD>(a, m, R2, rgi, ngD, nbD, r, j, bv, bi);
+    if (rgi + 2 * stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + 2 * stride, lane, R1[0]);
+    head_rows<S>(a, m, R2, rgi, lane, bv, bi);
     rgi += stride;
   }
 #pragma unroll
@@ -468,18 +622,16 @@ __device__ __forceinline__ int head_phase(const PArgs a, const PSmem m, int s, i
     ll_put(LARG + 2 * wg + 1, (uint32_t)bi, eph);
   }
   prof_mark(a, s, a.NL * 16 + 1);
-  // everyone reduces everyone's (value, index): the same token in every workgroup
-  uint32_t* raw = (uint32_t*)m.terms;
   {
     uint32_t v[2];
     ll_recv<2>(LARG, 2 * G, eph, a.st, bad, v);
-    raw[tid] = v[0];
-    if (tid + 256 < 2 * G) raw[tid + 256] = v[1];
+    m.raw[tid] = v[0];
+    if (tid + kPThreads < 2 * G) m.raw[tid + kPThreads] = v[1];
   }
   if (__syncthreads_or(bad)) return -1;
   bv = 0.0f;
   bi = -1;
-  for (int g = tid; g < G; g += kPThreads) arg_merge(bv, bi, __uint_as_float(raw[2 * g]), (int)raw[2 * g + 1]);
+  for (int g = tid; g < G; g += kPThreads) arg_merge(bv, bi, __uint_as_float(m.raw[2 * g]), (int)m.raw[2 * g + 1]);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o);
@@ -500,313 +652,329 @@ __device__ __forceinline__ int head_phase(const PArgs a, const PSmem m, int s, i
   return next;
 }
 
-// ---------------------------------------------------------------- roles
+// ---------------------------------------------------------------- roles (one step each)
 
-// o and down rows 16w..16w+15; the residual x of those rows lives in m.own.
-template <int NGO, int NGDN, int NGD>
-__device__ __forceinline__ void role_od(const PArgs a, const PSmem m, uint32_t ep0, int pos, int tok) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane >> 2, j = lane & 3;
-  const int wg = blockIdx.x, D = a.D, nbD = D / 32, nbF = a.F / 32, E = 4 * a.NL + 1;
-  const int row = wg * 16 + r;
-  uint64_t* LX1 = a.ll;
-  uint64_t* LX2 = a.ll + D;
-  uint64_t* LATT = a.ll + 2 * D;
-  uint64_t* LACT = a.ll + 3 * D;
-  bool bad = false;
-  for (int s = 0; s < a.steps; s++, pos++) {
-    if (tid < 16) m.own[tid] = embed_value(a.embd, D, tok, wg * 16 + tid);
-    for (int l = 0; l < a.NL; l++) {
-      const LayerView L = a.layers[l];
-      int g0, cnt;
-      // ---- o: x1 = x + W_o . quantize(att)
-      wave_range(L.o.ng, wave, g0, cnt);
-      RG<NGO> ro;
-      rg_load<NGO>(L.o, wg, r, j, g0, cnt, ro);
-      const uint32_t ep_att = phase_epoch(ep0, s, E, 4 * l + 0);
-      {
-        uint32_t v[kRecvD];
-        ll_recv<kRecvD>(LATT, D, ep_att, a.st, bad, v);
+// o and down rows 16w..16w+15 for wave W's share of the blocks; the residual x of those rows lives
+// in m.own.  Wave 0 runs the serial passes and the stores.
+template <class S, int W>
+__device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int tok, bool& bad) {
+  constexpr int G0o = split_g0(S::NGD, W), Co = split_cnt(S::NGD, W);
+  constexpr int G0d = split_g0(S::NGF, W), Cd = split_cnt(S::NGF, W);
+  const int tid = threadIdx.x, lane = tid & 63, r = lane >> 2, j = lane & 3;
+  const int wg = blockIdx.x, row = wg * 16 + r, E = 4 * a.NL + 1;
+  if (tid < 16) m.own[tid] = embed_value(a.embd, S::D, tok, wg * 16 + tid);
+  for (int l = 0; l < a.NL; l++) {
+    const LayerView& L = a.layers[l];
+    // ---- o: x1 = x + W_o . quantize(att)
+    WR<Co> ro;
+    wr_load<S::NGD, S::NB8D, G0o, Co>(L.o, wg, lane, ro);
+    {
+      uint32_t v[S::KD];
+      ll_recv<S::KD>(a.ll + S::oATT, S::D, phase_epoch(ep0, s, E, 4 * l + 0), a.st, bad, v);
 #pragma unroll
-        for (int k = 0; k < kRecvD; k++)
-          if (tid + 256 * k < D) m.xl[tid + 256 * k] = __uint_as_float(v[k]);
-      }
-      if (__syncthreads_or(bad)) return;
-      if (wg == 0) prof_mark(a, s, l * 16 + 0);
-      quantize_row_dev<QM_PLAIN>(m.xl, nullptr, 0, D, nullptr, 0.0f, m.xq, tid, kPThreads);
-      __syncthreads();
-      rg_terms<NGO>(ro, g0, cnt, nbD, m.xq, j, m.terms, lane);
-      __syncthreads();
-      if (wave == 0) {
-        const float v = hsum4(serial_sum(m.terms, nbD, lane));
-        if (j == 0) {
-          const float x1 = m.own[r] + v;
-          m.own[r] = x1;
-          ll_put(LX1 + row, __float_as_uint(x1), phase_epoch(ep0, s, E, 4 * l + 1));
-        }
-        if (wg == 0) prof_mark(a, s, l * 16 + 1);
-      }
-      // ---- down: x2 = x1 + W_down . act (act arrives quantized)
-      wave_range(L.down.ng, wave, g0, cnt);
-      RG<NGDN> rd;
-      rg_load<NGDN>(L.down, wg, r, j, g0, cnt, rd);
-      const uint32_t ep_act = phase_epoch(ep0, s, E, 4 * l + 2);
-      {
-        uint32_t v[kRecvAct];
-        uint32_t* raw = (uint32_t*)m.terms;
-        ll_recv<kRecvAct>(LACT, nbF * 9, ep_act, a.st, bad, v);
-        __syncthreads();   // wave 0's serial pass over m.terms has finished
-#pragma unroll
-        for (int k = 0; k < kRecvAct; k++)
-          if (tid + 256 * k < nbF * 9) raw[tid + 256 * k] = v[k];
-        if (__syncthreads_or(bad)) return;
-        for (int b = tid; b < nbF; b += kPThreads) {
-          uint32_t e[9];
-#pragma unroll
-          for (int k = 0; k < 9; k++) e[k] = raw[b * 9 + k];
-#pragma unroll
-          for (int jj = 0; jj < 4; jj++) {
-            const int c = -8 * (sdot4(e[jj], 0x01010101u, 0) + sdot4(e[4 + jj], 0x01010101u, 0));
-            m.xq[b * 4 + jj] = make_uint4(e[jj], e[4 + jj], (uint32_t)c, e[8]);
-          }
-        }
-        __syncthreads();
-      }
-      if (wg == 0) prof_mark(a, s, l * 16 + 2);
-      rg_terms<NGDN>(rd, g0, cnt, nbF, m.xq, j, m.terms, lane);
-      __syncthreads();
-      if (wave == 0) {
-        const float v = hsum4(serial_sum(m.terms, nbF, lane));
-        if (j == 0) {
-          const float x2 = m.own[r] + v;
-          m.own[r] = x2;
-          ll_put(LX2 + row, __float_as_uint(x2), phase_epoch(ep0, s, E, 4 * l + 3));
-        }
-        if (wg == 0) prof_mark(a, s, l * 16 + 3);
-      }
-      __syncthreads();
+      for (int k = 0; k < S::KD; k++)
+        if (tid + kPThreads * k < S::D) m.xl[tid + kPThreads * k] = __uint_as_float(v[k]);
     }
-    tok = head_phase<NGD>(a, m, s, pos, ep0, E, bad);
-    if (tok < 0) return;
+    if (__syncthreads_or(bad)) return false;
+    if (wg == 0) prof_mark(a, s, l * 16 + 0);
+    if (tid < S::NBD * 4) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k] = m.xl[lane_elem(tid, k)];
+      m.xq[tid] = quant_lane(v);
+    }
+    __syncthreads();
+    wr_terms<S::NBD, G0o, Co>(ro, m.xq, lane, m.terms);
+    __syncthreads();
+    if constexpr (W == 0) {
+      const float v = hsum4(serial_sum<S::NBD>(m.terms, lane));
+      if (j == 0) {
+        const float x1 = m.own[r] + v;
+        m.own[r] = x1;
+        ll_put(a.ll + S::oX1 + row, __float_as_uint(x1), phase_epoch(ep0, s, E, 4 * l + 1));
+      }
+      if (wg == 0) prof_mark(a, s, l * 16 + 1);
+    }
+    // ---- down: x2 = x1 + W_down . act (act arrives quantized)
+    WR<Cd> rd;
+    wr_load<S::NGF, S::NB8F, G0d, Cd>(L.down, wg, lane, rd);
+    {
+      uint32_t v[S::KACT];
+      ll_recv<S::KACT>(a.ll + S::oACT, S::NACT, phase_epoch(ep0, s, E, 4 * l + 2), a.st, bad, v);
+#pragma unroll
+      for (int k = 0; k < S::KACT; k++)
+        if (tid + kPThreads * k < S::NACT) m.raw[tid + kPThreads * k] = v[k];
+    }
+    if (__syncthreads_or(bad)) return false;
+    for (int b = tid; b < S::NBF; b += kPThreads) {
+      uint32_t e[9];
+#pragma unroll
+      for (int k = 0; k < 9; k++) e[k] = m.raw[b * 9 + k];
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++) {
+        const int c = -8 * (sdot4(e[jj], 0x01010101u, 0) + sdot4(e[4 + jj], 0x01010101u, 0));
+        m.xq[b * 4 + jj] = make_uint4(e[jj], e[4 + jj], (uint32_t)c, e[8]);
+      }
+    }
+    __syncthreads();
+    if (wg == 0) prof_mark(a, s, l * 16 + 2);
+    wr_terms<S::NBF, G0d, Cd>(rd, m.xq, lane, m.terms);
+    __syncthreads();
+    if constexpr (W == 0) {
+      const float v = hsum4(serial_sum<S::NBF>(m.terms, lane));
+      if (j == 0) {
+        const float x2 = m.own[r] + v;
+        m.own[r] = x2;
+        ll_put(a.ll + (l == a.NL - 1 ? S::oXH : S::oX2) + row, __float_as_uint(x2), phase_epoch(ep0, s, E, 4 * l + 3));
+      }
+      if (wg == 0) prof_mark(a, s, l * 16 + 3);
+    }
   }
-  if (blockIdx.x == 0 && tid == 0) {
-    a.st->pos0 = pos;
-    a.st->next = tok;
-    a.st->epoch = ep0 + (uint32_t)(a.steps * E) + 1u;
-  }
+  return true;
 }
 
 // One attention head h: q rows of h and k, v rows of its kv group, RoPE, K/V append (first head of
 // the group), attention over the cache (kernels.c:333-377).  Past K/V rows (up to kv_tile of them)
 // are staged in shared memory while the role waits for x.
-template <int NGD>
-__device__ __forceinline__ void role_attn(const PArgs a, const PSmem m, uint32_t ep0, int pos, int tok) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane >> 2, j = lane & 3;
-  const int D = a.D, nbD = D / 32, E = 4 * a.NL + 1;
-  const int h = blockIdx.x - a.nOD, grp = a.H / a.KVH, kh = h / grp;
-  const bool writer = (h % grp) == 0;
-  uint64_t* LX2 = a.ll + D;
-  uint64_t* LATT = a.ll + 2 * D;
-  const int rq = (h * kHD) / 16 + wave, rk = (D + kh * kHD) / 16 + wave, rv = (D + a.KVH * kHD + kh * kHD) / 16 + wave;
+//
+// K/V of a position are written once per launch (agent-scope stores), by the first head of the
+// group, and are first read by the other heads at least one step later: each position is read only
+// once pos has moved past it.
+template <class S>
+__device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int pos, int tok,
+                                          bool& bad) {
+  constexpr int GRP = S::H / S::KVH;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), r = lane >> 2, j = lane & 3;
+  const int E = 4 * a.NL + 1;
+  const int h = blockIdx.x - S::nOD, kh = h / GRP;
+  const bool writer = (h % GRP) == 0;
+  const int rq = (h * kHD) / 16 + wave, rk = (S::D + kh * kHD) / 16 + wave;
+  const int rv = (S::D + S::KVH * kHD + kh * kHD) / 16 + wave;
   float* qv = m.qv;
   float* kv = m.qv + 64;
   float* vv = m.qv + 128;
   float* sc = m.terms;
-  float* kt = m.kvt;                              // [kv_tile][kKVRow] K
+  float* kt = m.kvt;                               // [kv_tile][kKVRow] K
   float* vt = m.kvt + (size_t)a.kv_tile * kKVRow;  // [kv_tile][kKVRow] V
-  bool bad = false;
-  for (int s = 0; s < a.steps; s++, pos++) {
-    const int nt = pos < a.kv_tile ? pos : a.kv_tile;    // staged past positions
-    for (int l = 0; l < a.NL; l++) {
-      const LayerView L = a.layers[l];
-      const int ng = L.qkv.ng;
-      RG<NGD> w3[3];
-      rg_load<NGD>(L.qkv, rq, r, j, 0, ng, w3[0]);
-      rg_load<NGD>(L.qkv, rk, r, j, 0, ng, w3[1]);
-      rg_load<NGD>(L.qkv, rv, r, j, 0, ng, w3[2]);
-      const size_t cbase = ((size_t)l * a.KVH + kh) * a.ctx * kHD;
-      // stage K and V of positions [0, nt) (written by earlier steps or launches)
-      for (int idx = tid; idx < nt * 32; idx += kPThreads) {
-        const int which = idx >= nt * 16, rem = idx - which * nt * 16, t = rem >> 4, c4 = (rem & 15) * 4;
-        const float4 v4 = gld4f((which ? a.vc : a.kc) + cbase + (size_t)t * kHD + c4);
-        float* dst = (which ? vt : kt) + t * kKVRow + c4;
-        *reinterpret_cast<float4*>(dst) = v4;
-      }
-      if (l == 0) {
-        const int stv = run_stride(D);
-        for (int i = tid; i < D; i += kPThreads) m.xl[(i & 3) * stv + (i >> 2)] = embed_value(a.embd, D, tok, i);
-      } else {
-        recv_x(LX2, D, phase_epoch(ep0, s, E, 4 * (l - 1) + 3), a.st, m.xl, bad);
-      }
-      if (__syncthreads_or(bad)) return;
-      if (h == 0) prof_mark(a, s, l * 16 + 4);
-      norm_quant(m, D, L.attn_norm, a.eps);
-      float acc[3] = {0.0f, 0.0f, 0.0f};
-      rg_dot<NGD, 3>(w3, 0, ng, nbD, m.xq, j, acc);
-      const float q = hsum4(acc[0]), k = hsum4(acc[1]), v = hsum4(acc[2]);
-      if (j == 0) {
-        qv[16 * wave + r] = q + L.bqkv[rq * 16 + r];
-        kv[16 * wave + r] = k + L.bqkv[rk * 16 + r];
-        vv[16 * wave + r] = v + L.bqkv[rv * 16 + r];
-      }
-      __syncthreads();
-      if (h == 0) prof_mark(a, s, l * 16 + 5);
-      // RoPE (kernels.c:340-344): threads 0..31 rotate q pairs, 32..63 k pairs
-      if (tid < 64) {
-        const int i = tid & 31;
-        float* x = tid < 32 ? qv : kv;
-        const float c = a.rope[(size_t)pos * kHD + 2 * i], sn = a.rope[(size_t)pos * kHD + 2 * i + 1];
-        const float x0 = x[i], x1 = x[i + 32];
-        x[i] = x0 * c - x1 * sn;
-        x[i + 32] = x1 * c + x0 * sn;
-      }
-      __syncthreads();
-      if (writer && tid < 64) {
-        st_coherent(a.kc + cbase + (size_t)pos * kHD + tid, kv[tid]);
-        st_coherent(a.vc + cbase + (size_t)pos * kHD + tid, vv[tid]);
-      }
-      // scores: four lane sums over i = j mod 4, hsum, scale (kernels.c:362-366)
-      const int T = pos + 1;
-      const float scale = 1.0f / __builtin_sqrtf((float)kHD);
-      float lmax = -1e30f;
-      for (int t = tid; t < T; t += kPThreads) {
-        float4 kk[kHD / 4];
-        if (t == pos) {
-#pragma unroll
-          for (int i = 0; i < kHD / 4; i++) kk[i] = reinterpret_cast<const float4*>(kv)[i];
-        } else if (t < nt) {
-#pragma unroll
-          for (int i = 0; i < kHD / 4; i++) kk[i] = reinterpret_cast<const float4*>(kt + t * kKVRow)[i];
-        } else {
-#pragma unroll
-          for (int i = 0; i < kHD / 4; i++) kk[i] = gld4f(a.kc + cbase + (size_t)t * kHD + 4 * i);
-        }
-        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kHD / 4; i++) {
-          const float4 q4 = reinterpret_cast<const float4*>(qv)[i];
-          s0 = s0 + q4.x * kk[i].x;
-          s1 = s1 + q4.y * kk[i].y;
-          s2 = s2 + q4.z * kk[i].z;
-          s3 = s3 + q4.w * kk[i].w;
-        }
-        const float sv = (s0 + s1 + s2 + s3) * scale;
-        sc[t] = sv;
-        lmax = __builtin_fmaxf(lmax, sv);
-      }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) lmax = __builtin_fmaxf(lmax, __shfl_xor(lmax, o));
-      if (lane == 0) m.red[wave] = lmax;
-      __syncthreads();
-      const float mx = __builtin_fmaxf(__builtin_fmaxf(m.red[0], m.red[1]), __builtin_fmaxf(m.red[2], m.red[3]));
-      for (int t = tid; t < T; t += kPThreads) sc[t] = fast_exp(sc[t] - mx);
-      __syncthreads();
-      if (tid == 0) {
-        const int T4 = T & ~3;
-        float sum = serial_sum_vec(sc, T4);
-        for (int t = T4; t < T; t++) sum = sum + sc[t];
-        m.red[8] = sum;
-      }
-      __syncthreads();
-      const float sum = m.red[8];
-      for (int t = tid; t < T; t += kPThreads) sc[t] = sc[t] / sum;
-      __syncthreads();
-      // out_i = sum over t in order of p_t * v_t[i] (kernels.c:372-375)
-      if (tid < kHD) {
-        float accv = 0.0f;
-        int t = 0;
-        for (; t + 8 <= nt; t += 8) {
-          float vx[8];
-#pragma unroll
-          for (int u = 0; u < 8; u++) vx[u] = vt[(t + u) * kKVRow + tid];
-#pragma unroll
-          for (int u = 0; u < 8; u++) accv = accv + sc[t + u] * vx[u];
-        }
-        for (; t < nt; t++) accv = accv + sc[t] * vt[t * kKVRow + tid];
-        constexpr int TB = 32;     // positions past the staged tile: streamed, 32 loads ahead
-        for (; t < pos; t += TB) {
-          float vx[TB];
-#pragma unroll
-          for (int u = 0; u < TB; u++) vx[u] = t + u < pos ? gldf(a.vc + cbase + (size_t)(t + u) * kHD + tid) : 0.0f;
-#pragma unroll
-          for (int u = 0; u < TB; u++)
-            if (t + u < pos) accv = accv + sc[t + u] * vx[u];
-        }
-        accv = accv + sc[pos] * vv[tid];
-        ll_put(LATT + h * kHD + tid, __float_as_uint(accv), phase_epoch(ep0, s, E, 4 * l + 0));
-      }
-      if (h == 0) prof_mark(a, s, l * 16 + 6);
-      __syncthreads();
+  const int nt = pos < a.kv_tile ? pos : a.kv_tile;   // staged past positions
+  for (int l = 0; l < a.NL; l++) {
+    const LayerView& L = a.layers[l];
+    WR<S::NGD> w3[3];
+    wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.qkv, rq, lane, w3[0]);
+    wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.qkv, rk, lane, w3[1]);
+    wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.qkv, rv, lane, w3[2]);
+    float nw[8];
+    normw_load<S>(L.attn_norm, nw);
+    float bq = 0.0f, bk = 0.0f, bvv = 0.0f;
+    if (j == 0) {
+      bq = gldf(L.bqkv + rq * 16 + r);
+      bk = gldf(L.bqkv + rk * 16 + r);
+      bvv = gldf(L.bqkv + rv * 16 + r);
     }
-    tok = head_phase<NGD>(a, m, s, pos, ep0, E, bad);
-    if (tok < 0) return;
+    float rc = 0.0f, rsn = 0.0f;
+    if (tid < 64) {
+      const float2 cs = gld2f(a.rope + (size_t)pos * kHD + 2 * (tid & 31));
+      rc = cs.x;
+      rsn = cs.y;
+    }
+    const size_t cbase = ((size_t)l * S::KVH + kh) * a.ctx * kHD;
+    // stage K and V of positions [0, nt), four 16-byte loads in flight per thread
+    for (int i0 = 0; i0 < nt * 32; i0 += 4 * kPThreads) {
+      float4 v4[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int idx = i0 + u * kPThreads + tid;
+        if (idx < nt * 32) {
+          const int which = idx >= nt * 16, rem = idx - which * nt * 16, t = rem >> 4, c4 = (rem & 15) * 4;
+          v4[u] = gld4f((which ? a.vc : a.kc) + cbase + (size_t)t * kHD + c4);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int idx = i0 + u * kPThreads + tid;
+        if (idx < nt * 32) {
+          const int which = idx >= nt * 16, rem = idx - which * nt * 16, t = rem >> 4, c4 = (rem & 15) * 4;
+          *reinterpret_cast<float4*>((which ? vt : kt) + t * kKVRow + c4) = v4[u];
+        }
+      }
+    }
+    if (l == 0) {
+      for (int i = tid; i < S::D; i += kPThreads) stage_x<S>(m, i, embed_value(a.embd, S::D, tok, i));
+    } else {
+      recv_x<S>(a.ll + S::oX2, phase_epoch(ep0, s, E, 4 * (l - 1) + 3), a.st, m, bad);
+    }
+    if (__syncthreads_or(bad)) return false;
+    if (h == 0) prof_mark(a, s, l * 16 + 4);
+    norm_quant<S>(m, nw, a.eps);
+    if (h == 0) prof_mark(a, s, l * 16 + 9);
+    float acc[3] = {0.0f, 0.0f, 0.0f};
+    wr_dot<S::NBD, 0, S::NGD, 3>(w3, m.xq, j, acc);
+    const float q = hsum4(acc[0]), k = hsum4(acc[1]), v = hsum4(acc[2]);
+    if (j == 0) {
+      qv[16 * wave + r] = q + bq;
+      kv[16 * wave + r] = k + bk;
+      vv[16 * wave + r] = v + bvv;
+    }
+    __syncthreads();
+    if (h == 0) prof_mark(a, s, l * 16 + 5);
+    // RoPE (kernels.c:340-344): threads 0..31 rotate q pairs, 32..63 k pairs
+    if (tid < 64) {
+      const int i = tid & 31;
+      float* x = tid < 32 ? qv : kv;
+      const float x0 = x[i], x1 = x[i + 32];
+      x[i] = x0 * rc - x1 * rsn;
+      x[i + 32] = x1 * rc + x0 * rsn;
+    }
+    __syncthreads();
+    if (writer && tid < 64) {
+      st_coherent(a.kc + cbase + (size_t)pos * kHD + tid, kv[tid]);
+      st_coherent(a.vc + cbase + (size_t)pos * kHD + tid, vv[tid]);
+    }
+    // scores: four lane sums over i = j mod 4, hsum, scale (kernels.c:362-366)
+    const int T = pos + 1;
+    const float scale = 1.0f / __builtin_sqrtf((float)kHD);
+    float lmax = -1e30f;
+    for (int t = tid; t < T; t += kPThreads) {
+      float4 kk[kHD / 4];
+      if (t == pos) {
+#pragma unroll
+        for (int i = 0; i < kHD / 4; i++) kk[i] = reinterpret_cast<const float4*>(kv)[i];
+      } else if (t < nt) {
+#pragma unroll
+        for (int i = 0; i < kHD / 4; i++) kk[i] = reinterpret_cast<const float4*>(kt + t * kKVRow)[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < kHD / 4; i++) kk[i] = gld4f(a.kc + cbase + (size_t)t * kHD + 4 * i);
+      }
+      float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kHD / 4; i++) {
+        const float4 q4 = reinterpret_cast<const float4*>(qv)[i];
+        s0 = s0 + q4.x * kk[i].x;
+        s1 = s1 + q4.y * kk[i].y;
+        s2 = s2 + q4.z * kk[i].z;
+        s3 = s3 + q4.w * kk[i].w;
+      }
+      const float sv = (s0 + s1 + s2 + s3) * scale;
+      sc[t] = sv;
+      lmax = __builtin_fmaxf(lmax, sv);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) lmax = __builtin_fmaxf(lmax, __shfl_xor(lmax, o));
+    if (lane == 0) m.red[wave] = lmax;
+    __syncthreads();
+    const float mx = __builtin_fmaxf(__builtin_fmaxf(m.red[0], m.red[1]), __builtin_fmaxf(m.red[2], m.red[3]));
+    for (int t = tid; t < T; t += kPThreads) sc[t] = fast_exp(sc[t] - mx);
+    __syncthreads();
+    if (tid == 0) m.red[8] = seq_sum(sc, T);
+    __syncthreads();
+    const float sum = m.red[8];
+    for (int t = tid; t < T; t += kPThreads) sc[t] = sc[t] / sum;
+    __syncthreads();
+    // out_i = sum over t in order of p_t * v_t[i] (kernels.c:372-375)
+    if (tid < kHD) {
+      float accv = seq_dot(0.0f, sc, vt + tid, kKVRow, nt);
+      int t = nt;
+      constexpr int TB = 32;     // positions past the staged tile: streamed, 32 loads ahead
+      for (; t < pos; t += TB) {
+        float vx[TB];
+#pragma unroll
+        for (int u = 0; u < TB; u++) vx[u] = t + u < pos ? gldf(a.vc + cbase + (size_t)(t + u) * kHD + tid) : 0.0f;
+#pragma unroll
+        for (int u = 0; u < TB; u++)
+          if (t + u < pos) accv = accv + sc[t + u] * vx[u];
+      }
+      accv = accv + sc[pos] * vv[tid];
+      ll_put(a.ll + S::oATT + h * kHD + tid, __float_as_uint(accv), phase_epoch(ep0, s, E, 4 * l + 0));
+    }
+    if (h == 0) prof_mark(a, s, l * 16 + 6);
+    __syncthreads();
   }
+  return true;
 }
 
 // One 32-value block u of the SwiGLU activation: gate rows 32u.., up rows F+32u.. (one 16-row
 // group per wave), then silu(gate)*up and quantize_row of the block (kernels.c:390-397).
-template <int NGD>
-__device__ __forceinline__ void role_gu(const PArgs a, const PSmem m, uint32_t ep0, int pos, int tok) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane >> 2, j = lane & 3;
-  const int D = a.D, nbD = D / 32, E = 4 * a.NL + 1;
-  const int u = blockIdx.x - a.nOD - a.nA;
-  const int rg = wave < 2 ? 2 * u + wave : a.F / 16 + 2 * u + (wave - 2);
-  uint64_t* LX1 = a.ll;
-  uint64_t* LACT = a.ll + 3 * D;
-  bool bad = false;
-  for (int s = 0; s < a.steps; s++, pos++) {
-    for (int l = 0; l < a.NL; l++) {
-      const LayerView L = a.layers[l];
-      const int ng = L.gu.ng;
-      RG<NGD> w[1];
-      rg_load<NGD>(L.gu, rg, r, j, 0, ng, w[0]);
-      recv_x(LX1, D, phase_epoch(ep0, s, E, 4 * l + 1), a.st, m.xl, bad);
-      if (__syncthreads_or(bad)) return;
-      if (u == 0) prof_mark(a, s, l * 16 + 7);
-      norm_quant(m, D, L.ffn_norm, a.eps);
-      float acc[1] = {0.0f};
-      rg_dot<NGD, 1>(w, 0, ng, nbD, m.xq, j, acc);
-      const float v = hsum4(acc[0]);
-      if (j == 0) m.gu[16 * wave + r] = v;
-      __syncthreads();
-      if (tid < 4) quantize_row_dev<QM_SWIGLU>(m.gu, nullptr, 0, 32, nullptr, 0.0f, m.tq, tid, 4);
-      __syncthreads();
-      if (tid < 9) {
-        const uint32_t pay = tid < 4 ? m.tq[tid].x : tid < 8 ? m.tq[tid - 4].y : m.tq[0].w;
-        ll_put(LACT + u * 9 + tid, pay, phase_epoch(ep0, s, E, 4 * l + 2));
-      }
-      if (u == 0) prof_mark(a, s, l * 16 + 8);
-      __syncthreads();
-    }
-    tok = head_phase<NGD>(a, m, s, pos, ep0, E, bad);
-    if (tok < 0) return;
-  }
-}
-
-template <int NGD>
-__device__ __forceinline__ void role_head_only(const PArgs a, const PSmem m, uint32_t ep0, int pos, int tok) {
+template <class S>
+__device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t ep0, int s, bool& bad) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), r = lane >> 2, j = lane & 3;
   const int E = 4 * a.NL + 1;
-  bool bad = false;
-  for (int s = 0; s < a.steps; s++, pos++) {
-    tok = head_phase<NGD>(a, m, s, pos, ep0, E, bad);
-    if (tok < 0) return;
+  const int u = blockIdx.x - S::nOD - S::nA;
+  const int rg = wave < 2 ? 2 * u + wave : S::F / 16 + 2 * u + (wave - 2);
+  for (int l = 0; l < a.NL; l++) {
+    const LayerView& L = a.layers[l];
+    WR<S::NGD> w[1];
+    wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.gu, rg, lane, w[0]);
+    float nw[8];
+    normw_load<S>(L.ffn_norm, nw);
+    recv_x<S>(a.ll + S::oX1, phase_epoch(ep0, s, E, 4 * l + 1), a.st, m, bad);
+    if (__syncthreads_or(bad)) return false;
+    if (u == 0) prof_mark(a, s, l * 16 + 7);
+    norm_quant<S>(m, nw, a.eps);
+    if (u == 0) prof_mark(a, s, l * 16 + 10);
+    float acc[1] = {0.0f};
+    wr_dot<S::NBD, 0, S::NGD, 1>(w, m.xq, j, acc);
+    const float v = hsum4(acc[0]);
+    if (j == 0) m.gu[16 * wave + r] = v;
+    __syncthreads();
+    // silu(gate) * up, one value per lane of wave 0, then quantize_row of the block; word w of the
+    // block (A_j for w = j, B_j for w = 4 + j, kernels.h layout) gathers its four int8 by shuffles
+    if (tid < 64) {
+      const int i = tid & 31;
+      const float g = m.gu[i];
+      const float x = g / (1.0f + fast_exp(-g)) * m.gu[32 + i];
+      float am = __builtin_fabsf(x);
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) am = __builtin_fmaxf(am, __shfl_xor(am, o));
+      const float dd = am / 127.0f;
+      const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+      const int q = quant_one(x * id);
+      const int w = tid & 7, e0 = ((w >> 2) << 4) + ((w & 3) << 1);
+      const int q0 = __shfl(q, e0), q1 = __shfl(q, e0 + 1), q2 = __shfl(q, e0 + 8), q3 = __shfl(q, e0 + 9);
+      const uint32_t ep = phase_epoch(ep0, s, E, 4 * l + 2);
+      if (tid < 8) ll_put(a.ll + S::oACT + u * 9 + tid, pack4(q0, q1, q2, q3), ep);
+      else if (tid == 8) ll_put(a.ll + S::oACT + u * 9 + 8, __float_as_uint(dd), ep);
+    }
+    if (u == 0) prof_mark(a, s, l * 16 + 8);
   }
+  return true;
 }
 
-// NGD: groups of 4 blocks for K = D; NGO/NGDN: per-wave groups of o / down after the 4-way split.
-template <int NGD, int NGO, int NGDN>
+template <class S>
 __global__ __launch_bounds__(kPThreads, 1) void k_decode_persistent(PArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const PSmem m = psmem(smem, a.D, a.F);
+  const PSmem m = psmem<S>(smem);
   const uint32_t ep0 = a.st->epoch;
-  const int pos = a.st->pos0;
-  const int tok = a.tokens[pos];
-  const int wg = blockIdx.x;
+  int pos = a.st->pos0;
+  int tok = a.tokens[pos];
+  const int wg = blockIdx.x, wave = wave_id();
   if (wg == 0) prof_mark(a, 0, a.NL * 16 + 3);
   if (a.prof && wg == 0 && threadIdx.x == 0) a.prof[a.NL * 16 + 4] = clock64();
-  if (wg < a.nOD) role_od<NGO, NGDN, NGD>(a, m, ep0, pos, tok);
-  else if (wg < a.nOD + a.nA) role_attn<NGD>(a, m, ep0, pos, tok);
-  else if (wg < a.nOD + a.nA + a.nGU) role_gu<NGD>(a, m, ep0, pos, tok);
-  else role_head_only<NGD>(a, m, ep0, pos, tok);
+  bool bad = false;
+  for (int s = 0; s < a.steps; s++, pos++) {
+    bool ok = true;
+    if (wg < S::nOD) {
+      switch (wave) {
+        case 0: ok = od_step<S, 0>(a, m, ep0, s, tok, bad); break;
+        case 1: ok = od_step<S, 1>(a, m, ep0, s, tok, bad); break;
+        case 2: ok = od_step<S, 2>(a, m, ep0, s, tok, bad); break;
+        default: ok = od_step<S, 3>(a, m, ep0, s, tok, bad); break;
+      }
+    } else if (wg < S::nOD + S::nA) {
+      ok = attn_step<S>(a, m, ep0, s, pos, tok, bad);
+    } else if (wg < S::nRoles) {
+      ok = gu_step<S>(a, m, ep0, s, bad);
+    }
+    if (!ok) return;
+    tok = head_phase<S>(a, m, ep0, s, pos, bad);
+    if (tok < 0) return;
+  }
+  if (wg == 0 && threadIdx.x == 0) {
+    const int E = 4 * a.NL + 1;
+    a.st->pos0 = pos;
+    a.st->next = tok;
+    a.st->epoch = ep0 + (uint32_t)(a.steps * E) + 1u;
+  }
 }
 
 }  // namespace q4

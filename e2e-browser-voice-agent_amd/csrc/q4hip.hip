@@ -518,32 +518,52 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
   prof_mark(h, -1);
 }
 
-int wave_groups(int ng) { return (((ng + 3) >> 2) + 1) & ~1; }
+// The model shapes the persistent decode kernel is compiled for: Qwen2.5-0.5B and the two small
+// shapes of the parity tests.  Any other shape decodes through the graph path.
+struct PersInstance {
+  int D, F, H, KVH;
+  const void* fn;
+  size_t lds_base;
+  size_t (*ll_entries)(int);
+  int nRoles, nbm;
+};
+
+template <class S>
+PersInstance pers_instance() {
+  return PersInstance{S::D, S::F, S::H, S::KVH, (const void*)k_decode_persistent<S>, psmem_base_bytes<S>(),
+                      &S::ll_entries, S::nRoles, S::NBM};
+}
+
+const PersInstance* find_pers_instance(int D, int F, int H, int KVH) {
+  static const PersInstance table[] = {
+      pers_instance<PShape<896, 4864, 14, 2>>(),   // Qwen2.5-0.5B
+      pers_instance<PShape<128, 256, 2, 1>>(),
+      pers_instance<PShape<256, 512, 4, 1>>(),
+  };
+  for (const PersInstance& p : table)
+    if (p.D == D && p.F == F && p.H == H && p.KVH == KVH) return &p;
+  return nullptr;
+}
 
 // Decide once whether this model and device admit the persistent decode kernel, and set it up.
 // On refusal h->pers_why says which requirement failed.
 void setup_persistent(q4hip* h) {
   if (h->pers_ok || h->pers_broken || h->mode == Q4HIP_DECODE_GRAPH) return;
   h->pers_broken = true;   // until proven otherwise
-  const int D = h->D, F = h->F;
   auto no = [h](const char* why) { h->pers_why = why; };
   if (h->HD != kHD) return no("head_dim is not 64");
-  if (D % 64 || F % 32 || D > 1024 || (F / 32) * 9 > 256 * kRecvAct) return no("dim or ffn out of range");
-  const Layer& y0 = h->L[0];
-  const int ngD = y0.qkv.ng, perO = wave_groups(y0.o.ng), perDn = wave_groups(y0.down.ng);
-  if (ngD <= 7 && perO <= 2 && perDn <= 10) h->pers_fn = (const void*)k_decode_persistent<7, 2, 10>;
-  else if (ngD <= 8 && perO <= 4 && perDn <= 18) h->pers_fn = (const void*)k_decode_persistent<8, 4, 18>;
-  else return no("no kernel instance for these block counts");
-  const int nbm = std::max(D, F) / 32;
-  if (h->ctx > 64 * nbm) return no("ctx too large for the score buffer");
+  const PersInstance* pi = find_pers_instance(h->D, h->F, h->H, h->KVH);
+  if (!pi) return no("no kernel instance for this model shape");
+  h->pers_fn = pi->fn;
+  if (h->ctx > 64 * pi->nbm) return no("ctx too large for the score buffer");
   int lds_max = 0;
   if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, h->device) != hipSuccess)
     return no("cannot query shared memory size");
-  const size_t base = psmem_base_bytes(D, F), budget = (size_t)lds_max > 4096 ? (size_t)lds_max - 4096 : 0;
+  const size_t base = pi->lds_base, budget = (size_t)lds_max > 4096 ? (size_t)lds_max - 4096 : 0;
   if (base > budget) return no("shared memory too small");
   // past K/V rows the attention role stages in shared memory; the rest are streamed
   h->pers_kv_tile = (int)std::min<size_t>({(size_t)h->ctx, (size_t)192, (budget - base) / (2 * kKVRow * 4)});
-  h->pers_lds = psmem_bytes(D, F, h->pers_kv_tile);
+  h->pers_lds = base + (size_t)h->pers_kv_tile * 2 * kKVRow * 4;
   if (hipFuncSetAttribute(h->pers_fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)h->pers_lds) != hipSuccess) {
     (void)hipGetLastError();
     return no("cannot raise the kernel's shared memory limit");
@@ -557,15 +577,14 @@ void setup_persistent(q4hip* h) {
   }
   // One workgroup per CU: all of them fit on the device at once, which the waits between them
   // rely on (a workgroup that could not start would only make the others time out and abort).
-  const int need = D / 16 + h->H + F / 32;
   const int G = cus;
-  if (need > G || G > 256) return no("more roles than CUs");   // the argmax exchange gives one entry per thread
+  if (pi->nRoles > G || G > 256) return no("more roles than CUs");   // the argmax exchange gives one entry per thread
   std::vector<LayerView> lv(h->NL);
   for (int l = 0; l < h->NL; l++) {
     const Layer& y = h->L[l];
     lv[l] = LayerView{y.qkv.view(), y.o.view(), y.gu.view(), y.down.view(), y.attn_norm, y.ffn_norm, y.bqkv};
   }
-  const size_t ll_entries = (size_t)3 * D + (size_t)(F / 32) * 9 + 2 * (size_t)G;
+  const size_t ll_entries = pi->ll_entries(G);
   if (hipMalloc(&h->d_layers, lv.size() * sizeof(LayerView)) != hipSuccess ||
       hipMemcpy(h->d_layers, lv.data(), lv.size() * sizeof(LayerView), hipMemcpyHostToDevice) != hipSuccess ||
       hipMalloc(&h->ll, ll_entries * 8) != hipSuccess || hipMemset(h->ll, 0, ll_entries * 8) != hipSuccess) {
@@ -585,7 +604,7 @@ bool use_persistent(q4hip* h) {
 
 hipError_t launch_persistent(q4hip* h, int steps, unsigned long long* prof = nullptr) {
   PArgs a;
-  a.D = h->D; a.F = h->F; a.H = h->H; a.KVH = h->KVH; a.QKV = h->QKV; a.V = h->V; a.NL = h->NL; a.ctx = h->ctx;
+  a.V = h->V; a.NL = h->NL; a.ctx = h->ctx;
   a.eps = h->eps;
   a.embd = h->embd;
   a.out_norm = h->out_norm;
@@ -599,9 +618,6 @@ hipError_t launch_persistent(q4hip* h, int steps, unsigned long long* prof = nul
   a.st = h->st;
   a.ll = h->ll;
   a.steps = steps;
-  a.nOD = h->D / 16;
-  a.nA = h->H;
-  a.nGU = h->F / 32;
   a.kv_tile = h->pers_kv_tile;
   a.prof = prof;
   void* args[] = {&a};
