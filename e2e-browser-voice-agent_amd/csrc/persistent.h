@@ -191,18 +191,44 @@ __device__ __forceinline__ void wr_load(const Q4Mat& W, int rg16, int lane, WR<C
   }
 }
 
-// One block's term f32(p_j) * (dw * dx) (kernels.c:137); xv = {A_j, B_j, c_j, dx}.  g, k are
-// constants after unrolling.
-template <int CNT>
-__device__ __forceinline__ float wr_term(const WR<CNT>& R, int g, int k, uint4 xv) {
-  const uint32_t wv = k == 0 ? R.w[g].x : k == 1 ? R.w[g].y : k == 2 ? R.w[g].z : R.w[g].w;
-  const uint4 sv = R.s[g >> 1];
-  const int hb = ((g & 1) << 2) + k;
-  const uint32_t sw = (hb >> 1) == 0 ? sv.x : (hb >> 1) == 1 ? sv.y : (hb >> 1) == 2 ? sv.z : sv.w;
-  const float dw = half_bits_to_float((hb & 1) ? (sw >> 16) : (sw & 0xffffu));
-  int p = sdot4(wv & 0x0F0F0F0Fu, xv.x, (int)xv.z);
-  p = sdot4((wv >> 4) & 0x0F0F0F0Fu, xv.y, p);
-  return (float)p * (dw * __uint_as_float(xv.w));
+// Terms f32(p_j) * (dw * dx) (kernels.c:137) of the 4 blocks of local group g for N row groups,
+// xv[k] = {A_j, B_j, c_j, dx} of block k.  Computed stage by stage (all low-nibble dots, all
+// high-nibble dots, then the products) so that the independent blocks and rows interleave; each
+// term's own operation order is unchanged.  Blocks past NB (b >= NB) are skipped.
+template <int NB, int G0, int CNT, int N>
+__device__ __forceinline__ void wr_group_terms(const WR<CNT> (&R)[N], int g, const uint4 (&xv)[4],
+                                               float (&t)[N][4]) {
+  int p[N][4];
+#pragma unroll
+  for (int n = 0; n < N; n++)
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      if ((G0 + g) * 4 + k < NB) {
+        const uint32_t wv = k == 0 ? R[n].w[g].x : k == 1 ? R[n].w[g].y : k == 2 ? R[n].w[g].z : R[n].w[g].w;
+        p[n][k] = sdot4(wv & 0x0F0F0F0Fu, xv[k].x, (int)xv[k].z);
+      }
+    }
+#pragma unroll
+  for (int n = 0; n < N; n++)
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      if ((G0 + g) * 4 + k < NB) {
+        const uint32_t wv = k == 0 ? R[n].w[g].x : k == 1 ? R[n].w[g].y : k == 2 ? R[n].w[g].z : R[n].w[g].w;
+        p[n][k] = sdot4((wv >> 4) & 0x0F0F0F0Fu, xv[k].y, p[n][k]);
+      }
+    }
+#pragma unroll
+  for (int n = 0; n < N; n++)
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      if ((G0 + g) * 4 + k < NB) {
+        const uint4 sv = R[n].s[g >> 1];
+        const int hb = ((g & 1) << 2) + k;
+        const uint32_t sw = (hb >> 1) == 0 ? sv.x : (hb >> 1) == 1 ? sv.y : (hb >> 1) == 2 ? sv.z : sv.w;
+        const float dw = half_bits_to_float((hb & 1) ? (sw >> 16) : (sw & 0xffffu));
+        t[n][k] = (float)p[n][k] * (dw * __uint_as_float(xv[k].w));
+      }
+    }
 }
 
 // Mark a value as used here: the loads that produced it complete before this point, and code after
@@ -213,32 +239,36 @@ __device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(float4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
 __device__ __forceinline__ void pin(uint4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
 
+// Activation blocks of local group g (xq[b * 4 + j]); zero past NB.
+template <int NB, int G0>
+__device__ __forceinline__ void xg_load(const uint4* xq, int g, int j, uint4 (&xv)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int b = (G0 + g) * 4 + k;
+    xv[k] = b < NB ? xq[b * 4 + j] : make_uint4(0, 0, 0, 0);
+  }
+}
+
 // acc_n = acc_n + term over blocks [4 G0, min(NB, 4 (G0 + CNT))) in order (kernels.c:217-218), for N
 // row groups sharing each activation read; the next group's activation blocks are read ahead.
 template <int NB, int G0, int CNT, int N>
 __device__ __forceinline__ void wr_dot(const WR<CNT> (&R)[N], const uint4* xq, int j, float (&acc)[N]) {
   if constexpr (CNT > 0) {
     uint4 xb[2][4];
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-      if (G0 * 4 + k < NB) xb[0][k] = xq[(G0 * 4 + k) * 4 + j];
+    xg_load<NB, G0>(xq, 0, j, xb[0]);
 #pragma unroll
     for (int g = 0; g < CNT; g++) {
-      if (g + 1 < CNT) {
+      if (g + 1 < CNT) xg_load<NB, G0>(xq, g + 1, j, xb[(g + 1) & 1]);
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-          if ((G0 + g + 1) * 4 + k < NB) xb[(g + 1) & 1][k] = xq[((G0 + g + 1) * 4 + k) * 4 + j];
-      }
+      for (int k = 0; k < 4; k++) pin(xb[g & 1][k]);
+      float t[N][4];
+      wr_group_terms<NB, G0, CNT, N>(R, g, xb[g & 1], t);
 #pragma unroll
       for (int k = 0; k < 4; k++)
-        if ((G0 + g) * 4 + k < NB) pin(xb[g & 1][k]);
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
         if ((G0 + g) * 4 + k < NB) {
 #pragma unroll
-          for (int n = 0; n < N; n++) acc[n] = acc[n] + wr_term(R[n], g, k, xb[g & 1][k]);
+          for (int n = 0; n < N; n++) acc[n] = acc[n] + t[n][k];
         }
-      }
     }
   }
 }
@@ -247,25 +277,20 @@ __device__ __forceinline__ void wr_dot(const WR<CNT> (&R)[N], const uint4* xq, i
 template <int NB, int G0, int CNT>
 __device__ __forceinline__ void wr_terms(const WR<CNT>& R, const uint4* xq, int lane, float* terms) {
   if constexpr (CNT > 0) {
-    const int j = lane & 3;
+    const WR<CNT> RR[1] = {R};
     uint4 xb[2][4];
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-      if (G0 * 4 + k < NB) xb[0][k] = xq[(G0 * 4 + k) * 4 + j];
+    xg_load<NB, G0>(xq, 0, lane & 3, xb[0]);
 #pragma unroll
     for (int g = 0; g < CNT; g++) {
-      if (g + 1 < CNT) {
+      if (g + 1 < CNT) xg_load<NB, G0>(xq, g + 1, lane & 3, xb[(g + 1) & 1]);
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-          if ((G0 + g + 1) * 4 + k < NB) xb[(g + 1) & 1][k] = xq[((G0 + g + 1) * 4 + k) * 4 + j];
-      }
-#pragma unroll
-      for (int k = 0; k < 4; k++)
-        if ((G0 + g) * 4 + k < NB) pin(xb[g & 1][k]);
+      for (int k = 0; k < 4; k++) pin(xb[g & 1][k]);
+      float t[1][4];
+      wr_group_terms<NB, G0, CNT, 1>(RR, g, xb[g & 1], t);
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         const int b = (G0 + g) * 4 + k;
-        if (b < NB) terms[b * 64 + lane] = wr_term(R, g, k, xb[g & 1][k]);
+        if (b < NB) terms[b * 64 + lane] = t[0][k];
       }
     }
   }
@@ -328,77 +353,111 @@ __device__ __forceinline__ float run_sum(const float* run) {
   return s;
 }
 
-// ((0 + x_0) + x_1) + ... + x_{n-1} for x in shared memory (16-byte aligned): chunks of 16 values
-// with the next chunk read ahead (its index clamped, so every chunk's loads are issued
-// unconditionally), the last n % 16 values read before the loop and added under selects.
+// Serial sums over values in shared memory, in index order.  Each loop iteration reads two chunks
+// of 16 values (the second chunk's reads kept after the first's, so the first can be used while
+// the second is in flight) and adds them; nothing is carried across the loop's back edge, so the
+// compiler's waits stay exact.  The last partial chunk is added under selects.
+
+// ((0 + x_0) + x_1) + ... + x_{n-1}, x 16-byte aligned and readable up to the next multiple of 16
+// past n.
 __device__ __forceinline__ float seq_sum(const float* x, int n) {
   const float4* p = reinterpret_cast<const float4*>(x);
-  const int nc = n >> 4, t0 = nc << 4, last = n > 0 ? n - 1 : 0;
-  float tail[15];
-#pragma unroll
-  for (int i = 0; i < 15; i++) tail[i] = x[t0 + i < last ? t0 + i : last];
+  const int nc = n >> 4;
   float s = 0.0f;
-  if (nc > 0) {
+  int c = 0;
+  for (; c + 2 <= nc; c += 2) {
     float4 A[4], B[4];
 #pragma unroll
-    for (int u = 0; u < 4; u++) A[u] = p[u];
-    int c = 0;
-    for (;;) {
-      const int nb = c + 1 < nc ? c + 1 : c;
+    for (int u = 0; u < 4; u++) A[u] = p[c * 4 + u];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < 4; u++) B[u] = p[nb * 4 + u];
+    for (int u = 0; u < 4; u++) B[u] = p[c * 4 + 4 + u];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < 4; u++) pin(A[u]);
+    for (int u = 0; u < 4; u++) { s = s + A[u].x; s = s + A[u].y; s = s + A[u].z; s = s + A[u].w; }
 #pragma unroll
-      for (int u = 0; u < 4; u++) { s = s + A[u].x; s = s + A[u].y; s = s + A[u].z; s = s + A[u].w; }
-      if (++c == nc) break;
-      const int na = c + 1 < nc ? c + 1 : c;
-#pragma unroll
-      for (int u = 0; u < 4; u++) A[u] = p[na * 4 + u];
-#pragma unroll
-      for (int u = 0; u < 4; u++) pin(B[u]);
-#pragma unroll
-      for (int u = 0; u < 4; u++) { s = s + B[u].x; s = s + B[u].y; s = s + B[u].z; s = s + B[u].w; }
-      if (++c == nc) break;
-    }
+    for (int u = 0; u < 4; u++) { s = s + B[u].x; s = s + B[u].y; s = s + B[u].z; s = s + B[u].w; }
   }
+  float4 A[4], B[4];
+  const int ca = c < nc ? c : nc;
 #pragma unroll
-  for (int i = 0; i < 15; i++) {
-    const float t = s + tail[i];
-    s = t0 + i < n ? t : s;
+  for (int u = 0; u < 4; u++) A[u] = p[ca * 4 + u];
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < 4; u++) B[u] = p[nc * 4 + u];
+  __builtin_amdgcn_sched_barrier(0);
+  if (c < nc) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) { s = s + A[u].x; s = s + A[u].y; s = s + A[u].z; s = s + A[u].w; }
+  }
+  const int r = n - (nc << 4);
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    float t;
+    t = s + B[u].x; s = 4 * u + 0 < r ? t : s;
+    t = s + B[u].y; s = 4 * u + 1 < r ? t : s;
+    t = s + B[u].z; s = 4 * u + 2 < r ? t : s;
+    t = s + B[u].w; s = 4 * u + 3 < r ? t : s;
   }
   return s;
 }
 
-// acc = ((acc + p_0 * v_0) + p_1 * v_1) + ... over t in [0, n): p_t = pr[t], v_t = vrow[t * stride]
-// in shared memory, chunks of 8 positions with the next chunk read ahead (clamped index).
-__device__ __forceinline__ float seq_dot(float acc, const float* pr, const float* vrow, int stride, int n) {
-  const int nc = n >> 3;
-  if (nc > 0) {
-    float pa[8], va[8], pb[8], vb[8];
+// acc = ((acc + p_0 * v_0) + p_1 * v_1) + ... over t in [0, n), p and v contiguous in shared
+// memory, 16-byte aligned, readable up to the next multiple of 16 past n.
+__device__ __forceinline__ float seq_dot4(float acc, const float* p, const float* v, int n) {
+  const float4* p4 = reinterpret_cast<const float4*>(p);
+  const float4* v4 = reinterpret_cast<const float4*>(v);
+  const int nc = n >> 4;
+  int c = 0;
+  for (; c + 2 <= nc; c += 2) {
+    float4 pa[4], va[4], pb[4], vb[4];
 #pragma unroll
-    for (int u = 0; u < 8; u++) { pa[u] = pr[u]; va[u] = vrow[u * stride]; }
-    int c = 0;
-    for (;;) {
-      const int nb = (c + 1 < nc ? c + 1 : c) * 8;
+    for (int u = 0; u < 4; u++) { pa[u] = p4[c * 4 + u]; va[u] = v4[c * 4 + u]; }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < 8; u++) { pb[u] = pr[nb + u]; vb[u] = vrow[(nb + u) * stride]; }
+    for (int u = 0; u < 4; u++) { pb[u] = p4[c * 4 + 4 + u]; vb[u] = v4[c * 4 + 4 + u]; }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < 8; u++) { pin(pa[u]); pin(va[u]); }
+    for (int u = 0; u < 4; u++) {
+      acc = acc + pa[u].x * va[u].x;
+      acc = acc + pa[u].y * va[u].y;
+      acc = acc + pa[u].z * va[u].z;
+      acc = acc + pa[u].w * va[u].w;
+    }
 #pragma unroll
-      for (int u = 0; u < 8; u++) acc = acc + pa[u] * va[u];
-      if (++c == nc) break;
-      const int na = (c + 1 < nc ? c + 1 : c) * 8;
-#pragma unroll
-      for (int u = 0; u < 8; u++) { pa[u] = pr[na + u]; va[u] = vrow[(na + u) * stride]; }
-#pragma unroll
-      for (int u = 0; u < 8; u++) { pin(pb[u]); pin(vb[u]); }
-#pragma unroll
-      for (int u = 0; u < 8; u++) acc = acc + pb[u] * vb[u];
-      if (++c == nc) break;
+    for (int u = 0; u < 4; u++) {
+      acc = acc + pb[u].x * vb[u].x;
+      acc = acc + pb[u].y * vb[u].y;
+      acc = acc + pb[u].z * vb[u].z;
+      acc = acc + pb[u].w * vb[u].w;
     }
   }
-  for (int t = nc * 8; t < n; t++) acc = acc + pr[t] * vrow[t * stride];
+  float4 pa[4], va[4], pb[4], vb[4];
+  const int ca = c < nc ? c : nc;
+#pragma unroll
+  for (int u = 0; u < 4; u++) { pa[u] = p4[ca * 4 + u]; va[u] = v4[ca * 4 + u]; }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < 4; u++) { pb[u] = p4[nc * 4 + u]; vb[u] = v4[nc * 4 + u]; }
+  __builtin_amdgcn_sched_barrier(0);
+  if (c < nc) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      acc = acc + pa[u].x * va[u].x;
+      acc = acc + pa[u].y * va[u].y;
+      acc = acc + pa[u].z * va[u].z;
+      acc = acc + pa[u].w * va[u].w;
+    }
+  }
+  const int r = n - (nc << 4);
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    float t;
+    t = acc + pb[u].x * vb[u].x; acc = 4 * u + 0 < r ? t : acc;
+    t = acc + pb[u].y * vb[u].y; acc = 4 * u + 1 < r ? t : acc;
+    t = acc + pb[u].z * vb[u].z; acc = 4 * u + 2 < r ? t : acc;
+    t = acc + pb[u].w * vb[u].w; acc = 4 * u + 3 < r ? t : acc;
+  }
   return acc;
 }
 
@@ -449,8 +508,16 @@ struct PSmem {
   float* gu;      // 64: gate, up (GU)
   float* argv;    // 8
   int* argi;      // 8
-  float* kvt;     // kv_tile * 2 * kKVRow: staged past K and V rows (A)
+  float* kvt;     // kv_lds_bytes(kv_tile): staged past K rows and transposed V (A)
 };
+
+// Staged K/V of the attention role: K as rows [kv_tile][kKVRow], V transposed [64][kv_vstride]
+// (a lane reads its dimension of 4 positions at once; the stride is 4 mod 64 floats, so the 16
+// lanes of a 16-byte read hit distinct banks), both readable 16 positions past the tile.
+__host__ __device__ constexpr int kv_vstride(int kv_tile) { return ((kv_tile + 16 + 63) & ~63) + 4; }
+__host__ __device__ constexpr size_t kv_lds_bytes(int kv_tile) {
+  return ((size_t)(kv_tile + 16) * kKVRow + (size_t)kHD * kv_vstride(kv_tile)) * 4;
+}
 
 template <class S>
 constexpr size_t psmem_base_bytes() {
@@ -754,8 +821,9 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
   float* kv = m.qv + 64;
   float* vv = m.qv + 128;
   float* sc = m.terms;
-  float* kt = m.kvt;                               // [kv_tile][kKVRow] K
-  float* vt = m.kvt + (size_t)a.kv_tile * kKVRow;  // [kv_tile][kKVRow] V
+  const int vstride = kv_vstride(a.kv_tile);
+  float* kt = m.kvt;                                       // [kv_tile][kKVRow] K
+  float* vT = m.kvt + (size_t)(a.kv_tile + 16) * kKVRow;   // [64][vstride] V transposed
   const int nt = pos < a.kv_tile ? pos : a.kv_tile;   // staged past positions
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
@@ -794,7 +862,14 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
         const int idx = i0 + u * kPThreads + tid;
         if (idx < nt * 32) {
           const int which = idx >= nt * 16, rem = idx - which * nt * 16, t = rem >> 4, c4 = (rem & 15) * 4;
-          *reinterpret_cast<float4*>((which ? vt : kt) + t * kKVRow + c4) = v4[u];
+          if (which) {
+            vT[(c4 + 0) * vstride + t] = v4[u].x;
+            vT[(c4 + 1) * vstride + t] = v4[u].y;
+            vT[(c4 + 2) * vstride + t] = v4[u].z;
+            vT[(c4 + 3) * vstride + t] = v4[u].w;
+          } else {
+            *reinterpret_cast<float4*>(kt + t * kKVRow + c4) = v4[u];
+          }
         }
       }
     }
@@ -826,6 +901,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       x[i + 32] = x1 * rc + x0 * rsn;
     }
     __syncthreads();
+    if (h == 0) prof_mark(a, s, l * 16 + 11);
     if (writer && tid < 64) {
       st_coherent(a.kc + cbase + (size_t)pos * kHD + tid, kv[tid]);
       st_coherent(a.vc + cbase + (size_t)pos * kHD + tid, vv[tid]);
@@ -834,46 +910,74 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     const int T = pos + 1;
     const float scale = 1.0f / __builtin_sqrtf((float)kHD);
     float lmax = -1e30f;
-    for (int t = tid; t < T; t += kPThreads) {
-      float4 kk[kHD / 4];
-      if (t == pos) {
+    if (tid < T) {
+      float4 qr[kHD / 4];
 #pragma unroll
-        for (int i = 0; i < kHD / 4; i++) kk[i] = reinterpret_cast<const float4*>(kv)[i];
-      } else if (t < nt) {
+      for (int i = 0; i < kHD / 4; i++) qr[i] = reinterpret_cast<const float4*>(qv)[i];
 #pragma unroll
-        for (int i = 0; i < kHD / 4; i++) kk[i] = reinterpret_cast<const float4*>(kt + t * kKVRow)[i];
-      } else {
+      for (int i = 0; i < kHD / 4; i++) pin(qr[i]);
+      for (int t = tid; t < T; t += kPThreads) {
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+        if (t == pos || t < nt) {
+          const float4* kr = reinterpret_cast<const float4*>(t == pos ? kv : kt + t * kKVRow);
+          float4 ka[8], kb[8];
 #pragma unroll
-        for (int i = 0; i < kHD / 4; i++) kk[i] = gld4f(a.kc + cbase + (size_t)t * kHD + 4 * i);
+          for (int i = 0; i < 8; i++) ka[i] = kr[i];
+#pragma unroll
+          for (int i = 0; i < 8; i++) kb[i] = kr[8 + i];
+#pragma unroll
+          for (int i = 0; i < 8; i++) pin(ka[i]);
+#pragma unroll
+          for (int i = 0; i < 8; i++) {
+            s0 = s0 + qr[i].x * ka[i].x;
+            s1 = s1 + qr[i].y * ka[i].y;
+            s2 = s2 + qr[i].z * ka[i].z;
+            s3 = s3 + qr[i].w * ka[i].w;
+          }
+#pragma unroll
+          for (int i = 0; i < 8; i++) pin(kb[i]);
+#pragma unroll
+          for (int i = 0; i < 8; i++) {
+            s0 = s0 + qr[8 + i].x * kb[i].x;
+            s1 = s1 + qr[8 + i].y * kb[i].y;
+            s2 = s2 + qr[8 + i].z * kb[i].z;
+            s3 = s3 + qr[8 + i].w * kb[i].w;
+          }
+        } else {
+          float4 kk[kHD / 4];
+#pragma unroll
+          for (int i = 0; i < kHD / 4; i++) kk[i] = gld4f(a.kc + cbase + (size_t)t * kHD + 4 * i);
+#pragma unroll
+          for (int i = 0; i < kHD / 4; i++) {
+            s0 = s0 + qr[i].x * kk[i].x;
+            s1 = s1 + qr[i].y * kk[i].y;
+            s2 = s2 + qr[i].z * kk[i].z;
+            s3 = s3 + qr[i].w * kk[i].w;
+          }
+        }
+        const float sv = (s0 + s1 + s2 + s3) * scale;
+        sc[t] = sv;
+        lmax = __builtin_fmaxf(lmax, sv);
       }
-      float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
-#pragma unroll
-      for (int i = 0; i < kHD / 4; i++) {
-        const float4 q4 = reinterpret_cast<const float4*>(qv)[i];
-        s0 = s0 + q4.x * kk[i].x;
-        s1 = s1 + q4.y * kk[i].y;
-        s2 = s2 + q4.z * kk[i].z;
-        s3 = s3 + q4.w * kk[i].w;
-      }
-      const float sv = (s0 + s1 + s2 + s3) * scale;
-      sc[t] = sv;
-      lmax = __builtin_fmaxf(lmax, sv);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) lmax = __builtin_fmaxf(lmax, __shfl_xor(lmax, o));
     if (lane == 0) m.red[wave] = lmax;
     __syncthreads();
     const float mx = __builtin_fmaxf(__builtin_fmaxf(m.red[0], m.red[1]), __builtin_fmaxf(m.red[2], m.red[3]));
+    if (h == 0) prof_mark(a, s, l * 16 + 12);
     for (int t = tid; t < T; t += kPThreads) sc[t] = fast_exp(sc[t] - mx);
     __syncthreads();
     if (tid == 0) m.red[8] = seq_sum(sc, T);
     __syncthreads();
+    if (h == 0) prof_mark(a, s, l * 16 + 13);
     const float sum = m.red[8];
     for (int t = tid; t < T; t += kPThreads) sc[t] = sc[t] / sum;
     __syncthreads();
+    if (h == 0) prof_mark(a, s, l * 16 + 14);
     // out_i = sum over t in order of p_t * v_t[i] (kernels.c:372-375)
     if (tid < kHD) {
-      float accv = seq_dot(0.0f, sc, vt + tid, kKVRow, nt);
+      float accv = seq_dot4(0.0f, sc, vT + tid * vstride, nt);
       int t = nt;
       constexpr int TB = 32;     // positions past the staged tile: streamed, 32 loads ahead
       for (; t < pos; t += TB) {

@@ -555,15 +555,17 @@ void setup_persistent(q4hip* h) {
   const PersInstance* pi = find_pers_instance(h->D, h->F, h->H, h->KVH);
   if (!pi) return no("no kernel instance for this model shape");
   h->pers_fn = pi->fn;
-  if (h->ctx > 64 * pi->nbm) return no("ctx too large for the score buffer");
+  if (h->ctx + 16 > 64 * pi->nbm) return no("ctx too large for the score buffer");
   int lds_max = 0;
   if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, h->device) != hipSuccess)
     return no("cannot query shared memory size");
   const size_t base = pi->lds_base, budget = (size_t)lds_max > 4096 ? (size_t)lds_max - 4096 : 0;
   if (base > budget) return no("shared memory too small");
   // past K/V rows the attention role stages in shared memory; the rest are streamed
-  h->pers_kv_tile = (int)std::min<size_t>({(size_t)h->ctx, (size_t)192, (budget - base) / (2 * kKVRow * 4)});
-  h->pers_lds = base + (size_t)h->pers_kv_tile * 2 * kKVRow * 4;
+  int kv_tile = std::min(h->ctx, 192);
+  while (kv_tile > 0 && base + kv_lds_bytes(kv_tile) > budget) kv_tile--;
+  h->pers_kv_tile = kv_tile;
+  h->pers_lds = base + kv_lds_bytes(kv_tile);
   if (hipFuncSetAttribute(h->pers_fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)h->pers_lds) != hipSuccess) {
     (void)hipGetLastError();
     return no("cannot raise the kernel's shared memory limit");
