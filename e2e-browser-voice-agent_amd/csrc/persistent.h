@@ -50,6 +50,7 @@ struct PArgs {
   uint64_t* ll;   // exchange area, offsets in PShape
   int steps;
   int kv_tile;    // past positions of K and V the attention role stages in shared memory
+  int nap;        // sleep between polls of a wait, in units of 64 cycles
   unsigned long long* prof;   // optional: phase timestamps of step 0, [(NL + 1) * 16]
 };
 
@@ -131,11 +132,13 @@ __device__ __forceinline__ uint64_t ll_peek(const uint64_t* p) {
 
 // Wait for entries base[tid + 256k] (k < K, index < n) to carry epoch ep.  All K loads are in
 // flight together and only the entries still missing are polled again, so a hand-off costs one
-// memory round trip however many entries a thread receives.  Bounded: after kSpinLimit polls the
-// thread raises st->abort; a raised flag makes every waiter give up (`bad`).
+// memory round trip however many entries a thread receives; between polls the wave sleeps
+// `nap` x 64 cycles (polls of every waiting workgroup share the memory system with the weight
+// stream).  Bounded: after kSpinLimit polls the thread raises st->abort; a raised flag makes
+// every waiter give up (`bad`).
 template <int K>
 __device__ __forceinline__ void ll_recv(const uint64_t* base, int n, uint32_t ep, State* st, bool& bad,
-                                        uint32_t (&out)[K]) {
+                                        uint32_t (&out)[K], int nap) {
   uint64_t w[K];
 #pragma unroll
   for (int k = 0; k < K; k++) {
@@ -148,7 +151,7 @@ __device__ __forceinline__ void ll_recv(const uint64_t* base, int n, uint32_t ep
 #pragma unroll
     for (int k = 0; k < K; k++) ok = ok && (uint32_t)(w[k] >> 32) == ep;
     if (ok || bad) break;
-    __builtin_amdgcn_s_sleep(1);
+    for (int z = 0; z < nap; z++) __builtin_amdgcn_s_sleep(1);
 #pragma unroll
     for (int k = 0; k < K; k++) {
       const int i = (int)threadIdx.x + kPThreads * k;
@@ -553,6 +556,12 @@ __device__ __forceinline__ void prof_mark(const PArgs& a, int s, int slot) {
   if (a.prof && s == 0 && threadIdx.x == 0) a.prof[slot] = wall_clock64();
 }
 
+// Per-workgroup timestamps of step 0, after the (NL + 1) * 16 phase slots: [layer][workgroup][4].
+__device__ __forceinline__ void prof_wg(const PArgs& a, int s, int l, int k) {
+  if (a.prof && s == 0 && threadIdx.x == 0)
+    a.prof[(size_t)(a.NL + 1) * 16 + ((size_t)l * gridDim.x + blockIdx.x) * 4 + k] = wall_clock64();
+}
+
 // ---------------------------------------------------------------- RMSNorm + quantize
 
 template <class S>
@@ -564,9 +573,10 @@ __device__ __forceinline__ void stage_x(const PSmem& m, int i, float x) {
 
 // Wait for the D-vector at src (epoch ep) and stage it by lane runs, with its squares.
 template <class S>
-__device__ __forceinline__ void recv_x(const uint64_t* src, uint32_t ep, State* st, const PSmem& m, bool& bad) {
+__device__ __forceinline__ void recv_x(const uint64_t* src, uint32_t ep, State* st, const PSmem& m, bool& bad,
+                                       int nap) {
   uint32_t v[S::KD];
-  ll_recv<S::KD>(src, S::D, ep, st, bad, v);
+  ll_recv<S::KD>(src, S::D, ep, st, bad, v, nap);
 #pragma unroll
   for (int k = 0; k < S::KD; k++) {
     const int i = (int)threadIdx.x + kPThreads * k;
@@ -654,7 +664,7 @@ __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32
   WR<S::NGD> R0[1], R1[1], R2[1];
   if (rgi < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi, lane, R0[0]);
   if (rgi + stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + stride, lane, R1[0]);
-  recv_x<S>(LXH, epx, a.st, m, bad);
+  recv_x<S>(LXH, epx, a.st, m, bad, a.nap);
   if (__syncthreads_or(bad)) return -1;
   prof_mark(a, s, a.NL * 16 + 0);
   norm_quant<S>(m, nw, a.eps);
@@ -691,7 +701,7 @@ __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32
   prof_mark(a, s, a.NL * 16 + 1);
   {
     uint32_t v[2];
-    ll_recv<2>(LARG, 2 * G, eph, a.st, bad, v);
+    ll_recv<2>(LARG, 2 * G, eph, a.st, bad, v, a.nap);
     m.raw[tid] = v[0];
     if (tid + kPThreads < 2 * G) m.raw[tid + kPThreads] = v[1];
   }
@@ -737,13 +747,14 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
     wr_load<S::NGD, S::NB8D, G0o, Co>(L.o, wg, lane, ro);
     {
       uint32_t v[S::KD];
-      ll_recv<S::KD>(a.ll + S::oATT, S::D, phase_epoch(ep0, s, E, 4 * l + 0), a.st, bad, v);
+      ll_recv<S::KD>(a.ll + S::oATT, S::D, phase_epoch(ep0, s, E, 4 * l + 0), a.st, bad, v, a.nap);
 #pragma unroll
       for (int k = 0; k < S::KD; k++)
         if (tid + kPThreads * k < S::D) m.xl[tid + kPThreads * k] = __uint_as_float(v[k]);
     }
     if (__syncthreads_or(bad)) return false;
     if (wg == 0) prof_mark(a, s, l * 16 + 0);
+    prof_wg(a, s, l, 0);
     if (tid < S::NBD * 4) {
       float v[8];
 #pragma unroll
@@ -761,13 +772,14 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
         ll_put(a.ll + S::oX1 + row, __float_as_uint(x1), phase_epoch(ep0, s, E, 4 * l + 1));
       }
       if (wg == 0) prof_mark(a, s, l * 16 + 1);
+      prof_wg(a, s, l, 1);
     }
     // ---- down: x2 = x1 + W_down . act (act arrives quantized)
     WR<Cd> rd;
     wr_load<S::NGF, S::NB8F, G0d, Cd>(L.down, wg, lane, rd);
     {
       uint32_t v[S::KACT];
-      ll_recv<S::KACT>(a.ll + S::oACT, S::NACT, phase_epoch(ep0, s, E, 4 * l + 2), a.st, bad, v);
+      ll_recv<S::KACT>(a.ll + S::oACT, S::NACT, phase_epoch(ep0, s, E, 4 * l + 2), a.st, bad, v, a.nap);
 #pragma unroll
       for (int k = 0; k < S::KACT; k++)
         if (tid + kPThreads * k < S::NACT) m.raw[tid + kPThreads * k] = v[k];
@@ -785,6 +797,7 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
     }
     __syncthreads();
     if (wg == 0) prof_mark(a, s, l * 16 + 2);
+    prof_wg(a, s, l, 2);
     wr_terms<S::NBF, G0d, Cd>(rd, m.xq, lane, m.terms);
     __syncthreads();
     if constexpr (W == 0) {
@@ -795,6 +808,7 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
         ll_put(a.ll + (l == a.NL - 1 ? S::oXH : S::oX2) + row, __float_as_uint(x2), phase_epoch(ep0, s, E, 4 * l + 3));
       }
       if (wg == 0) prof_mark(a, s, l * 16 + 3);
+      prof_wg(a, s, l, 3);
     }
   }
   return true;
@@ -876,10 +890,11 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     if (l == 0) {
       for (int i = tid; i < S::D; i += kPThreads) stage_x<S>(m, i, embed_value(a.embd, S::D, tok, i));
     } else {
-      recv_x<S>(a.ll + S::oX2, phase_epoch(ep0, s, E, 4 * (l - 1) + 3), a.st, m, bad);
+      recv_x<S>(a.ll + S::oX2, phase_epoch(ep0, s, E, 4 * (l - 1) + 3), a.st, m, bad, a.nap);
     }
     if (__syncthreads_or(bad)) return false;
     if (h == 0) prof_mark(a, s, l * 16 + 4);
+    prof_wg(a, s, l, 0);
     norm_quant<S>(m, nw, a.eps);
     if (h == 0) prof_mark(a, s, l * 16 + 9);
     float acc[3] = {0.0f, 0.0f, 0.0f};
@@ -992,6 +1007,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       ll_put(a.ll + S::oATT + h * kHD + tid, __float_as_uint(accv), phase_epoch(ep0, s, E, 4 * l + 0));
     }
     if (h == 0) prof_mark(a, s, l * 16 + 6);
+    prof_wg(a, s, l, 1);
     __syncthreads();
   }
   return true;
@@ -1011,9 +1027,10 @@ __device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t
     wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.gu, rg, lane, w[0]);
     float nw[8];
     normw_load<S>(L.ffn_norm, nw);
-    recv_x<S>(a.ll + S::oX1, phase_epoch(ep0, s, E, 4 * l + 1), a.st, m, bad);
+    recv_x<S>(a.ll + S::oX1, phase_epoch(ep0, s, E, 4 * l + 1), a.st, m, bad, a.nap);
     if (__syncthreads_or(bad)) return false;
     if (u == 0) prof_mark(a, s, l * 16 + 7);
+    prof_wg(a, s, l, 0);
     norm_quant<S>(m, nw, a.eps);
     if (u == 0) prof_mark(a, s, l * 16 + 10);
     float acc[1] = {0.0f};
@@ -1040,6 +1057,7 @@ __device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t
       else if (tid == 8) ll_put(a.ll + S::oACT + u * 9 + 8, __float_as_uint(dd), ep);
     }
     if (u == 0) prof_mark(a, s, l * 16 + 8);
+    prof_wg(a, s, l, 1);
   }
   return true;
 }

@@ -426,6 +426,7 @@ struct q4hip {
   const char* pers_why = "";
   int pers_kv_tile = 0;
   size_t pers_lds = 0;
+  int pers_nap = 1;
   const void* pers_fn = nullptr;
   // profiling: events recorded around each launch of an eager step
   std::vector<std::pair<int, hipEvent_t>>* prof = nullptr;
@@ -594,6 +595,7 @@ void setup_persistent(q4hip* h) {
     return no("device allocation failed");
   }
   h->pers_grid = G;
+  if (const char* e = getenv("Q4HIP_POLL_SLEEP")) h->pers_nap = std::max(0, std::min(64, atoi(e)));
   h->pers_ok = true;
   h->pers_broken = false;
 }
@@ -621,6 +623,7 @@ hipError_t launch_persistent(q4hip* h, int steps, unsigned long long* prof = nul
   a.ll = h->ll;
   a.steps = steps;
   a.kv_tile = h->pers_kv_tile;
+  a.nap = h->pers_nap;
   a.prof = prof;
   void* args[] = {&a};
   return hipLaunchKernel(h->pers_fn, dim3(h->pers_grid), dim3(kPThreads), args, h->pers_lds, h->stream);
@@ -998,7 +1001,8 @@ int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n) {
   if (rc) return rc;
   HIPCHK(hipSetDevice(h->device));
   if (!use_persistent(h)) return fail(Q4HIP_EINVAL, "the persistent decode kernel is not in use");
-  const int cnt = (h->NL + 1) * 16;
+  const int G = h->pers_grid;
+  const int cnt = (h->NL + 1) * 16 + 4 * h->NL * G;
   unsigned long long* d = nullptr;
   HIPCHK(hipMalloc(&d, (size_t)cnt * 8));
   std::vector<unsigned long long> t(cnt, 0);
@@ -1015,12 +1019,13 @@ int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n) {
   if (e != hipSuccess) return fail(Q4HIP_EHIP, "persistent profile: %s", hipGetErrorString(e));
   if (aborted(h)) return fail(Q4HIP_EHIP, "persistent profile: a bounded wait timed out");
   const unsigned long long t0 = t[h->NL * 16 + 3];
-  for (int i = 0; i < cnt; i++) us[i] = t[i] ? (float)((double)(long long)(t[i] - t0) * 0.01) : -1.0f;
+  const int out = std::min(n, cnt);
+  for (int i = 0; i < out; i++) us[i] = t[i] ? (float)((double)(long long)(t[i] - t0) * 0.01) : -1.0f;
   // slots 16L+4/5 hold the shader clock counter at kernel start / step end: report its MHz
   const double wall_us = (double)(long long)(t[h->NL * 16 + 2] - t0) * 0.01;
   const double cycles = (double)(long long)(t[h->NL * 16 + 5] - t[h->NL * 16 + 4]);
   us[h->NL * 16 + 4] = wall_us > 0 ? (float)(cycles / wall_us) : -1.0f;
-  us[h->NL * 16 + 5] = -1.0f;
+  us[h->NL * 16 + 5] = (float)G;
   return Q4HIP_OK;
 }
 

@@ -122,9 +122,13 @@ int q4hip_profile(q4hip* h, int token, int pos, float* us, int n);
  * kernel's start, for (layers + 1) * 16 slots; -1 where nothing was recorded.  Per layer l, slot
  * 16l + k: 0 att received, 1 x after o sent, 2 act received, 3 x after down sent (first o/down
  * workgroup); 4 x received, 5 q/k/v done, 6 att sent (head 0); 7 x received, 8 act sent (first
- * gate/up workgroup).  Slots 16L + 0..2: head x received, (value, index) sent, token known;
- * slot 16L + 4: the shader clock over the step in MHz.  Measured with the device's constant
- * 100 MHz clock and its shader cycle counter. */
+ * gate/up workgroup); 9 A normalised, 10 gate/up normalised, 11..14 attention after RoPE, max,
+ * sum, normalisation (head 0).  Slots 16L + 0..2: head x received, (value, index) sent, token
+ * known; slot 16L + 4: the shader clock over the step in MHz; slot 16L + 5: the grid size G.
+ * Then, if n allows, 4 * L * G per-workgroup entries [layer][workgroup][k]: o/down workgroups
+ * k = 0 att received, 1 x after o sent, 2 act received, 3 x after down sent; attention
+ * workgroups 0 x received, 1 att sent; gate/up workgroups 0 x received, 1 act sent.  Measured
+ * with the device's constant 100 MHz clock and its shader cycle counter. */
 int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n);
 
 /* Time `steps` greedy decode steps (as q4hip_generate) with HIP events on the context's stream;
