@@ -6,9 +6,12 @@ a 64-token seeded prompt, then greedy decode.  One step = one decode token.  W w
 from position 64; then K timed steps run again from position 64 (same tokens, K/V overwritten),
 bracketed by device synchronisation.  value = K / elapsed seconds.
 
-Also reported: algorithmic HBM bytes per token / time per token (achieved GB/s), the roofline of
-the kernel that takes the most time per step (HIP events around each launch of one eager step,
-averaged over several steps), and the oracle timed on the host cores as the CPU baseline.
+The K timed steps are one launch of the persistent decode kernel (every workgroup resident, one
+role per workgroup, the whole greedy loop on the device); its duration comes from HIP events on the
+library's stream.  Also reported: algorithmic HBM bytes per token / time per token (achieved GB/s),
+the roofline of that kernel (the only kernel in the timed region), the HBM traffic per launch from
+the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, the same K steps on the multi-kernel
+hipGraph path for comparison, and the oracle timed on the host cores as the CPU baseline.
 
 Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 8]
 """
@@ -44,17 +47,19 @@ def algorithmic_bytes(shape, T):
             "total": layers + head + norms + bias + emb + logits + kv}
 
 
-def kernel_bytes(shape):
-    """Algorithmic bytes per launch of each per-step kernel class (weights + input + output)."""
-    D, F, V, QKV = shape.dim, shape.ffn, shape.vocab, shape.qkv
-    q4 = lambda n, k: n * k // 32 * 18  # noqa: E731
-    return {
-        "matvec qkv": q4(QKV, D) + D + QKV * 4 * 2,
-        "matvec o": q4(D, D) + D + D * 4 * 2,
-        "matvec gate+up": q4(2 * F, D) + D + 2 * F * 4,
-        "matvec down": q4(D, F) + F + D * 4 * 2,
-        "matvec output": q4(V, D) + D * 4 + V * 4,
-    }
+PROFILE = os.path.join(REPO, "profiles", "decode_persistent_qwen05b_prompt64_steps64.md")
+
+
+def profiled_traffic():
+    """Per-step HBM bytes (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration) from
+    the committed rocprofv3 summary of this workload, or None."""
+    try:
+        text = open(PROFILE).read()
+        blob = text[text.index("```json") + 7:]
+        data = json.loads(blob[:blob.index("```")])
+        return data["fetch_bytes_per_step"] + data["write_bytes_per_step"]
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def cpu_baseline(shape, tensors, ids, first_tokens):
@@ -125,43 +130,43 @@ def main():
     ms_per_step = dev_ms / args.steps
     value = args.steps / (dev_ms / 1e3)
 
+    mode = m.decode_mode_used()
+
     # algorithmic bytes over the timed steps (T = 65 .. 64+K)
     tot = sum(algorithmic_bytes(shape, PROMPT + i + 1)["total"] for i in range(args.steps))
     achieved_gbps = tot / (dev_ms / 1e3) / 1e9
 
-    # per-kernel time of real decode steps (eager, HIP events around each launch)
-    prof = {k: 0.0 for k in q4hip.PROF_NAMES}
-    nprof = 8
-    tok = first
-    for i in range(nprof):
-        p = m.profile(tok, PROMPT + i)
-        for k, v in p.items():
-            prof[k] += v / nprof
-        tok = toks[i]
-    launches = {"matvec qkv": shape.layers, "matvec o": shape.layers, "matvec gate+up": shape.layers,
-                "matvec down": shape.layers, "matvec output": 1}
-    kb = kernel_bytes(shape)
-    dom = max(launches, key=lambda k: prof[k])
-    avg_us = prof[dom] / launches[dom]
-    ach = kb[dom] / (avg_us * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
-                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None,
-                "bytes_per_launch": kb[dom], "avg_launch_us": round(avg_us, 3)}
+    # the timed region is one launch of the persistent kernel: its roofline is the whole region's
+    per_step_traffic = profiled_traffic()
+    roofline = {"bound": "hbm", "kernel": "k_decode_persistent" if mode == 2 else "decode graph",
+                "achieved": round(achieved_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved_gbps / HBM_PEAK_GBPS, 4),
+                "traffic": round(per_step_traffic * args.steps) if per_step_traffic and mode == 2 else None,
+                "bytes_per_launch": tot, "avg_launch_us": round(dev_ms * 1e3, 1), "steps_per_launch": args.steps,
+                "profile": os.path.relpath(PROFILE, REPO)}
+
+    # the same K steps on the multi-kernel path (hipGraph replay per step), for comparison
+    m.set_decode_mode(q4hip.DECODE_GRAPH)
+    m.generate(first, PROMPT, min(args.warmup, 4) or 1)
+    toks_g, graph_ms = m.time_generate(first, PROMPT, args.steps)
+    m.set_decode_mode(q4hip.DECODE_AUTO)
 
     out = {
         "metric": "decode tokens/s at batch 1 (Qwen2.5-0.5B Q4_0 shape); achieved HBM GB/s",
         "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "int8xq4->fp32", "data": "synthetic",
+        "scaling": "weak", "vs_baseline": None, "dtype": "i8xq4/f32", "data": "synthetic",
         "config": {"workload": "qwen2.5-0.5b-shape Q4_0 greedy decode, batch 1, 64-token prompt",
                    "global_batch": 1, "seq_len": PROMPT + args.steps, "prompt": PROMPT,
-                   "parallelism": "single-gpu"},
+                   "parallelism": "single-gpu",
+                   "decode_path": {2: "persistent", 1: "graph"}.get(mode, str(mode))},
         "achieved_gbps": round(achieved_gbps, 1),
         "hbm_roofline_frac": round(achieved_gbps / HBM_PEAK_GBPS, 4),
         "algorithmic_mb_per_token": round(tot / args.steps / 1e6, 2),
         "wall_ms_timed": round(wall_ms, 2),
         "prefill64_ms": round(prefill_ms, 2),
-        "profile_us_per_step": {k: round(v, 2) for k, v in prof.items()},
+        "graph_path_ms_per_step": round(graph_ms / args.steps, 4),
+        "graph_path_tokens_identical": toks_g == toks,
         "roofline": roofline,
         "model_gen_s": round(t_gen, 1),
     }
