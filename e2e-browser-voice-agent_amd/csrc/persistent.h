@@ -39,7 +39,8 @@ struct PArgs {
   float eps;
   const uint8_t* embd;
   const float* out_norm;
-  Q4Mat head;
+  Q4Mat head;       // Q4_0 layout, or the Q8_0 layout of k_repack_q8 when head_q8
+  int head_q8;
   const LayerView* layers;
   const float* rope;
   float* kc;
@@ -644,34 +645,23 @@ __device__ __forceinline__ void head_rows(const PArgs& a, const PSmem& m, const 
   }
 }
 
-// Final RMSNorm, logits of this workgroup's row groups, then every workgroup reduces every
-// workgroup's (value, index): the same token everywhere.  Returns the token, or -1 on abort.
+// Logits of this workgroup's Q4_0 row groups (three rotating register buffers: two row groups in
+// flight while one is computed); x is received and normalised after the first two are issued.
 template <class S>
-__device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int pos, bool& bad) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int G = gridDim.x, wg = blockIdx.x, E = 4 * a.NL + 1;
-  const int nRG = a.head.Np / 16;
-  const uint64_t* LXH = a.ll + S::oXH;
-  uint64_t* LARG = a.ll + S::oARG + (size_t)(s & 1) * 2 * G;
-  const uint32_t epx = phase_epoch(ep0, s, E, 4 * (a.NL - 1) + 3);
-  const uint32_t eph = phase_epoch(ep0, s, E, 4 * a.NL);
-
-  // the first two row groups' weights and the norm weights are in flight before waiting for x
+__device__ __forceinline__ bool head_scan_q4(const PArgs& a, const PSmem& m, uint32_t epx, int s, bool& bad,
+                                             float& bv, int& bi) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int G = gridDim.x, wg = blockIdx.x, nRG = a.head.Np / 16, stride = 4 * G;
   float nw[8];
   normw_load<S>(a.out_norm, nw);
-  const int stride = 4 * G;
   int rgi = wg + G * wave;
   WR<S::NGD> R0[1], R1[1], R2[1];
   if (rgi < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi, lane, R0[0]);
   if (rgi + stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + stride, lane, R1[0]);
-  recv_x<S>(LXH, epx, a.st, m, bad, a.nap);
-  if (__syncthreads_or(bad)) return -1;
+  recv_x<S>(a.ll + S::oXH, epx, a.st, m, bad, a.nap);
+  if (__syncthreads_or(bad)) return false;
   prof_mark(a, s, a.NL * 16 + 0);
   norm_quant<S>(m, nw, a.eps);
-
-  float bv = 0.0f;
-  int bi = -1;
-  // three rotating buffers: two row groups in flight while one is computed
   while (rgi < nRG) {
     if (rgi + 2 * stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + 2 * stride, lane, R2[0]);
     head_rows<S>(a, m, R0, rgi, lane, bv, bi);
@@ -685,6 +675,125 @@ __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32
     head_rows<S>(a, m, R2, rgi, lane, bv, bi);
     rgi += stride;
   }
+  return true;
+}
+
+// Q8_0 head rows (k_repack_q8 layout): lane (r, j) holds {A_j, B_j} of two blocks per uint4.
+template <int NG8, int NB8>
+struct WR8 {
+  uint4 w[NG8];
+  uint4 s[NB8];
+};
+
+template <int NG8, int NB8>
+__device__ __forceinline__ void wr8_load(const Q4Mat& W, int rg16, int lane, WR8<NG8, NB8>& R) {
+  const int row = rg16 * 16 + (lane >> 2), j = lane & 3;
+  const int tile = row >> 6, rr = row & 63;
+  const uint4* wq = W.qs + ((size_t)tile * NG8 * 64 + rr) * 4 + j;
+  const uint4* wd = W.d + (size_t)tile * NB8 * 64 + rr;
+#pragma unroll
+  for (int g = 0; g < NG8; g++) R.w[g] = gld(wq + (size_t)g * 256);
+#pragma unroll
+  for (int c = 0; c < NB8; c++) R.s[c] = gld(wd + (size_t)c * 64);
+}
+
+// dot_q8_q8 of one lane (kernels.c:157-170): per block p = A_j . xA_j + B_j . xB_j, then
+// acc = acc + f32(p) * (dw * dx), blocks in order; four blocks per stage, next four read ahead.
+template <int NB, int NG8, int NB8>
+__device__ __forceinline__ float wr8_dot(const WR8<NG8, NB8>& R, const uint4* xq, int j) {
+  constexpr int NQ = (NB + 3) / 4;
+  float acc = 0.0f;
+  uint4 xb[2][4];
+  xg_load<NB, 0>(xq, 0, j, xb[0]);
+#pragma unroll
+  for (int q = 0; q < NQ; q++) {
+    if (q + 1 < NQ) xg_load<NB, 0>(xq, q + 1, j, xb[(q + 1) & 1]);
+#pragma unroll
+    for (int k = 0; k < 4; k++) pin(xb[q & 1][k]);
+    int p[4];
+    float t[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int b = 4 * q + k;
+      if (b < NB) p[k] = sdot4((b & 1) ? R.w[b >> 1].z : R.w[b >> 1].x, xb[q & 1][k].x, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int b = 4 * q + k;
+      if (b < NB) p[k] = sdot4((b & 1) ? R.w[b >> 1].w : R.w[b >> 1].y, xb[q & 1][k].y, p[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int b = 4 * q + k;
+      if (b < NB) {
+        const uint4 sv = R.s[b >> 3];
+        const int hb = b & 7;
+        const uint32_t sw = (hb >> 1) == 0 ? sv.x : (hb >> 1) == 1 ? sv.y : (hb >> 1) == 2 ? sv.z : sv.w;
+        const float dw = half_bits_to_float((hb & 1) ? (sw >> 16) : (sw & 0xffffu));
+        t[k] = (float)p[k] * (dw * __uint_as_float(xb[q & 1][k].w));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (4 * q + k < NB) acc = acc + t[k];
+  }
+  return acc;
+}
+
+template <class S>
+__device__ __forceinline__ void head_rows8(const PArgs& a, const PSmem& m,
+                                           const WR8<(S::NBD + 1) / 2, S::NB8D>& R, int rg, int lane,
+                                           float& bv, int& bi) {
+  const float v = hsum4(wr8_dot<S::NBD, (S::NBD + 1) / 2, S::NB8D>(R, m.xq, lane & 3));
+  const int row = rg * 16 + (lane >> 2);
+  if ((lane & 3) == 0 && row < a.V) {
+    a.logits[row] = v;
+    arg_merge(bv, bi, v, row);
+  }
+}
+
+// Logits of this workgroup's Q8_0 row groups (two rotating register buffers).
+template <class S>
+__device__ __forceinline__ bool head_scan_q8(const PArgs& a, const PSmem& m, uint32_t epx, int s, bool& bad,
+                                             float& bv, int& bi) {
+  constexpr int NG8 = (S::NBD + 1) / 2;
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int G = gridDim.x, wg = blockIdx.x, nRG = a.head.Np / 16, stride = 4 * G;
+  float nw[8];
+  normw_load<S>(a.out_norm, nw);
+  int rgi = wg + G * wave;
+  WR8<NG8, S::NB8D> R0, R1;
+  if (rgi < nRG) wr8_load<NG8, S::NB8D>(a.head, rgi, lane, R0);
+  recv_x<S>(a.ll + S::oXH, epx, a.st, m, bad, a.nap);
+  if (__syncthreads_or(bad)) return false;
+  prof_mark(a, s, a.NL * 16 + 0);
+  norm_quant<S>(m, nw, a.eps);
+  while (rgi < nRG) {
+    if (rgi + stride < nRG) wr8_load<NG8, S::NB8D>(a.head, rgi + stride, lane, R1);
+    head_rows8<S>(a, m, R0, rgi, lane, bv, bi);
+    rgi += stride;
+    if (rgi >= nRG) break;
+    if (rgi + stride < nRG) wr8_load<NG8, S::NB8D>(a.head, rgi + stride, lane, R0);
+    head_rows8<S>(a, m, R1, rgi, lane, bv, bi);
+    rgi += stride;
+  }
+  return true;
+}
+
+// Final RMSNorm, logits of this workgroup's row groups, then every workgroup reduces every
+// workgroup's (value, index): the same token everywhere.  Returns the token, or -1 on abort.
+template <class S>
+__device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int pos, bool& bad) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int G = gridDim.x, wg = blockIdx.x, E = 4 * a.NL + 1;
+  uint64_t* LARG = a.ll + S::oARG + (size_t)(s & 1) * 2 * G;
+  const uint32_t epx = phase_epoch(ep0, s, E, 4 * (a.NL - 1) + 3);
+  const uint32_t eph = phase_epoch(ep0, s, E, 4 * a.NL);
+
+  float bv = 0.0f;
+  int bi = -1;
+  const bool ok = a.head_q8 ? head_scan_q8<S>(a, m, epx, s, bad, bv, bi) : head_scan_q4<S>(a, m, epx, s, bad, bv, bi);
+  if (!ok) return -1;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o);

@@ -44,6 +44,32 @@ __global__ void k_repack_q4(const uint8_t* __restrict__ raw, int64_t rows, int n
                ((uint32_t)q[9 + 2 * j] << 24);
 }
 
+// GGUF Q8_0 rows [rows][nb][34 B] -> the Q8 tiled layout: qs uint4 [N/64][ceil(nb/2)][64 rows][4 lanes j],
+// the uint4 of lane j and group g = {A_j, B_j} of block 2g then of block 2g+1, where A_j = int8 values
+// {2j, 2j+1, 8+2j, 9+2j} and B_j = {16+2j, 17+2j, 24+2j, 25+2j} (the elements of reference lane j,
+// kernels.c:157-170); d: the fp16 scales as for Q4_0.
+__global__ void k_repack_q8(const uint8_t* __restrict__ raw, int64_t rows, int nb, int ng, int nb8, int row0,
+                            uint32_t* __restrict__ qs, uint16_t* __restrict__ dsc) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * nb) return;
+  const int64_t r = idx / nb;
+  const int b = (int)(idx - r * nb);
+  const int64_t R = row0 + r;
+  const int64_t tile = R >> 6;
+  const int rr = (int)(R & 63);
+  const uint8_t* s = raw + idx * 34;
+  dsc[((tile * nb8 + (b >> 3)) * 64 + rr) * 8 + (b & 7)] = (uint16_t)(s[0] | (s[1] << 8));
+  const uint8_t* q = s + 2;
+  uint32_t* o = qs + (((tile * ng + (b >> 1)) * 64 + rr) * 4) * 4 + (b & 1) * 2;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    o[j * 4] = (uint32_t)q[2 * j] | ((uint32_t)q[2 * j + 1] << 8) | ((uint32_t)q[8 + 2 * j] << 16) |
+               ((uint32_t)q[9 + 2 * j] << 24);
+    o[j * 4 + 1] = (uint32_t)q[16 + 2 * j] | ((uint32_t)q[17 + 2 * j] << 8) | ((uint32_t)q[24 + 2 * j] << 16) |
+                   ((uint32_t)q[25 + 2 * j] << 24);
+  }
+}
+
 // Embedding rows (kernels.c:312-322): x[m][32b+j] = ((q&15)-8)*d, x[m][32b+16+j] = ((q>>4)-8)*d.
 // The table stays in GGUF layout [vocab][D/32][18 B]; one token reads 18*D/32 bytes.
 __global__ void k_embed(const uint8_t* __restrict__ emb, int D, const int* __restrict__ tokens,
@@ -117,6 +143,43 @@ __global__ __launch_bounds__(64) void k_matvec(Q4Mat W, const uint4* __restrict_
       }
     }
   }
+}
+
+// logits[n] = dot_q8_q8(W[n], x) for one token (kernels.c:157-170, 412): the Q8_0 output head.  One wave
+// = 16 rows, lane (r, j) owns accumulator j of row r; per block p = A_j . xA_j + B_j . xB_j, then
+// acc = acc + f32(p) * (dw * dx); activation blocks staged in shared memory (nb * 64 bytes).
+__global__ __launch_bounds__(64) void k_matvec_q8(Q4Mat W, const uint4* __restrict__ xq, float* __restrict__ y) {
+  extern __shared__ uint4 xs[];
+  const int lane = threadIdx.x, r = lane >> 2, j = lane & 3;
+  const int wv = blockIdx.x, tile = wv >> 2, rr = ((wv & 3) << 4) + r;
+  const int row = (tile << 6) + rr;
+  for (int i = lane; i < W.nb * 4; i += 64) xs[i] = xq[i];
+  __syncthreads();
+  const uint4* wq = W.qs + ((size_t)tile * W.ng * 64 + rr) * 4 + j;
+  const uint4* wd = W.d + (size_t)tile * W.nb8 * 64 + rr;
+  float acc = 0.0f;
+  uint4 sc = make_uint4(0, 0, 0, 0);
+  uint4 wn = wq[0];
+  for (int g = 0; g < W.ng; g++) {
+    const uint4 w = wn;
+    if (g + 1 < W.ng) wn = wq[(size_t)(g + 1) * 256];
+    if ((g & 3) == 0) sc = wd[(size_t)(g >> 2) * 64];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int b = 2 * g + h;
+      if (b < W.nb) {
+        const int hb = b & 7;
+        const uint32_t sw = (hb >> 1) == 0 ? sc.x : (hb >> 1) == 1 ? sc.y : (hb >> 1) == 2 ? sc.z : sc.w;
+        const float dw = half_bits_to_float((hb & 1) ? (sw >> 16) : (sw & 0xffffu));
+        const uint4 xv = xs[b * 4 + j];
+        int p = sdot4(h ? w.z : w.x, xv.x, 0);
+        p = sdot4(h ? w.w : w.y, xv.y, p);
+        acc = acc + (float)p * (dw * __uint_as_float(xv.w));
+      }
+    }
+  }
+  const float v = hsum4(acc);
+  if (j == 0 && row < W.N) y[row] = v;
 }
 
 // RoPE on the q and k heads, then K (roped) and V appended to the fp32 cache at pos
@@ -336,16 +399,19 @@ int fail(int code, const char* fmt, ...) {
 struct Mat {
   uint32_t* qs = nullptr;
   uint16_t* d = nullptr;
+  int fmt = Q4HIP_TYPE_Q4_0;   // Q4HIP_TYPE_Q4_0 or Q4HIP_TYPE_Q8_0 (the output head only)
   int N = 0, K = 0, nb = 0, ng = 0, nb8 = 0, Np = 0;
   int64_t loaded = 0;
   Q4Mat view() const { return Q4Mat{(const uint4*)qs, (const uint4*)d, N, nb, ng, nb8, Np}; }
 };
 
-int mat_alloc(Mat& m, int N, int K) {
+int mat_alloc(Mat& m, int N, int K, int fmt = Q4HIP_TYPE_Q4_0) {
+  m.fmt = fmt;
   m.N = N;
   m.K = K;
   m.nb = K / 32;
-  m.ng = (m.nb + 3) / 4;
+  m.ng = fmt == Q4HIP_TYPE_Q8_0 ? (m.nb + 1) / 2 : (m.nb + 3) / 4;
+  m.loaded = 0;
   m.nb8 = (m.nb + 7) / 8;
   m.Np = (N + kRowTile - 1) / kRowTile * kRowTile;
   const size_t qbytes = (size_t)m.Np * m.ng * 64, dbytes = (size_t)m.Np * m.nb8 * 16;
@@ -363,21 +429,26 @@ void mat_free(Mat& m) {
   m.d = nullptr;
 }
 
-// Upload GGUF Q4_0 rows [row0, row0+rows) of m through a device staging buffer.
+// Upload GGUF Q4_0 (or, for a Q8 matrix, Q8_0) rows [row0, row0+rows) of m through a device
+// staging buffer.
 int mat_upload(Mat& m, int row0, int64_t rows, const void* data, hipStream_t s) {
   if (row0 < 0 || rows <= 0 || row0 + rows > m.N) return fail(Q4HIP_EINVAL, "rows %d..%lld outside 0..%d", row0, (long long)(row0 + rows), m.N);
-  const size_t bytes = (size_t)rows * m.nb * 18;
+  const bool q8 = m.fmt == Q4HIP_TYPE_Q8_0;
+  const size_t bytes = (size_t)rows * m.nb * (q8 ? 34 : 18);
   uint8_t* raw = nullptr;
   HIPCHK(hipMalloc(&raw, bytes));
   hipError_t e = hipMemcpyAsync(raw, data, bytes, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) {
     const int64_t n = rows * m.nb;
-    k_repack_q4<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(raw, rows, m.nb, m.ng, m.nb8, row0, m.qs, m.d);
+    if (q8)
+      k_repack_q8<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(raw, rows, m.nb, m.ng, m.nb8, row0, m.qs, m.d);
+    else
+      k_repack_q4<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(raw, rows, m.nb, m.ng, m.nb8, row0, m.qs, m.d);
     e = hipGetLastError();
   }
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   (void)hipFree(raw);
-  if (e != hipSuccess) return fail(Q4HIP_EHIP, "Q4_0 upload: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return fail(Q4HIP_EHIP, "%s upload: %s", q8 ? "Q8_0" : "Q4_0", hipGetErrorString(e));
   m.loaded += rows;
   return Q4HIP_OK;
 }
@@ -467,6 +538,14 @@ void launch_matvec(hipStream_t s, const Mat& W, const uint4* xq, int xstride, in
     k_matvec<kMaxChunk, OP><<<grid, 64, 0, s>>>(W.view(), xq, xstride, M, y, ldy, bias);
 }
 
+// logits = head . x for one token: Q4_0 (the synthetic configurations) or Q8_0 (real files).
+void launch_head(hipStream_t s, const Mat& W, const uint4* xq, float* logits) {
+  if (W.fmt == Q4HIP_TYPE_Q8_0)
+    k_matvec_q8<<<(unsigned)(W.Np / 16), 64, (size_t)W.nb * 64, s>>>(W.view(), xq, logits);
+  else
+    launch_matvec<OP_STORE>(s, W, xq, 0, 1, logits, W.N, nullptr);
+}
+
 template <int MODE>
 void launch_quant(hipStream_t s, int rows, const float* in, int ld_in, int n, const float* w, float eps,
                   uint4* xq, int xstride, int m_first) {
@@ -511,7 +590,7 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
     prof_mark(h, Q4HIP_PROF_NORM_Q);
     launch_quant<QM_NORM>(s, 1, h->x, D, D, h->out_norm, h->eps, h->xq, h->xstride, M - 1);
     prof_mark(h, Q4HIP_PROF_OUT);
-    launch_matvec<OP_STORE>(s, h->head, h->xq, h->xstride, 1, h->logits, h->V, nullptr);
+    launch_head(s, h->head, h->xq, h->logits);
     prof_mark(h, Q4HIP_PROF_SAMPLE);
     k_argmax1<<<h->am_parts, 256, 0, s>>>(h->logits, h->V, h->am_v, h->am_i);
     k_argmax2<<<1, 256, 0, s>>>(h->am_v, h->am_i, h->am_parts, h->tokens, h->st, M);
@@ -613,6 +692,7 @@ hipError_t launch_persistent(q4hip* h, int steps, unsigned long long* prof = nul
   a.embd = h->embd;
   a.out_norm = h->out_norm;
   a.head = h->head.view();
+  a.head_q8 = h->head.fmt == Q4HIP_TYPE_Q8_0;
   a.layers = h->d_layers;
   a.rope = h->rope;
   a.kc = h->kc;
@@ -821,7 +901,17 @@ int q4hip_set_tensor(q4hip* h, int kind, int layer, int row0, int type, const vo
     return Q4HIP_OK;
   }
   if (kind == 8) {
-    if (type != Q4HIP_TYPE_Q4_0) return fail(Q4HIP_ETYPE, "kind 8: expected Q4_0");
+    if (type != Q4HIP_TYPE_Q4_0 && type != Q4HIP_TYPE_Q8_0) return fail(Q4HIP_ETYPE, "kind 8: expected Q4_0 or Q8_0");
+    if (type != h->head.fmt) {
+      if (h->head.loaded > 0) return fail(Q4HIP_ETYPE, "kind 8: rows of Q4_0 and Q8_0 mixed");
+      if (h->graph) {   // the captured pass holds the old head's addresses
+        (void)hipGraphExecDestroy(h->graph);
+        h->graph = nullptr;
+      }
+      mat_free(h->head);
+      const int rc = mat_alloc(h->head, h->V, h->D, type);
+      if (rc != Q4HIP_OK) return rc;
+    }
     return mat_upload(h->head, row0, rows, data, h->stream);
   }
   return fail(Q4HIP_EINVAL, "unknown tensor kind %d", kind);
@@ -1038,7 +1128,7 @@ int q4hip_time_head(q4hip* h, int iters, float* us_per_launch) {
   HIPCHK(hipEventCreate(&e0));
   HIPCHK(hipEventCreate(&e1));
   HIPCHK(hipEventRecord(e0, h->stream));
-  for (int i = 0; i < iters; i++) launch_matvec<OP_STORE>(h->stream, h->head, h->xq, h->xstride, 1, h->logits, h->V, nullptr);
+  for (int i = 0; i < iters; i++) launch_head(h->stream, h->head, h->xq, h->logits);
   HIPCHK(hipEventRecord(e1, h->stream));
   HIPCHK(hipGetLastError());
   HIPCHK(hipEventSynchronize(e1));

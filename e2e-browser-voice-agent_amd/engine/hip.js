@@ -93,7 +93,8 @@ async function createHIP(gguf, bytes, cfg, opts = {}) {
     });
   }
   const embd = check(T, "token_embd.weight", Q4, "Q4_0");
-  const out = check(T, "output.weight", Q4, "Q4_0");
+  // the head: Q4_0 in the synthetic configurations, Q8_0 in real Qwen2.5 files (cpu-worker.js:126)
+  const out = check(T, "output.weight", [TYPE.Q4_0, TYPE.Q8_0], "Q4_0 or Q8_0");
   const outNorm = check(T, "output_norm.weight", F32, "F32");
 
   const a = loadAddon();
@@ -126,7 +127,7 @@ async function createHIP(gguf, bytes, cfg, opts = {}) {
     name: "hip",
     ctx,
     device,
-    info: `HIP device ${device}, Q4_0 x int8 kernels, fp32 KV cache, hipGraph decode`,
+    info: `HIP device ${device}, Q4_0 x int8 kernels, ${out.type === TYPE.Q8_0 ? "Q8_0" : "Q4_0"} head, fp32 KV cache, persistent decode kernel`,
     // Run ids at positions pos.. and return the next token (engine/cpu-worker.js:169-182).
     async forward(ids, pos, { temperature = 0, seed = 1, wantLogits = false } = {}) {
       if (pos + ids.length >= ctx) throw new Error("context full");

@@ -77,6 +77,32 @@ def quantize_q4_0(x: np.ndarray) -> np.ndarray:
     return out
 
 
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    """GGUF Q8_0 of float32 values (length a multiple of 32) -> uint8 [nblocks, 34].
+
+    Block rule of the GGUF format: amax = max |x|, d = amax / 127, q = round(x / d) with halves
+    away from zero (computed as x * (1/d)), d stored as fp16 in the first two bytes.
+    """
+    b = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, 32)
+    amax = np.max(np.abs(b), axis=1)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, np.float32(1.0)), np.float32(0.0)).astype(np.float32)
+    v = b * inv[:, None]
+    q = (np.sign(v) * np.floor(np.abs(v) + np.float32(0.5))).astype(np.int32)
+    q = np.clip(q, -127, 127).astype(np.int8)
+    out = np.empty((b.shape[0], 34), dtype=np.uint8)
+    out[:, 0:2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = q.view(np.uint8)
+    return out
+
+
+def dequantize_q8_0(raw: np.ndarray) -> np.ndarray:
+    raw = raw.reshape(-1, 34)
+    d = raw[:, 0:2].copy().view(np.float16).reshape(-1).astype(np.float32)
+    return (raw[:, 2:].copy().view(np.int8).astype(np.float32) * d[:, None]).reshape(-1)
+
+
 def q4_0_blocks(raw: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """uint8 [nb,18] -> (nibble bytes [nb,16], fp32 scales [nb]), as copyBlocks does
     (engine/cpu-worker.js:97-104)."""
@@ -109,15 +135,19 @@ def _rng(seed: int, name: str) -> np.random.Generator:
     return np.random.Generator(np.random.PCG64([seed & 0xFFFFFFFF, zlib.crc32(name.encode())]))
 
 
-def _normal_q4(seed: int, name: str, count: int, std: float = 0.02, chunk: int = 1 << 24) -> np.ndarray:
+def _normal_q(seed: int, name: str, count: int, quant, std: float = 0.02, chunk: int = 1 << 24) -> np.ndarray:
     rng = _rng(seed, name)
     parts = []
     done = 0
     while done < count:
         n = min(chunk, count - done)
-        parts.append(quantize_q4_0(rng.standard_normal(n, dtype=np.float32) * np.float32(std)))
+        parts.append(quant(rng.standard_normal(n, dtype=np.float32) * np.float32(std)))
         done += n
     return np.concatenate(parts) if len(parts) > 1 else parts[0]
+
+
+def _normal_q4(seed: int, name: str, count: int, std: float = 0.02) -> np.ndarray:
+    return _normal_q(seed, name, count, quantize_q4_0, std)
 
 
 @dataclasses.dataclass
@@ -138,8 +168,9 @@ class Tensor:
         return self.data.tobytes()
 
 
-def make_model(shape: Shape, seed: int = 1234) -> dict:
-    """All tensors of a synthetic Qwen2 model, keyed by GGUF tensor name."""
+def make_model(shape: Shape, seed: int = 1234, head_type: int = GGML_Q4_0) -> dict:
+    """All tensors of a synthetic Qwen2 model, keyed by GGUF tensor name.  head_type GGML_Q8_0
+    gives the output head the type real Qwen2.5 GGUF files use."""
     D, F, KV = shape.dim, shape.ffn, shape.kv_heads * shape.head_dim
     t = {}
 
@@ -167,7 +198,11 @@ def make_model(shape: Shape, seed: int = 1234) -> dict:
         q4(p + "ffn_up.weight", D, F)
         q4(p + "ffn_down.weight", F, D)
     f32("output_norm.weight", D, 1.0)
-    q4("output.weight", D, shape.vocab)
+    if head_type == GGML_Q8_0:
+        t["output.weight"] = Tensor("output.weight", (D, shape.vocab), GGML_Q8_0,
+                                    _normal_q(seed, "output.weight", D * shape.vocab, quantize_q8_0))
+    else:
+        q4("output.weight", D, shape.vocab)
     return t
 
 

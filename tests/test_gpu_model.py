@@ -16,10 +16,10 @@ pytestmark = pytest.mark.gpu
 _cache = {}
 
 
-def _model(name, seed):
-    key = (name, seed)
+def _model(name, seed, head_type=synth.GGML_Q4_0):
+    key = (name, seed, head_type)
     if key not in _cache:
-        _cache[key] = synth.make_model(synth.SHAPES[name], seed)
+        _cache[key] = synth.make_model(synth.SHAPES[name], seed, head_type=head_type)
     return _cache[key]
 
 
@@ -30,10 +30,10 @@ def _bits(a):
 MODES = ["graph", "persistent"]
 
 
-def _pair(name, seed, ctx, mt=16, threads=8, mode="graph"):
+def _pair(name, seed, ctx, mt=16, threads=8, mode="graph", head_type=synth.GGML_Q4_0):
     import q4hip
     shape = synth.SHAPES[name]
-    t = _model(name, seed)
+    t = _model(name, seed, head_type)
     g = q4hip.Model(shape, ctx=ctx, mt=mt)
     g.load(t)
     g.set_decode_mode(q4hip.DECODE_PERSISTENT if mode == "persistent" else q4hip.DECODE_GRAPH)
@@ -178,6 +178,54 @@ def test_decode_rewrites_positions(mode):
         for step in range(3):                       # and single steps over the same positions
             nxt = g.forward([dev[step] if step else first], 30 + step)
             assert nxt == dev[step]
+    finally:
+        g.close()
+        o.close()
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("name,seed,n_prompt", [("tiny", 21, 9), ("small", 22, 33)])
+def test_q8_head_matches(name, seed, n_prompt, mode):
+    """A Q8_0 output head (the type of real Qwen2.5 files, dot_q8_q8 in kernels.c:157-170):
+    prefill and decode steps give the oracle's logits bit for bit."""
+    print(f"q8 head {name} seed {seed} mode {mode}", flush=True)
+    shape, g, o = _pair(name, seed, ctx=128, mode=mode, head_type=synth.GGML_Q8_0)
+    try:
+        ids = synth.prompt_ids(seed, n_prompt, shape.vocab)
+        ng, no = g.forward(ids, 0), o.forward(ids, 0)
+        assert ng == no
+        _compare_logits(g, o, "prefill")
+        pos = n_prompt
+        for step in range(6):
+            ng, no = g.forward([ng], pos), o.forward([no], pos)
+            assert ng == no, f"step {step}"
+            _compare_logits(g, o, f"step {step}")
+            pos += 1
+        assert g.decode_mode_used() == (2 if mode == "persistent" else 1)
+    finally:
+        g.close()
+        o.close()
+
+
+@pytest.mark.slow
+def test_q8_head_qwen05b():
+    """0.5B shape with a Q8_0 head: prompt, decode steps on both paths, device loop."""
+    import q4hip
+    print("q8 head qwen2.5-0.5b", flush=True)
+    shape, g, o = _pair("qwen2.5-0.5b", 2, ctx=256, threads=16, mode="persistent", head_type=synth.GGML_Q8_0)
+    try:
+        ids = synth.prompt_ids(2, 64, shape.vocab)
+        ng, no = g.forward(ids, 0), o.forward(ids, 0)
+        assert ng == no
+        _compare_logits(g, o, "prefill")
+        toks = [no]
+        for step in range(8):
+            no = o.forward([no], 64 + step)
+            toks.append(no)
+        for mode in (q4hip.DECODE_PERSISTENT, q4hip.DECODE_GRAPH):
+            g.set_decode_mode(mode)
+            assert [toks[0]] + g.generate(toks[0], 64, 8) == toks
+        _compare_logits(g, o, "last step")
     finally:
         g.close()
         o.close()

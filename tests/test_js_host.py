@@ -95,3 +95,23 @@ def test_generate_through_napi_matches_oracle(tiny_gguf, tmp_path):
     assert np.array_equal(lg.view(np.uint32), o.logits().view(np.uint32))
     assert out["ctxError"] == "context full"
     o.close()
+
+
+@pytest.mark.gpu
+def test_q8_head_through_napi_matches_oracle(tmp_path):
+    """A GGUF with a Q8_0 output head, the type real Qwen2.5 files carry, loads through createHIP
+    and decodes to the oracle's tokens and logits."""
+    import oracle
+    shape = synth.SHAPES["tiny"]
+    t = synth.make_model(shape, 78, head_type=synth.GGML_Q8_0)
+    p = str(tmp_path / "q8head.gguf")
+    synth.write_gguf(p, shape, t)
+    ids = synth.prompt_ids(78, 17, shape.vocab)
+    (tmp_path / "ids.json").write_text(json.dumps(ids))
+    out = node("generate", p, 128, tmp_path / "ids.json", 12, tmp_path / "lg.f32")
+    o = oracle.Model(shape, t, ctx=128)
+    ref = o.generate(ids, 12)
+    assert out["tokens"] == ref and out["device"] == ref
+    lg = np.frombuffer((tmp_path / "lg.f32").read_bytes(), np.float32)
+    assert np.array_equal(lg.view(np.uint32), o.logits().view(np.uint32))
+    o.close()

@@ -54,6 +54,18 @@ def simd_dot_q4_q8(wq, wd, xq, xd):
     return f32(f32(f32(acc[0] + acc[1]) + acc[2]) + acc[3])
 
 
+def simd_dot_q8_q8(wq, wd, xq, xd):
+    """dot_q8_q8 (kernels.c:157-170) with emulated instructions."""
+    acc = np.zeros(4, f32)
+    for b in range(wd.size):
+        w0, w1 = wq[32 * b:32 * b + 16], wq[32 * b + 16:32 * b + 32]
+        x0, x1 = xq[32 * b:32 * b + 16], xq[32 * b + 16:32 * b + 32]
+        p = (dot_i16x8(ext_lo(w0), ext_lo(x0)) + dot_i16x8(ext_hi(w0), ext_hi(x0))) + \
+            (dot_i16x8(ext_lo(w1), ext_lo(x1)) + dot_i16x8(ext_hi(w1), ext_hi(x1)))
+        acc = (acc + p.astype(f32) * (f32(wd[b]) * f32(xd[b]))).astype(f32)
+    return f32(f32(f32(acc[0] + acc[1]) + acc[2]) + acc[3])
+
+
 def simd_quantize_row(x):
     """quantize_row (kernels.c:90-114) with emulated f32x4 ops."""
     n = x.size
@@ -208,6 +220,39 @@ def test_dot_q8_equals_dot_q4_on_reencoded_head():
         a = oracle.dot_q4_q8(qs.reshape(-1), d, xq, xd)
         b = oracle.dot_q8_q8(q8.reshape(-1), d, xq, xd)
         assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32)
+
+
+def test_dot_q8_q8_matches_emulation_on_full_int8_range():
+    """The Q8_0 head of real files: int8 weights over the whole range, not only re-encoded nibbles."""
+    rng = np.random.default_rng(15)
+    for nb in (1, 5, 28):
+        wq = rng.integers(-128, 128, 32 * nb).astype(np.int8)
+        wd = (rng.standard_normal(nb) * 0.002).astype(np.float16).astype(f32)
+        x = rng.standard_normal(32 * nb).astype(f32)
+        xq, xd, _ = oracle.quantize_row(x)
+        got = f32(oracle.dot_q8_q8(wq, wd, xq, xd))
+        assert np.float32(got).view(np.uint32) == np.float32(simd_dot_q8_q8(wq, wd, xq, xd)).view(np.uint32)
+        exact = float(np.sum(wq.reshape(nb, 32).astype(np.float64) * wd[:, None] * xq.reshape(nb, 32) * xd[:, None]))
+        mag = float(np.sum(np.abs(wq.reshape(nb, 32).astype(np.float64) * wd[:, None] * xq.reshape(nb, 32) * xd[:, None])))
+        assert abs(float(got) - exact) <= (nb + 4) * 1.2e-7 * mag + 1e-30
+
+
+def test_synthetic_q8_0_quantizer():
+    """The GGUF Q8_0 block rule of the synthetic heads: amax -> +-127, error within half a step of
+    the fp32 scale (plus its fp16 rounding), zero blocks stay zero."""
+    rng = np.random.default_rng(16)
+    x = (rng.standard_normal(32 * 64) * 0.02).astype(f32)
+    x[:32] = 0.0
+    raw = synth.quantize_q8_0(x)
+    q = raw[:, 2:].copy().view(np.int8).astype(np.int64)
+    d16 = raw[:, 0:2].copy().view(np.float16).reshape(-1).astype(np.float64)
+    xb = x.reshape(-1, 32).astype(np.float64)
+    assert not q[0].any() and d16[0] == 0
+    idx = np.argmax(np.abs(xb[1:]), axis=1)
+    assert np.all(np.abs(q[1:][np.arange(63), idx]) == 127)
+    d32 = np.abs(xb).max(1) / 127.0
+    assert np.all(np.abs(xb - q * d32[:, None]) <= d32[:, None] * 0.5 * (1 + 1e-5))
+    assert np.allclose(synth.dequantize_q8_0(raw).reshape(-1, 32), q * d16[:, None])
 
 
 def test_matvec_vs_float64():
