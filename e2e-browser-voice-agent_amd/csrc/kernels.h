@@ -27,7 +27,8 @@
 namespace q4 {
 
 constexpr int kRowTile = 64;        // rows per weight tile
-constexpr int kMaxChunk = 16;       // tokens per prefill pass (the reference's MT default, engine/cpu.js:228)
+constexpr int kMaxChunk = 16;       // the reference's prompt chunk (MT, engine/cpu.js:228): the per-token matvec's tile
+constexpr int kMaxPass = 1024;      // tokens per device pass; results do not depend on the chunking
 
 // Device-resident step state: pos0 of the current pass, last sampled token.  Kernels read
 // pos0 from here so one captured graph replays every decode step.  The persistent decode kernel

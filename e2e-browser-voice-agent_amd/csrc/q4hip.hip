@@ -145,6 +145,87 @@ __global__ __launch_bounds__(64) void k_matvec(Q4Mat W, const uint4* __restrict_
   }
 }
 
+// y[m][n] (op)= W[n] . x[m] for a pass of M tokens (matmul_q4, kernels.c:200-273): the prefill
+// projections.  A workgroup computes 16 rows x 32 tokens: lane (r, j) of wave w owns reference lane
+// j of row r for tokens 8w..8w+7 of the tile, so every output is acc_j = acc_j + f32(p_j) * (dw * dx)
+// over the blocks in order and then ((acc_0 + acc_1) + acc_2) + acc_3 across the four lanes, exactly
+// as for one token.  A block's nibbles are split once and used for 8 tokens; the activation blocks
+// of the tile's tokens are staged in shared memory one group of 4 blocks at a time
+// (double-buffered).  16-row tiles keep narrow matrices (o, down: 896 rows) on many CUs.
+constexpr int kGemmRows = 16, kGemmTokens = 32;
+
+template <int OP>
+__global__ __launch_bounds__(256) void k_gemm_q4(Q4Mat W, const uint4* __restrict__ xq, int xstride, int M,
+                                                float* __restrict__ y, int ldy, const float* __restrict__ bias) {
+  __shared__ uint4 xs[2][kGemmTokens][16];   // [buffer][token][block of the group * 4 + j]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane >> 2, j = lane & 3;
+  const int m0 = blockIdx.y * kGemmTokens, row = blockIdx.x * kGemmRows + r;
+  const int tile = row >> 6, rr = row & 63;
+  const uint4* wq = W.qs + ((size_t)tile * W.ng * 64 + rr) * 4 + j;
+  const uint4* wd = W.d + (size_t)tile * W.nb8 * 64 + rr;
+  const bool active = m0 + wave * 8 < M;
+  float acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; t++) acc[t] = 0.0f;
+  auto stage = [&](int g, int buf) {
+    for (int i = tid; i < kGemmTokens * 16; i += 256) {
+      const int t = i >> 4, k = i & 15, m = m0 + t, b = g * 4 + (k >> 2);
+      xs[buf][t][k] = (m < M && b < W.nb) ? xq[(size_t)m * xstride * 4 + b * 4 + (k & 3)] : make_uint4(0, 0, 0, 0);
+    }
+  };
+  stage(0, 0);
+  uint4 w = wq[0], sc = wd[0];
+  __syncthreads();
+  for (int g = 0; g < W.ng; g++) {
+    const int buf = g & 1;
+    uint4 wn = w, scn = sc;
+    if (g + 1 < W.ng) {
+      stage(g + 1, buf ^ 1);
+      wn = wq[(size_t)(g + 1) * 256];
+      if (((g + 1) & 1) == 0) scn = wd[(size_t)((g + 1) >> 1) * 64];
+    }
+    if (active) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int b = g * 4 + k;
+        if (b < W.nb) {
+          const int hb = ((g & 1) << 2) + k;
+          const uint32_t sw = (hb >> 1) == 0 ? sc.x : (hb >> 1) == 1 ? sc.y : (hb >> 1) == 2 ? sc.z : sc.w;
+          const float dw = half_bits_to_float((hb & 1) ? (sw >> 16) : (sw & 0xffffu));
+          const uint32_t wv = k == 0 ? w.x : k == 1 ? w.y : k == 2 ? w.z : w.w;
+          const uint32_t lo = wv & 0x0F0F0F0Fu, hi = (wv >> 4) & 0x0F0F0F0Fu;
+          int p[8];
+#pragma unroll
+          for (int t = 0; t < 8; t++) {
+            const uint4 xv = xs[buf][wave * 8 + t][k * 4 + j];
+            p[t] = sdot4(lo, xv.x, (int)xv.z);
+            p[t] = sdot4(hi, xv.y, p[t]);
+          }
+#pragma unroll
+          for (int t = 0; t < 8; t++) {
+            const float dx = __uint_as_float(xs[buf][wave * 8 + t][k * 4 + j].w);
+            acc[t] = acc[t] + (float)p[t] * (dw * dx);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    w = wn;
+    sc = scn;
+  }
+#pragma unroll
+  for (int t = 0; t < 8; t++) {
+    const float v = hsum4(acc[t]);
+    const int m = m0 + wave * 8 + t;
+    if (j == 0 && m < M && row < W.N) {
+      float* o = y + (size_t)m * ldy + row;
+      if (OP == OP_ADD) *o = *o + v;
+      else if (OP == OP_BIAS) *o = v + bias[row];
+      else *o = v;
+    }
+  }
+}
+
 // logits[n] = dot_q8_q8(W[n], x) for one token (kernels.c:157-170, 412): the Q8_0 output head.  One wave
 // = 16 rows, lane (r, j) owns accumulator j of row r; per block p = A_j . xA_j + B_j . xB_j, then
 // acc = acc + f32(p) * (dw * dx); activation blocks staged in shared memory (nb * 64 bytes).
@@ -203,6 +284,119 @@ __global__ void k_rope_kv(float* __restrict__ qkv, int QKV, int D, int H, int KV
     kc[off + i + half] = y1;
     vc[off + i] = vs[i];
     vc[off + i + half] = vs[i + half];
+  }
+}
+
+// Attention for a block of 32 query tokens of one head in a multi-token pass (kernels.c:355-377), in
+// the reference's per-(token, head) order: scores as four lane sums over i = j mod 4 times the scale,
+// the maximum, e_t = fast_exp(s_t - max) summed in t order, then out_i = sum over t in order of
+// (e_t / sum) * v_t[i].  Thread (token mi = tid/8, sub = tid%8) scores positions t = sub (mod 8) and
+// accumulates output elements [sub*HD/8, (sub+1)*HD/8) of its token.  K and V come in chunks of 32
+// positions staged in shared memory and used by all 32 tokens; scores and e_t go to a global scratch
+// row per (token, head) of ctx floats.  Grid (H, ceil(M/32)).
+constexpr int kAttnTokens = 32, kAttnChunk = 32;
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ qkv, int QKV, int H, int KVH,
+                                                      const float* __restrict__ kc, const float* __restrict__ vc,
+                                                      int ctx, int layer, float* __restrict__ att, int D,
+                                                      const State* __restrict__ st, int M, float* __restrict__ scr) {
+  constexpr int RS = HD + 4, DPT = HD / 8;
+  __shared__ __attribute__((aligned(16))) float qs[kAttnTokens][RS];
+  __shared__ __attribute__((aligned(16))) float cs[kAttnChunk][RS];     // a K chunk, then V chunks
+  __shared__ float ps[kAttnTokens][kAttnChunk + 1];
+  __shared__ float rsum[kAttnTokens];
+  const int h = blockIdx.x, mb = blockIdx.y * kAttnTokens, tid = threadIdx.x, mi = tid >> 3, sub = tid & 7;
+  const int pos0 = st->pos0, kh = h / (H / KVH);
+  const int m = mb + mi;
+  const int Tm = m < M ? pos0 + m + 1 : 0;
+  const int Tb = pos0 + (mb + kAttnTokens < M ? mb + kAttnTokens : M);
+  const float* kb = kc + ((size_t)layer * KVH + kh) * ctx * HD;
+  const float* vb = vc + ((size_t)layer * KVH + kh) * ctx * HD;
+  float* srow = scr + ((size_t)(m < M ? m : 0) * H + h) * ctx;
+  for (int i = tid; i < kAttnTokens * HD; i += 256) {
+    const int r = i / HD, c = i - r * HD;
+    qs[r][c] = mb + r < M ? qkv[(size_t)(mb + r) * QKV + h * HD + c] : 0.0f;
+  }
+  const float scale = 1.0f / __builtin_sqrtf((float)HD);
+  float lmax = -1e30f;
+  for (int t0 = 0; t0 < Tb; t0 += kAttnChunk) {
+    __syncthreads();
+    for (int i = tid; i < kAttnChunk * HD / 4; i += 256) {
+      const int r = i / (HD / 4), c4 = i - r * (HD / 4), t = t0 + r;
+      const float4 v = t < Tb ? reinterpret_cast<const float4*>(kb + (size_t)t * HD)[c4] : make_float4(0, 0, 0, 0);
+      *reinterpret_cast<float4*>(&cs[r][4 * c4]) = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kAttnChunk / 8; k++) {
+      const int r = sub + 8 * k, t = t0 + r;
+      if (t < Tm) {
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+        for (int i4 = 0; i4 < HD / 4; i4++) {
+          const float4 q4 = *reinterpret_cast<const float4*>(&qs[mi][4 * i4]);
+          const float4 k4 = *reinterpret_cast<const float4*>(&cs[r][4 * i4]);
+          s0 = s0 + q4.x * k4.x;
+          s1 = s1 + q4.y * k4.y;
+          s2 = s2 + q4.z * k4.z;
+          s3 = s3 + q4.w * k4.w;
+        }
+        const float v = (s0 + s1 + s2 + s3) * scale;
+        srow[t] = v;
+        lmax = __builtin_fmaxf(lmax, v);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) lmax = __builtin_fmaxf(lmax, __shfl_xor(lmax, o));
+  __syncthreads();
+  for (int t = sub; t < Tm; t += 8) srow[t] = fast_exp(srow[t] - lmax);
+  __syncthreads();
+  if (sub == 0 && Tm > 0) {
+    float sum = 0.0f;
+    int t = 0;
+    for (; t + 8 <= Tm; t += 8) {
+      float e[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) e[u] = srow[t + u];
+#pragma unroll
+      for (int u = 0; u < 8; u++) sum = sum + e[u];
+    }
+    for (; t < Tm; t++) sum = sum + srow[t];
+    rsum[mi] = sum;
+  }
+  float acc[DPT];
+#pragma unroll
+  for (int d = 0; d < DPT; d++) acc[d] = 0.0f;
+  for (int t0 = 0; t0 < Tb; t0 += kAttnChunk) {
+    __syncthreads();
+    for (int i = tid; i < kAttnChunk * HD / 4; i += 256) {
+      const int r = i / (HD / 4), c4 = i - r * (HD / 4), t = t0 + r;
+      const float4 v = t < Tb ? reinterpret_cast<const float4*>(vb + (size_t)t * HD)[c4] : make_float4(0, 0, 0, 0);
+      *reinterpret_cast<float4*>(&cs[r][4 * c4]) = v;
+    }
+    for (int i = tid; i < kAttnTokens * kAttnChunk; i += 256) {
+      const int r = i / kAttnChunk, c = i - r * kAttnChunk, mm = mb + r, t = t0 + c;
+      ps[r][c] = (mm < M && t < pos0 + mm + 1) ? scr[((size_t)mm * H + h) * ctx + t] / rsum[r] : 0.0f;
+    }
+    __syncthreads();
+    const int n = Tm - t0 < kAttnChunk ? Tm - t0 : kAttnChunk;
+    for (int c = 0; c < n; c++) {
+      const float p = ps[mi][c];
+#pragma unroll
+      for (int d4 = 0; d4 < DPT / 4; d4++) {
+        const float4 v4 = *reinterpret_cast<const float4*>(&cs[c][sub * DPT + 4 * d4]);
+        acc[4 * d4 + 0] = acc[4 * d4 + 0] + p * v4.x;
+        acc[4 * d4 + 1] = acc[4 * d4 + 1] + p * v4.y;
+        acc[4 * d4 + 2] = acc[4 * d4 + 2] + p * v4.z;
+        acc[4 * d4 + 3] = acc[4 * d4 + 3] + p * v4.w;
+      }
+    }
+  }
+  if (m < M) {
+#pragma unroll
+    for (int d = 0; d < DPT; d++) att[(size_t)m * D + h * HD + sub * DPT + d] = acc[d];
   }
 }
 
@@ -477,6 +671,7 @@ struct q4hip {
   float *kc = nullptr, *vc = nullptr;
   uint4* xq = nullptr;
   int xstride = 0;   // activation blocks per token row of xq
+  float* ascr = nullptr;   // attention scratch of multi-token passes: [MT][H][ctx] scores, allocated on first use
   float* am_v = nullptr;
   int* am_i = nullptr;
   int am_parts = 0;
@@ -534,8 +729,11 @@ void launch_matvec(hipStream_t s, const Mat& W, const uint4* xq, int xstride, in
   const unsigned grid = (unsigned)(W.Np / 16);
   if (M == 1)
     k_matvec<1, OP><<<grid, 64, (size_t)W.nb * 64, s>>>(W.view(), xq, xstride, 1, y, ldy, bias);
-  else
+  else if (M <= 8)
     k_matvec<kMaxChunk, OP><<<grid, 64, 0, s>>>(W.view(), xq, xstride, M, y, ldy, bias);
+  else
+    k_gemm_q4<OP><<<dim3((unsigned)(W.Np / kGemmRows), (unsigned)((M + kGemmTokens - 1) / kGemmTokens)), 256, 0, s>>>(
+        W.view(), xq, xstride, M, y, ldy, bias);
 }
 
 // logits = head . x for one token: Q4_0 (the synthetic configurations) or Q8_0 (real files).
@@ -569,10 +767,17 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
     prof_mark(h, Q4HIP_PROF_ROPE);
     k_rope_kv<<<dim3(h->H + h->KVH, M), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, h->kc, h->vc, h->ctx, l, h->st);
     prof_mark(h, Q4HIP_PROF_ATTN);
-    if (HD == 64)
+    if (M > 1 && h->ascr) {
+      const dim3 ag(h->H, (M + kAttnTokens - 1) / kAttnTokens);
+      if (HD == 64)
+        k_attn_prefill<64><<<ag, 256, 0, s>>>(h->qkv, QKV, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, D, h->st, M, h->ascr);
+      else
+        k_attn_prefill<128><<<ag, 256, 0, s>>>(h->qkv, QKV, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, D, h->st, M, h->ascr);
+    } else if (HD == 64) {
       k_attn<64><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, h->st);
-    else
+    } else {
       k_attn<128><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, h->st);
+    }
     prof_mark(h, Q4HIP_PROF_QUANT);
     launch_quant<QM_PLAIN>(s, M, h->att, D, D, nullptr, 0.0f, h->xq, h->xstride, 0);
     prof_mark(h, Q4HIP_PROF_O);
@@ -780,7 +985,7 @@ void q4hip_destroy(q4hip* h) {
   }
   mat_free(h->head);
   void* bufs[] = {h->embd, h->out_norm, h->rope, h->x, h->qkv, h->att, h->gu, h->logits, h->kc, h->vc,
-                  h->xq, h->am_v, h->am_i, h->tokens, h->st, h->d_layers, h->ll};
+                  h->xq, h->am_v, h->am_i, h->tokens, h->st, h->d_layers, h->ll, h->ascr};
   for (void* p : bufs) if (p) (void)hipFree(p);
   if (h->pin_ids) (void)hipHostFree(h->pin_ids);
   if (h->pin_next) (void)hipHostFree(h->pin_next);
@@ -799,7 +1004,8 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
   const int HD = dim / heads;
   if (HD != 64 && HD != 128) return fail(Q4HIP_EINVAL, "head_dim %d unsupported (64 or 128)", HD);
   if ((size_t)(HD + ctx) * 4 > 65536) return fail(Q4HIP_EINVAL, "ctx %d too large for the attention kernel", ctx);
-  if (mt <= 0 || mt > kMaxChunk) mt = kMaxChunk;
+  if (mt <= 0 || mt > kMaxPass) mt = kMaxPass;
+  mt = std::min(mt, ctx);
   int ndev = 0;
   HIPCHK(hipGetDeviceCount(&ndev));
   if (device < 0 || device >= ndev) return fail(Q4HIP_EINVAL, "device %d of %d", device, ndev);
@@ -943,6 +1149,13 @@ int q4hip_forward(q4hip* h, const int* ids, int n, int pos, int* next) {
   HIPCHK(hipSetDevice(h->device));
   const bool pers = n == 1 && use_persistent(h);
   if (n == 1 && !pers) build_graph(h);
+  if (n > 1 && h->MT > 1 && !h->ascr) {
+    // scores of a multi-token pass; without it, passes use the per-(token, head) attention kernel
+    if (hipMalloc(&h->ascr, (size_t)h->MT * h->H * h->ctx * sizeof(float)) != hipSuccess) {
+      h->ascr = nullptr;
+      (void)hipGetLastError();
+    }
+  }
   memcpy(h->pin_ids, ids, (size_t)n * 4);
   HIPCHK(hipMemcpyAsync(h->tokens + pos, h->pin_ids, (size_t)n * 4, hipMemcpyHostToDevice, h->stream));
   for (int c = 0; c < n; c += h->MT) {

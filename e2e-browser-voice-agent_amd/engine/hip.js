@@ -98,7 +98,7 @@ async function createHIP(gguf, bytes, cfg, opts = {}) {
   const outNorm = check(T, "output_norm.weight", F32, "F32");
 
   const a = loadAddon();
-  const h = a.create(D, NL, F, H, KVH, vocab, ctx, opts.prefillChunk || 16, eps, device);
+  const h = a.create(D, NL, F, H, KVH, vocab, ctx, opts.prefillChunk || 0, eps, device);
   const rows = (t) => (t.type === TYPE.F32 ? t.count : t.count / t.shape[0]);
   const up = (kind, layer, row0, t) =>
     a.setTensor(h, kind, layer, row0, t.type, src.subarray(t.start, t.start + t.bytes), rows(t));

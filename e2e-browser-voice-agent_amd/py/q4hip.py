@@ -92,7 +92,7 @@ def device_count() -> int:
 class Model:
     """One loaded model on one GPU: the backend object's C side."""
 
-    def __init__(self, shape: synth.Shape, ctx: int = 2048, mt: int = 16, device: int = 0):
+    def __init__(self, shape: synth.Shape, ctx: int = 2048, mt: int = 0, device: int = 0):
         self.shape, self.ctx = shape, ctx
         h = ctypes.c_void_p()
         _check(lib().q4hip_create(ctypes.byref(h), shape.dim, shape.layers, shape.ffn, shape.heads,

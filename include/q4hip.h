@@ -54,8 +54,10 @@ const char* q4hip_last_error(void);
 int q4hip_device_count(int* count);
 
 /* Create a context: replaces set_config (engine/kernels.c:418-421) and the memory plan of
- * engine/cpu-worker.js:52-88.  Allocates weights, activations for chunks of up to `mt` tokens,
- * the fp32 KV cache for `ctx` positions and the token array on `device`.  head_dim = dim/heads. */
+ * engine/cpu-worker.js:52-88.  Allocates weights, activations for device passes of up to `mt`
+ * tokens (1..1024, capped at ctx; 0 or out of range = 1024: a prompt runs as passes of that many
+ * tokens, with results identical to the reference's 16-token chunks), the fp32 KV cache for `ctx`
+ * positions and the token array on `device`.  head_dim = dim/heads. */
 int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_heads, int vocab,
                  int ctx, int mt, float eps, int device);
 

@@ -30,14 +30,16 @@ def _bits(a):
 MODES = ["graph", "persistent"]
 
 
-def _pair(name, seed, ctx, mt=16, threads=8, mode="graph", head_type=synth.GGML_Q4_0):
+def _pair(name, seed, ctx, mt=0, threads=8, mode="graph", head_type=synth.GGML_Q4_0):
+    """The library with passes of `mt` tokens (0: its default, whole prompts up to 1024) and the
+    oracle with the reference's 16-token chunks."""
     import q4hip
     shape = synth.SHAPES[name]
     t = _model(name, seed, head_type)
     g = q4hip.Model(shape, ctx=ctx, mt=mt)
     g.load(t)
     g.set_decode_mode(q4hip.DECODE_PERSISTENT if mode == "persistent" else q4hip.DECODE_GRAPH)
-    o = oracle.Model(shape, t, ctx=ctx, mt=mt, threads=threads)
+    o = oracle.Model(shape, t, ctx=ctx, mt=16, threads=threads)
     return shape, g, o
 
 
@@ -100,7 +102,7 @@ def test_chunking_and_prefix_reuse():
     t = _model("tiny", 21)
     ids = synth.prompt_ids(21, 45, shape.vocab)
     outs = []
-    for mt in (16, 5, 1):
+    for mt in (0, 40, 16, 9, 5, 1):      # one pass, tiled GEMM passes, matvec passes, single tokens
         g = q4hip.Model(shape, ctx=128, mt=mt)
         g.load(t)
         n = g.forward(ids, 0)
