@@ -51,6 +51,7 @@ struct PArgs {
   uint64_t* ll;   // exchange area, offsets in PShape
   int steps;
   int kv_tile;    // past positions of K and V the attention role stages in shared memory
+  int ring;       // slots (kRingRows positions each) of the ring that streams the rest: 3 or 7
   int nap;        // sleep between polls of a wait, in units of 64 cycles
   unsigned long long* prof;   // optional: phase timestamps of step 0, [(NL + 1) * 16]
 };
@@ -503,8 +504,6 @@ struct PSmem {
   float* xl;      // 4 * STV floats: x by lane runs (value i at (i & 3) * STV + (i >> 2)), or plain
   float* sq;      // 4 * STV floats: x*x in the same layout
   uint4* xq;      // NBM * 4 activation block lanes
-  float* terms;   // 64 * NBM floats: per-block terms; attention scores
-  uint32_t* raw;  // RAW words: exchange entries
   uint4* tq;      // 4
   float* red;     // 16
   float* qv;      // 3 * 64: q, k, v of one head
@@ -512,7 +511,9 @@ struct PSmem {
   float* gu;      // 64: gate, up (GU)
   float* argv;    // 8
   int* argi;      // 8
-  float* kvt;     // kv_lds_bytes(kv_tile): staged past K rows and transposed V (A)
+  uint32_t* raw;  // RAW words: exchange entries
+  float* terms;   // last: 64 * NBM per-block terms (OD); for the attention role its ctx + kRingRows
+                  // scores, then its K/V ring and staged tile
 };
 
 // Staged K/V of the attention role: K as rows [kv_tile][kKVRow], V transposed [64][kv_vstride]
@@ -520,13 +521,33 @@ struct PSmem {
 // lanes of a 16-byte read hit distinct banks), both readable 16 positions past the tile.
 __host__ __device__ constexpr int kv_vstride(int kv_tile) { return ((kv_tile + 16 + 63) & ~63) + 4; }
 __host__ __device__ constexpr size_t kv_lds_bytes(int kv_tile) {
-  return ((size_t)(kv_tile + 16) * kKVRow + (size_t)kHD * kv_vstride(kv_tile)) * 4;
+  return kv_tile == 0 ? 0 : ((size_t)(kv_tile + 16) * kKVRow + (size_t)kHD * kv_vstride(kv_tile)) * 4;
+}
+
+// Past K/V rows beyond the staged tile are streamed from HBM through a ring of slots of kRingRows
+// rows in shared memory, filled by asynchronous global-to-LDS loads (each wave instruction moves
+// 4 rows = 1 KB; a slot is 12 instructions, 3 per wave).
+constexpr int kRingRows = 48;
+__host__ __device__ constexpr size_t ring_lds_bytes(int slots) { return (size_t)slots * kRingRows * kHD * 4; }
+
+template <class S>
+constexpr size_t psmem_terms_offset() {
+  return (size_t)8 * S::STV * 4 + (size_t)S::NBM * 64 + (size_t)(16 + 16 + 192 + 16 + 64 + 8 + 8) * 4 +
+         (size_t)S::RAW * 4;
 }
 
 template <class S>
 constexpr size_t psmem_base_bytes() {
-  return (size_t)8 * S::STV * 4 + (size_t)S::NBM * 64 + (size_t)64 * S::NBM * 4 + (size_t)S::RAW * 4 +
-         (size_t)(16 + 16 + 192 + 16 + 64 + 8 + 8) * 4;
+  return psmem_terms_offset<S>() + (size_t)64 * S::NBM * 4;
+}
+
+// What the attention role uses: its scores (ctx + kRingRows floats, 16-byte aligned), then the
+// ring and the staged tile.  They overlap the other roles' term buffer, not anything it shares.
+__host__ __device__ constexpr size_t attn_scores_floats(int ctx) { return (size_t)((ctx + kRingRows + 3) & ~3); }
+
+template <class S>
+constexpr size_t psmem_attn_bytes(int ctx, int ring_slots, int kv_tile) {
+  return psmem_terms_offset<S>() + attn_scores_floats(ctx) * 4 + ring_lds_bytes(ring_slots) + kv_lds_bytes(kv_tile);
 }
 
 template <class S>
@@ -536,8 +557,6 @@ __device__ __forceinline__ PSmem psmem(unsigned char* base) {
   m.xl = (float*)(base + off);      off += (size_t)4 * S::STV * 4;
   m.sq = (float*)(base + off);      off += (size_t)4 * S::STV * 4;
   m.xq = (uint4*)(base + off);      off += (size_t)S::NBM * 64;
-  m.terms = (float*)(base + off);   off += (size_t)64 * S::NBM * 4;
-  m.raw = (uint32_t*)(base + off);  off += (size_t)S::RAW * 4;
   m.tq = (uint4*)(base + off);      off += 16 * 4;
   m.red = (float*)(base + off);     off += 16 * 4;
   m.qv = (float*)(base + off);      off += 192 * 4;
@@ -545,7 +564,8 @@ __device__ __forceinline__ PSmem psmem(unsigned char* base) {
   m.gu = (float*)(base + off);      off += 64 * 4;
   m.argv = (float*)(base + off);    off += 8 * 4;
   m.argi = (int*)(base + off);      off += 8 * 4;
-  m.kvt = (float*)(base + off);
+  m.raw = (uint32_t*)(base + off);  off += (size_t)S::RAW * 4;
+  m.terms = (float*)(base + off);
   return m;
 }
 
@@ -838,6 +858,34 @@ __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32
   return next;
 }
 
+// ---------------------------------------------------------------- the K/V ring of the attention role
+
+typedef __attribute__((address_space(3))) void LdsVoid;
+typedef __attribute__((address_space(1))) const void GlobalVoid;
+
+// Issue the asynchronous loads of rows [t0, t0 + kRingRows) of one (layer, kv head) K or V block
+// into `slot`: wave w issues instructions w, w+4, w+8, each moving rows t0+4i .. t0+4i+3.  Rows at
+// or past ctx are read from row ctx-1 (their values are never used).
+__device__ __forceinline__ void ring_issue(const float* src, int t0, int ctx, float* slot) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+#pragma unroll
+  for (int k = 0; k < 3; k++) {
+    const int i = wave + 4 * k;
+    const int t = t0 + 4 * i + (lane >> 4);
+    const float* g = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + 4 * (lane & 15);
+    __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + i * 256), 16, 0, 0);
+  }
+}
+
+// Wait until this wave's loads of the oldest slot in flight have landed: R - 2 newer slots of 3
+// instructions each may still be outstanding (s_waitcnt vmcnt(3 (R - 2)), no other counter waited).
+__device__ __forceinline__ void ring_wait(int slots) {
+  if (slots == 7) __builtin_amdgcn_s_waitcnt(0x0F7F);        // vmcnt(15)
+  else __builtin_amdgcn_s_waitcnt(0x0F73);                    // vmcnt(3)
+}
+
+__device__ __forceinline__ void ring_drain() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
+
 // ---------------------------------------------------------------- roles (one step each)
 
 // o and down rows 16w..16w+15 for wave W's share of the blocks; the residual x of those rows lives
@@ -943,10 +991,11 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
   float* qv = m.qv;
   float* kv = m.qv + 64;
   float* vv = m.qv + 128;
-  float* sc = m.terms;
+  float* sc = m.terms;                                     // ctx + kRingRows scores
+  float* ring = sc + attn_scores_floats(a.ctx);            // a.ring slots of kRingRows rows
   const int vstride = kv_vstride(a.kv_tile);
-  float* kt = m.kvt;                                       // [kv_tile][kKVRow] K
-  float* vT = m.kvt + (size_t)(a.kv_tile + 16) * kKVRow;   // [64][vstride] V transposed
+  float* kt = ring + (size_t)a.ring * kRingRows * kHD;     // [kv_tile][kKVRow] K
+  float* vT = kt + (size_t)(a.kv_tile + 16) * kKVRow;      // [64][vstride] V transposed
   const int nt = pos < a.kv_tile ? pos : a.kv_tile;   // staged past positions
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
@@ -996,6 +1045,13 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
         }
       }
     }
+    // past positions [nt, pos) stream through the ring; its first K slots load during the wait
+    const int nstream = pos - nt, nck = (nstream + kRingRows - 1) / kRingRows;
+    const float* kgl = a.kc + cbase;
+    const float* vgl = a.vc + cbase;
+    if (nck > 0)
+      for (int c = 0; c < a.ring - 1; c++)
+        ring_issue(kgl, nt + (c < nck ? c : nck - 1) * kRingRows, a.ctx, ring + (size_t)c * kRingRows * kHD);
     if (l == 0) {
       for (int i = tid; i < S::D; i += kPThreads) stage_x<S>(m, i, embed_value(a.embd, S::D, tok, i));
     } else {
@@ -1034,6 +1090,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     const int T = pos + 1;
     const float scale = 1.0f / __builtin_sqrtf((float)kHD);
     float lmax = -1e30f;
+    // staged positions [0, nt) and the current one: one thread per position
     if (tid < T) {
       float4 qr[kHD / 4];
 #pragma unroll
@@ -1041,8 +1098,8 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
 #pragma unroll
       for (int i = 0; i < kHD / 4; i++) pin(qr[i]);
       for (int t = tid; t < T; t += kPThreads) {
-        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
         if (t == pos || t < nt) {
+          float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
           const float4* kr = reinterpret_cast<const float4*>(t == pos ? kv : kt + t * kKVRow);
           float4 ka[8], kb[8];
 #pragma unroll
@@ -1067,22 +1124,40 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
             s2 = s2 + qr[8 + i].z * kb[i].z;
             s3 = s3 + qr[8 + i].w * kb[i].w;
           }
-        } else {
-          float4 kk[kHD / 4];
-#pragma unroll
-          for (int i = 0; i < kHD / 4; i++) kk[i] = gld4f(a.kc + cbase + (size_t)t * kHD + 4 * i);
-#pragma unroll
-          for (int i = 0; i < kHD / 4; i++) {
-            s0 = s0 + qr[i].x * kk[i].x;
-            s1 = s1 + qr[i].y * kk[i].y;
-            s2 = s2 + qr[i].z * kk[i].z;
-            s3 = s3 + qr[i].w * kk[i].w;
-          }
+          const float sv = (s0 + s1 + s2 + s3) * scale;
+          sc[t] = sv;
+          lmax = __builtin_fmaxf(lmax, sv);
         }
-        const float sv = (s0 + s1 + s2 + s3) * scale;
-        sc[t] = sv;
-        lmax = __builtin_fmaxf(lmax, sv);
       }
+    }
+    // positions [nt, pos) streamed through the ring: 4 threads per position, thread j runs the
+    // reference's lane j (i = j mod 4), the lanes are combined in hsum order
+    if (nck > 0) {
+      const int R = a.ring;
+      const int pj = tid & 3, pr = tid >> 2;
+      for (int c = 0; c < nck; c++) {
+        ring_wait(R);
+        __syncthreads();
+        const float* slot = ring + (size_t)(c % R) * kRingRows * kHD;
+        float sj = 0.0f;
+        if (pr < kRingRows) {
+#pragma unroll
+          for (int i = 0; i < kHD / 4; i++) sj = sj + qv[4 * i + pj] * slot[pr * kHD + 4 * i + pj];
+        }
+        const float s1 = __shfl_down(sj, 1, 4), s2 = __shfl_down(sj, 2, 4), s3 = __shfl_down(sj, 3, 4);
+        const int t = nt + c * kRingRows + pr;
+        if (pj == 0 && pr < kRingRows && t < pos) {
+          const float sv = (((sj + s1) + s2) + s3) * scale;
+          sc[t] = sv;
+          lmax = __builtin_fmaxf(lmax, sv);
+        }
+        const int cn = c + R - 1;
+        ring_issue(kgl, nt + (cn < nck ? cn : nck - 1) * kRingRows, a.ctx, ring + (size_t)(cn % R) * kRingRows * kHD);
+      }
+      ring_drain();
+      __syncthreads();
+      // the ring is free: the first V slots stream in while exp, sum and division run
+      for (int c = 0; c < R - 1; c++) ring_issue(vgl, nt + (c < nck ? c : nck - 1) * kRingRows, a.ctx, ring + (size_t)c * kRingRows * kHD);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) lmax = __builtin_fmaxf(lmax, __shfl_xor(lmax, o));
@@ -1099,19 +1174,34 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     for (int t = tid; t < T; t += kPThreads) sc[t] = sc[t] / sum;
     __syncthreads();
     if (h == 0) prof_mark(a, s, l * 16 + 14);
-    // out_i = sum over t in order of p_t * v_t[i] (kernels.c:372-375)
-    if (tid < kHD) {
-      float accv = seq_dot4(0.0f, sc, vT + tid * vstride, nt);
-      int t = nt;
-      constexpr int TB = 32;     // positions past the staged tile: streamed, 32 loads ahead
-      for (; t < pos; t += TB) {
-        float vx[TB];
+    // out_i = sum over t in order of p_t * v_t[i] (kernels.c:372-375): staged positions, then the
+    // streamed ones slot by slot (wave 0 adds while every wave keeps the ring filled), then pos
+    float accv = 0.0f;
+    if (tid < kHD && nt > 0) accv = seq_dot4(0.0f, sc, vT + tid * vstride, nt);
+    if (nck > 0) {
+      const int R = a.ring;
+      for (int c = 0; c < nck; c++) {
+        ring_wait(R);
+        __syncthreads();
+        if (tid < kHD) {
+          const float* slot = ring + (size_t)(c % R) * kRingRows * kHD + tid;
+          const float* pc = sc + nt + c * kRingRows;
+          const int n = nstream - c * kRingRows;
+          float pv[kRingRows], vx[kRingRows];
 #pragma unroll
-        for (int u = 0; u < TB; u++) vx[u] = t + u < pos ? gldf(a.vc + cbase + (size_t)(t + u) * kHD + tid) : 0.0f;
+          for (int u = 0; u < kRingRows; u++) { pv[u] = pc[u]; vx[u] = slot[u * kHD]; }
 #pragma unroll
-        for (int u = 0; u < TB; u++)
-          if (t + u < pos) accv = accv + sc[t + u] * vx[u];
+          for (int u = 0; u < kRingRows; u++) {
+            const float t = accv + pv[u] * vx[u];
+            accv = u < n ? t : accv;
+          }
+        }
+        const int cn = c + R - 1;
+        ring_issue(vgl, nt + (cn < nck ? cn : nck - 1) * kRingRows, a.ctx, ring + (size_t)(cn % R) * kRingRows * kHD);
       }
+      ring_drain();
+    }
+    if (tid < kHD) {
       accv = accv + sc[pos] * vv[tid];
       ll_put(a.ll + S::oATT + h * kHD + tid, __float_as_uint(accv), phase_epoch(ep0, s, E, 4 * l + 0));
     }

@@ -692,6 +692,7 @@ struct q4hip {
   const char* pers_why = "";
   int pers_kv_tile = 0;
   size_t pers_lds = 0;
+  int pers_ring = 0;
   int pers_nap = 1;
   const void* pers_fn = nullptr;
   // profiling: events recorded around each launch of an eager step
@@ -809,6 +810,7 @@ struct PersInstance {
   int D, F, H, KVH;
   const void* fn;
   size_t lds_base;
+  size_t (*attn_bytes)(int ctx, int ring_slots, int kv_tile);
   size_t (*ll_entries)(int);
   int nRoles, nbm;
 };
@@ -816,7 +818,7 @@ struct PersInstance {
 template <class S>
 PersInstance pers_instance() {
   return PersInstance{S::D, S::F, S::H, S::KVH, (const void*)k_decode_persistent<S>, psmem_base_bytes<S>(),
-                      &S::ll_entries, S::nRoles, S::NBM};
+                      &psmem_attn_bytes<S>, &S::ll_entries, S::nRoles, S::NBM};
 }
 
 const PersInstance* find_pers_instance(int D, int F, int H, int KVH) {
@@ -840,17 +842,28 @@ void setup_persistent(q4hip* h) {
   const PersInstance* pi = find_pers_instance(h->D, h->F, h->H, h->KVH);
   if (!pi) return no("no kernel instance for this model shape");
   h->pers_fn = pi->fn;
-  if (h->ctx + 16 > 64 * pi->nbm) return no("ctx too large for the score buffer");
   int lds_max = 0;
   if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, h->device) != hipSuccess)
     return no("cannot query shared memory size");
   const size_t base = pi->lds_base, budget = (size_t)lds_max > 4096 ? (size_t)lds_max - 4096 : 0;
   if (base > budget) return no("shared memory too small");
   // past K/V rows the attention role stages in shared memory; the rest are streamed
-  int kv_tile = std::min(h->ctx, 192);
-  while (kv_tile > 0 && base + kv_lds_bytes(kv_tile) > budget) kv_tile--;
+  // past K/V rows: staged whole in shared memory when the context fits (no ring), else the first
+  // kv_tile positions staged and the rest streamed through a ring of 3 (ctx <= 1024) or 7 slots
+  int cap = 192;
+  if (const char* e = getenv("Q4HIP_KV_TILE")) cap = std::max(0, std::min(cap, atoi(e)));
+  int kv_tile = std::min(h->ctx, cap), ring = 0;
+  auto need = [&](int r, int t) { return std::max(base, pi->attn_bytes(h->ctx, r, t)); };
+  while (kv_tile > 0 && need(0, kv_tile) > budget) kv_tile--;
+  if (kv_tile < h->ctx) {
+    ring = h->ctx <= 1024 ? 3 : 7;
+    if (need(ring, 0) > budget) ring = 3;
+    if (need(ring, 0) > budget) return no("shared memory too small for the K/V ring");
+    while (kv_tile > 0 && need(ring, kv_tile) > budget) kv_tile--;
+  }
   h->pers_kv_tile = kv_tile;
-  h->pers_lds = base + kv_lds_bytes(kv_tile);
+  h->pers_ring = ring;
+  h->pers_lds = need(ring, kv_tile);
   if (hipFuncSetAttribute(h->pers_fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)h->pers_lds) != hipSuccess) {
     (void)hipGetLastError();
     return no("cannot raise the kernel's shared memory limit");
@@ -908,6 +921,7 @@ hipError_t launch_persistent(q4hip* h, int steps, unsigned long long* prof = nul
   a.ll = h->ll;
   a.steps = steps;
   a.kv_tile = h->pers_kv_tile;
+  a.ring = h->pers_ring;
   a.nap = h->pers_nap;
   a.prof = prof;
   void* args[] = {&a};
@@ -1178,6 +1192,19 @@ int q4hip_forward(q4hip* h, const int* ids, int n, int pos, int* next) {
   HIPCHK(hipStreamSynchronize(h->stream));
   if (pers && aborted(h)) return q4hip_forward(h, ids, n, pos, next);
   *next = h->pin_next[0];
+  return Q4HIP_OK;
+}
+
+int q4hip_set_kv(q4hip* h, int layer, int kv_head, int pos0, int n, const float* k, const float* v) {
+  if (!h || !k || !v) return fail(Q4HIP_EINVAL, "null argument");
+  if (layer < 0 || layer >= h->NL) return fail(Q4HIP_EINVAL, "layer %d of %d", layer, h->NL);
+  if (kv_head < 0 || kv_head >= h->KVH) return fail(Q4HIP_EINVAL, "kv head %d of %d", kv_head, h->KVH);
+  if (n <= 0 || pos0 < 0 || (int64_t)pos0 + n > h->ctx) return fail(Q4HIP_ECONTEXT, "positions %d..%lld outside 0..%d", pos0, (long long)pos0 + n, h->ctx);
+  HIPCHK(hipSetDevice(h->device));
+  HIPCHK(hipStreamSynchronize(h->stream));
+  const size_t off = (((size_t)layer * h->KVH + kv_head) * h->ctx + pos0) * h->HD, bytes = (size_t)n * h->HD * 4;
+  HIPCHK(hipMemcpy(h->kc + off, k, bytes, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(h->vc + off, v, bytes, hipMemcpyHostToDevice));
   return Q4HIP_OK;
 }
 

@@ -26,6 +26,7 @@ EXPORTS = [
     "q4hip_forward", "q4hip_read_logits", "q4hip_generate", "q4hip_profile", "q4hip_time_generate",
     "q4hip_time_head", "q4hip_destroy", "q4hip_mv_create", "q4hip_mv_run", "q4hip_mv_time",
     "q4hip_mv_destroy", "q4hip_set_decode_mode", "q4hip_decode_mode_used", "q4hip_profile_persistent",
+    "q4hip_set_kv",
 ]
 
 _lib = None
@@ -65,6 +66,7 @@ def lib() -> ctypes.CDLL:
         "q4hip_set_decode_mode": (I, [P, I]),
         "q4hip_decode_mode_used": (I, [P, ctypes.POINTER(I)]),
         "q4hip_profile_persistent": (I, [P, I, I, P, I]),
+        "q4hip_set_kv": (I, [P, I, I, I, I, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -137,6 +139,13 @@ class Model:
             rope = synth.rope_table(self.ctx, s.head_dim, s.rope_theta)
         rope = np.ascontiguousarray(rope, dtype=np.float32)
         _check(lib().q4hip_set_rope(self.h, _ptr(rope), rope.shape[0]))
+
+    def set_kv(self, layer: int, kv_head: int, pos0: int, k: np.ndarray, v: np.ndarray) -> None:
+        """Write K and V rows [n][head_dim] of one layer and kv head at positions pos0.."""
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        assert k.shape == v.shape and k.shape[1] == self.shape.head_dim
+        _check(lib().q4hip_set_kv(self.h, layer, kv_head, pos0, k.shape[0], _ptr(k), _ptr(v)))
 
     def set_decode_mode(self, mode: int) -> None:
         _check(lib().q4hip_set_decode_mode(self.h, mode))

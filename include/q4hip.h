@@ -133,6 +133,12 @@ int q4hip_profile(q4hip* h, int token, int pos, float* us, int n);
  * with the device's constant 100 MHz clock and its shader cycle counter. */
 int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n);
 
+/* Write the K and V rows of one layer and kv head at positions [pos0, pos0 + n): `k` and `v` are
+ * [n][head_dim] fp32.  The reference's cache is memory its host owns and hands to the kernels
+ * (kc/vc of set_buffers, engine/kernels.c:433-440); this fills ours directly, e.g. with a cache
+ * prefilled from stored activations.  Positions must lie below ctx. */
+int q4hip_set_kv(q4hip* h, int layer, int kv_head, int pos0, int n, const float* k, const float* v);
+
 /* Time `steps` greedy decode steps (as q4hip_generate) with HIP events on the context's stream;
  * *ms = elapsed device time of the whole loop. */
 int q4hip_time_generate(q4hip* h, int first, int pos, int steps, int* out, float* ms);

@@ -231,3 +231,47 @@ def test_q8_head_qwen05b():
     finally:
         g.close()
         o.close()
+
+
+def _fill_kv(shape, P, seed):
+    """fp16-rounded N(0, 1) K and V rows for positions [0, P) of every layer and kv head (the
+    long-context configuration's cache prefilled from stored activations)."""
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((shape.layers, shape.kv_heads, P, shape.head_dim)).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((shape.layers, shape.kv_heads, P, shape.head_dim)).astype(np.float16).astype(np.float32)
+    return k, v
+
+
+@pytest.mark.parametrize("mode,tile", [("graph", None), ("persistent", None), ("persistent", "16"), ("persistent", "0")])
+def test_prefilled_cache_long_context(mode, tile, monkeypatch):
+    """Decode over a cache of 500 positions written through q4hip_set_kv (the reference's host-owned
+    kc/vc, kernels.c:433-440): positions past the attention role's staged tile are streamed from
+    HBM; logits and tokens equal the oracle's with the same cache."""
+    import q4hip
+    if tile is not None:
+        monkeypatch.setenv("Q4HIP_KV_TILE", tile)
+    print(f"prefilled cache mode {mode} tile {tile}", flush=True)
+    P = 500
+    shape, g, o = _pair("small", 31, ctx=640, mode=mode)
+    try:
+        k, v = _fill_kv(shape, P, 31)
+        ok, ov = o.kv()
+        ok[:, :, :P] = k
+        ov[:, :, :P] = v
+        for l in range(shape.layers):
+            for kh in range(shape.kv_heads):
+                g.set_kv(l, kh, 0, k[l, kh], v[l, kh])
+        tok = 7
+        for step in range(6):
+            ng, no = g.forward([tok], P + step), o.forward([tok], P + step)
+            assert ng == no, f"step {step}"
+            _compare_logits(g, o, f"step {step}")
+            tok = ng
+        assert g.decode_mode_used() == (2 if mode == "persistent" else 1)
+        with pytest.raises(q4hip.Q4Error):
+            g.set_kv(0, shape.kv_heads, 0, k[0, 0], v[0, 0])
+        with pytest.raises(q4hip.Q4Error):
+            g.set_kv(0, 0, 640 - 3, k[0, 0, :8], v[0, 0, :8])
+    finally:
+        g.close()
+        o.close()
