@@ -13,7 +13,13 @@ the roofline of that kernel (the only kernel in the timed region), the HBM traff
 the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, the same K steps on the multi-kernel
 hipGraph path for comparison, and the oracle timed on the host cores as the CPU baseline.
 
-Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 8]
+Other workloads of the same model (one JSON line each, same keys):
+  --workload long-context  batch-1 decode after a 4096-position cache filled with seeded fp16-valued
+                           K/V (written through q4hip_set_kv), 256 greedy steps by default
+  --workload prefill       one 1024-token seeded prompt per step
+  --workload matvec        the isolated Q4_0 matvec at the model's five shapes, 1000 launches each
+
+Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 8] [--workload decode]
 """
 import argparse
 import json
@@ -94,17 +100,36 @@ def cpu_baseline(shape, tensors, ids, first_tokens):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=64)
-    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="decode", choices=["decode", "long-context", "prefill", "matvec"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the batch-1 decode loop runs on a single device "
               "(multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
         sys.exit(2)
+    defaults = {"decode": (64, 8), "long-context": (256, 8), "prefill": (3, 1), "matvec": (1000, 10)}[args.workload]
+    args.steps = defaults[0] if args.steps is None else args.steps
+    args.warmup = defaults[1] if args.warmup is None else args.warmup
     if args.steps < 1 or args.warmup < 0:
         sys.exit("--steps must be >= 1 and --warmup >= 0")
+    {"decode": bench_decode, "long-context": bench_long_context, "prefill": bench_prefill,
+     "matvec": bench_matvec}[args.workload](args)
 
+
+def _oracle():
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle
+    return oracle
+
+
+def _cores():
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return min(cores, 16)
+
+
+def bench_decode(args):
     import q4hip
     import synth
 
@@ -173,6 +198,181 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(shape, tensors, ids, [first] + toks)
     m.close()
+    print(json.dumps(out))
+
+
+LONG_CTX = 4096
+
+
+def fill_cache(shape, P, seed=SEED):
+    """fp16-valued N(0, 1) K and V rows for positions [0, P), seeded per (layer, kv head)."""
+    import numpy as np
+    for l in range(shape.layers):
+        for kh in range(shape.kv_heads):
+            rng = np.random.default_rng([seed, l, kh])
+            k = rng.standard_normal((P, shape.head_dim), dtype=np.float32).astype(np.float16).astype(np.float32)
+            v = rng.standard_normal((P, shape.head_dim), dtype=np.float32).astype(np.float16).astype(np.float32)
+            yield l, kh, k, v
+
+
+def bench_long_context(args):
+    """Decode after a 4096-position cache of seeded fp16-valued K/V (stored fp32, as the reference's
+    cache is): the attention role streams past rows through its LDS ring."""
+    import q4hip
+    import synth
+    shape = synth.SHAPES["qwen2.5-0.5b"]
+    P = LONG_CTX
+    ctx = P + max(args.steps, args.warmup) + 2
+    tensors = synth.make_model(shape, SEED)
+    m = q4hip.Model(shape, ctx=ctx)
+    m.load(tensors)
+    for l, kh, k, v in fill_cache(shape, P):
+        m.set_kv(l, kh, 0, k, v)
+    first = synth.prompt_ids(SEED + 1, 1, shape.vocab)[0]
+    if args.warmup:
+        m.generate(first, P, args.warmup)
+    toks, dev_ms = m.time_generate(first, P, args.steps)
+    mode = m.decode_mode_used()
+    # algorithmic bytes with the fp16 cache of the configuration: 12,288 B per position
+    base = algorithmic_bytes(shape, 0)["total"]
+    per_pos = shape.layers * shape.kv_heads * shape.head_dim * 2 * 2
+    tot = sum(base + per_pos * (P + i + 1) for i in range(args.steps))
+    gbps = tot / (dev_ms / 1e3) / 1e9
+    out = {
+        "metric": "decode tokens/s at batch 1 (Qwen2.5-0.5B Q4_0 shape) after a 4096-position fp16 KV cache; achieved HBM GB/s",
+        "value": round(args.steps / (dev_ms / 1e3), 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dev_ms / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "i8xq4/f32", "data": "synthetic",
+        "config": {"workload": "qwen2.5-0.5b-shape Q4_0 greedy decode, batch 1, 4096-position cache + 256 steps",
+                   "global_batch": 1, "seq_len": P + args.steps, "cache_positions": P,
+                   "kv_cache": "fp16 values stored fp32", "parallelism": "single-gpu",
+                   "decode_path": {2: "persistent", 1: "graph"}.get(mode, str(mode))},
+        "achieved_gbps": round(gbps, 1),
+        "roofline": {"bound": "hbm", "kernel": "k_decode_persistent" if mode == 2 else "decode graph",
+                     "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "bytes_per_launch": tot,
+                     "avg_launch_us": round(dev_ms * 1e3, 1), "steps_per_launch": args.steps},
+    }
+    if not args.no_cpu:
+        oracle = _oracle()
+        cores = _cores()
+        th = max(1, math.ceil(cores / 2))
+        o = oracle.Model(shape, tensors, ctx=ctx, threads=th)
+        ok, ov = o.kv()
+        for l, kh, k, v in fill_cache(shape, P):
+            ok[l, kh, :P] = k
+            ov[l, kh, :P] = v
+        times, got, tok = [], [], first
+        budget = time.time() + 20.0
+        while len(times) < 16 and time.time() < budget:
+            t0 = time.perf_counter()
+            tok = o.forward([tok], P + len(times))
+            times.append(time.perf_counter() - t0)
+            got.append(tok)
+        o.close()
+        med = statistics.median(times)
+        out["cpu_baseline"] = {"value": round(1.0 / med, 3), "unit": "tokens/s", "cores": th, "kind": "port",
+                               "sample": f"oracle decode of {len(times)} greedy tokens after the same 4096-position cache, "
+                                         f"median ms/token {med * 1e3:.1f}, {th} of {cores} threads",
+                               "tokens_agree_with_gpu": got == toks[:len(got)]}
+    m.close()
+    print(json.dumps(out))
+
+
+def bench_prefill(args):
+    """One 1024-token prompt per step, a whole-prompt device pass: tiled exact Q4 GEMMs and tiled
+    causal attention; the roofline is the integer dot throughput of the largest projection."""
+    import q4hip
+    import synth
+    shape = synth.SHAPES["qwen2.5-0.5b"]
+    n = 1024
+    tensors = synth.make_model(shape, SEED)
+    m = q4hip.Model(shape, ctx=n + 2)
+    m.load(tensors)
+    ids = synth.prompt_ids(SEED + 2, n, shape.vocab)
+    for _ in range(args.warmup):
+        m.forward(ids, 0)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        nxt = m.forward(ids, 0)
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    prof = m.profile_pass(ids, 0)
+    gu_us = prof["matvec gate+up"] / shape.layers
+    macs = n * 2 * shape.ffn * shape.dim
+    tops = 2 * macs / (gu_us * 1e-6) / 1e12
+    out = {
+        "metric": "prefill tokens/s of a 1024-token prompt (Qwen2.5-0.5B Q4_0 shape)",
+        "value": round(n / (ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "i8xq4/f32", "data": "synthetic",
+        "config": {"workload": "qwen2.5-0.5b-shape Q4_0 prefill of 1024 seeded ids", "global_batch": 1,
+                   "seq_len": n, "parallelism": "single-gpu"},
+        "profile_us_per_pass": {k: round(v, 1) for k, v in prof.items()},
+        "roofline": {"bound": "mfma", "kernel": "k_gemm_q4 gate+up (exact int8 x q4 dot on VALU)",
+                     "achieved": round(tops, 2), "peak": 5000.0, "unit": "TOP/s (int8)",
+                     "frac": round(tops / 5000.0, 5), "traffic": None, "ops_per_launch": 2 * macs,
+                     "avg_launch_us": round(gu_us, 1)},
+        "next_token": nxt,
+    }
+    if not args.no_cpu:
+        oracle = _oracle()
+        cores = _cores()
+        o = oracle.Model(shape, tensors, ctx=n + 2, threads=cores)
+        k = 256
+        t0 = time.perf_counter()
+        o.forward(ids[:k], 0)
+        sec = time.perf_counter() - t0
+        o.close()
+        out["cpu_baseline"] = {"value": round(k / sec, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+                               "sample": f"oracle prefill of the first {k} of the 1024 ids (16-token chunks), "
+                                         f"{sec:.1f} s, {cores} threads"}
+    m.close()
+    print(json.dumps(out))
+
+
+def bench_matvec(args):
+    """The isolated matvec (y = W x, x quantized per 32-block) at the model's five shapes, cache-hot."""
+    import numpy as np
+    import q4hip
+    import synth
+    shapes = [(896, 896), (128, 896), (4864, 896), (896, 4864), (151936, 896)]
+    rows = []
+    for N, K in shapes:
+        raw = synth.quantize_q4_0((np.random.default_rng([SEED, N, K]).standard_normal(N * K, dtype=np.float32)
+                                   * np.float32(0.02)))
+        mv = q4hip.Matvec(raw, N, K)
+        mv.time(args.warmup)
+        us = mv.time(args.steps)
+        mv.close()
+        nbytes = N * K // 32 * 18 + K * 4 + N * 4
+        rows.append({"shape": [N, K], "us": round(us, 2), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1)})
+    head = rows[-1]
+    out = {
+        "metric": "isolated Q4_0 matvec achieved GB/s (Qwen2.5-0.5B shapes, fp32 x quantized per 32-block)",
+        "value": head["gbps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(head["us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "i8xq4/f32", "data": "synthetic",
+        "config": {"workload": "Q4_0 matvec sweep, value = the 151936x896 head shape, cache-hot",
+                   "shapes": [r["shape"] for r in rows], "parallelism": "single-gpu"},
+        "per_shape": rows,
+        "roofline": {"bound": "hbm", "kernel": "k_matvec<1> 151936x896", "achieved": head["gbps"],
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "avg_launch_us": head["us"]},
+    }
+    if not args.no_cpu:
+        oracle = _oracle()
+        N, K = 151936, 896
+        raw = synth.quantize_q4_0((np.random.default_rng([SEED, N, K]).standard_normal(N * K, dtype=np.float32)
+                                   * np.float32(0.02)))
+        x = np.random.default_rng(SEED).standard_normal(K, dtype=np.float32)
+        t0 = time.perf_counter()
+        reps = 3
+        for _ in range(reps):
+            oracle.matvec_q4(raw, N, K, x)
+        sec = (time.perf_counter() - t0) / reps
+        out["cpu_baseline"] = {"value": round((N * K // 32 * 18) / sec / 1e9, 3), "unit": "GB/s", "cores": 1,
+                               "kind": "port", "sample": f"oracle matvec of the 151936x896 head, {reps} calls, "
+                                                          f"{sec * 1e3:.1f} ms each, one thread"}
     print(json.dumps(out))
 
 

@@ -1292,21 +1292,24 @@ int q4hip_time_generate(q4hip* h, int first, int pos, int steps, int* out, float
   return run_generate(h, first, pos, steps, out, ms);
 }
 
-int q4hip_profile(q4hip* h, int token, int pos, float* us, int n) {
-  if (!h || !us) return fail(Q4HIP_EINVAL, "null argument");
+int q4hip_profile_pass(q4hip* h, const int* ids, int ntok, int pos, float* us, int n) {
+  if (!h || !us || !ids) return fail(Q4HIP_EINVAL, "null argument");
   if (n < Q4HIP_PROF_N) return fail(Q4HIP_EINVAL, "need %d entries", Q4HIP_PROF_N);
-  if (pos < 0 || pos + 1 >= h->ctx) return fail(Q4HIP_ECONTEXT, "context full");
+  if (ntok <= 0 || ntok > h->MT) return fail(Q4HIP_EINVAL, "%d tokens: one pass takes 1..%d", ntok, h->MT);
+  if (pos < 0 || (int64_t)pos + ntok >= h->ctx) return fail(Q4HIP_ECONTEXT, "context full");
   int rc = check_ready(h);
   if (rc) return rc;
-  rc = check_ids(h, &token, 1);
+  rc = check_ids(h, ids, ntok);
   if (rc) return rc;
   HIPCHK(hipSetDevice(h->device));
-  h->pin_ids[0] = token;
-  HIPCHK(hipMemcpyAsync(h->tokens + pos, h->pin_ids, 4, hipMemcpyHostToDevice, h->stream));
+  if (ntok > 1 && !h->ascr) (void)hipMalloc(&h->ascr, (size_t)h->MT * h->H * h->ctx * sizeof(float));
+  (void)hipGetLastError();
+  memcpy(h->pin_ids, ids, (size_t)ntok * 4);
+  HIPCHK(hipMemcpyAsync(h->tokens + pos, h->pin_ids, (size_t)ntok * 4, hipMemcpyHostToDevice, h->stream));
   k_set_pos<<<1, 64, 0, h->stream>>>(h->st, pos);
   std::vector<std::pair<int, hipEvent_t>> marks;
   h->prof = &marks;
-  enqueue_pass(h, 1, true);
+  enqueue_pass(h, ntok, true);
   h->prof = nullptr;
   hipError_t e = hipStreamSynchronize(h->stream);
   for (int i = 0; i < Q4HIP_PROF_N; i++) us[i] = 0.0f;
@@ -1319,6 +1322,10 @@ int q4hip_profile(q4hip* h, int token, int pos, float* us, int n) {
   for (auto& p : marks) (void)hipEventDestroy(p.second);
   if (e != hipSuccess) return fail(Q4HIP_EHIP, "profile: %s", hipGetErrorString(e));
   return Q4HIP_OK;
+}
+
+int q4hip_profile(q4hip* h, int token, int pos, float* us, int n) {
+  return q4hip_profile_pass(h, &token, 1, pos, us, n);
 }
 
 int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n) {

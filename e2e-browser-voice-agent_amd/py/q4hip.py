@@ -26,7 +26,7 @@ EXPORTS = [
     "q4hip_forward", "q4hip_read_logits", "q4hip_generate", "q4hip_profile", "q4hip_time_generate",
     "q4hip_time_head", "q4hip_destroy", "q4hip_mv_create", "q4hip_mv_run", "q4hip_mv_time",
     "q4hip_mv_destroy", "q4hip_set_decode_mode", "q4hip_decode_mode_used", "q4hip_profile_persistent",
-    "q4hip_set_kv",
+    "q4hip_set_kv", "q4hip_profile_pass",
 ]
 
 _lib = None
@@ -67,6 +67,7 @@ def lib() -> ctypes.CDLL:
         "q4hip_decode_mode_used": (I, [P, ctypes.POINTER(I)]),
         "q4hip_profile_persistent": (I, [P, I, I, P, I]),
         "q4hip_set_kv": (I, [P, I, I, I, I, P, P]),
+        "q4hip_profile_pass": (I, [P, P, I, I, P, I]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -180,6 +181,13 @@ class Model:
     def profile(self, token: int, pos: int) -> dict:
         us = np.zeros(len(PROF_NAMES), dtype=np.float32)
         _check(lib().q4hip_profile(self.h, token, pos, _ptr(us), us.size))
+        return dict(zip(PROF_NAMES, us.tolist()))
+
+    def profile_pass(self, ids, pos: int) -> dict:
+        """Device microseconds per kernel class of one eager pass over `ids` at positions pos.."""
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        us = np.zeros(len(PROF_NAMES), dtype=np.float32)
+        _check(lib().q4hip_profile_pass(self.h, _ptr(a), a.size, pos, _ptr(us), us.size))
         return dict(zip(PROF_NAMES, us.tolist()))
 
     def profile_persistent(self, token: int, pos: int, per_workgroup: bool = False):

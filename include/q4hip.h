@@ -120,6 +120,9 @@ int q4hip_generate(q4hip* h, int first, int pos, int steps, int* out);
 #define Q4HIP_PROF_N 12
 int q4hip_profile(q4hip* h, int token, int pos, float* us, int n);
 
+/* The same per-class device times for one pass of `ntok` prompt tokens (1..mt) at positions pos.. */
+int q4hip_profile_pass(q4hip* h, const int* ids, int ntok, int pos, float* us, int n);
+
 /* Timeline of one persistent decode step (forward([token], pos)), in microseconds from the
  * kernel's start, for (layers + 1) * 16 slots; -1 where nothing was recorded.  Per layer l, slot
  * 16l + k: 0 att received, 1 x after o sent, 2 act received, 3 x after down sent (first o/down
