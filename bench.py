@@ -18,6 +18,8 @@ Other workloads of the same model (one JSON line each, same keys):
                            K/V (written through q4hip_set_kv), 256 greedy steps by default
   --workload prefill       one 1024-token seeded prompt per step
   --workload matvec        the isolated Q4_0 matvec at the model's five shapes, 1000 launches each
+  --workload batched       32 independent sequences on the Qwen2.5-1.5B shape, each after a
+                           1024-token seeded prompt, decoded together; one step = 32 tokens
 
 Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 8] [--workload decode]
 """
@@ -102,20 +104,21 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="decode", choices=["decode", "long-context", "prefill", "matvec"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "long-context", "prefill", "matvec", "batched"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the batch-1 decode loop runs on a single device "
-              "(multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
+              "(multi-GPU sharding is not run)", file=sys.stderr)
         sys.exit(2)
-    defaults = {"decode": (64, 8), "long-context": (256, 8), "prefill": (3, 1), "matvec": (1000, 10)}[args.workload]
+    defaults = {"decode": (64, 8), "long-context": (256, 8), "prefill": (3, 1), "matvec": (1000, 10),
+                "batched": (32, 4)}[args.workload]
     args.steps = defaults[0] if args.steps is None else args.steps
     args.warmup = defaults[1] if args.warmup is None else args.warmup
     if args.steps < 1 or args.warmup < 0:
         sys.exit("--steps must be >= 1 and --warmup >= 0")
     {"decode": bench_decode, "long-context": bench_long_context, "prefill": bench_prefill,
-     "matvec": bench_matvec}[args.workload](args)
+     "matvec": bench_matvec, "batched": bench_batched}[args.workload](args)
 
 
 def _oracle():
@@ -373,6 +376,79 @@ def bench_matvec(args):
         out["cpu_baseline"] = {"value": round((N * K // 32 * 18) / sec / 1e9, 3), "unit": "GB/s", "cores": 1,
                                "kind": "port", "sample": f"oracle matvec of the 151936x896 head, {reps} calls, "
                                                           f"{sec * 1e3:.1f} ms each, one thread"}
+    print(json.dumps(out))
+
+
+
+BATCH = 32
+BATCH_PROMPT = 1024
+
+
+def bench_batched(args):
+    """32 sequences of the Qwen2.5-1.5B shape (hidden 1536, 28 layers, 12/2 heads, head_dim 128,
+    FFN 8960), each prefilled with its own 1024-token seeded prompt, then decoded together: every
+    step runs the 32 tokens through one pass of B-token GEMMs, per-sequence attention over 1025+
+    positions and a per-row greedy argmax.  Warmup steps run from position 1024, then the timed
+    steps again from 1024 (same tokens, K/V overwritten)."""
+    import q4hip
+    import synth
+    shape = synth.SHAPES["qwen2.5-1.5b"]
+    ctx = BATCH_PROMPT + max(args.steps, args.warmup) + 2
+    t0 = time.time()
+    tensors = synth.make_model(shape, SEED)
+    m = q4hip.Model(shape, ctx=ctx)
+    m.load(tensors)
+    bt = q4hip.Batch(m, BATCH)
+    first = [bt.prefill(b, synth.prompt_ids(SEED + 10 + b, BATCH_PROMPT, shape.vocab), 0) for b in range(BATCH)]
+    print(f"batched: model and {BATCH} prefills ready in {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
+    pos = [BATCH_PROMPT] * BATCH
+    if args.warmup:
+        bt.generate(first, pos, args.warmup)
+    toks, dev_ms = bt.time_generate(first, pos, args.steps)
+    tok_s = BATCH * args.steps / (dev_ms / 1e3)
+    # algorithmic bytes per step: the weights once, then every sequence's K/V with the fp16 cache of
+    # the configuration (4 bytes per element pair would be the fp32 storage)
+    base = algorithmic_bytes(shape, 0)
+    weights = base["layers"] + base["head"] + base["other"] - shape.vocab * 4
+    per_pos = shape.layers * shape.kv_heads * shape.head_dim * 2 * 2
+    logits = BATCH * shape.vocab * 4
+    tot = sum(weights + logits + BATCH * per_pos * (BATCH_PROMPT + i + 1) for i in range(args.steps))
+    gbps = tot / (dev_ms / 1e3) / 1e9
+    out = {
+        "metric": "batched decode tokens/s, 32 sequences at 1024-token context (Qwen2.5-1.5B Q4_0 shape)",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dev_ms / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "i8xq4/f32", "data": "synthetic",
+        "config": {"workload": "qwen2.5-1.5b-shape Q4_0 greedy decode, 32 sequences, 1024-token prompts",
+                   "global_batch": BATCH, "seq_len": BATCH_PROMPT + args.steps,
+                   "kv_cache": "fp32 (the reference's cache type)", "parallelism": "single-gpu"},
+        "achieved_gbps": round(gbps, 1),
+        "roofline": {"bound": "hbm", "kernel": "batched decode step (all kernels)",
+                     "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "bytes_per_launch": tot,
+                     "avg_launch_us": round(dev_ms * 1e3, 1), "steps_per_launch": args.steps},
+        "first_tokens": toks[0, :4].tolist(),
+    }
+    bt.close()
+    m.close()
+    if not args.no_cpu:
+        oracle = _oracle()
+        cores = _cores()
+        th = max(1, math.ceil(cores / 2))
+        o = oracle.Model(shape, tensors, ctx=ctx, threads=th)
+        times, tok = [], first[0]
+        budget = time.time() + 20.0
+        while len(times) < 8 and time.time() < budget:
+            t1 = time.perf_counter()
+            tok = o.forward([tok], BATCH_PROMPT + len(times))
+            times.append(time.perf_counter() - t1)
+        o.close()
+        med = statistics.median(times)
+        out["cpu_baseline"] = {"value": round(1.0 / med, 3), "unit": "tokens/s", "cores": th, "kind": "port",
+                               "sample": f"oracle decode of {len(times)} tokens of one sequence at positions "
+                                         f"{BATCH_PROMPT}.. (the reference decodes one sequence at a time; cache "
+                                         f"contents not matched, timing only), median ms/token {med * 1e3:.1f}, "
+                                         f"{th} of {cores} threads"}
     print(json.dumps(out))
 
 

@@ -78,6 +78,10 @@ __device__ __forceinline__ int quant_one(float v) {
   return (int)r;
 }
 
+__device__ __forceinline__ uint32_t pack_f16x2(int a, int b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
+}
+
 // Stage a row of n floats into shared memory "by lane": value i goes to xl[(i & 3) * st + (i >> 2)],
 // st = n/4 + 1, so reference lane j (the values i = j mod 4, kernels.c:81-82) is one contiguous run
 // and the four runs start in different banks.
@@ -100,10 +104,14 @@ enum QuantMode { QM_PLAIN = 0, QM_NORM = 1, QM_SWIGLU = 2 };
 // block sit in consecutive threads of one wave and exchange the block maximum by shuffles.
 // QM_NORM reads x from the row staged by lane (xl, st); the others read xr (SwiGLU: gate at xr[i],
 // up at xr[n + i]).
+// `outh` (optional): the matrix-core operand of the multi-token GEMM, 32 bytes per (block, lane j):
+// the 8 int8 values as fp16 (exact) in the order of `out`'s two words, then -sum of the 8 values
+// as fp16 (exact, |sum| <= 1016), then 7 zero halves.
 template <int MODE>
 __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, const float* xl, int st, int n,
                                                  const float* __restrict__ w, float rs,
-                                                 uint4* __restrict__ out, int tid, int nthreads) {
+                                                 uint4* __restrict__ out, int tid, int nthreads,
+                                                 uint4* __restrict__ outh = nullptr) {
   const int nb = n >> 5;
   for (int t = tid; t < (nb << 2); t += nthreads) {
     const int b = t >> 2, j = t & 3;
@@ -135,6 +143,11 @@ __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, c
     for (int k = 0; k < 8; k++) { q[k] = quant_one(v[k] * id); sum += q[k]; }
     out[(b << 2) + j] = make_uint4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]),
                                    (uint32_t)(-8 * sum), __float_as_uint(dd));
+    if (outh) {
+      outh[2 * ((b << 2) + j)] = make_uint4(pack_f16x2(q[0], q[1]), pack_f16x2(q[2], q[3]), pack_f16x2(q[4], q[5]),
+                                            pack_f16x2(q[6], q[7]));
+      outh[2 * ((b << 2) + j) + 1] = make_uint4(pack_f16x2(-sum, 0), 0u, 0u, 0u);
+    }
   }
 }
 

@@ -94,7 +94,8 @@ __global__ void k_embed(const uint8_t* __restrict__ emb, int D, const int* __res
 template <int MODE>
 __global__ __launch_bounds__(256) void k_quant(const float* __restrict__ in, int ld_in, int n,
                                                const float* __restrict__ w, float eps,
-                                               uint4* __restrict__ xq, int xstride, int m_first) {
+                                               uint4* __restrict__ xq, int xstride, int m_first,
+                                               uint4* __restrict__ xh) {
   extern __shared__ float xl[];
   __shared__ float red[8];
   const float* xr = in + (size_t)(m_first + blockIdx.x) * ld_in;
@@ -105,7 +106,8 @@ __global__ __launch_bounds__(256) void k_quant(const float* __restrict__ in, int
     __syncthreads();
     rs = rms_scale_staged(xl, n, st, eps, red);
   }
-  quantize_row_dev<MODE>(xr, xl, st, n, w, rs, xq + (size_t)blockIdx.x * xstride * 4, threadIdx.x, blockDim.x);
+  quantize_row_dev<MODE>(xr, xl, st, n, w, rs, xq + (size_t)blockIdx.x * xstride * 4, threadIdx.x, blockDim.x,
+                         xh ? xh + (size_t)blockIdx.x * xstride * 8 : nullptr);
 }
 
 enum { OP_STORE = 0, OP_BIAS = 1, OP_ADD = 2 };   // put() of kernels.c:190-194
@@ -568,6 +570,663 @@ __global__ void k_set_pos(State* st, int pos0) {
   if (threadIdx.x == 0) st->pos0 = pos0;
 }
 
+// Q4_0 GEMM for few tokens: y[m][n] (+)= W[n] . x[m] for M <= a few dozen tokens, with every
+// output accumulated exactly as matmul_q4 does (four lane chains over the blocks in order, then
+// the lane sum; kernels.c:200-229), so results equal k_matvec's and k_gemm_q4's bit for bit.
+// Workgroup: 4 waves x 16 rows (lane = row r, chain j) = 64 rows, TPW tokens shared by the waves.
+// The activations of a chunk of 8 groups (32 blocks) are staged in shared memory, double
+// buffered (the next chunk's loads are in flight during the current chunk); each lane keeps its
+// weights 8 groups ahead in registers.  Grid (Np / 64, ceil(M / TPW)).
+constexpr int kRowsChunk = 8;   // groups per activation chunk = weight groups in flight
+
+template <int OP, int TPW>
+__global__ __launch_bounds__(256) void k_gemm_rows(Q4Mat W, const uint4* __restrict__ xq, int xstride, int M,
+                                                  float* __restrict__ y, int ldy, const float* __restrict__ bias) {
+  constexpr int PD = kRowsChunk, CU = PD * 16;              // uint4 per token per chunk
+  constexpr int NX = (TPW * CU + 255) / 256;                // staged uint4 per thread
+  __shared__ uint4 xs[2][TPW][CU];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane >> 2, j = lane & 3;
+  const int m0 = blockIdx.y * TPW;
+  const int row = blockIdx.x * 64 + wave * 16 + r;
+  const int tile = row >> 6, rr = row & 63;
+  const uint4* wq = W.qs + ((size_t)tile * W.ng * 64 + rr) * 4 + j;
+  const uint4* wd = W.d + (size_t)tile * W.nb8 * 64 + rr;
+  const int ng = W.ng, nb = W.nb, nb8 = W.nb8;
+  auto xload = [&](int c, uint4* v) {
+#pragma unroll
+    for (int u = 0; u < NX; u++) {
+      const int i = tid + 256 * u, t = i / CU, k = i - t * CU, m = m0 + t, blk = c * PD * 4 + (k >> 2);
+      v[u] = (i < TPW * CU && m < M && blk < nb) ? xq[(size_t)m * xstride * 4 + blk * 4 + (k & 3)] : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto xstore = [&](int buf, const uint4* v) {
+#pragma unroll
+    for (int u = 0; u < NX; u++) {
+      const int i = tid + 256 * u, t = i / CU, k = i - t * CU;
+      if (i < TPW * CU) xs[buf][t][k] = v[u];
+    }
+  };
+  uint4 wr[PD], sr[PD / 2];
+#pragma unroll
+  for (int u = 0; u < PD; u++) wr[u] = u < ng ? wq[(size_t)u * 256] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int u = 0; u < PD / 2; u++) sr[u] = u < nb8 ? wd[(size_t)u * 64] : make_uint4(0, 0, 0, 0);
+  {
+    uint4 v[NX];
+    xload(0, v);
+    xstore(0, v);
+  }
+  __syncthreads();
+  float acc[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; t++) acc[t] = 0.0f;
+  const int nchunks = (ng + PD - 1) / PD;
+  for (int c = 0; c < nchunks; c++) {
+    const int buf = c & 1;
+    uint4 xn[NX];
+    if (c + 1 < nchunks) xload(c + 1, xn);
+#pragma unroll
+    for (int u = 0; u < PD; u++) {
+      const int g = c * PD + u;
+      if (g < ng) {
+        const uint4 w = wr[u], sc = sr[u >> 1];
+        if (g + PD < ng) wr[u] = wq[(size_t)(g + PD) * 256];
+        if ((u & 1) && ((g + PD) >> 1) < nb8) sr[u >> 1] = wd[(size_t)((g + PD) >> 1) * 64];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const int b = g * 4 + k;
+          if (b < nb) {
+            const int hb = ((u & 1) << 2) + k;
+            const uint32_t sw = (hb >> 1) == 0 ? sc.x : (hb >> 1) == 1 ? sc.y : (hb >> 1) == 2 ? sc.z : sc.w;
+            const float dw = half_bits_to_float((hb & 1) ? (sw >> 16) : (sw & 0xffffu));
+            const uint32_t wv = k == 0 ? w.x : k == 1 ? w.y : k == 2 ? w.z : w.w;
+            const uint32_t lo = wv & 0x0F0F0F0Fu, hi = (wv >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int t = 0; t < TPW; t++) {
+              const uint4 xv = xs[buf][t][u * 16 + k * 4 + j];
+              int p = sdot4(lo, xv.x, (int)xv.z);
+              p = sdot4(hi, xv.y, p);
+              acc[t] = acc[t] + (float)p * (dw * __uint_as_float(xv.w));
+            }
+          }
+        }
+      }
+    }
+    if (c + 1 < nchunks) xstore(buf ^ 1, xn);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = 0; t < TPW; t++) {
+    const float v = hsum4(acc[t]);
+    const int m = m0 + t;
+    if (j == 0 && m < M && row < W.N) {
+      float* o = y + (size_t)m * ldy + row;
+      if (OP == OP_ADD) *o = *o + v;
+      else if (OP == OP_BIAS) *o = v + bias[row];
+      else *o = v;
+    }
+  }
+}
+
+// Q4_0 GEMM on the matrix cores, exact: y[m][n] (+)= W[n] . x[m] with the same lane chains as
+// matmul_q4 (kernels.c:200-229).  For lane chain j of block b, the integer dot p of its 8 nibbles
+// n_k (as n_k - 8) with the 8 int8 activations x_k is one v_mfma_f32_16x16x16_f16:
+//   k = 0..7: x_k * (1024 + n_k)      (the nibble as fp16 0x6400 | n, no arithmetic)
+//   k = 8:    (-sum_k x_k) * 1032     (folds the -8 offset and the 1024 back out)
+//   k = 9..15: 0
+// Every product and partial sum is an integer of magnitude below 2^21, so the fp32 result is
+// exactly p whatever the order of the sums inside the instruction.  The chain update
+// acc_j += p * (dw * dx) then runs on the vector ALUs in block order, as in the other kernels.
+// Operands: A = 16 tokens (32 bytes per token, block and chain from the quantizer), B = 16 weight
+// rows; D[token][row], lane = row + 16 * (token / 4).  A wave takes 16 rows x 32 tokens (two
+// products per chain and block share the weight operand) and all four chains; a workgroup four
+// waves of consecutive rows.  The activations and scales of one group (4 blocks) at a time are
+// staged in shared memory, double buffered; weights run 4 groups ahead in registers.
+// Grid (Np / 64, ceil(M / 32)).
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+constexpr int kMfmaTok = 32;     // tokens per wave and workgroup
+constexpr int kMfmaPD = 4;       // weight groups in flight
+
+template <int OP>
+__global__ __launch_bounds__(256) void k_gemm_mfma(Q4Mat W, const uint4* __restrict__ xq, const uint4* __restrict__ xh,
+                                                  int xstride, int M, float* __restrict__ y, int ldy,
+                                                  const float* __restrict__ bias) {
+  constexpr int TT = kMfmaTok / 16, PD = kMfmaPD;
+  __shared__ uint4 xs[2][4][4][kMfmaTok][2];          // [buf][block][j][token][half]: 16 fp16 operand values
+  __shared__ float dxs[2][4][kMfmaTok];               // [buf][block][token]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, kg = lane >> 4;
+  const int T0 = blockIdx.y * kMfmaTok;
+  const int R0 = blockIdx.x * 64 + wave * 16;
+  const int row = R0 + li, tile = row >> 6, rr = row & 63;
+  const uint4* wq = W.qs + ((size_t)tile * W.ng * 64 + rr) * 4;
+  const uint4* wd = W.d + (size_t)tile * W.nb8 * 64 + rr;
+  const int ng = W.ng, nb = W.nb, nb8 = W.nb8;
+  // weight operand of this lane: k = 4 kg .. 4 kg + 3.  kg 0: low nibbles, 1: high nibbles (as fp16
+  // 1024 + n via a byte permute with 0x64 bytes); kg 2: (1032, 0, 0, 0) -- the nibbles are masked to
+  // 8 and the permute takes only byte 0; kg 3: zeros.
+  const uint32_t sh = (kg & 1) << 2;
+  const uint32_t mask = kg < 2 ? 0x0F0F0F0Fu : 0u, orv = kg < 2 ? 0u : 0x08080808u;
+  const uint32_t sel0 = kg < 2 ? 0x04010400u : kg == 2 ? 0x0C0C0400u : 0x0C0C0C0Cu;
+  const uint32_t sel1 = kg < 2 ? 0x04030402u : 0x0C0C0C0Cu;
+  auto xload = [&](int g, uint4* v, float& d) {      // group g: 4 blocks x 4 chains x 32 tokens x 2 halves
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int i = tid + 256 * u, t = i >> 5, k = i & 31, m = T0 + t, blk = g * 4 + (k >> 3);
+      v[u] = (m < M && blk < nb) ? xh[((size_t)m * xstride * 4 + blk * 4 + ((k >> 1) & 3)) * 2 + (k & 1)]
+                                 : make_uint4(0, 0, 0, 0);
+    }
+    const int t = tid >> 2, kb = tid & 3, m = T0 + t, blk = g * 4 + kb;
+    d = (tid < 4 * kMfmaTok && m < M && blk < nb) ? __uint_as_float(xq[(size_t)m * xstride * 4 + blk * 4].w) : 0.0f;
+  };
+  auto xstore = [&](int buf, const uint4* v, float d) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int i = tid + 256 * u, t = i >> 5, k = i & 31;
+      xs[buf][k >> 3][(k >> 1) & 3][t][k & 1] = v[u];
+    }
+    if (tid < 4 * kMfmaTok) dxs[buf][tid & 3][tid >> 2] = d;
+  };
+  uint4 wr[PD][4], sr[PD / 2];
+#pragma unroll
+  for (int u = 0; u < PD; u++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) wr[u][j] = u < ng ? wq[(size_t)u * 256 + j] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int u = 0; u < PD / 2; u++) sr[u] = u < nb8 ? wd[(size_t)u * 64] : make_uint4(0, 0, 0, 0);
+  // activations: group g + 2 loads into registers at the start of group g and is stored to shared
+  // memory at the end of group g + 1, so each load has two groups of work to arrive
+  uint4 xr[2][4];
+  float dr[2];
+  xload(0, xr[0], dr[0]);
+  xstore(0, xr[0], dr[0]);
+  if (ng > 1) xload(1, xr[1], dr[1]);
+  __syncthreads();
+  float acc[4][TT][4];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) acc[j][tt][0] = acc[j][tt][1] = acc[j][tt][2] = acc[j][tt][3] = 0.0f;
+  const uint2* xs2 = reinterpret_cast<const uint2*>(&xs[0][0][0][0][0]);
+  for (int g0 = 0; g0 < ng; g0 += PD) {
+#pragma unroll
+    for (int u = 0; u < PD; u++) {
+      const int g = g0 + u, buf = g & 1;
+      if (g < ng) {
+        if (g + 2 < ng) xload(g + 2, xr[u & 1], dr[u & 1]);   // u & 1 == g & 1 (PD is even)
+        uint4 w[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          w[j] = wr[u][j];
+          if (g + PD < ng) wr[u][j] = wq[(size_t)(g + PD) * 256 + j];
+        }
+        const uint4 sc = sr[u >> 1];
+        if ((u & 1) && ((g + PD) >> 1) < nb8) sr[u >> 1] = wd[(size_t)((g + PD) >> 1) * 64];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          if (g * 4 + k < nb) {
+            f4_t d[4][TT];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              const uint32_t wv = k == 0 ? w[j].x : k == 1 ? w[j].y : k == 2 ? w[j].z : w[j].w;
+              const uint32_t v = ((wv >> sh) & mask) | orv;
+              const h4_t bw = __builtin_bit_cast(h4_t, make_uint2(__builtin_amdgcn_perm(0x64646464u, v, sel0),
+                                                                  __builtin_amdgcn_perm(0x64646464u, v, sel1)));
+#pragma unroll
+              for (int tt = 0; tt < TT; tt++) {
+                // 8 bytes at quarter kg of the 32-byte operand of token tt*16 + li
+                const uint2 aw = xs2[((((buf * 4 + k) * 4 + j) * kMfmaTok + tt * 16 + li) * 2) * 2 + kg];
+                d[j][tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4_t, aw), bw,
+                                                                 (f4_t){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+              }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const int hb = ((u & 1) << 2) + k;
+            const uint32_t sw = (hb >> 1) == 0 ? sc.x : (hb >> 1) == 1 ? sc.y : (hb >> 1) == 2 ? sc.z : sc.w;
+            const float dw = half_bits_to_float((hb & 1) ? (sw >> 16) : (sw & 0xffffu));
+            float s4[TT][4];
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++) {
+              const float4 dx = *reinterpret_cast<const float4*>(&dxs[buf][k][tt * 16 + 4 * kg]);
+              s4[tt][0] = dw * dx.x;
+              s4[tt][1] = dw * dx.y;
+              s4[tt][2] = dw * dx.z;
+              s4[tt][3] = dw * dx.w;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+              for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[j][tt][r] = acc[j][tt][r] + d[j][tt][r] * s4[tt][r];
+          }
+        }
+        if (g + 1 < ng) xstore(buf ^ 1, xr[(u + 1) & 1], dr[(u + 1) & 1]);
+        __syncthreads();
+      }
+    }
+  }
+  // lane holds tokens T0 + 16 tt + 4 kg + r of row R0 + li; chains combine as ((a0 + a1) + a2) + a3
+#pragma unroll
+  for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int m = T0 + tt * 16 + 4 * kg + r;
+      if (m < M && row < W.N) {
+        const float v = ((acc[0][tt][r] + acc[1][tt][r]) + acc[2][tt][r]) + acc[3][tt][r];
+        float* o = y + (size_t)m * ldy + row;
+        if (OP == OP_ADD) *o = *o + v;
+        else if (OP == OP_BIAS) *o = v + bias[row];
+        else *o = v;
+      }
+    }
+}
+
+// ================================================================ batched decode kernels
+//
+// B independent sequences decode one token each per step.  Sequence b has its own fp32 cache
+// [layer][kv_head][ctx][head_dim] at kc + b * seq_stride and its own position pos[b]; projections run
+// as one pass of B tokens (k_gemm_q4), so every per-output operation order is the one-token one.
+
+// Embedding rows of tokens tok[0..B) (kernels.c:312-322).
+__global__ void k_embed_list(const uint8_t* __restrict__ emb, int D, const int* __restrict__ tok,
+                             float* __restrict__ x) {
+  const int m = blockIdx.x;
+  const uint8_t* row = emb + (size_t)tok[m] * (D / 32) * 18;
+  float* xr = x + (size_t)m * D;
+  for (int idx = threadIdx.x; idx < D / 2; idx += blockDim.x) {
+    const int blk = idx >> 4, j = idx & 15;
+    const uint8_t* bp = row + blk * 18;
+    const float d = half_bits_to_float((uint32_t)bp[0] | ((uint32_t)bp[1] << 8));
+    const int q = bp[2 + j];
+    xr[32 * blk + j] = (float)((q & 15) - 8) * d;
+    xr[32 * blk + 16 + j] = (float)((q >> 4) - 8) * d;
+  }
+}
+
+// RoPE of token b's q and k heads at position pos[b], then K and V appended to sequence b's cache
+// (kernels.c:337-352).  Grid (H + KVH, B), HD/2 threads.
+__global__ void k_rope_kv_list(float* __restrict__ qkv, int QKV, int D, int H, int KVH, int HD,
+                               const float* __restrict__ rope, float* __restrict__ kc, float* __restrict__ vc,
+                               int ctx, int layer, const int* __restrict__ pos, size_t seq_stride) {
+  const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x, half = HD / 2;
+  const int p = pos[b];
+  float* v = qkv + (size_t)b * QKV + h * HD;
+  const float* cs = rope + (size_t)p * HD;
+  const float c = cs[2 * i], s = cs[2 * i + 1], x0 = v[i], x1 = v[i + half];
+  const float y0 = x0 * c - x1 * s, y1 = x1 * c + x0 * s;
+  v[i] = y0;
+  v[i + half] = y1;
+  if (h >= H) {
+    const int kh = h - H;
+    const size_t off = (size_t)b * seq_stride + (((size_t)layer * KVH + kh) * ctx + p) * HD;
+    const float* vs = qkv + (size_t)b * QKV + D + KVH * HD + kh * HD;
+    kc[off + i] = y0;
+    kc[off + i + half] = y1;
+    vc[off + i] = vs[i];
+    vc[off + i + half] = vs[i + half];
+  }
+}
+
+// Attention of token b over positions [0, pos[b]] of sequence b's cache (kernels.c:355-377), in
+// two launches that keep the reference's per-head operation order:
+//   k_attn_scores_list  scores s_t = (q . k_t) * 1/sqrt(head_dim) of the G = H/KVH heads of kv
+//                       head g, 64 positions per workgroup: grid (ctx/64, KVH, B), 64*G threads
+//                       (thread = head, position); K rows staged once in shared memory.
+//   k_attn_pv_list      per (column slice, kv head, sequence): max, e_t = fast_exp(s_t - max), the
+//                       sum in position order, p_t = e_t / sum, then out[c] = sum_t p_t * v_t[c] in
+//                       position order, one thread per (head, column).  Every workgroup of a
+//                       (sequence, kv head) recomputes the same softmax from the scores.
+// Scores live in sc [B][H][ctx].
+constexpr int kScoreRows = 64;
+constexpr int kPvCols = 32, kPvRows = 256;
+constexpr int kMaxGroup = 8;    // query heads per kv head
+
+// Floats per head row of the softmax array: room for every position plus the sum's read-ahead.
+__host__ __device__ inline int pv_row_stride(int ctx) { return ((ctx + 31) & ~31) + 64; }
+// Floats per head row of the scores array (rows start 16-byte aligned).
+__host__ __device__ inline int score_stride(int ctx) { return (ctx + 3) & ~3; }
+
+template <int HD>
+__global__ __launch_bounds__(64) void k_attn_scores_list(const float* __restrict__ qkv, int QKV, int H, int KVH,
+                                                         const float* __restrict__ kc, int ctx, int layer,
+                                                         float* __restrict__ sc, const int* __restrict__ pos,
+                                                         size_t seq_stride) {
+  __shared__ __attribute__((aligned(16))) float qs[kMaxGroup * HD];
+  const int g = blockIdx.y, b = blockIdx.z, t0 = blockIdx.x * kScoreRows, tid = threadIdx.x, G = H / KVH;
+  const int T = pos[b] + 1;
+  if (t0 >= T) return;
+  {
+    float4 qv[kMaxGroup * HD / 256];
+    const float4* qg = reinterpret_cast<const float4*>(qkv + (size_t)b * QKV + g * G * HD);
+#pragma unroll
+    for (int u = 0; u < kMaxGroup * HD / 256; u++) {
+      const int i = tid + 64 * u;
+      qv[u] = i < G * HD / 4 ? qg[i] : make_float4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kMaxGroup * HD / 256; u++) reinterpret_cast<float4*>(qs)[tid + 64 * u] = qv[u];
+  }
+  __syncthreads();
+  const int t = t0 + tid;
+  if (t >= T) return;
+  const float4* kr = reinterpret_cast<const float4*>(kc + (size_t)b * seq_stride + (((size_t)layer * KVH + g) * ctx + t) * HD);
+  float4 kv[HD / 4];                     // the whole K row: one round trip to memory
+#pragma unroll
+  for (int u = 0; u < HD / 4; u++) kv[u] = kr[u];
+  float s[kMaxGroup][4];
+#pragma unroll
+  for (int gh = 0; gh < kMaxGroup; gh++) {
+    s[gh][0] = s[gh][1] = s[gh][2] = s[gh][3] = 0.0f;
+    if (gh < G) {
+#pragma unroll
+      for (int u = 0; u < HD / 4; u++) {
+        const float4 q4 = *reinterpret_cast<const float4*>(&qs[gh * HD + 4 * u]);
+        s[gh][0] = s[gh][0] + q4.x * kv[u].x;
+        s[gh][1] = s[gh][1] + q4.y * kv[u].y;
+        s[gh][2] = s[gh][2] + q4.z * kv[u].z;
+        s[gh][3] = s[gh][3] + q4.w * kv[u].w;
+      }
+    }
+  }
+  const float scale = 1.0f / __builtin_sqrtf((float)HD);
+#pragma unroll
+  for (int gh = 0; gh < kMaxGroup; gh++)
+    if (gh < G) sc[((size_t)b * H + g * G + gh) * score_stride(ctx) + t] = (s[gh][0] + s[gh][1] + s[gh][2] + s[gh][3]) * scale;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ sc, int H, int KVH,
+                                                      const float* __restrict__ vc, int ctx, int layer,
+                                                      float* __restrict__ att, int D, const int* __restrict__ pos,
+                                                      size_t seq_stride) {
+  extern __shared__ __attribute__((aligned(16))) float lsm[];
+  constexpr int CR = kPvRows, CRS = kPvRows + 4, NV = CR * kPvCols / 4 / 256;
+  constexpr int PB = 2;                   // score float4 per thread and head in one pass (2048 positions)
+  const int c0 = blockIdx.x * kPvCols, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6, G = H / KVH;
+  const int T = pos[b] + 1, TS = pv_row_stride(ctx), nch = (T + CR - 1) / CR, CS = score_stride(ctx);
+  const int T4 = (T + 3) >> 2;
+  float* vs = lsm;                        // [2][kPvCols][CRS]: V chunks, column-major
+  float* p = vs + 2 * kPvCols * CRS;      // [G][TS]
+  float* red = p + G * TS;                // [4 waves][kMaxGroup] maxima, [kMaxGroup] max, [kMaxGroup] sum
+  float* rmax = red + 4 * kMaxGroup;
+  float* rsum = rmax + kMaxGroup;
+  const float* sb = sc + ((size_t)b * H + g * G) * CS;
+  const float* vb = vc + (size_t)b * seq_stride + ((size_t)layer * KVH + g) * ctx * HD + c0;
+  auto vload = [&](int ch, float4* r) {
+#pragma unroll
+    for (int u = 0; u < NV; u++) {
+      const int i = tid + 256 * u, row = i / (kPvCols / 4), c4 = i - row * (kPvCols / 4), t = ch * CR + row;
+      r[u] = t < T ? *reinterpret_cast<const float4*>(vb + (size_t)t * HD + 4 * c4) : make_float4(0, 0, 0, 0);
+    }
+  };
+  auto vstore = [&](int buf, const float4* r) {
+#pragma unroll
+    for (int u = 0; u < NV; u++) {
+      const int i = tid + 256 * u, row = i / (kPvCols / 4), c4 = i - row * (kPvCols / 4);
+      float* d = vs + (buf * kPvCols + 4 * c4) * CRS + row;
+      d[0] = r[u].x;
+      d[CRS] = r[u].y;
+      d[2 * CRS] = r[u].z;
+      d[3 * CRS] = r[u].w;
+    }
+  };
+  auto head_max = [&](float* mxh) {       // block-wide maximum of each head (order-free)
+#pragma unroll
+    for (int gh = 0; gh < kMaxGroup; gh++) {
+      float m = mxh[gh];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o));
+      if (lane == 0) red[wave * kMaxGroup + gh] = m;
+    }
+    __syncthreads();
+    if (tid < G)
+      rmax[tid] = __builtin_fmaxf(__builtin_fmaxf(red[tid], red[kMaxGroup + tid]),
+                                  __builtin_fmaxf(red[2 * kMaxGroup + tid], red[3 * kMaxGroup + tid]));
+    __syncthreads();
+  };
+  auto load_scores = [&](int q0, float4 (*v)[PB]) {
+#pragma unroll
+    for (int gh = 0; gh < kMaxGroup; gh++)
+#pragma unroll
+      for (int k = 0; k < PB; k++) {
+        const int q = q0 + tid + 256 * k;
+        v[gh][k] = (gh < G && q < T4) ? *reinterpret_cast<const float4*>(sb + (size_t)gh * CS + 4 * q)
+                                      : make_float4(-1e30f, -1e30f, -1e30f, -1e30f);
+      }
+  };
+  auto fold_max = [&](int q0, float4 (*v)[PB], float* mxh) {
+#pragma unroll
+    for (int gh = 0; gh < kMaxGroup; gh++)
+#pragma unroll
+      for (int k = 0; k < PB; k++) {
+        const int t = 4 * (q0 + tid + 256 * k);
+        float m = mxh[gh];
+        m = __builtin_fmaxf(m, t < T ? v[gh][k].x : -1e30f);
+        m = __builtin_fmaxf(m, t + 1 < T ? v[gh][k].y : -1e30f);
+        m = __builtin_fmaxf(m, t + 2 < T ? v[gh][k].z : -1e30f);
+        m = __builtin_fmaxf(m, t + 3 < T ? v[gh][k].w : -1e30f);
+        mxh[gh] = m;
+      }
+  };
+  auto store_exp = [&](int q0, float4 (*v)[PB]) {   // e_t = fast_exp(s_t - max), kept in v too
+#pragma unroll
+    for (int gh = 0; gh < kMaxGroup; gh++)
+#pragma unroll
+      for (int k = 0; k < PB; k++) {
+        const int q = q0 + tid + 256 * k;
+        if (gh < G && q < T4) {
+          const float mx = rmax[gh];
+          float4 e;
+          e.x = fast_exp(v[gh][k].x - mx);
+          e.y = fast_exp(v[gh][k].y - mx);
+          e.z = fast_exp(v[gh][k].z - mx);
+          e.w = fast_exp(v[gh][k].w - mx);
+          v[gh][k] = e;
+          *reinterpret_cast<float4*>(&p[gh * TS + 4 * q]) = e;
+        }
+      }
+  };
+  float4 vr[NV];
+  vload(0, vr);                           // the first V chunk loads while the softmax runs
+  float mxh[kMaxGroup];
+#pragma unroll
+  for (int gh = 0; gh < kMaxGroup; gh++) mxh[gh] = -1e30f;
+  float4 v[kMaxGroup][PB];
+  const bool one_pass = T4 <= 256 * PB;   // the scores stay in registers from load to division
+  if (one_pass) {
+    load_scores(0, v);
+    fold_max(0, v, mxh);
+    head_max(mxh);
+    store_exp(0, v);
+  } else {
+    for (int q0 = 0; q0 < T4; q0 += 256 * PB) {
+      load_scores(q0, v);
+      fold_max(q0, v, mxh);
+    }
+    head_max(mxh);
+    for (int q0 = 0; q0 < T4; q0 += 256 * PB) {
+      load_scores(q0, v);
+      store_exp(q0, v);
+    }
+  }
+  vstore(0, vr);                          // V work overlaps the sum below
+  if (nch > 1) vload(1, vr);
+  __syncthreads();
+  if (tid < G) {                          // the sum in position order; the next 32 values load ahead
+    const float* e = p + tid * TS;
+    const int T32 = T & ~31;
+    float sum = 0.0f;
+    float4 a[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) a[u] = *reinterpret_cast<const float4*>(e + 4 * u);
+    for (int t = 0; t < T32; t += 32) {
+      float4 nx[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) nx[u] = *reinterpret_cast<const float4*>(e + t + 32 + 4 * u);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        sum = sum + a[u].x;
+        sum = sum + a[u].y;
+        sum = sum + a[u].z;
+        sum = sum + a[u].w;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 8; u++) a[u] = nx[u];
+    }
+    for (int t = T32; t < T; t++) sum = sum + e[t];
+    rsum[tid] = sum;
+  }
+  __syncthreads();
+  if (one_pass) {
+#pragma unroll
+    for (int gh = 0; gh < kMaxGroup; gh++)
+#pragma unroll
+      for (int k = 0; k < PB; k++) {
+        const int q = tid + 256 * k;
+        if (gh < G && q < T4) {
+          const float sum = rsum[gh];
+          float4 e = v[gh][k];
+          e.x = e.x / sum;
+          e.y = e.y / sum;
+          e.z = e.z / sum;
+          e.w = e.w / sum;
+          *reinterpret_cast<float4*>(&p[gh * TS + 4 * q]) = e;
+        }
+      }
+  } else {
+    for (int q = tid; q < T4; q += 256) {
+#pragma unroll
+      for (int gh = 0; gh < kMaxGroup; gh++) {
+        if (gh < G) {
+          const float sum = rsum[gh];
+          float4 e = *reinterpret_cast<const float4*>(&p[gh * TS + 4 * q]);
+          e.x = e.x / sum;
+          e.y = e.y / sum;
+          e.z = e.z / sum;
+          e.w = e.w / sum;
+          *reinterpret_cast<float4*>(&p[gh * TS + 4 * q]) = e;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // P.V: thread (head, column); positions in order.  The shared-memory reads of the next 16
+  // positions are issued before the current 16 are added.
+  const int gh = tid / kPvCols, c = tid - gh * kPvCols;
+  const bool active = gh < G;
+  const float* pr = p + (active ? gh : 0) * TS;
+  float acc = 0.0f;
+  for (int ch = 0; ch < nch; ch++) {
+    const int buf = ch & 1, t0 = ch * CR, m = min(CR, T - t0);
+    const float* vcol = vs + (buf * kPvCols + c) * CRS;
+    if (active) {
+      if (m == CR) {
+        float4 pa[4], va[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          pa[u] = *reinterpret_cast<const float4*>(pr + t0 + 4 * u);
+          va[u] = *reinterpret_cast<const float4*>(vcol + 4 * u);
+        }
+        for (int r0 = 0; r0 < CR; r0 += 16) {
+          float4 pn[4], vn[4];
+          const int r1 = r0 + 16 < CR ? r0 + 16 : r0;
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            pn[u] = *reinterpret_cast<const float4*>(pr + t0 + r1 + 4 * u);
+            vn[u] = *reinterpret_cast<const float4*>(vcol + r1 + 4 * u);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            acc = acc + pa[u].x * va[u].x;
+            acc = acc + pa[u].y * va[u].y;
+            acc = acc + pa[u].z * va[u].z;
+            acc = acc + pa[u].w * va[u].w;
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            pa[u] = pn[u];
+            va[u] = vn[u];
+          }
+        }
+      } else {
+        for (int r = 0; r < m; r++) acc = acc + pr[t0 + r] * vcol[r];
+      }
+    }
+    if (ch + 1 < nch) {
+      vstore(buf ^ 1, vr);
+      if (ch + 2 < nch) vload(ch + 2, vr);
+    }
+    __syncthreads();
+  }
+  if (active) att[(size_t)b * D + (g * G + gh) * HD + c0 + c] = acc;
+}
+
+// Greedy token of every row of logits [B][V] (first maximum, cpu-worker.js:157): partial maxima
+// over 4096-entry slices, grid (slices, B).
+__global__ __launch_bounds__(256) void k_argmax_rows1(const float* __restrict__ lg, int V, float* __restrict__ pv,
+                                                      int* __restrict__ pi, int P) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const int tid = threadIdx.x, b = blockIdx.y;
+  const float* row = lg + (size_t)b * V;
+  const int lo = blockIdx.x * 4096, hi = min(V, lo + 4096);
+  float bv = 0.0f;
+  int bi = -1;
+  for (int i = lo + tid; i < hi; i += 256) amax_merge(bv, bi, row[i], i);
+  sv[tid] = bv;
+  si[tid] = bi;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) {
+      float v = sv[tid];
+      int i = si[tid];
+      amax_merge(v, i, sv[tid + s], si[tid + s]);
+      sv[tid] = v;
+      si[tid] = i;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) { pv[b * P + blockIdx.x] = sv[0]; pi[b * P + blockIdx.x] = si[0]; }
+}
+
+// Reduce the slices of row b: next token into tok[b] (the next step's input) and out[b], pos[b] + 1.
+__global__ __launch_bounds__(256) void k_argmax_rows2(const float* __restrict__ pv, const int* __restrict__ pi, int P,
+                                                      int* __restrict__ tok, int* __restrict__ pos,
+                                                      int* __restrict__ out) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const int tid = threadIdx.x, b = blockIdx.x;
+  float bv = 0.0f;
+  int bi = -1;
+  for (int i = tid; i < P; i += 256) amax_merge(bv, bi, pv[b * P + i], pi[b * P + i]);
+  sv[tid] = bv;
+  si[tid] = bi;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) {
+      float v = sv[tid];
+      int i = si[tid];
+      amax_merge(v, i, sv[tid + s], si[tid + s]);
+      sv[tid] = v;
+      si[tid] = i;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const int next = si[0] < 0 ? 0 : si[0];
+    tok[b] = next;
+    pos[b] = pos[b] + 1;
+    if (out) out[b] = next;
+  }
+}
+
 // ================================================================ host side
 
 namespace {
@@ -670,6 +1329,7 @@ struct q4hip {
   float *x = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *logits = nullptr;
   float *kc = nullptr, *vc = nullptr;
   uint4* xq = nullptr;
+  uint4* xh = nullptr;     // the same activations as fp16 matrix-core operands (multi-token passes)
   int xstride = 0;   // activation blocks per token row of xq
   float* ascr = nullptr;   // attention scratch of multi-token passes: [MT][H][ctx] scores, allocated on first use
   float* am_v = nullptr;
@@ -724,17 +1384,58 @@ int check_ready(q4hip* h) {
   return Q4HIP_OK;
 }
 
+// Kernel choice for passes of M > 8 tokens, by an estimate of each candidate's time: max(one wave's
+// serial work, total work / SIMDs), counting vector instructions per block and lane --
+// k_gemm_rows 5 + 7 * TPW (TPW tokens per wave), k_gemm_mfma 88 (32 tokens), k_gemm_q4 61
+// (8 tokens).  Q4HIP_GEMM=valu keeps the matrix cores out (all kernels give the same bits).
+enum { GK_ROWS8, GK_ROWS4, GK_ROWS2, GK_ROWS1, GK_MFMA, GK_TILED };
+
+int pick_gemm(const Mat& W, int M, bool have_xh) {
+  static const bool no_mfma = [] { const char* e = getenv("Q4HIP_GEMM"); return e && strcmp(e, "valu") == 0; }();
+  const double rt = (double)(W.Np / 16), nb = W.nb;
+  auto cost = [](double waves, double per_wave) { return std::max(per_wave, waves * per_wave / 1024.0); };
+  int best = GK_TILED;
+  double bc = cost(rt * ((M + 31) / 32) * 4, nb * 61);
+  auto consider = [&](int k, double c) { if (c < bc * 0.97) { bc = c; best = k; } };
+  if (M <= 64) {
+    const int tp[] = {8, 4, 2, 1};
+    for (int i = 0; i < 4; i++) consider(GK_ROWS8 + i, cost(rt * ((M + tp[i] - 1) / tp[i]), nb * (5 + 7 * tp[i])));
+  }
+  if (have_xh && !no_mfma) consider(GK_MFMA, cost(rt * ((M + kMfmaTok - 1) / kMfmaTok), nb * 88));
+  return best;
+}
+
+template <int OP, int TPW>
+void launch_rows(hipStream_t s, const Mat& W, const uint4* xq, int xstride, int M, float* y, int ldy, const float* bias) {
+  k_gemm_rows<OP, TPW><<<dim3((unsigned)(W.Np / 64), (unsigned)((M + TPW - 1) / TPW)), 256, 0, s>>>(
+      W.view(), xq, xstride, M, y, ldy, bias);
+}
+
 template <int OP>
 void launch_matvec(hipStream_t s, const Mat& W, const uint4* xq, int xstride, int M, float* y, int ldy,
-                   const float* bias) {
+                   const float* bias, const uint4* xh = nullptr) {
   const unsigned grid = (unsigned)(W.Np / 16);
-  if (M == 1)
+  if (M == 1) {
     k_matvec<1, OP><<<grid, 64, (size_t)W.nb * 64, s>>>(W.view(), xq, xstride, 1, y, ldy, bias);
-  else if (M <= 8)
+    return;
+  }
+  if (M <= 8) {
     k_matvec<kMaxChunk, OP><<<grid, 64, 0, s>>>(W.view(), xq, xstride, M, y, ldy, bias);
-  else
-    k_gemm_q4<OP><<<dim3((unsigned)(W.Np / kGemmRows), (unsigned)((M + kGemmTokens - 1) / kGemmTokens)), 256, 0, s>>>(
-        W.view(), xq, xstride, M, y, ldy, bias);
+    return;
+  }
+  switch (pick_gemm(W, M, xh != nullptr)) {
+    case GK_ROWS8: launch_rows<OP, 8>(s, W, xq, xstride, M, y, ldy, bias); break;
+    case GK_ROWS4: launch_rows<OP, 4>(s, W, xq, xstride, M, y, ldy, bias); break;
+    case GK_ROWS2: launch_rows<OP, 2>(s, W, xq, xstride, M, y, ldy, bias); break;
+    case GK_ROWS1: launch_rows<OP, 1>(s, W, xq, xstride, M, y, ldy, bias); break;
+    case GK_MFMA:
+      k_gemm_mfma<OP><<<dim3((unsigned)(W.Np / 64), (unsigned)((M + kMfmaTok - 1) / kMfmaTok)), 256, 0, s>>>(
+          W.view(), xq, xh, xstride, M, y, ldy, bias);
+      break;
+    default:
+      k_gemm_q4<OP><<<dim3((unsigned)(W.Np / kGemmRows), (unsigned)((M + kGemmTokens - 1) / kGemmTokens)), 256, 0, s>>>(
+          W.view(), xq, xstride, M, y, ldy, bias);
+  }
 }
 
 // logits = head . x for one token: Q4_0 (the synthetic configurations) or Q8_0 (real files).
@@ -747,24 +1448,25 @@ void launch_head(hipStream_t s, const Mat& W, const uint4* xq, float* logits) {
 
 template <int MODE>
 void launch_quant(hipStream_t s, int rows, const float* in, int ld_in, int n, const float* w, float eps,
-                  uint4* xq, int xstride, int m_first) {
+                  uint4* xq, int xstride, int m_first, uint4* xh = nullptr) {
   const size_t lds = MODE == QM_NORM ? (size_t)((n >> 2) + 1) * 4 * sizeof(float) : 0;
-  k_quant<MODE><<<rows, 256, lds, s>>>(in, ld_in, n, w, eps, xq, xstride, m_first);
+  k_quant<MODE><<<rows, 256, lds, s>>>(in, ld_in, n, w, eps, xq, xstride, m_first, xh);
 }
 
 // One pass over M <= MT tokens at device position st->pos0 (forward_pass, kernels.c:306-415).
 void enqueue_pass(q4hip* h, int M, bool want_logits) {
   const int D = h->D, F = h->F, HD = h->HD, QKV = h->QKV;
   hipStream_t s = h->stream;
+  uint4* xh = M > 8 ? h->xh : nullptr;
   prof_mark(h, Q4HIP_PROF_EMBED);
   k_embed<<<M, 256, 0, s>>>(h->embd, D, h->tokens, h->st, h->x);
   const size_t attn_lds = (size_t)(HD + h->ctx) * sizeof(float);
   for (int l = 0; l < h->NL; l++) {
     Layer& y = h->L[l];
     prof_mark(h, Q4HIP_PROF_NORM_Q);
-    launch_quant<QM_NORM>(s, M, h->x, D, D, y.attn_norm, h->eps, h->xq, h->xstride, 0);
+    launch_quant<QM_NORM>(s, M, h->x, D, D, y.attn_norm, h->eps, h->xq, h->xstride, 0, xh);
     prof_mark(h, Q4HIP_PROF_QKV);
-    launch_matvec<OP_BIAS>(s, y.qkv, h->xq, h->xstride, M, h->qkv, QKV, y.bqkv);
+    launch_matvec<OP_BIAS>(s, y.qkv, h->xq, h->xstride, M, h->qkv, QKV, y.bqkv, xh);
     prof_mark(h, Q4HIP_PROF_ROPE);
     k_rope_kv<<<dim3(h->H + h->KVH, M), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, h->kc, h->vc, h->ctx, l, h->st);
     prof_mark(h, Q4HIP_PROF_ATTN);
@@ -780,17 +1482,17 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
       k_attn<128><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, h->st);
     }
     prof_mark(h, Q4HIP_PROF_QUANT);
-    launch_quant<QM_PLAIN>(s, M, h->att, D, D, nullptr, 0.0f, h->xq, h->xstride, 0);
+    launch_quant<QM_PLAIN>(s, M, h->att, D, D, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
     prof_mark(h, Q4HIP_PROF_O);
-    launch_matvec<OP_ADD>(s, y.o, h->xq, h->xstride, M, h->x, D, nullptr);
+    launch_matvec<OP_ADD>(s, y.o, h->xq, h->xstride, M, h->x, D, nullptr, xh);
     prof_mark(h, Q4HIP_PROF_NORM_Q);
-    launch_quant<QM_NORM>(s, M, h->x, D, D, y.ffn_norm, h->eps, h->xq, h->xstride, 0);
+    launch_quant<QM_NORM>(s, M, h->x, D, D, y.ffn_norm, h->eps, h->xq, h->xstride, 0, xh);
     prof_mark(h, Q4HIP_PROF_GU);
-    launch_matvec<OP_STORE>(s, y.gu, h->xq, h->xstride, M, h->gu, 2 * F, nullptr);
+    launch_matvec<OP_STORE>(s, y.gu, h->xq, h->xstride, M, h->gu, 2 * F, nullptr, xh);
     prof_mark(h, Q4HIP_PROF_SWIGLU);
-    launch_quant<QM_SWIGLU>(s, M, h->gu, 2 * F, F, nullptr, 0.0f, h->xq, h->xstride, 0);
+    launch_quant<QM_SWIGLU>(s, M, h->gu, 2 * F, F, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
     prof_mark(h, Q4HIP_PROF_DOWN);
-    launch_matvec<OP_ADD>(s, y.down, h->xq, h->xstride, M, h->x, D, nullptr);
+    launch_matvec<OP_ADD>(s, y.down, h->xq, h->xstride, M, h->x, D, nullptr, xh);
   }
   if (want_logits) {
     prof_mark(h, Q4HIP_PROF_NORM_Q);
@@ -999,7 +1701,7 @@ void q4hip_destroy(q4hip* h) {
   }
   mat_free(h->head);
   void* bufs[] = {h->embd, h->out_norm, h->rope, h->x, h->qkv, h->att, h->gu, h->logits, h->kc, h->vc,
-                  h->xq, h->am_v, h->am_i, h->tokens, h->st, h->d_layers, h->ll, h->ascr};
+                  h->xq, h->am_v, h->am_i, h->tokens, h->st, h->d_layers, h->ll, h->ascr, h->xh};
   for (void* p : bufs) if (p) (void)hipFree(p);
   if (h->pin_ids) (void)hipHostFree(h->pin_ids);
   if (h->pin_next) (void)hipHostFree(h->pin_next);
@@ -1060,6 +1762,7 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
   TRYHIP(hipMemset(h->kc, 0, kvbytes));
   TRYHIP(hipMemset(h->vc, 0, kvbytes));
   TRYHIP(hipMalloc(&h->xq, (size_t)M * h->xstride * 64));
+  TRYHIP(hipMalloc(&h->xh, (size_t)M * h->xstride * 128));
   h->am_parts = (vocab + 4095) / 4096;
   TRYHIP(hipMalloc(&h->am_v, (size_t)h->am_parts * 4));
   TRYHIP(hipMalloc(&h->am_i, (size_t)h->am_parts * 4));
@@ -1384,6 +2087,239 @@ int q4hip_time_head(q4hip* h, int iters, float* us_per_launch) {
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
   *us_per_launch = ms * 1000.0f / iters;
+  return Q4HIP_OK;
+}
+
+// ---------------------------------------------------------------- batched decode
+
+struct q4hip_batch {
+  q4hip* h = nullptr;
+  int B = 0, P = 0;
+  size_t seq_stride = 0;     // floats of one sequence's K (or V) cache: layers * kv_heads * ctx * head_dim
+  size_t attn_lds = 0;
+  float *kc = nullptr, *vc = nullptr, *logits = nullptr, *am_v = nullptr;
+  float* sc = nullptr;       // attention scores [B][heads][ctx]
+  int *am_i = nullptr, *tok = nullptr, *pos = nullptr, *out = nullptr;
+  int out_cap = 0;           // ints of `out`
+  int* pin = nullptr;        // pinned staging: B tokens, B positions
+};
+
+namespace {
+
+size_t attn_pv_lds(int H, int KVH, int ctx) {
+  const int G = H / KVH;
+  return (size_t)(2 * kPvCols * (kPvRows + 4) + G * pv_row_stride(ctx) + 6 * kMaxGroup) * sizeof(float);
+}
+
+// One decode step of all B sequences: tokens bt->tok at positions bt->pos; the greedy tokens go to
+// bt->tok (and out[0..B) when given) and every position advances by one.
+void enqueue_batch_step(q4hip_batch* bt, int* out) {
+  q4hip* h = bt->h;
+  const int B = bt->B, D = h->D, F = h->F, HD = h->HD, QKV = h->QKV;
+  hipStream_t s = h->stream;
+  uint4* xh = B > 8 ? h->xh : nullptr;
+  k_embed_list<<<B, 256, 0, s>>>(h->embd, D, bt->tok, h->x);
+  for (int l = 0; l < h->NL; l++) {
+    Layer& y = h->L[l];
+    launch_quant<QM_NORM>(s, B, h->x, D, D, y.attn_norm, h->eps, h->xq, h->xstride, 0, xh);
+    launch_matvec<OP_BIAS>(s, y.qkv, h->xq, h->xstride, B, h->qkv, QKV, y.bqkv, xh);
+    k_rope_kv_list<<<dim3(h->H + h->KVH, B), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, bt->kc,
+                                                             bt->vc, h->ctx, l, bt->pos, bt->seq_stride);
+    const dim3 sg((unsigned)((h->ctx + kScoreRows - 1) / kScoreRows), (unsigned)h->KVH, (unsigned)B);
+    const dim3 pg((unsigned)(HD / kPvCols), (unsigned)h->KVH, (unsigned)B);
+    if (HD == 64) {
+      k_attn_scores_list<64><<<sg, 64, 0, s>>>(h->qkv, QKV, h->H, h->KVH, bt->kc, h->ctx, l, bt->sc, bt->pos, bt->seq_stride);
+      k_attn_pv_list<64><<<pg, 256, bt->attn_lds, s>>>(bt->sc, h->H, h->KVH, bt->vc, h->ctx, l, h->att, D, bt->pos, bt->seq_stride);
+    } else {
+      k_attn_scores_list<128><<<sg, 64, 0, s>>>(h->qkv, QKV, h->H, h->KVH, bt->kc, h->ctx, l, bt->sc, bt->pos, bt->seq_stride);
+      k_attn_pv_list<128><<<pg, 256, bt->attn_lds, s>>>(bt->sc, h->H, h->KVH, bt->vc, h->ctx, l, h->att, D, bt->pos, bt->seq_stride);
+    }
+    launch_quant<QM_PLAIN>(s, B, h->att, D, D, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
+    launch_matvec<OP_ADD>(s, y.o, h->xq, h->xstride, B, h->x, D, nullptr, xh);
+    launch_quant<QM_NORM>(s, B, h->x, D, D, y.ffn_norm, h->eps, h->xq, h->xstride, 0, xh);
+    launch_matvec<OP_STORE>(s, y.gu, h->xq, h->xstride, B, h->gu, 2 * F, nullptr, xh);
+    launch_quant<QM_SWIGLU>(s, B, h->gu, 2 * F, F, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
+    launch_matvec<OP_ADD>(s, y.down, h->xq, h->xstride, B, h->x, D, nullptr, xh);
+  }
+  launch_quant<QM_NORM>(s, B, h->x, D, D, h->out_norm, h->eps, h->xq, h->xstride, 0, xh);
+  if (h->head.fmt == Q4HIP_TYPE_Q8_0) {
+    for (int b = 0; b < B; b++)
+      k_matvec_q8<<<(unsigned)(h->head.Np / 16), 64, (size_t)h->head.nb * 64, s>>>(
+          h->head.view(), h->xq + (size_t)b * h->xstride * 4, bt->logits + (size_t)b * h->V);
+  } else {
+    launch_matvec<OP_STORE>(s, h->head, h->xq, h->xstride, B, bt->logits, h->V, nullptr, xh);
+  }
+  k_argmax_rows1<<<dim3(bt->P, B), 256, 0, s>>>(bt->logits, h->V, bt->am_v, bt->am_i, bt->P);
+  k_argmax_rows2<<<B, 256, 0, s>>>(bt->am_v, bt->am_i, bt->P, bt->tok, bt->pos, out);
+}
+
+}  // namespace
+
+void q4hip_batch_destroy(q4hip_batch* bt) {
+  if (!bt) return;
+  (void)hipSetDevice(bt->h->device);
+  (void)hipStreamSynchronize(bt->h->stream);
+  void* bufs[] = {bt->kc, bt->vc, bt->logits, bt->am_v, bt->am_i, bt->tok, bt->pos, bt->out, bt->sc};
+  for (void* p : bufs) if (p) (void)hipFree(p);
+  if (bt->pin) (void)hipHostFree(bt->pin);
+  delete bt;
+}
+
+int q4hip_batch_create(q4hip_batch** out, q4hip* h, int B) {
+  if (!out || !h) return fail(Q4HIP_EINVAL, "null argument");
+  *out = nullptr;
+  if (B <= 0 || B > h->MT) return fail(Q4HIP_EINVAL, "%d sequences: a batch holds 1..%d (the context's pass size)", B, h->MT);
+  if (h->H / h->KVH > kMaxGroup) return fail(Q4HIP_EINVAL, "more than %d query heads per kv head", kMaxGroup);
+  HIPCHK(hipSetDevice(h->device));
+  const size_t lds = attn_pv_lds(h->H, h->KVH, h->ctx);
+  if (lds > 160 * 1024) return fail(Q4HIP_EINVAL, "ctx %d: batched attention needs %zu bytes of shared memory", h->ctx, lds);
+  if (lds > 64 * 1024) {
+    HIPCHK(hipFuncSetAttribute((const void*)(h->HD == 64 ? (const void*)k_attn_pv_list<64> : (const void*)k_attn_pv_list<128>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  }
+  q4hip_batch* bt = new q4hip_batch();
+  bt->h = h;
+  bt->B = B;
+  bt->P = (h->V + 4095) / 4096;
+  bt->seq_stride = (size_t)h->NL * h->KVH * h->ctx * h->HD;
+  bt->attn_lds = lds;
+  const size_t kvbytes = (size_t)B * bt->seq_stride * 4;
+  hipError_t e = hipSuccess;
+  auto al = [&](void** p, size_t bytes) { if (e == hipSuccess) e = hipMalloc(p, bytes); };
+  al((void**)&bt->kc, kvbytes);
+  al((void**)&bt->vc, kvbytes);
+  al((void**)&bt->logits, (size_t)B * h->V * 4);
+  al((void**)&bt->am_v, (size_t)B * bt->P * 4);
+  al((void**)&bt->am_i, (size_t)B * bt->P * 4);
+  al((void**)&bt->tok, (size_t)B * 4);
+  al((void**)&bt->pos, (size_t)B * 4);
+  al((void**)&bt->sc, (size_t)B * h->H * score_stride(h->ctx) * 4);
+  if (e == hipSuccess) e = hipMemset(bt->kc, 0, kvbytes);
+  if (e == hipSuccess) e = hipMemset(bt->vc, 0, kvbytes);
+  if (e == hipSuccess) e = hipHostMalloc((void**)&bt->pin, (size_t)2 * B * 4, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    const int rc = fail(Q4HIP_EHIP, "batch of %d: %s", B, hipGetErrorString(e));
+    q4hip_batch_destroy(bt);
+    return rc;
+  }
+  *out = bt;
+  return Q4HIP_OK;
+}
+
+int q4hip_batch_set_kv(q4hip_batch* bt, int seq, int layer, int kv_head, int pos0, int n, const float* k,
+                       const float* v) {
+  if (!bt || !k || !v) return fail(Q4HIP_EINVAL, "null argument");
+  q4hip* h = bt->h;
+  if (seq < 0 || seq >= bt->B) return fail(Q4HIP_EINVAL, "sequence %d of %d", seq, bt->B);
+  if (layer < 0 || layer >= h->NL) return fail(Q4HIP_EINVAL, "layer %d of %d", layer, h->NL);
+  if (kv_head < 0 || kv_head >= h->KVH) return fail(Q4HIP_EINVAL, "kv head %d of %d", kv_head, h->KVH);
+  if (n <= 0 || pos0 < 0 || (int64_t)pos0 + n > h->ctx) return fail(Q4HIP_ECONTEXT, "positions %d..%lld outside 0..%d", pos0, (long long)pos0 + n, h->ctx);
+  HIPCHK(hipSetDevice(h->device));
+  HIPCHK(hipStreamSynchronize(h->stream));
+  const size_t off = (size_t)seq * bt->seq_stride + (((size_t)layer * h->KVH + kv_head) * h->ctx + pos0) * h->HD;
+  const size_t bytes = (size_t)n * h->HD * 4;
+  HIPCHK(hipMemcpy(bt->kc + off, k, bytes, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(bt->vc + off, v, bytes, hipMemcpyHostToDevice));
+  return Q4HIP_OK;
+}
+
+int q4hip_batch_prefill(q4hip_batch* bt, int seq, const int* ids, int n, int pos, int* next) {
+  if (!bt || !ids || !next) return fail(Q4HIP_EINVAL, "null argument");
+  q4hip* h = bt->h;
+  if (seq < 0 || seq >= bt->B) return fail(Q4HIP_EINVAL, "sequence %d of %d", seq, bt->B);
+  if (n <= 0) return fail(Q4HIP_EINVAL, "no tokens");
+  if (pos < 0 || (int64_t)pos + n >= h->ctx) return fail(Q4HIP_ECONTEXT, "context full");
+  int rc = check_ready(h);
+  if (rc) return rc;
+  rc = check_ids(h, ids, n);
+  if (rc) return rc;
+  HIPCHK(hipSetDevice(h->device));
+  if (n > 1 && h->MT > 1 && !h->ascr) {
+    if (hipMalloc(&h->ascr, (size_t)h->MT * h->H * h->ctx * sizeof(float)) != hipSuccess) {
+      h->ascr = nullptr;
+      (void)hipGetLastError();
+    }
+  }
+  // the passes run eagerly against this sequence's cache; the context's own cache is untouched
+  float* kc = h->kc;
+  float* vc = h->vc;
+  h->kc = bt->kc + (size_t)seq * bt->seq_stride;
+  h->vc = bt->vc + (size_t)seq * bt->seq_stride;
+  memcpy(h->pin_ids, ids, (size_t)n * 4);
+  hipError_t e = hipMemcpyAsync(h->tokens + pos, h->pin_ids, (size_t)n * 4, hipMemcpyHostToDevice, h->stream);
+  for (int c = 0; e == hipSuccess && c < n; c += h->MT) {
+    const int k = std::min(h->MT, n - c);
+    k_set_pos<<<1, 64, 0, h->stream>>>(h->st, pos + c);
+    enqueue_pass(h, k, c + k >= n);
+  }
+  h->kc = kc;
+  h->vc = vc;
+  if (e == hipSuccess) e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(h->pin_next, &h->st->next, 4, hipMemcpyDeviceToHost, h->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+  if (e != hipSuccess) return fail(Q4HIP_EHIP, "batch prefill: %s", hipGetErrorString(e));
+  *next = h->pin_next[0];
+  return Q4HIP_OK;
+}
+
+static int run_batch(q4hip_batch* bt, const int* first, const int* pos, int steps, int* out, float* ms) {
+  if (!bt || !first || !pos || !out) return fail(Q4HIP_EINVAL, "null argument");
+  q4hip* h = bt->h;
+  const int B = bt->B;
+  if (steps <= 0) return fail(Q4HIP_EINVAL, "steps must be positive");
+  for (int b = 0; b < B; b++)
+    if (pos[b] < 0 || (int64_t)pos[b] + steps >= h->ctx) return fail(Q4HIP_ECONTEXT, "context full (sequence %d)", b);
+  int rc = check_ready(h);
+  if (rc) return rc;
+  rc = check_ids(h, first, B);
+  if (rc) return rc;
+  HIPCHK(hipSetDevice(h->device));
+  if ((int64_t)steps * B > bt->out_cap) {
+    if (bt->out) HIPCHK(hipFree(bt->out));
+    bt->out = nullptr;
+    bt->out_cap = 0;
+    HIPCHK(hipMalloc(&bt->out, (size_t)steps * B * 4));
+    bt->out_cap = steps * B;
+  }
+  memcpy(bt->pin, first, (size_t)B * 4);
+  memcpy(bt->pin + B, pos, (size_t)B * 4);
+  HIPCHK(hipMemcpyAsync(bt->tok, bt->pin, (size_t)B * 4, hipMemcpyHostToDevice, h->stream));
+  HIPCHK(hipMemcpyAsync(bt->pos, bt->pin + B, (size_t)B * 4, hipMemcpyHostToDevice, h->stream));
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (ms) {
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    HIPCHK(hipEventRecord(e0, h->stream));
+  }
+  for (int i = 0; i < steps; i++) enqueue_batch_step(bt, bt->out + (size_t)i * B);
+  if (ms) HIPCHK(hipEventRecord(e1, h->stream));
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipStreamSynchronize(h->stream));
+  if (ms) {
+    HIPCHK(hipEventElapsedTime(ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+  }
+  HIPCHK(hipMemcpy(out, bt->out, (size_t)steps * B * 4, hipMemcpyDeviceToHost));
+  return Q4HIP_OK;
+}
+
+int q4hip_batch_generate(q4hip_batch* bt, const int* first, const int* pos, int steps, int* out) {
+  return run_batch(bt, first, pos, steps, out, nullptr);
+}
+
+int q4hip_batch_time_generate(q4hip_batch* bt, const int* first, const int* pos, int steps, int* out, float* ms) {
+  if (!ms) return fail(Q4HIP_EINVAL, "null argument");
+  return run_batch(bt, first, pos, steps, out, ms);
+}
+
+int q4hip_batch_read_logits(q4hip_batch* bt, float* out, int64_t n) {
+  if (!bt || !out) return fail(Q4HIP_EINVAL, "null argument");
+  q4hip* h = bt->h;
+  if (n < (int64_t)bt->B * h->V) return fail(Q4HIP_EINVAL, "buffer of %lld floats, batch logits are %lld", (long long)n, (long long)bt->B * h->V);
+  HIPCHK(hipSetDevice(h->device));
+  HIPCHK(hipStreamSynchronize(h->stream));
+  HIPCHK(hipMemcpy(out, bt->logits, (size_t)bt->B * h->V * 4, hipMemcpyDeviceToHost));
   return Q4HIP_OK;
 }
 

@@ -26,7 +26,9 @@ EXPORTS = [
     "q4hip_forward", "q4hip_read_logits", "q4hip_generate", "q4hip_profile", "q4hip_time_generate",
     "q4hip_time_head", "q4hip_destroy", "q4hip_mv_create", "q4hip_mv_run", "q4hip_mv_time",
     "q4hip_mv_destroy", "q4hip_set_decode_mode", "q4hip_decode_mode_used", "q4hip_profile_persistent",
-    "q4hip_set_kv", "q4hip_profile_pass",
+    "q4hip_set_kv", "q4hip_profile_pass", "q4hip_batch_create", "q4hip_batch_destroy",
+    "q4hip_batch_prefill", "q4hip_batch_set_kv", "q4hip_batch_generate", "q4hip_batch_time_generate",
+    "q4hip_batch_read_logits",
 ]
 
 _lib = None
@@ -68,6 +70,13 @@ def lib() -> ctypes.CDLL:
         "q4hip_profile_persistent": (I, [P, I, I, P, I]),
         "q4hip_set_kv": (I, [P, I, I, I, I, P, P]),
         "q4hip_profile_pass": (I, [P, P, I, I, P, I]),
+        "q4hip_batch_create": (I, [ctypes.POINTER(P), P, I]),
+        "q4hip_batch_destroy": (None, [P]),
+        "q4hip_batch_prefill": (I, [P, I, P, I, I, ctypes.POINTER(I)]),
+        "q4hip_batch_set_kv": (I, [P, I, I, I, I, I, P, P]),
+        "q4hip_batch_generate": (I, [P, P, P, I, P]),
+        "q4hip_batch_time_generate": (I, [P, P, P, I, P, ctypes.POINTER(F)]),
+        "q4hip_batch_read_logits": (I, [P, P, I64]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -208,6 +217,66 @@ class Model:
         us = ctypes.c_float(0)
         _check(lib().q4hip_time_head(self.h, iters, ctypes.byref(us)))
         return us.value
+
+
+class Batch:
+    """B sequences decoded together with one Model's weights, each with its own K/V cache.
+    Holds a reference to the model; close the batch before closing the model explicitly."""
+
+    def __init__(self, model: Model, B: int):
+        self.model, self.B = model, B
+        h = ctypes.c_void_p()
+        _check(lib().q4hip_batch_create(ctypes.byref(h), model.h, B))
+        self.h = h
+
+    def prefill(self, seq: int, ids, pos: int) -> int:
+        """Prompt of sequence `seq` at positions pos..; returns its greedy next token."""
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        nxt = ctypes.c_int(0)
+        _check(lib().q4hip_batch_prefill(self.h, seq, _ptr(a), a.size, pos, ctypes.byref(nxt)))
+        return nxt.value
+
+    def set_kv(self, seq: int, layer: int, kv_head: int, pos0: int, k: np.ndarray, v: np.ndarray) -> None:
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        assert k.shape == v.shape and k.shape[1] == self.model.shape.head_dim
+        _check(lib().q4hip_batch_set_kv(self.h, seq, layer, kv_head, pos0, k.shape[0], _ptr(k), _ptr(v)))
+
+    def _args(self, first, pos):
+        f = np.ascontiguousarray(first, dtype=np.int32)
+        p = np.ascontiguousarray(pos, dtype=np.int32)
+        assert f.size == self.B and p.size == self.B
+        return f, p
+
+    def generate(self, first, pos, steps: int) -> np.ndarray:
+        """[steps][B] greedy tokens: row i holds every sequence's token at its position pos[b]+1+i."""
+        f, p = self._args(first, pos)
+        out = np.empty((steps, self.B), dtype=np.int32)
+        _check(lib().q4hip_batch_generate(self.h, _ptr(f), _ptr(p), steps, _ptr(out)))
+        return out
+
+    def time_generate(self, first, pos, steps: int) -> tuple:
+        f, p = self._args(first, pos)
+        out = np.empty((steps, self.B), dtype=np.int32)
+        ms = ctypes.c_float(0)
+        _check(lib().q4hip_batch_time_generate(self.h, _ptr(f), _ptr(p), steps, _ptr(out), ctypes.byref(ms)))
+        return out, ms.value
+
+    def read_logits(self) -> np.ndarray:
+        out = np.empty((self.B, self.model.shape.vocab), dtype=np.float32)
+        _check(lib().q4hip_batch_read_logits(self.h, _ptr(out), out.size))
+        return out
+
+    def close(self) -> None:
+        if self.h:
+            lib().q4hip_batch_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Matvec:

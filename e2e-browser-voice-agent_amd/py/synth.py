@@ -10,8 +10,10 @@ Qwen2 GGUF file (h2-own-inference-engine/engine/gguf.js:72-88, engine/cpu-worker
 """
 from __future__ import annotations
 
+import concurrent.futures
 import dataclasses
 import math
+import os
 import struct
 import zlib
 
@@ -168,19 +170,22 @@ class Tensor:
         return self.data.tobytes()
 
 
-def make_model(shape: Shape, seed: int = 1234, head_type: int = GGML_Q4_0) -> dict:
+def make_model(shape: Shape, seed: int = 1234, head_type: int = GGML_Q4_0, workers: int = 0) -> dict:
     """All tensors of a synthetic Qwen2 model, keyed by GGUF tensor name.  head_type GGML_Q8_0
-    gives the output head the type real Qwen2.5 GGUF files use."""
+    gives the output head the type real Qwen2.5 GGUF files use.  Tensors are generated on
+    `workers` threads (0: up to 8); each has its own stream, so the result does not depend on it."""
     D, F, KV = shape.dim, shape.ffn, shape.kv_heads * shape.head_dim
-    t = {}
+    jobs = []   # (name, dims, type, thunk) in GGUF order
 
     def q4(name, k, n):
-        t[name] = Tensor(name, (k, n), GGML_Q4_0, _normal_q4(seed, name, k * n))
+        jobs.append((name, (k, n), GGML_Q4_0, lambda: _normal_q4(seed, name, k * n)))
 
     def f32(name, n, value=None):
-        data = np.full(n, value, dtype=np.float32) if value is not None else \
-            _rng(seed, name).standard_normal(n, dtype=np.float32) * np.float32(0.02)
-        t[name] = Tensor(name, (n,), GGML_F32, data.astype(np.float32))
+        def make():
+            data = np.full(n, value, dtype=np.float32) if value is not None else \
+                _rng(seed, name).standard_normal(n, dtype=np.float32) * np.float32(0.02)
+            return data.astype(np.float32)
+        jobs.append((name, (n,), GGML_F32, make))
 
     q4("token_embd.weight", D, shape.vocab)
     for layer in range(shape.layers):
@@ -199,11 +204,17 @@ def make_model(shape: Shape, seed: int = 1234, head_type: int = GGML_Q4_0) -> di
         q4(p + "ffn_down.weight", F, D)
     f32("output_norm.weight", D, 1.0)
     if head_type == GGML_Q8_0:
-        t["output.weight"] = Tensor("output.weight", (D, shape.vocab), GGML_Q8_0,
-                                    _normal_q(seed, "output.weight", D * shape.vocab, quantize_q8_0))
+        jobs.append(("output.weight", (D, shape.vocab), GGML_Q8_0,
+                     lambda: _normal_q(seed, "output.weight", D * shape.vocab, quantize_q8_0)))
     else:
         q4("output.weight", D, shape.vocab)
-    return t
+    n = workers if workers > 0 else min(8, os.cpu_count() or 1)
+    if n > 1:
+        with concurrent.futures.ThreadPoolExecutor(n) as pool:
+            data = list(pool.map(lambda j: j[3](), jobs))
+    else:
+        data = [j[3]() for j in jobs]
+    return {name: Tensor(name, dims, typ, d) for (name, dims, typ, _), d in zip(jobs, data)}
 
 
 def prompt_ids(seed: int, n: int, vocab: int) -> list:

@@ -153,6 +153,31 @@ int q4hip_time_head(q4hip* h, int iters, float* us_per_launch);
 /* Release all device memory of the context. */
 void q4hip_destroy(q4hip* h);
 
+/* ---- batched decode -------------------------------------------------------------------------
+ * B independent sequences decoded together, one token each per step, with the context's weights.
+ * The reference decodes one sequence per backend (engine/cpu.js:215-232, engine/llm.js:86-97); a
+ * batch runs B such loops at once, and every sequence's tokens and logits are the ones its own
+ * loop would give.  Each sequence has its own fp32 K/V cache of the context's ctx positions; the
+ * context's activation buffers are shared, so B <= the context's pass size and calls on a batch and
+ * on its context are serialized by the caller.  Destroy batches before their context. */
+typedef struct q4hip_batch q4hip_batch;
+int q4hip_batch_create(q4hip_batch** out, q4hip* h, int B);
+void q4hip_batch_destroy(q4hip_batch* bt);
+/* Run prompt ids[0..n) of sequence `seq` at positions pos.. (as q4hip_forward, against that
+ * sequence's cache) and return its greedy next token. */
+int q4hip_batch_prefill(q4hip_batch* bt, int seq, const int* ids, int n, int pos, int* next);
+/* Write K and V rows of sequence `seq` (as q4hip_set_kv). */
+int q4hip_batch_set_kv(q4hip_batch* bt, int seq, int layer, int kv_head, int pos0, int n, const float* k,
+                       const float* v);
+/* `steps` greedy steps of every sequence: sequence b starts with token first[b] at position pos[b]
+ * (the positions may differ); out[i * B + b] = its token at position pos[b] + 1 + i.  Fails with
+ * Q4HIP_ECONTEXT when pos[b] + steps >= ctx for any b. */
+int q4hip_batch_generate(q4hip_batch* bt, const int* first, const int* pos, int steps, int* out);
+/* The same, timed with HIP events on the context's stream; *ms = device time of all steps. */
+int q4hip_batch_time_generate(q4hip_batch* bt, const int* first, const int* pos, int steps, int* out, float* ms);
+/* Logits of the last step, [B][vocab] floats; n >= B * vocab. */
+int q4hip_batch_read_logits(q4hip_batch* bt, float* out, int64_t n);
+
 /* ---- isolated Q4_0 matvec (the kernel of every projection) ---------------------------------
  * y[n] = W[n] . x for an N x K Q4_0 matrix given in GGUF layout, with x quantized to int8 per
  * 32-block exactly as quantize_row (engine/kernels.c:90-114) and each output accumulated as

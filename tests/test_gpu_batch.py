@@ -1,0 +1,175 @@
+"""Batched decode (q4hip_batch_*) on the GPU against the oracle run one sequence at a time.
+
+The reference decodes one sequence per backend (engine/cpu.js, engine/llm.js:86-97); a batch of B
+sequences must give every sequence the greedy tokens and bit-identical logits its own loop gives.
+Prompts are ragged (positions differ per sequence) and include a one-token prompt.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import synth
+
+pytestmark = pytest.mark.gpu
+
+_cache = {}
+
+
+def _model(name, seed, head_type=synth.GGML_Q4_0):
+    key = (name, seed, head_type)
+    if key not in _cache:
+        _cache[key] = synth.make_model(synth.SHAPES[name], seed, head_type=head_type)
+    return _cache[key]
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _same_logits(lg, lo, what):
+    diff = float(np.max(np.abs(lg - lo)))
+    assert diff <= 1e-3, f"{what}: max-abs logit error {diff}"
+    bad = np.flatnonzero(_bits(lg) != _bits(lo))
+    assert bad.size == 0, f"{what}: {bad.size} logits differ (max-abs {diff}), first {bad[:5]}"
+
+
+def _oracle_loop(o, prompt, steps):
+    """Greedy loop of one sequence on the oracle: (tokens after the prompt, logits of the last step)."""
+    tok = o.forward(prompt, 0)
+    toks = [tok]
+    for i in range(steps):
+        tok = o.forward([tok], len(prompt) + i)
+        toks.append(tok)
+    return toks, o.logits().copy()
+
+
+@pytest.mark.parametrize("name,seed,lens,head_type", [
+    ("tiny", 41, [1, 7, 20, 33, 3], synth.GGML_Q4_0),
+    ("small", 42, [12, 5, 40], synth.GGML_Q4_0),
+    ("small128", 43, [9, 30, 1, 17], synth.GGML_Q4_0),
+    ("small", 44, [6, 19], synth.GGML_Q8_0),
+])
+def test_batch_matches_independent_loops(name, seed, lens, head_type):
+    import q4hip
+    print(f"batch {name} seed {seed} lens {lens} head {head_type}", flush=True)
+    shape = synth.SHAPES[name]
+    t = _model(name, seed, head_type)
+    B, steps, ctx = len(lens), 6, 96
+    rng = np.random.default_rng(seed)
+    prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in lens]
+    g = q4hip.Model(shape, ctx=ctx)
+    g.load(t)
+    o = oracle.Model(shape, t, ctx=ctx, mt=16, threads=8)
+    bt = q4hip.Batch(g, B)
+    try:
+        first = [bt.prefill(b, prompts[b], 0) for b in range(B)]
+        out = bt.generate(first, lens, steps)
+        lg = bt.read_logits()
+        for b in range(B):
+            want, lo = _oracle_loop(o, prompts[b], steps)
+            assert first[b] == want[0], f"sequence {b}: prefill token"
+            assert out[:, b].tolist() == want[1:], f"sequence {b}: tokens"
+            _same_logits(lg[b], lo, f"sequence {b} last step")
+    finally:
+        bt.close()
+        g.close()
+        o.close()
+
+
+def test_batch_steps_continue():
+    """Two generate calls in a row continue each sequence where the first left it, and a batch's
+    decode leaves the context's own cache and single-sequence decode untouched."""
+    import q4hip
+    shape = synth.SHAPES["tiny"]
+    t = _model("tiny", 45)
+    lens = [4, 11, 2]
+    rng = np.random.default_rng(45)
+    prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in lens]
+    g = q4hip.Model(shape, ctx=64)
+    g.load(t)
+    o = oracle.Model(shape, t, ctx=64, mt=16, threads=8)
+    bt = q4hip.Batch(g, 3)
+    try:
+        single = g.forward(prompts[1], 0)
+        first = [bt.prefill(b, prompts[b], 0) for b in range(3)]
+        a = bt.generate(first, lens, 3)
+        pos2 = [n + 3 for n in lens]
+        b2 = bt.generate(a[-1], pos2, 4)
+        both = np.concatenate([a, b2])
+        for b in range(3):
+            want, _ = _oracle_loop(o, prompts[b], 7)
+            assert both[:, b].tolist() == want[1:], f"sequence {b}"
+        # the context's own sequence continues as if no batch had run
+        want1, lo = _oracle_loop(o, prompts[1], 1)
+        assert g.forward([single], lens[1]) == want1[1]
+        _same_logits(g.read_logits(), lo, "context after batch")
+    finally:
+        bt.close()
+        g.close()
+        o.close()
+
+
+def test_batch_prefilled_cache():
+    """Sequences whose caches were written through q4hip_batch_set_kv (a 300-position cache per
+    sequence, different contents) decode as the oracle does over the same cache."""
+    import q4hip
+    shape = synth.SHAPES["small128"]
+    t = _model("small128", 46)
+    P, B, ctx, steps = 300, 3, 320, 4
+    g = q4hip.Model(shape, ctx=ctx)
+    g.load(t)
+    o = oracle.Model(shape, t, ctx=ctx, mt=16, threads=8)
+    bt = q4hip.Batch(g, B)
+    try:
+        caches = []
+        for b in range(B):
+            r = np.random.default_rng(100 + b)
+            k = r.standard_normal((shape.layers, shape.kv_heads, P, shape.head_dim)).astype(np.float16).astype(np.float32)
+            v = r.standard_normal((shape.layers, shape.kv_heads, P, shape.head_dim)).astype(np.float16).astype(np.float32)
+            caches.append((k, v))
+            for l in range(shape.layers):
+                for kh in range(shape.kv_heads):
+                    bt.set_kv(b, l, kh, 0, k[l, kh], v[l, kh])
+        first = [5, 17, 900]
+        pos = [P, P - 40, P - 7]
+        out = bt.generate(first, pos, steps)
+        lg = bt.read_logits()
+        for b in range(B):
+            ok, ov = o.kv()
+            ok[:, :, :P] = caches[b][0]
+            ov[:, :, :P] = caches[b][1]
+            tok = first[b]
+            for i in range(steps):
+                tok = o.forward([tok], pos[b] + i)
+                assert out[i, b] == tok, f"sequence {b} step {i}"
+            _same_logits(lg[b], o.logits(), f"sequence {b}")
+    finally:
+        bt.close()
+        g.close()
+        o.close()
+
+
+def test_batch_errors():
+    import q4hip
+    shape = synth.SHAPES["tiny"]
+    g = q4hip.Model(shape, ctx=32, mt=4)
+    g.load(_model("tiny", 47))
+    try:
+        with pytest.raises(q4hip.Q4Error):
+            q4hip.Batch(g, 5)                      # more sequences than the pass size
+        bt = q4hip.Batch(g, 2)
+        try:
+            with pytest.raises(q4hip.Q4Error) as e:
+                bt.generate([1, 2], [3, 30], 2)    # 30 + 2 >= ctx
+            assert e.value.code == q4hip.ECONTEXT
+            with pytest.raises(q4hip.Q4Error):
+                bt.generate([1, shape.vocab], [0, 0], 1)
+            with pytest.raises(q4hip.Q4Error):
+                bt.prefill(2, [1, 2], 0)
+            with pytest.raises(q4hip.Q4Error):
+                bt.set_kv(0, 0, 0, 31, np.zeros((2, shape.head_dim)), np.zeros((2, shape.head_dim)))
+            assert bt.generate([1, 2], [0, 5], 2).shape == (2, 2)
+        finally:
+            bt.close()
+    finally:
+        g.close()
