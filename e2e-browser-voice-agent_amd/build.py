@@ -20,8 +20,9 @@ NODE_INCLUDE = os.environ.get("NODE_INCLUDE", "/usr/include/node")
 # -ffp-contract=off: no multiply-add fusion, so every binary32 operation rounds once as on the CPU.
 # Correctly rounded fp32 divide and sqrt (hipcc's default, stated explicitly).
 # Packed-FP32 instructions are disabled for all device code.
+# -amdgpu-mfma-vgpr-form: matrix-core results in ordinary VGPRs (they feed vector ALU chains at once).
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
-             "-fhip-fp32-correctly-rounded-divide-sqrt",
+             "-fhip-fp32-correctly-rounded-divide-sqrt", "-mllvm", "-amdgpu-mfma-vgpr-form=1",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-I" + os.path.join(REPO, "include")]
 
