@@ -11,6 +11,11 @@
         --pmc WRITE_SIZE pass), scales each counter by what it reads for the copy kernel, and
         writes a short markdown summary with per-launch and per-step figures.
 
+    python profile_decode.py steps --trace DIR --marker KERNEL --skip N --title T --command C --out FILE
+        Per-step kernel times of a multi-kernel workload from a rocprofv3 kernel trace: the dispatches
+        from the (N+1)-th launch of KERNEL (the first kernel of a step) on, grouped by kernel name
+        and grid, averaged per step (e.g. the batched decode steps of bench.py --workload batched).
+
 The counters are read by rocprofv3 per dispatch, in KiB.  For the persistent kernel they include
 every byte the launch moves between the L2s and the memory fabric: weights, K/V, logits and the
 polling of the exchange area between workgroups.
@@ -144,6 +149,38 @@ def summarize(a) -> None:
     print("\n".join(lines))
 
 
+def steps(a) -> None:
+    rows = _rows(a.trace, "*kernel_trace.csv")
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    marks = [i for i, r in enumerate(rows) if a.marker in r["Kernel_Name"]]
+    if len(marks) <= a.skip:
+        raise SystemExit(f"fewer than {a.skip + 1} launches of {a.marker}")
+    rest = rows[marks[a.skip]:]
+    nsteps = len(marks) - a.skip
+    agg = {}
+    for r in rest:
+        name = r["Kernel_Name"].split("(")[0]
+        key = (name, r.get("Grid_Size_X", "?") + "x" + r.get("Grid_Size_Y", "?"))
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        c = agg.setdefault(key, [0, 0.0])
+        c[0] += 1
+        c[1] += d
+    busy = sum(v[1] for v in agg.values()) / nsteps
+    span = (int(rest[-1]["End_Timestamp"]) - int(rest[0]["Start_Timestamp"])) / 1e3 / nsteps
+    lines = [f"# {a.title}", "", "Commands (repo root on the GPU box, `cd /tmp && export TMPDIR=/tmp` first; paths absolute):",
+             "", "```", a.command,
+             f"python3 e2e-browser-voice-agent_amd/py/profile_decode.py steps --trace T --marker {a.marker} --skip {a.skip} "
+             f"--title ... --command ... --out <this file>", "```", "",
+             f"{nsteps} steps; kernel time {busy:.1f} us per step; first kernel start to last kernel end {span:.1f} us per step.",
+             "", "| kernel | grid (threads x, y) | launches per step | us per step | us per launch |", "|---|---|---|---|---|"]
+    for (name, grid), (n, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        lines.append(f"| {name} | {grid} | {n / nsteps:g} | {t / nsteps:.1f} | {t / n:.1f} |")
+    lines.append("")
+    with open(a.out, "w") as f:
+        f.write("\n".join(lines))
+    print("\n".join(lines))
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -155,9 +192,18 @@ def main() -> None:
     s.add_argument("--write", required=True)
     s.add_argument("--steps", type=int, default=64)
     s.add_argument("--out", required=True)
+    t = sub.add_parser("steps")
+    t.add_argument("--trace", required=True)
+    t.add_argument("--marker", required=True)
+    t.add_argument("--skip", type=int, default=0)
+    t.add_argument("--title", required=True)
+    t.add_argument("--command", required=True)
+    t.add_argument("--out", required=True)
     a = ap.parse_args()
     if a.cmd == "run":
         run(a.steps)
+    elif a.cmd == "steps":
+        steps(a)
     else:
         summarize(a)
 
