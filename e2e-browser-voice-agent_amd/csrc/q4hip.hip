@@ -566,6 +566,12 @@ __global__ __launch_bounds__(256) void k_argmax2(const float* __restrict__ pv, c
   }
 }
 
+// Positions of the M tokens of a pass (pos0 + m), the per-token positions the list attention reads.
+__global__ void k_pass_pos(const State* __restrict__ st, int M, int* __restrict__ pos) {
+  const int m = blockIdx.x * blockDim.x + threadIdx.x;
+  if (m < M) pos[m] = st->pos0 + m;
+}
+
 __global__ void k_set_pos(State* st, int pos0) {
   if (threadIdx.x == 0) st->pos0 = pos0;
 }
@@ -898,7 +904,7 @@ __global__ void k_rope_kv_list(float* __restrict__ qkv, int QKV, int D, int H, i
 //                       (sequence, kv head) recomputes the same softmax from the scores.
 // Scores live in sc [B][H][ctx].
 constexpr int kScoreRows = 64;
-constexpr int kPvCols = 32, kPvRows = 256;
+constexpr int kPvCols = 32;
 constexpr int kMaxGroup = 8;    // query heads per kv head
 
 // Floats per head row of the softmax array: room for every position plus the sum's read-ahead.
@@ -954,13 +960,13 @@ __global__ __launch_bounds__(64) void k_attn_scores_list(const float* __restrict
     if (gh < G) sc[((size_t)b * H + g * G + gh) * score_stride(ctx) + t] = (s[gh][0] + s[gh][1] + s[gh][2] + s[gh][3]) * scale;
 }
 
-template <int HD>
+template <int HD, int CR>
 __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ sc, int H, int KVH,
                                                       const float* __restrict__ vc, int ctx, int layer,
                                                       float* __restrict__ att, int D, const int* __restrict__ pos,
                                                       size_t seq_stride) {
   extern __shared__ __attribute__((aligned(16))) float lsm[];
-  constexpr int CR = kPvRows, CRS = kPvRows + 4, NV = CR * kPvCols / 4 / 256;
+  constexpr int CRS = CR + 4, NV = CR * kPvCols / 4 / 256;      // V rows per chunk (stride), float4 per thread
   constexpr int PB = 2;                   // score float4 per thread and head in one pass (2048 positions)
   const int c0 = blockIdx.x * kPvCols, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, G = H / KVH;
@@ -1352,7 +1358,9 @@ struct q4hip {
   uint4* xq = nullptr;
   uint4* xh = nullptr;     // the same activations as fp16 matrix-core operands (multi-token passes)
   int xstride = 0;   // activation blocks per token row of xq
-  float* ascr = nullptr;   // attention scratch of multi-token passes: [MT][H][ctx] scores, allocated on first use
+  float* ascr = nullptr;   // attention scores of multi-token passes: [MT][H][score_stride(ctx)], allocated on first use
+  int* tpos = nullptr;     // positions of the tokens of a pass
+  int list_attn = -1;      // multi-token passes use the list attention kernels (1), k_attn_prefill (0), unknown (-1)
   float* am_v = nullptr;
   int* am_i = nullptr;
   int am_parts = 0;
@@ -1474,6 +1482,45 @@ void launch_quant(hipStream_t s, int rows, const float* in, int ld_in, int n, co
   k_quant<MODE><<<rows, 256, lds, s>>>(in, ld_in, n, w, eps, xq, xstride, m_first, xh);
 }
 
+// V rows per chunk of k_attn_pv_list: 64 keeps a workgroup at about 48 KB of LDS (three per CU).
+constexpr int kPvRows = 64;
+
+size_t attn_pv_lds(int H, int KVH, int ctx) {
+  const int G = H / KVH;
+  return (size_t)(2 * kPvCols * (kPvRows + 4) + G * pv_row_stride(ctx) + 6 * kMaxGroup) * sizeof(float);
+}
+
+void launch_attn_list(hipStream_t s, int HD, int B, int H, int KVH, const float* qkv, int QKV, const float* kc,
+                      const float* vc, int ctx, int layer, float* sc, float* att, int D, const int* pos,
+                      size_t seq_stride) {
+  const dim3 sg((unsigned)((ctx + kScoreRows - 1) / kScoreRows), (unsigned)KVH, (unsigned)B);
+  const dim3 pg((unsigned)(HD / kPvCols), (unsigned)KVH, (unsigned)B);
+  const size_t lds = attn_pv_lds(H, KVH, ctx);
+  if (HD == 64) {
+    k_attn_scores_list<64><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, seq_stride);
+    k_attn_pv_list<64, kPvRows><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride);
+  } else {
+    k_attn_scores_list<128><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, seq_stride);
+    k_attn_pv_list<128, kPvRows><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride);
+  }
+}
+
+// Whether the list attention kernels take this shape (query heads per kv head, LDS), and their LDS
+// limit raised where needed.  Checked once per shape.
+bool attn_list_ok(int H, int KVH, int HD, int ctx) {
+  if (H / KVH > kMaxGroup) return false;
+  const size_t lds = attn_pv_lds(H, KVH, ctx);
+  if (lds > 160 * 1024) return false;
+  if (lds > 64 * 1024) {
+    const void* fn = HD == 64 ? (const void*)k_attn_pv_list<64, kPvRows> : (const void*)k_attn_pv_list<128, kPvRows>;
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+      (void)hipGetLastError();
+      return false;
+    }
+  }
+  return true;
+}
+
 // One pass over M <= MT tokens at device position st->pos0 (forward_pass, kernels.c:306-415).
 void enqueue_pass(q4hip* h, int M, bool want_logits) {
   const int D = h->D, F = h->F, HD = h->HD, QKV = h->QKV;
@@ -1481,6 +1528,10 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
   uint4* xh = M > 8 ? h->xh : nullptr;
   prof_mark(h, Q4HIP_PROF_EMBED);
   k_embed<<<M, 256, 0, s>>>(h->embd, D, h->tokens, h->st, h->x);
+  if (M > 1) {
+    if (h->list_attn < 0) h->list_attn = attn_list_ok(h->H, h->KVH, HD, h->ctx) ? 1 : 0;
+    if (h->list_attn == 1) k_pass_pos<<<(M + 255) / 256, 256, 0, s>>>(h->st, M, h->tpos);
+  }
   const size_t attn_lds = (size_t)(HD + h->ctx) * sizeof(float);
   for (int l = 0; l < h->NL; l++) {
     Layer& y = h->L[l];
@@ -1491,7 +1542,9 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
     prof_mark(h, Q4HIP_PROF_ROPE);
     k_rope_kv<<<dim3(h->H + h->KVH, M), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, h->kc, h->vc, h->ctx, l, h->st);
     prof_mark(h, Q4HIP_PROF_ATTN);
-    if (M > 1 && h->ascr) {
+    if (M > 1 && h->ascr && h->list_attn == 1) {
+      launch_attn_list(s, HD, M, h->H, h->KVH, h->qkv, QKV, h->kc, h->vc, h->ctx, l, h->ascr, h->att, D, h->tpos, 0);
+    } else if (M > 1 && h->ascr) {
       const dim3 ag(h->H, (M + kAttnTokens - 1) / kAttnTokens);
       if (HD == 64)
         k_attn_prefill<64><<<ag, 256, 0, s>>>(h->qkv, QKV, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, D, h->st, M, h->ascr);
@@ -1722,7 +1775,7 @@ void q4hip_destroy(q4hip* h) {
   }
   mat_free(h->head);
   void* bufs[] = {h->embd, h->out_norm, h->rope, h->x, h->qkv, h->att, h->gu, h->logits, h->kc, h->vc,
-                  h->xq, h->am_v, h->am_i, h->tokens, h->st, h->d_layers, h->ll, h->ascr, h->xh};
+                  h->xq, h->am_v, h->am_i, h->tokens, h->st, h->d_layers, h->ll, h->ascr, h->xh, h->tpos};
   for (void* p : bufs) if (p) (void)hipFree(p);
   if (h->pin_ids) (void)hipHostFree(h->pin_ids);
   if (h->pin_next) (void)hipHostFree(h->pin_next);
@@ -1784,6 +1837,7 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
   TRYHIP(hipMemset(h->vc, 0, kvbytes));
   TRYHIP(hipMalloc(&h->xq, (size_t)M * h->xstride * 64));
   TRYHIP(hipMalloc(&h->xh, (size_t)M * h->xstride * 128));
+  TRYHIP(hipMalloc(&h->tpos, (size_t)M * sizeof(int)));
   h->am_parts = (vocab + 4095) / 4096;
   TRYHIP(hipMalloc(&h->am_v, (size_t)h->am_parts * 4));
   TRYHIP(hipMalloc(&h->am_i, (size_t)h->am_parts * 4));
@@ -1889,7 +1943,7 @@ int q4hip_forward(q4hip* h, const int* ids, int n, int pos, int* next) {
   if (n == 1 && !pers) build_graph(h);
   if (n > 1 && h->MT > 1 && !h->ascr) {
     // scores of a multi-token pass; without it, passes use the per-(token, head) attention kernel
-    if (hipMalloc(&h->ascr, (size_t)h->MT * h->H * h->ctx * sizeof(float)) != hipSuccess) {
+    if (hipMalloc(&h->ascr, (size_t)h->MT * h->H * score_stride(h->ctx) * sizeof(float)) != hipSuccess) {
       h->ascr = nullptr;
       (void)hipGetLastError();
     }
@@ -2026,7 +2080,7 @@ int q4hip_profile_pass(q4hip* h, const int* ids, int ntok, int pos, float* us, i
   rc = check_ids(h, ids, ntok);
   if (rc) return rc;
   HIPCHK(hipSetDevice(h->device));
-  if (ntok > 1 && !h->ascr) (void)hipMalloc(&h->ascr, (size_t)h->MT * h->H * h->ctx * sizeof(float));
+  if (ntok > 1 && !h->ascr) (void)hipMalloc(&h->ascr, (size_t)h->MT * h->H * score_stride(h->ctx) * sizeof(float));
   (void)hipGetLastError();
   memcpy(h->pin_ids, ids, (size_t)ntok * 4);
   HIPCHK(hipMemcpyAsync(h->tokens + pos, h->pin_ids, (size_t)ntok * 4, hipMemcpyHostToDevice, h->stream));
@@ -2127,11 +2181,6 @@ struct q4hip_batch {
 
 namespace {
 
-size_t attn_pv_lds(int H, int KVH, int ctx) {
-  const int G = H / KVH;
-  return (size_t)(2 * kPvCols * (kPvRows + 4) + G * pv_row_stride(ctx) + 6 * kMaxGroup) * sizeof(float);
-}
-
 // One decode step of all B sequences: tokens bt->tok at positions bt->pos; the greedy tokens go to
 // bt->tok (and out[0..B) when given) and every position advances by one.
 void enqueue_batch_step(q4hip_batch* bt, int* out) {
@@ -2146,15 +2195,8 @@ void enqueue_batch_step(q4hip_batch* bt, int* out) {
     launch_matvec<OP_BIAS>(s, y.qkv, h->xq, h->xstride, B, h->qkv, QKV, y.bqkv, xh);
     k_rope_kv_list<<<dim3(h->H + h->KVH, B), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, bt->kc,
                                                              bt->vc, h->ctx, l, bt->pos, bt->seq_stride);
-    const dim3 sg((unsigned)((h->ctx + kScoreRows - 1) / kScoreRows), (unsigned)h->KVH, (unsigned)B);
-    const dim3 pg((unsigned)(HD / kPvCols), (unsigned)h->KVH, (unsigned)B);
-    if (HD == 64) {
-      k_attn_scores_list<64><<<sg, 64, 0, s>>>(h->qkv, QKV, h->H, h->KVH, bt->kc, h->ctx, l, bt->sc, bt->pos, bt->seq_stride);
-      k_attn_pv_list<64><<<pg, 256, bt->attn_lds, s>>>(bt->sc, h->H, h->KVH, bt->vc, h->ctx, l, h->att, D, bt->pos, bt->seq_stride);
-    } else {
-      k_attn_scores_list<128><<<sg, 64, 0, s>>>(h->qkv, QKV, h->H, h->KVH, bt->kc, h->ctx, l, bt->sc, bt->pos, bt->seq_stride);
-      k_attn_pv_list<128><<<pg, 256, bt->attn_lds, s>>>(bt->sc, h->H, h->KVH, bt->vc, h->ctx, l, h->att, D, bt->pos, bt->seq_stride);
-    }
+    launch_attn_list(s, HD, B, h->H, h->KVH, h->qkv, QKV, bt->kc, bt->vc, h->ctx, l, bt->sc, h->att, D, bt->pos,
+                     bt->seq_stride);
     launch_quant<QM_PLAIN>(s, B, h->att, D, D, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
     launch_matvec<OP_ADD>(s, y.o, h->xq, h->xstride, B, h->x, D, nullptr, xh);
     launch_quant<QM_NORM>(s, B, h->x, D, D, y.ffn_norm, h->eps, h->xq, h->xstride, 0, xh);
@@ -2193,11 +2235,8 @@ int q4hip_batch_create(q4hip_batch** out, q4hip* h, int B) {
   if (h->H / h->KVH > kMaxGroup) return fail(Q4HIP_EINVAL, "more than %d query heads per kv head", kMaxGroup);
   HIPCHK(hipSetDevice(h->device));
   const size_t lds = attn_pv_lds(h->H, h->KVH, h->ctx);
-  if (lds > 160 * 1024) return fail(Q4HIP_EINVAL, "ctx %d: batched attention needs %zu bytes of shared memory", h->ctx, lds);
-  if (lds > 64 * 1024) {
-    HIPCHK(hipFuncSetAttribute((const void*)(h->HD == 64 ? (const void*)k_attn_pv_list<64> : (const void*)k_attn_pv_list<128>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-  }
+  if (!attn_list_ok(h->H, h->KVH, h->HD, h->ctx))
+    return fail(Q4HIP_EINVAL, "ctx %d: batched attention needs %zu bytes of shared memory", h->ctx, lds);
   q4hip_batch* bt = new q4hip_batch();
   bt->h = h;
   bt->B = B;
@@ -2256,7 +2295,7 @@ int q4hip_batch_prefill(q4hip_batch* bt, int seq, const int* ids, int n, int pos
   if (rc) return rc;
   HIPCHK(hipSetDevice(h->device));
   if (n > 1 && h->MT > 1 && !h->ascr) {
-    if (hipMalloc(&h->ascr, (size_t)h->MT * h->H * h->ctx * sizeof(float)) != hipSuccess) {
+    if (hipMalloc(&h->ascr, (size_t)h->MT * h->H * score_stride(h->ctx) * sizeof(float)) != hipSuccess) {
       h->ascr = nullptr;
       (void)hipGetLastError();
     }
