@@ -1528,10 +1528,7 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
   uint4* xh = M > 8 ? h->xh : nullptr;
   prof_mark(h, Q4HIP_PROF_EMBED);
   k_embed<<<M, 256, 0, s>>>(h->embd, D, h->tokens, h->st, h->x);
-  if (M > 1) {
-    if (h->list_attn < 0) h->list_attn = attn_list_ok(h->H, h->KVH, HD, h->ctx) ? 1 : 0;
-    if (h->list_attn == 1) k_pass_pos<<<(M + 255) / 256, 256, 0, s>>>(h->st, M, h->tpos);
-  }
+  if (M > 1 && h->list_attn == 1) k_pass_pos<<<(M + 255) / 256, 256, 0, s>>>(h->st, M, h->tpos);
   const size_t attn_lds = (size_t)(HD + h->ctx) * sizeof(float);
   for (int l = 0; l < h->NL; l++) {
     Layer& y = h->L[l];
@@ -1550,6 +1547,8 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
         k_attn_prefill<64><<<ag, 256, 0, s>>>(h->qkv, QKV, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, D, h->st, M, h->ascr);
       else
         k_attn_prefill<128><<<ag, 256, 0, s>>>(h->qkv, QKV, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, D, h->st, M, h->ascr);
+    } else if (M == 1 && h->ascr && h->list_attn == 1) {
+      launch_attn_list(s, HD, 1, h->H, h->KVH, h->qkv, QKV, h->kc, h->vc, h->ctx, l, h->ascr, h->att, D, &h->st->pos0, 0);
     } else if (HD == 64) {
       k_attn<64><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, h->st);
     } else {
@@ -1677,6 +1676,27 @@ bool use_persistent(q4hip* h) {
   if (h->mode == Q4HIP_DECODE_GRAPH) return false;
   setup_persistent(h);
   return h->pers_ok && !h->pers_broken;
+}
+
+// Attention of the multi-kernel path: the list kernels (scores over 64-position workgroups, softmax
+// and P.V per 32-column slice) when the shape admits them, with the [MT][H][ctx] score buffer.
+void prepare_attention(q4hip* h) {
+  if (h->list_attn < 0) h->list_attn = attn_list_ok(h->H, h->KVH, h->HD, h->ctx) ? 1 : 0;
+  if (!h->ascr && (h->list_attn == 1 || h->MT > 1)) {
+    if (hipMalloc(&h->ascr, (size_t)h->MT * h->H * score_stride(h->ctx) * sizeof(float)) != hipSuccess) {
+      h->ascr = nullptr;
+      (void)hipGetLastError();
+    }
+  }
+}
+
+// In AUTO mode, decode steps whose context reaches this many positions run on the multi-kernel path:
+// its attention spreads the scores over many workgroups and reads each kv head's K once, where the
+// persistent kernel streams a kv head's K and V through one workgroup per query head.
+constexpr int kLongDecodePositions = 3072;
+
+bool long_decode(const q4hip* h, int64_t last_pos) {
+  return h->mode == Q4HIP_DECODE_AUTO && h->list_attn == 1 && h->ascr && last_pos >= kLongDecodePositions;
 }
 
 hipError_t launch_persistent(q4hip* h, int steps, unsigned long long* prof = nullptr) {
@@ -1939,15 +1959,9 @@ int q4hip_forward(q4hip* h, const int* ids, int n, int pos, int* next) {
   rc = check_ids(h, ids, n);
   if (rc) return rc;
   HIPCHK(hipSetDevice(h->device));
-  const bool pers = n == 1 && use_persistent(h);
+  prepare_attention(h);
+  const bool pers = n == 1 && use_persistent(h) && !long_decode(h, pos);
   if (n == 1 && !pers) build_graph(h);
-  if (n > 1 && h->MT > 1 && !h->ascr) {
-    // scores of a multi-token pass; without it, passes use the per-(token, head) attention kernel
-    if (hipMalloc(&h->ascr, (size_t)h->MT * h->H * score_stride(h->ctx) * sizeof(float)) != hipSuccess) {
-      h->ascr = nullptr;
-      (void)hipGetLastError();
-    }
-  }
   memcpy(h->pin_ids, ids, (size_t)n * 4);
   HIPCHK(hipMemcpyAsync(h->tokens + pos, h->pin_ids, (size_t)n * 4, hipMemcpyHostToDevice, h->stream));
   for (int c = 0; c < n; c += h->MT) {
@@ -2029,7 +2043,8 @@ static int run_generate(q4hip* h, int first, int pos, int steps, int* out, float
   rc = check_ids(h, &first, 1);
   if (rc) return rc;
   HIPCHK(hipSetDevice(h->device));
-  const bool pers = use_persistent(h);
+  prepare_attention(h);
+  const bool pers = use_persistent(h) && !long_decode(h, (int64_t)pos + steps - 1);
   if (!pers) build_graph(h);
   h->pin_ids[0] = first;
   HIPCHK(hipMemcpyAsync(h->tokens + pos, h->pin_ids, 4, hipMemcpyHostToDevice, h->stream));
@@ -2080,8 +2095,7 @@ int q4hip_profile_pass(q4hip* h, const int* ids, int ntok, int pos, float* us, i
   rc = check_ids(h, ids, ntok);
   if (rc) return rc;
   HIPCHK(hipSetDevice(h->device));
-  if (ntok > 1 && !h->ascr) (void)hipMalloc(&h->ascr, (size_t)h->MT * h->H * score_stride(h->ctx) * sizeof(float));
-  (void)hipGetLastError();
+  prepare_attention(h);
   memcpy(h->pin_ids, ids, (size_t)ntok * 4);
   HIPCHK(hipMemcpyAsync(h->tokens + pos, h->pin_ids, (size_t)ntok * 4, hipMemcpyHostToDevice, h->stream));
   k_set_pos<<<1, 64, 0, h->stream>>>(h->st, pos);
@@ -2294,12 +2308,7 @@ int q4hip_batch_prefill(q4hip_batch* bt, int seq, const int* ids, int n, int pos
   rc = check_ids(h, ids, n);
   if (rc) return rc;
   HIPCHK(hipSetDevice(h->device));
-  if (n > 1 && h->MT > 1 && !h->ascr) {
-    if (hipMalloc(&h->ascr, (size_t)h->MT * h->H * score_stride(h->ctx) * sizeof(float)) != hipSuccess) {
-      h->ascr = nullptr;
-      (void)hipGetLastError();
-    }
-  }
+  prepare_attention(h);
   // the passes run eagerly against this sequence's cache; the context's own cache is untouched
   float* kc = h->kc;
   float* vc = h->vc;
