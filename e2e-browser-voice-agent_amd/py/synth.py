@@ -246,8 +246,89 @@ def _str(s: str) -> bytes:
     return struct.pack("<Q", len(b)) + b
 
 
-def write_gguf(path: str, shape: Shape, tensors: dict, align: int = 32) -> None:
-    """Write a GGUF v3 file with the Qwen2 metadata the reference's qwen2Config reads."""
+# ---------------------------------------------------------------------------- tokenizer
+
+CONTROL_TOKEN = 3
+SPECIALS = ["<|endoftext|>", "<|im_start|>", "<|im_end|>"]
+_CORPUS = (
+    "The quick brown fox jumps over the lazy dog. It's a sunny day; we're going to the park, "
+    "aren't we? She'll read 3 books and 12 poems in 2024. Numbers like 42, 7 and 1000 appear often.\n"
+    "Caf\u00e9 cr\u00e8me br\u00fbl\u00e9e, na\u00efve r\u00e9sum\u00e9, \u00fcber stra\u00dfe. "
+    "\u4f60\u597d\uff0c\u4e16\u754c\uff01 \u3053\u3093\u306b\u3061\u306f "
+    "\u041f\u0440\u0438\u0432\u0435\u0442 \U0001f600\U0001f680 hello world\n\n"
+    "You are a helpful assistant. The user asks a question and the assistant answers it. "
+    "system user assistant hello hello hello the the the and and of of to to in in is is it it\n"
+)
+
+
+def byte_chars() -> list:
+    """GPT-2's printable stand-in for each byte value (printable Latin-1 bytes stand for themselves,
+    the other 68 take code points 256, 257, ... in byte order)."""
+    printable = lambda b: 33 <= b <= 126 or 161 <= b <= 172 or 174 <= b <= 255  # noqa: E731
+    out, extra = [], 0
+    for b in range(256):
+        if printable(b):
+            out.append(chr(b))
+        else:
+            out.append(chr(256 + extra))
+            extra += 1
+    return out
+
+
+def make_tokenizer(vocab: int, seed: int = 0) -> dict:
+    """A byte-level BPE tokenizer in GGUF form for a synthetic model of `vocab` ids: the 256 byte
+    symbols, merges learned greedily from a small built-in multilingual corpus, the three ChatML
+    special tokens, and reserved control tokens up to `vocab`.  Deterministic (`seed` only names the
+    reserved tokens).  Returns {tokens, token_type, merges, eos}."""
+    import regex
+    split = regex.compile(r"""(?:'[sS]|'[tT]|'[rR][eE]|'[vV][eE]|'[mM]|'[lL][lL]|'[dD])|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}| ?[^\s\p{L}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+""")
+    bc = byte_chars()
+    words = {}
+    for piece in split.findall(_CORPUS):
+        w = tuple(bc[b] for b in piece.encode("utf-8"))
+        words[w] = words.get(w, 0) + 1
+    tokens = list(bc)
+    n_merges = max(0, vocab - 256 - len(SPECIALS) - 8)
+    merges = []
+    while len(merges) < n_merges:
+        pairs = {}
+        for w, c in words.items():
+            for a, b in zip(w, w[1:]):
+                pairs[(a, b)] = pairs.get((a, b), 0) + c
+        if not pairs:
+            break
+        (a, b), _ = max(pairs.items(), key=lambda kv: (kv[1], kv[0]))
+        merges.append(f"{a} {b}")
+        tokens.append(a + b)
+        nw = {}
+        for w, c in words.items():
+            out, i = [], 0
+            while i < len(w):
+                if i + 1 < len(w) and w[i] == a and w[i + 1] == b:
+                    out.append(a + b)
+                    i += 2
+                else:
+                    out.append(w[i])
+                    i += 1
+            nw[tuple(out)] = nw.get(tuple(out), 0) + c
+        words = nw
+    types = [1] * len(tokens)
+    for sp in SPECIALS:
+        tokens.append(sp)
+        types.append(CONTROL_TOKEN)
+    k = 0
+    while len(tokens) < vocab:
+        tokens.append(f"<|reserved_{seed}_{k}|>")
+        types.append(CONTROL_TOKEN)
+        k += 1
+    if len(tokens) > vocab:
+        raise ValueError(f"vocab {vocab} too small for the tokenizer")
+    return {"tokens": tokens, "token_type": types, "merges": merges, "eos": tokens.index("<|im_end|>")}
+
+
+def write_gguf(path: str, shape: Shape, tensors: dict, align: int = 32, tokenizer: dict = None) -> None:
+    """Write a GGUF v3 file with the Qwen2 metadata the reference's qwen2Config reads; with
+    `tokenizer` (make_tokenizer) also its vocabulary, token types and merges."""
     meta = [
         ("general.architecture", 8, "qwen2"),
         ("general.alignment", 4, align),
@@ -259,7 +340,7 @@ def write_gguf(path: str, shape: Shape, tensors: dict, align: int = 32) -> None:
         ("qwen2.rope.freq_base", 6, shape.rope_theta),
         ("qwen2.attention.layer_norm_rms_epsilon", 6, shape.eps),
         ("qwen2.context_length", 4, shape.context_length),
-        ("tokenizer.ggml.eos_token_id", 4, shape.vocab - 1),
+        ("tokenizer.ggml.eos_token_id", 4, tokenizer["eos"] if tokenizer else shape.vocab - 1),
     ]
     kv = bytearray()
     for k, typ, v in meta:
@@ -270,9 +351,16 @@ def write_gguf(path: str, shape: Shape, tensors: dict, align: int = 32) -> None:
             kv += struct.pack("<I", v)
         elif typ == 6:
             kv += struct.pack("<f", v)
-    kv += _str("tokenizer.ggml.tokens") + struct.pack("<IIQ", 9, 8, shape.vocab)
-    kv += b"".join(_str(f"t{i}") for i in range(shape.vocab))
+    names = tokenizer["tokens"] if tokenizer else [f"t{i}" for i in range(shape.vocab)]
+    kv += _str("tokenizer.ggml.tokens") + struct.pack("<IIQ", 9, 8, len(names))
+    kv += b"".join(_str(t) for t in names)
     n_kv = len(meta) + 1
+    if tokenizer:
+        kv += _str("tokenizer.ggml.token_type") + struct.pack("<IIQ", 9, 5, len(tokenizer["token_type"]))
+        kv += b"".join(struct.pack("<i", t) for t in tokenizer["token_type"])
+        kv += _str("tokenizer.ggml.merges") + struct.pack("<IIQ", 9, 8, len(tokenizer["merges"]))
+        kv += b"".join(_str(m) for m in tokenizer["merges"])
+        n_kv += 2
 
     infos = bytearray()
     offset = 0

@@ -5,12 +5,15 @@
 //   generate <gguf> <ctx> <ids.json> <steps> <logits.f32>
 //        -> {tokens (per-step forward loop), device (device loop), stats}; last logits written raw
 //   sample <logits.f32> <temperature> <seed>      -> {id}
+//   tokenize <meta.json> <texts.json>              -> {ids, text, pieces} per text (tokenizer alone)
+//   chat <gguf> <ctx> <turns.json> <maxTokens>     -> per turn {pieces, ids, prompt, stats}
 const fs = require("fs");
 const path = require("path");
 const engine = path.join(__dirname, "..", "..", "e2e-browser-voice-agent_amd", "engine");
 const { parseGGUF, qwen2Config, readModel } = require(path.join(engine, "gguf.js"));
 const { LLM } = require(path.join(engine, "llm.js"));
 const { sample } = require(path.join(engine, "hip.js"));
+const { Tokenizer, chatPrompt } = require(path.join(engine, "tokenizer.js"));
 
 async function main() {
   const [cmd, ...args] = process.argv.slice(2);
@@ -47,6 +50,32 @@ async function main() {
     const b = fs.readFileSync(args[0]);
     const lg = new Float32Array(b.buffer, b.byteOffset, b.length / 4);
     return { id: sample(lg, Number(args[1]), Number(args[2]) >>> 0) };
+  }
+  if (cmd === "tokenize") {
+    const tok = new Tokenizer(JSON.parse(fs.readFileSync(args[0], "utf8")));
+    const texts = JSON.parse(fs.readFileSync(args[1], "utf8"));
+    return texts.map((t) => {
+      const ids = tok.encode(t);
+      const dec = tok.streamDecoder();
+      return { ids, text: tok.decode(ids), pieces: ids.map((id) => dec(id)) };
+    });
+  }
+  if (cmd === "chat") {
+    const turns = JSON.parse(fs.readFileSync(args[2], "utf8"));
+    const maxTokens = Number(args[3]);
+    const llm = await LLM.load({ path: args[0], ctx: Number(args[1]) });
+    const out = [];
+    const history = [];
+    for (const user of turns) {
+      history.push({ role: "user", content: user });
+      const prompt = llm.tok.encode(chatPrompt(history));
+      const pieces = [];
+      for await (const p of llm.chat(history, { maxTokens, temperature: 0 })) pieces.push(p);
+      out.push({ pieces, ids: llm.stats.ids, text: llm.tok.decode(llm.stats.ids), prompt, stats: llm.stats });
+      history.push({ role: "assistant", content: pieces.join("") });
+    }
+    llm.destroy();
+    return out;
   }
   throw new Error(`unknown command ${cmd}`);
 }

@@ -115,3 +115,143 @@ def test_q8_head_through_napi_matches_oracle(tmp_path):
     lg = np.frombuffer((tmp_path / "lg.f32").read_bytes(), np.float32)
     assert np.array_equal(lg.view(np.uint32), o.logits().view(np.uint32))
     o.close()
+
+
+# ---------------------------------------------------------------------------- tokenizer and chat
+
+TEXTS = [
+    "Hello world",
+    "The quick brown fox jumps over the lazy dog.",
+    "It's we're they'll I'd don't DON'T",
+    "numbers 1234567 and 3.14159, dates 2024-01-31",
+    "  leading spaces and trailing   ",
+    "line one\nline two\n\n\nthree\r\n",
+    "Café crème brûlée naïve",
+    "é composed by NFC",
+    "你好，世界！ こんにちは",
+    "emoji \U0001f600\U0001f680\U0001f44d\U0001f3fd end",
+    "<|im_start|>user\nhi<|im_end|>\n<|im_start|>assistant\n",
+    "tabs\tand non-breaking spaces",
+    "",
+]
+
+
+def _py_bpe_ids(tk, text):
+    """Independent byte-level BPE (GPT-2 style) over the same vocabulary: NFC, split on the special
+    tokens, Qwen2 pre-tokenization, then repeatedly merge the lowest-ranked adjacent pair."""
+    import unicodedata
+    import regex
+    split = regex.compile(r"""(?:'[sS]|'[tT]|'[rR][eE]|'[vV][eE]|'[mM]|'[lL][lL]|'[dD])|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}| ?[^\s\p{L}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+""")
+    ids = {t: i for i, t in reversed(list(enumerate(tk["tokens"])))}
+    ranks = {m: i for i, m in reversed(list(enumerate(tk["merges"])))}
+    bc = synth.byte_chars()
+    specials = sorted([t for t, ty in zip(tk["tokens"], tk["token_type"]) if ty == 3], key=len, reverse=True)
+    text = unicodedata.normalize("NFC", text)
+    out = []
+    parts = regex.split("(" + "|".join(regex.escape(s) for s in specials) + ")", text)
+    for k, part in enumerate(parts):
+        if not part:
+            continue
+        if k % 2 == 1:
+            out.append(ids[part])
+            continue
+        for piece in split.findall(part):
+            word = [bc[b] for b in piece.encode("utf-8")]
+            while len(word) > 1:
+                pairs = [(ranks.get(f"{a} {b}", 1 << 30), i) for i, (a, b) in enumerate(zip(word, word[1:]))]
+                r, _ = min(pairs)
+                if r == 1 << 30:
+                    break
+                a, b = tk["merges"][r].split(" ")
+                merged, i = [], 0
+                while i < len(word):
+                    if i + 1 < len(word) and word[i] == a and word[i + 1] == b:
+                        merged.append(a + b)
+                        i += 2
+                    else:
+                        merged.append(word[i])
+                        i += 1
+                word = merged
+            out.extend(ids[w] for w in word)
+    return out
+
+
+def test_tokenizer_matches_independent_bpe(tmp_path):
+    """engine/tokenizer.js against an independent Python BPE over a synthetic vocabulary (256 byte
+    symbols, merges learned from a multilingual corpus, ChatML specials): ids, decode round trip,
+    and the streaming decoder (emoji split over byte tokens come out whole).  The reference's real
+    vocabulary is only in the 429 MB model file, so parity on it is unpinned."""
+    tk = synth.make_tokenizer(4096)
+    meta = {"tokenizer.ggml.tokens": tk["tokens"], "tokenizer.ggml.token_type": tk["token_type"],
+            "tokenizer.ggml.merges": tk["merges"]}
+    mp, tp = tmp_path / "meta.json", tmp_path / "texts.json"
+    mp.write_text(json.dumps(meta))
+    tp.write_text(json.dumps(TEXTS))
+    res = node("tokenize", mp, tp)
+    import unicodedata
+    for text, r in zip(TEXTS, res):
+        want = _py_bpe_ids(tk, text)
+        assert r["ids"] == want, (text, r["ids"], want)
+        assert r["text"] == unicodedata.normalize("NFC", text)
+        assert "".join(r["pieces"]) == r["text"]
+        assert all("�" not in p for p in r["pieces"]), r["pieces"]
+    # merges shorten the ids of text the corpus covered; bytes always round trip
+    assert len(res[1]["ids"]) < len(TEXTS[1].encode())
+    assert any(len(p) == 0 for p in res[9]["pieces"])      # a partial emoji yields no text yet
+
+
+def test_chat_prompt_template():
+    """chatPrompt: Qwen2.5's ChatML with the default system message when none is given."""
+    r = subprocess.run(["node", "-e", """
+const { chatPrompt } = require(process.argv[1]);
+process.stdout.write(JSON.stringify([chatPrompt([{role: "user", content: "hi"}]),
+  chatPrompt([{role: "system", content: "S"}, {role: "user", content: "a"}, {role: "assistant", content: "b"}], false)]));
+""", os.path.join(REPO, "e2e-browser-voice-agent_amd", "engine", "tokenizer.js")], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    a, b = json.loads(r.stdout)
+    assert a == ("<|im_start|>system\nYou are Qwen, created by Alibaba Cloud. You are a helpful assistant.<|im_end|>\n"
+                 "<|im_start|>user\nhi<|im_end|>\n<|im_start|>assistant\n")
+    assert b == "<|im_start|>system\nS<|im_end|>\n<|im_start|>user\na<|im_end|>\n<|im_start|>assistant\nb<|im_end|>\n"
+
+
+def _chatml(k, res, turns=("Hello there, how are you?", "Tell me about the quick brown fox.")):
+    sysm = "You are Qwen, created by Alibaba Cloud. You are a helpful assistant."
+    s = f"<|im_start|>system\n{sysm}<|im_end|>\n"
+    for i in range(k + 1):
+        s += f"<|im_start|>user\n{turns[i]}<|im_end|>\n"
+        if i < k:
+            s += f"<|im_start|>assistant\n{''.join(res[i]['pieces'])}<|im_end|>\n"
+    return s + "<|im_start|>assistant\n"
+
+
+@pytest.mark.gpu
+def test_chat_through_napi_matches_oracle(tmp_path):
+    """LLM.chat on the GPU (tiny model with a synthetic tokenizer in its GGUF): the streamed text is
+    the decode of the generated ids, the ids are the oracle's greedy continuation of the encoded
+    ChatML prompt (up to an end-of-text id or maxTokens), and the second turn runs only what the
+    cache lacks."""
+    import oracle
+    shape = synth.SHAPES["tiny"]
+    tk = synth.make_tokenizer(shape.vocab)
+    t = synth.make_model(shape, 78)
+    p = str(tmp_path / "chat.gguf")
+    synth.write_gguf(p, shape, t, tokenizer=tk)
+    turns = tmp_path / "turns.json"
+    turns.write_text(json.dumps(["Hello there, how are you?", "Tell me about the quick brown fox."]))
+    res = node("chat", p, 512, turns, 12)
+    o = oracle.Model(shape, t, ctx=512, mt=16, threads=8)
+    try:
+        for k, r in enumerate(res):
+            ids = r["prompt"]
+            assert ids == _py_bpe_ids(tk, _chatml(k, res)), k
+            want, tok = [], o.forward(ids, 0)
+            while tok not in (tk["eos"], tk["tokens"].index("<|endoftext|>")) and len(want) < 12:
+                want.append(tok)
+                tok = o.forward([tok], len(ids) + len(want) - 1)
+            assert r["ids"] == want, (k, r["ids"], want)
+            joined = "".join(r["pieces"])            # streamed: an incomplete last character is held back
+            assert r["text"].startswith(joined) and r["text"][len(joined):] in ("", "\ufffd"), (joined, r["text"])
+        assert res[0]["stats"]["reused"] == 0
+        assert res[1]["stats"]["reused"] > 0 and res[1]["stats"]["prefilled"] < len(res[1]["prompt"])
+    finally:
+        o.close()
