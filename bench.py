@@ -90,13 +90,35 @@ def cpu_baseline(shape, tensors, ids, first_tokens):
         times.append(time.perf_counter() - t0)
         toks.append(nxt)
         pos += 1
+    # the same decode on one thread (a few tokens)
+    o.set_threads(1)
+    one = []
+    budget = time.time() + 6.0
+    while len(one) < 8 and time.time() < budget:
+        t0 = time.perf_counter()
+        o.forward([toks[len(one)]], len(ids) + len(one))
+        one.append(time.perf_counter() - t0)
     o.close()
     agree = toks[:len(first_tokens)] == first_tokens[:len(toks)]
     med = statistics.median(times)
+    med1 = statistics.median(one)
     return {"value": round(1.0 / med, 3), "unit": "tokens/s", "cores": decode_threads, "kind": "port",
             "sample": f"oracle (C restatement of kernels.c) decode of {len(times)} greedy tokens after the same "
                       f"64-token prompt, median ms/token {med * 1e3:.1f}, {decode_threads} of {cores} threads",
-            "tokens_agree_with_gpu": bool(agree)}
+            "tokens_agree_with_gpu": bool(agree),
+            "one_thread": {"value": round(1.0 / med1, 3), "unit": "tokens/s", "tokens": len(one)},
+            "cpu_model": cpu_model()}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -334,7 +356,9 @@ def bench_prefill(args):
 
 
 def bench_matvec(args):
-    """The isolated matvec (y = W x, x quantized per 32-block) at the model's five shapes, cache-hot."""
+    """The isolated matvec (y = W x, x quantized per 32-block) at the model's five shapes: cache-hot (the
+    same weights every launch) and cold (launches cycle through copies of the weights totalling more than
+    the 256 MB last-level cache)."""
     import numpy as np
     import q4hip
     import synth
@@ -346,16 +370,19 @@ def bench_matvec(args):
         mv = q4hip.Matvec(raw, N, K)
         mv.time(args.warmup)
         us = mv.time(args.steps)
+        cold_us, copies = mv.time_cold(args.steps)
         mv.close()
         nbytes = N * K // 32 * 18 + K * 4 + N * 4
-        rows.append({"shape": [N, K], "us": round(us, 2), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1)})
+        rows.append({"shape": [N, K], "us": round(us, 2), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "cold_us": round(cold_us, 2), "cold_gbps": round(nbytes / (cold_us * 1e-6) / 1e9, 1),
+                     "cold_copies": copies})
     head = rows[-1]
     out = {
         "metric": "isolated Q4_0 matvec achieved GB/s (Qwen2.5-0.5B shapes, fp32 x quantized per 32-block)",
         "value": head["gbps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(head["us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "i8xq4/f32", "data": "synthetic",
-        "config": {"workload": "Q4_0 matvec sweep, value = the 151936x896 head shape, cache-hot",
+        "config": {"workload": "Q4_0 matvec sweep, value = the 151936x896 head shape, cache-hot (cold per shape)",
                    "shapes": [r["shape"] for r in rows], "parallelism": "single-gpu"},
         "per_shape": rows,
         "roofline": {"bound": "hbm", "kernel": "k_matvec<1> 151936x896", "achieved": head["gbps"],

@@ -2474,4 +2474,49 @@ int q4hip_mv_time(q4hip_mv* m, int iters, float* us) {
   return Q4HIP_OK;
 }
 
+int q4hip_mv_time_cold(q4hip_mv* m, int64_t rotate_bytes, int iters, float* us, int* copies_used) {
+  if (!m || !us || iters <= 0 || rotate_bytes < 0) return fail(Q4HIP_EINVAL, "bad argument");
+  HIPCHK(hipSetDevice(m->device));
+  const Mat& W = m->W;
+  const size_t qb = (size_t)W.Np * W.ng * 64 + kWeightPadQ, db = (size_t)W.Np * W.nb8 * 16 + kWeightPadD;
+  const size_t qa = (qb + 255) / 256 * 256, per = qa + (db + 255) / 256 * 256;
+  const int copies = (int)std::max<int64_t>(2, (rotate_bytes + (int64_t)per - 1) / (int64_t)per);
+  uint8_t* buf = nullptr;
+  HIPCHK(hipMalloc(&buf, per * copies));
+  hipError_t e = hipSuccess;
+  std::vector<Mat> views(copies, W);
+  for (int c = 0; c < copies && e == hipSuccess; c++) {
+    uint8_t* base = buf + per * c;
+    views[c].qs = (uint32_t*)base;
+    views[c].d = (uint16_t*)(base + qa);
+    e = hipMemcpyAsync(views[c].qs, W.qs, qb, hipMemcpyDeviceToDevice, m->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(views[c].d, W.d, db, hipMemcpyDeviceToDevice, m->stream);
+  }
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  float ms = 0.0f;
+  if (e == hipSuccess) e = hipEventCreate(&e0);
+  if (e == hipSuccess) e = hipEventCreate(&e1);
+  if (e == hipSuccess) {
+    for (int i = 0; i < copies; i++)   // one pass over every copy before timing
+      launch_matvec<OP_STORE>(m->stream, views[i], m->xq, W.nb, 1, m->y, W.N, nullptr);
+    e = hipEventRecord(e0, m->stream);
+  }
+  if (e == hipSuccess) {
+    for (int i = 0; i < iters; i++)
+      launch_matvec<OP_STORE>(m->stream, views[i % copies], m->xq, W.nb, 1, m->y, W.N, nullptr);
+    e = hipEventRecord(e1, m->stream);
+  }
+  if (e == hipSuccess) e = hipGetLastError();
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  (void)hipStreamSynchronize(m->stream);
+  (void)hipFree(buf);
+  if (e != hipSuccess) return fail(Q4HIP_EHIP, "cold matvec timing: %s", hipGetErrorString(e));
+  *us = ms * 1000.0f / iters;
+  if (copies_used) *copies_used = copies;
+  return Q4HIP_OK;
+}
+
 }  // extern "C"

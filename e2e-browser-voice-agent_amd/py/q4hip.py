@@ -28,7 +28,7 @@ EXPORTS = [
     "q4hip_mv_destroy", "q4hip_set_decode_mode", "q4hip_decode_mode_used", "q4hip_profile_persistent",
     "q4hip_set_kv", "q4hip_profile_pass", "q4hip_batch_create", "q4hip_batch_destroy",
     "q4hip_batch_prefill", "q4hip_batch_set_kv", "q4hip_batch_generate", "q4hip_batch_time_generate",
-    "q4hip_batch_read_logits",
+    "q4hip_batch_read_logits", "q4hip_mv_time_cold",
 ]
 
 _lib = None
@@ -77,6 +77,7 @@ def lib() -> ctypes.CDLL:
         "q4hip_batch_generate": (I, [P, P, P, I, P]),
         "q4hip_batch_time_generate": (I, [P, P, P, I, P, ctypes.POINTER(F)]),
         "q4hip_batch_read_logits": (I, [P, P, I64]),
+        "q4hip_mv_time_cold": (I, [P, I64, I, ctypes.POINTER(F), ctypes.POINTER(I)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -301,6 +302,12 @@ class Matvec:
         us = ctypes.c_float(0)
         _check(lib().q4hip_mv_time(self.h, iters, ctypes.byref(us)))
         return us.value
+
+    def time_cold(self, iters: int, rotate_bytes: int = 320 << 20) -> tuple:
+        """(us per launch, copies): launches cycling through copies of W totalling >= rotate_bytes."""
+        us, n = ctypes.c_float(0), ctypes.c_int(0)
+        _check(lib().q4hip_mv_time_cold(self.h, rotate_bytes, iters, ctypes.byref(us), ctypes.byref(n)))
+        return us.value, n.value
 
     def close(self) -> None:
         if self.h:

@@ -189,6 +189,10 @@ int q4hip_mv_create(q4hip_mv** out, int N, int K, const void* gguf_q4_0, int dev
 int q4hip_mv_run(q4hip_mv* m, const float* x, float* y);
 /* Run `iters` matvecs on the resident x; *us = mean HIP-event duration per launch. */
 int q4hip_mv_time(q4hip_mv* m, int iters, float* us);
+/* The same with the weights not in any cache: `iters` launches cycling through device copies of W
+ * whose total size is at least `rotate_bytes` (e.g. more than the 256 MB last-level cache);
+ * *copies_used (optional) receives the number of copies. */
+int q4hip_mv_time_cold(q4hip_mv* m, int64_t rotate_bytes, int iters, float* us, int* copies_used);
 void q4hip_mv_destroy(q4hip_mv* m);
 
 #ifdef __cplusplus
