@@ -53,6 +53,10 @@ struct PArgs {
   int kv_tile;    // past positions of K and V the attention role stages in shared memory
   int ring;       // slots (kRingRows positions each) of the ring that streams the rest: 3 or 7
   int nap;        // sleep between polls of a wait, in units of 64 cycles
+  int asplit;     // attention workgroups per head: 1, or 2 for long contexts -- the pair splits the
+                  // past positions for the scores (exchanged through lsc) and the 64 output
+                  // columns for P.V, so each streams half of K and half of V
+  uint64_t* lsc;  // [H][ctx] score entries of the pair exchange (asplit 2)
   unsigned long long* prof;   // optional: phase timestamps of step 0, [(NL + 1) * 16]
 };
 
@@ -886,6 +890,20 @@ __device__ __forceinline__ void ring_wait(int slots) {
 
 __device__ __forceinline__ void ring_drain() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
 
+// Half-width slots for the split attention's P.V: kVRows rows x 32 of the 64 columns (from c0), the
+// footprint of a full slot and, like it, three instructions per wave (ring_wait applies).
+constexpr int kVRows = 96;
+__device__ __forceinline__ void ring_issue_half(const float* src, int t0, int ctx, int c0, float* slot) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+#pragma unroll
+  for (int k = 0; k < 3; k++) {
+    const int i = wave + 4 * k;
+    const int t = t0 + 8 * i + (lane >> 3);
+    const float* g = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + c0 + 4 * (lane & 7);
+    __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + i * 256), 16, 0, 0);
+  }
+}
+
 // ---------------------------------------------------------------- roles (one step each)
 
 // o and down rows 16w..16w+15 for wave W's share of the blocks; the residual x of those rows lives
@@ -984,8 +1002,10 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
   constexpr int GRP = S::H / S::KVH;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), r = lane >> 2, j = lane & 3;
   const int E = 4 * a.NL + 1;
-  const int h = blockIdx.x - S::nOD, kh = h / GRP;
-  const bool writer = (h % GRP) == 0;
+  const int aidx = blockIdx.x - S::nOD, h = aidx % S::H, half = aidx / S::H, kh = h / GRP;
+  const bool split = a.asplit > 1;
+  const bool writer = (h % GRP) == 0 && half == 0;
+  const bool mark = aidx == 0;
   const int rq = (h * kHD) / 16 + wave, rk = (S::D + kh * kHD) / 16 + wave;
   const int rv = (S::D + S::KVH * kHD + kh * kHD) / 16 + wave;
   float* qv = m.qv;
@@ -996,7 +1016,14 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
   const int vstride = kv_vstride(a.kv_tile);
   float* kt = ring + (size_t)a.ring * kRingRows * kHD;     // [kv_tile][kKVRow] K
   float* vT = kt + (size_t)(a.kv_tile + 16) * kKVRow;      // [64][vstride] V transposed
-  const int nt = pos < a.kv_tile ? pos : a.kv_tile;   // staged past positions
+  const int nt = split ? 0 : (pos < a.kv_tile ? pos : a.kv_tile);   // staged past positions
+  // K rows streamed for the scores: [kbeg, kend) in chunks of kRingRows -- positions [nt, pos), or
+  // in split mode this workgroup's half of the chunks of [0, pos) (the other half: [obeg, oend))
+  const int nall = (pos + kRingRows - 1) / kRingRows;
+  const int kbeg = split ? (half == 0 ? 0 : (nall / 2) * kRingRows) : nt;
+  const int kend = split ? (half == 0 ? (nall / 2) * kRingRows : pos) : pos;
+  const int obeg = split ? (half == 0 ? (nall / 2) * kRingRows : 0) : 0;
+  const int oend = split ? (half == 0 ? pos : (nall / 2) * kRingRows) : 0;
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
     WR<S::NGD> w3[3];
@@ -1045,23 +1072,23 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
         }
       }
     }
-    // past positions [nt, pos) stream through the ring; its first K slots load during the wait
-    const int nstream = pos - nt, nck = (nstream + kRingRows - 1) / kRingRows;
+    // past positions [kbeg, kend) stream through the ring; its first K slots load during the wait
+    const int nstream = kend - kbeg, nck = (nstream + kRingRows - 1) / kRingRows;
     const float* kgl = a.kc + cbase;
     const float* vgl = a.vc + cbase;
     if (nck > 0)
       for (int c = 0; c < a.ring - 1; c++)
-        ring_issue(kgl, nt + (c < nck ? c : nck - 1) * kRingRows, a.ctx, ring + (size_t)c * kRingRows * kHD);
+        ring_issue(kgl, kbeg + (c < nck ? c : nck - 1) * kRingRows, a.ctx, ring + (size_t)c * kRingRows * kHD);
     if (l == 0) {
       for (int i = tid; i < S::D; i += kPThreads) stage_x<S>(m, i, embed_value(a.embd, S::D, tok, i));
     } else {
       recv_x<S>(a.ll + S::oX2, phase_epoch(ep0, s, E, 4 * (l - 1) + 3), a.st, m, bad, a.nap);
     }
     if (__syncthreads_or(bad)) return false;
-    if (h == 0) prof_mark(a, s, l * 16 + 4);
+    if (mark) prof_mark(a, s, l * 16 + 4);
     prof_wg(a, s, l, 0);
     norm_quant<S>(m, nw, a.eps);
-    if (h == 0) prof_mark(a, s, l * 16 + 9);
+    if (mark) prof_mark(a, s, l * 16 + 9);
     float acc[3] = {0.0f, 0.0f, 0.0f};
     wr_dot<S::NBD, 0, S::NGD, 3>(w3, m.xq, j, acc);
     const float q = hsum4(acc[0]), k = hsum4(acc[1]), v = hsum4(acc[2]);
@@ -1071,7 +1098,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       vv[16 * wave + r] = v + bvv;
     }
     __syncthreads();
-    if (h == 0) prof_mark(a, s, l * 16 + 5);
+    if (mark) prof_mark(a, s, l * 16 + 5);
     // RoPE (kernels.c:340-344): threads 0..31 rotate q pairs, 32..63 k pairs
     if (tid < 64) {
       const int i = tid & 31;
@@ -1081,7 +1108,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       x[i + 32] = x1 * rc + x0 * rsn;
     }
     __syncthreads();
-    if (h == 0) prof_mark(a, s, l * 16 + 11);
+    if (mark) prof_mark(a, s, l * 16 + 11);
     if (writer && tid < 64) {
       st_coherent(a.kc + cbase + (size_t)pos * kHD + tid, kv[tid]);
       st_coherent(a.vc + cbase + (size_t)pos * kHD + tid, vv[tid]);
@@ -1145,38 +1172,126 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
           for (int i = 0; i < kHD / 4; i++) sj = sj + qv[4 * i + pj] * slot[pr * kHD + 4 * i + pj];
         }
         const float s1 = __shfl_down(sj, 1, 4), s2 = __shfl_down(sj, 2, 4), s3 = __shfl_down(sj, 3, 4);
-        const int t = nt + c * kRingRows + pr;
-        if (pj == 0 && pr < kRingRows && t < pos) {
+        const int t = kbeg + c * kRingRows + pr;
+        if (pj == 0 && pr < kRingRows && t < kend) {
           const float sv = (((sj + s1) + s2) + s3) * scale;
           sc[t] = sv;
           lmax = __builtin_fmaxf(lmax, sv);
         }
         const int cn = c + R - 1;
-        ring_issue(kgl, nt + (cn < nck ? cn : nck - 1) * kRingRows, a.ctx, ring + (size_t)(cn % R) * kRingRows * kHD);
+        ring_issue(kgl, kbeg + (cn < nck ? cn : nck - 1) * kRingRows, a.ctx, ring + (size_t)(cn % R) * kRingRows * kHD);
       }
       ring_drain();
       __syncthreads();
       // the ring is free: the first V slots stream in while exp, sum and division run
-      for (int c = 0; c < R - 1; c++) ring_issue(vgl, nt + (c < nck ? c : nck - 1) * kRingRows, a.ctx, ring + (size_t)c * kRingRows * kHD);
+      if (!split)
+        for (int c = 0; c < R - 1; c++)
+          ring_issue(vgl, nt + (c < nck ? c : nck - 1) * kRingRows, a.ctx, ring + (size_t)c * kRingRows * kHD);
+    }
+    const int nckv = split ? (pos + kVRows - 1) / kVRows : 0;     // split P.V: half-width V slots
+    if (split) {
+      // the pair exchanges its scores: publish [kbeg, kend), receive [obeg, oend) (8 entries in
+      // flight per thread, missing ones polled again; bounded like every wait)
+      const uint32_t eps = phase_epoch(ep0, s, E, 4 * l + 0);
+      uint64_t* ex = a.lsc + (size_t)h * a.ctx;
+      for (int t = kbeg + tid; t < kend; t += kPThreads) ll_put(ex + t, __float_as_uint(sc[t]), eps);
+      if (nckv > 0)
+        for (int c = 0; c < a.ring - 1; c++)
+          ring_issue_half(vgl, (c < nckv ? c : nckv - 1) * kVRows, a.ctx, 32 * half, ring + (size_t)c * kRingRows * kHD);
+      for (int b0 = obeg; b0 < oend; b0 += 8 * kPThreads) {
+        uint64_t w[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          const int t = b0 + kPThreads * k + tid;
+          w[k] = t < oend ? ll_peek(ex + t) : ((uint64_t)eps << 32);
+        }
+        int spins = 0;
+        for (;;) {
+          bool ok = true;
+#pragma unroll
+          for (int k = 0; k < 8; k++) ok = ok && (uint32_t)(w[k] >> 32) == eps;
+          if (ok || bad) break;
+          for (int z = 0; z < a.nap; z++) __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+          for (int k = 0; k < 8; k++) {
+            const int t = b0 + kPThreads * k + tid;
+            if (t < oend && (uint32_t)(w[k] >> 32) != eps) w[k] = ll_peek(ex + t);
+          }
+          if (++spins > kSpinLimit) {
+            bad = true;
+            __hip_atomic_store(&a.st->abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          } else if ((spins & 255) == 0 && __hip_atomic_load(&a.st->abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+            bad = true;
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          const int t = b0 + kPThreads * k + tid;
+          if (t < oend) sc[t] = __uint_as_float((uint32_t)w[k]);
+        }
+      }
+      if (__syncthreads_or(bad)) return false;
+      for (int t = obeg + tid; t < oend; t += kPThreads) lmax = __builtin_fmaxf(lmax, sc[t]);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) lmax = __builtin_fmaxf(lmax, __shfl_xor(lmax, o));
     if (lane == 0) m.red[wave] = lmax;
     __syncthreads();
     const float mx = __builtin_fmaxf(__builtin_fmaxf(m.red[0], m.red[1]), __builtin_fmaxf(m.red[2], m.red[3]));
-    if (h == 0) prof_mark(a, s, l * 16 + 12);
+    if (mark) prof_mark(a, s, l * 16 + 12);
     for (int t = tid; t < T; t += kPThreads) sc[t] = fast_exp(sc[t] - mx);
     __syncthreads();
     if (tid == 0) m.red[8] = seq_sum(sc, T);
     __syncthreads();
-    if (h == 0) prof_mark(a, s, l * 16 + 13);
+    if (mark) prof_mark(a, s, l * 16 + 13);
     const float sum = m.red[8];
     for (int t = tid; t < T; t += kPThreads) sc[t] = sc[t] / sum;
     __syncthreads();
-    if (h == 0) prof_mark(a, s, l * 16 + 14);
+    if (mark) prof_mark(a, s, l * 16 + 14);
     // out_i = sum over t in order of p_t * v_t[i] (kernels.c:372-375): staged positions, then the
     // streamed ones slot by slot (wave 0 adds while every wave keeps the ring filled), then pos
     float accv = 0.0f;
+    if (split) {
+      // this workgroup's 32 output columns, over [0, pos) in half-width slots of kVRows rows
+      const int R = a.ring;
+      for (int c = 0; c < nckv; c++) {
+        ring_wait(R);
+        __syncthreads();
+        if (tid < 32) {
+#pragma unroll
+          for (int b = 0; b < kVRows / 48; b++) {
+            const float* slot = ring + (size_t)(c % R) * kRingRows * kHD + b * 48 * 32 + tid;
+            const float* pc = sc + c * kVRows + b * 48;
+            const int n = pos - c * kVRows - b * 48;
+            float pv[48], vx[48];
+#pragma unroll
+            for (int u = 0; u < 48; u++) { pv[u] = pc[u]; vx[u] = slot[u * 32]; }
+            if (n >= 48) {                       // a full batch: no select on the chain
+#pragma unroll
+              for (int u = 0; u < 48; u++) accv = accv + pv[u] * vx[u];
+            } else {
+#pragma unroll
+              for (int u = 0; u < 48; u++) {
+                const float t = accv + pv[u] * vx[u];
+                accv = u < n ? t : accv;
+              }
+            }
+          }
+        }
+        const int cn = c + R - 1;
+        ring_issue_half(vgl, (cn < nckv ? cn : nckv - 1) * kVRows, a.ctx, 32 * half, ring + (size_t)(cn % R) * kRingRows * kHD);
+      }
+      if (nckv > 0) ring_drain();
+      if (tid < 32) {
+        const int d = 32 * half + tid;
+        accv = accv + sc[pos] * vv[d];
+        ll_put(a.ll + S::oATT + h * kHD + d, __float_as_uint(accv), phase_epoch(ep0, s, E, 4 * l + 0));
+      }
+      if (mark) prof_mark(a, s, l * 16 + 6);
+      prof_wg(a, s, l, 1);
+      __syncthreads();
+      continue;
+    }
     if (tid < kHD && nt > 0) accv = seq_dot4(0.0f, sc, vT + tid * vstride, nt);
     if (nck > 0) {
       const int R = a.ring;
@@ -1190,10 +1305,15 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
           float pv[kRingRows], vx[kRingRows];
 #pragma unroll
           for (int u = 0; u < kRingRows; u++) { pv[u] = pc[u]; vx[u] = slot[u * kHD]; }
+          if (n >= kRingRows) {                // a full slot: no select on the chain
 #pragma unroll
-          for (int u = 0; u < kRingRows; u++) {
-            const float t = accv + pv[u] * vx[u];
-            accv = u < n ? t : accv;
+            for (int u = 0; u < kRingRows; u++) accv = accv + pv[u] * vx[u];
+          } else {
+#pragma unroll
+            for (int u = 0; u < kRingRows; u++) {
+              const float t = accv + pv[u] * vx[u];
+              accv = u < n ? t : accv;
+            }
           }
         }
         const int cn = c + R - 1;
@@ -1205,7 +1325,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       accv = accv + sc[pos] * vv[tid];
       ll_put(a.ll + S::oATT + h * kHD + tid, __float_as_uint(accv), phase_epoch(ep0, s, E, 4 * l + 0));
     }
-    if (h == 0) prof_mark(a, s, l * 16 + 6);
+    if (mark) prof_mark(a, s, l * 16 + 6);
     prof_wg(a, s, l, 1);
     __syncthreads();
   }
@@ -1218,7 +1338,7 @@ template <class S>
 __device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t ep0, int s, bool& bad) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), r = lane >> 2, j = lane & 3;
   const int E = 4 * a.NL + 1;
-  const int u = blockIdx.x - S::nOD - S::nA;
+  const int u = blockIdx.x - S::nOD - S::H * a.asplit;
   const int rg = wave < 2 ? 2 * u + wave : S::F / 16 + 2 * u + (wave - 2);
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
@@ -1281,9 +1401,9 @@ __global__ __launch_bounds__(kPThreads, 1) void k_decode_persistent(PArgs a) {
         case 2: ok = od_step<S, 2>(a, m, ep0, s, tok, bad); break;
         default: ok = od_step<S, 3>(a, m, ep0, s, tok, bad); break;
       }
-    } else if (wg < S::nOD + S::nA) {
+    } else if (wg < S::nOD + S::H * a.asplit) {
       ok = attn_step<S>(a, m, ep0, s, pos, tok, bad);
-    } else if (wg < S::nRoles) {
+    } else if (wg < S::nOD + S::H * a.asplit + S::nGU) {
       ok = gu_step<S>(a, m, ep0, s, bad);
     }
     if (!ok) return;

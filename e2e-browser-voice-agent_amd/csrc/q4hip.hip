@@ -1384,6 +1384,9 @@ struct q4hip {
   int pers_ring = 0;
   int pers_nap = 1;
   const void* pers_fn = nullptr;
+  uint64_t* lsc = nullptr;     // score exchange of the split attention ([H][ctx] entries)
+  int pers_split_from = 512;   // launches starting at this position or later split each head over two workgroups
+  bool pers_split_ok = false;  // the roles fit the device with two attention workgroups per head
   // profiling: events recorded around each launch of an eager step
   std::vector<std::pair<int, hipEvent_t>>* prof = nullptr;
 };
@@ -1668,6 +1671,18 @@ void setup_persistent(q4hip* h) {
   }
   h->pers_grid = G;
   if (const char* e = getenv("Q4HIP_POLL_SLEEP")) h->pers_nap = std::max(0, std::min(64, atoi(e)));
+  // long contexts: two attention workgroups per head when the roles still fit one per CU
+  if (pi->nRoles + h->H <= G && h->pers_ring > 0) {
+    const size_t lbytes = (size_t)h->H * h->ctx * 8;
+    if (hipMalloc(&h->lsc, lbytes) == hipSuccess && hipMemset(h->lsc, 0, lbytes) == hipSuccess) {
+      h->pers_split_ok = true;
+    } else {
+      (void)hipGetLastError();
+      if (h->lsc) (void)hipFree(h->lsc);
+      h->lsc = nullptr;
+    }
+  }
+  if (const char* e = getenv("Q4HIP_SPLIT_FROM")) h->pers_split_from = std::max(0, atoi(e));
   h->pers_ok = true;
   h->pers_broken = false;
 }
@@ -1690,17 +1705,21 @@ void prepare_attention(q4hip* h) {
   }
 }
 
-// In AUTO mode, decode steps whose context reaches this many positions run on the multi-kernel path:
-// its attention spreads the scores over many workgroups and reads each kv head's K once, where the
+// In AUTO mode, when the persistent kernel cannot split attention over two workgroups per head (too
+// few CUs), decode steps whose context reaches this many positions run on the multi-kernel path: its
+// attention spreads the scores over many workgroups and reads each kv head's K once, where the
 // persistent kernel streams a kv head's K and V through one workgroup per query head.
 constexpr int kLongDecodePositions = 3072;
 
 bool long_decode(const q4hip* h, int64_t last_pos) {
-  return h->mode == Q4HIP_DECODE_AUTO && h->list_attn == 1 && h->ascr && last_pos >= kLongDecodePositions;
+  return h->mode == Q4HIP_DECODE_AUTO && !h->pers_split_ok && h->list_attn == 1 && h->ascr &&
+         last_pos >= kLongDecodePositions;
 }
 
-hipError_t launch_persistent(q4hip* h, int steps, unsigned long long* prof = nullptr) {
+hipError_t launch_persistent(q4hip* h, int pos0, int steps, unsigned long long* prof = nullptr) {
   PArgs a;
+  a.asplit = h->pers_split_ok && pos0 >= h->pers_split_from ? 2 : 1;
+  a.lsc = h->lsc;
   a.V = h->V; a.NL = h->NL; a.ctx = h->ctx;
   a.eps = h->eps;
   a.embd = h->embd;
@@ -1795,7 +1814,8 @@ void q4hip_destroy(q4hip* h) {
   }
   mat_free(h->head);
   void* bufs[] = {h->embd, h->out_norm, h->rope, h->x, h->qkv, h->att, h->gu, h->logits, h->kc, h->vc,
-                  h->xq, h->am_v, h->am_i, h->tokens, h->st, h->d_layers, h->ll, h->ascr, h->xh, h->tpos};
+                  h->xq, h->am_v, h->am_i, h->tokens, h->st, h->d_layers, h->ll, h->ascr, h->xh, h->tpos,
+                  h->lsc};
   for (void* p : bufs) if (p) (void)hipFree(p);
   if (h->pin_ids) (void)hipHostFree(h->pin_ids);
   if (h->pin_next) (void)hipHostFree(h->pin_next);
@@ -1969,7 +1989,7 @@ int q4hip_forward(q4hip* h, const int* ids, int n, int pos, int* next) {
     const bool last = c + k >= n;
     k_set_pos<<<1, 64, 0, h->stream>>>(h->st, pos + c);
     if (k == 1 && last && pers) {
-      HIPCHK(launch_persistent(h, 1));
+      HIPCHK(launch_persistent(h, pos + c, 1));
       h->last_mode = Q4HIP_DECODE_PERSISTENT;
     } else if (k == 1 && last && h->graph) {
       HIPCHK(hipGraphLaunch(h->graph, h->stream));
@@ -2056,7 +2076,7 @@ static int run_generate(q4hip* h, int first, int pos, int steps, int* out, float
     HIPCHK(hipEventRecord(e0, h->stream));
   }
   if (pers) {
-    HIPCHK(launch_persistent(h, steps));
+    HIPCHK(launch_persistent(h, pos, steps));
     h->last_mode = Q4HIP_DECODE_PERSISTENT;
   } else {
     for (int i = 0; i < steps; i++) decode_step(h);
@@ -2140,7 +2160,7 @@ int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n) {
   if (e == hipSuccess) e = hipMemcpyAsync(h->tokens + pos, h->pin_ids, 4, hipMemcpyHostToDevice, h->stream);
   if (e == hipSuccess) {
     k_set_pos<<<1, 64, 0, h->stream>>>(h->st, pos);
-    e = launch_persistent(h, 1, d);
+    e = launch_persistent(h, pos, 1, d);
   }
   if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
   if (e == hipSuccess) e = hipMemcpy(t.data(), d, (size_t)cnt * 8, hipMemcpyDeviceToHost);

@@ -242,15 +242,18 @@ def _fill_kv(shape, P, seed):
     return k, v
 
 
-@pytest.mark.parametrize("mode,tile", [("graph", None), ("persistent", None), ("persistent", "16"), ("persistent", "0")])
-def test_prefilled_cache_long_context(mode, tile, monkeypatch):
+@pytest.mark.parametrize("mode,tile,split", [("graph", None, None), ("persistent", None, None), ("persistent", "16", None),
+                                             ("persistent", "0", None), ("persistent", None, "0")])
+def test_prefilled_cache_long_context(mode, tile, split, monkeypatch):
     """Decode over a cache of 500 positions written through q4hip_set_kv (the reference's host-owned
     kc/vc, kernels.c:433-440): positions past the attention role's staged tile are streamed from
     HBM; logits and tokens equal the oracle's with the same cache."""
     import q4hip
     if tile is not None:
         monkeypatch.setenv("Q4HIP_KV_TILE", tile)
-    print(f"prefilled cache mode {mode} tile {tile}", flush=True)
+    if split is not None:                       # two attention workgroups per head from position `split`
+        monkeypatch.setenv("Q4HIP_SPLIT_FROM", split)
+    print(f"prefilled cache mode {mode} tile {tile} split {split}", flush=True)
     P = 500
     shape, g, o = _pair("small", 31, ctx=640, mode=mode)
     try:
@@ -272,6 +275,31 @@ def test_prefilled_cache_long_context(mode, tile, monkeypatch):
             g.set_kv(0, shape.kv_heads, 0, k[0, 0], v[0, 0])
         with pytest.raises(q4hip.Q4Error):
             g.set_kv(0, 0, 640 - 3, k[0, 0, :8], v[0, 0, :8])
+    finally:
+        g.close()
+        o.close()
+
+
+@pytest.mark.parametrize("name,seed,n_prompt", [("tiny", 51, 20), ("small", 52, 70), ("tiny", 53, 1)])
+def test_split_attention_decode(name, seed, n_prompt, monkeypatch):
+    """Persistent decode with two attention workgroups per head from the first position (the long-
+    context mode, forced): the pair splits the past positions for the scores and the output columns
+    for P.V; tokens and logits equal the oracle's at every step, including steps with fewer past
+    positions than one chunk (one workgroup of the pair has no rows)."""
+    monkeypatch.setenv("Q4HIP_SPLIT_FROM", "0")
+    print(f"split attention {name} seed {seed} prompt {n_prompt}", flush=True)
+    shape, g, o = _pair(name, seed, ctx=256, mode="persistent")
+    try:
+        ids = synth.prompt_ids(seed, n_prompt, shape.vocab)
+        ng, no = g.forward(ids, 0), o.forward(ids, 0)
+        assert ng == no
+        dev = g.generate(ng, n_prompt, 60)
+        tok = no
+        for i in range(60):
+            tok = o.forward([tok], n_prompt + i)
+            assert dev[i] == tok, f"step {i}"
+        _compare_logits(g, o, "last step")
+        assert g.decode_mode_used() == 2
     finally:
         g.close()
         o.close()
