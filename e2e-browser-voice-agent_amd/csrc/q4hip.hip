@@ -694,7 +694,7 @@ __global__ __launch_bounds__(256) void k_gemm_rows(Q4Mat W, const uint4* __restr
 // Grid (Np / (JS == 1 ? 64 : 16), ceil(M / (16 TT))).
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
-constexpr int kMfmaPD = 4;       // weight groups in flight
+constexpr int kMfmaPD = 2;       // weight groups in flight
 
 template <int OP, int TT, int JS>
 __global__ __launch_bounds__(256) void k_gemm_mfma(Q4Mat W, const uint4* __restrict__ xq, const uint4* __restrict__ xh,
@@ -1150,34 +1150,45 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
     const float* vcol = vs + (buf * kPvCols + c) * CRS;
     if (active) {
       if (m == CR) {
+        // products of the next 16 positions are formed while the current 16 are added (the multiplies
+        // fill the add chain's latency); shared-memory reads run one batch further ahead
         float4 pa[4], va[4];
+        float pd[16];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
           pa[u] = *reinterpret_cast<const float4*>(pr + t0 + 4 * u);
           va[u] = *reinterpret_cast<const float4*>(vcol + 4 * u);
         }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          pd[4 * u] = pa[u].x * va[u].x;
+          pd[4 * u + 1] = pa[u].y * va[u].y;
+          pd[4 * u + 2] = pa[u].z * va[u].z;
+          pd[4 * u + 3] = pa[u].w * va[u].w;
+        }
         for (int r0 = 0; r0 < CR; r0 += 16) {
-          float4 pn[4], vn[4];
           const int r1 = r0 + 16 < CR ? r0 + 16 : r0;
 #pragma unroll
           for (int u = 0; u < 4; u++) {
-            pn[u] = *reinterpret_cast<const float4*>(pr + t0 + r1 + 4 * u);
-            vn[u] = *reinterpret_cast<const float4*>(vcol + r1 + 4 * u);
+            pa[u] = *reinterpret_cast<const float4*>(pr + t0 + r1 + 4 * u);
+            va[u] = *reinterpret_cast<const float4*>(vcol + r1 + 4 * u);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          float pn[16];
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            acc = acc + pd[4 * u];
+            pn[4 * u] = pa[u].x * va[u].x;
+            acc = acc + pd[4 * u + 1];
+            pn[4 * u + 1] = pa[u].y * va[u].y;
+            acc = acc + pd[4 * u + 2];
+            pn[4 * u + 2] = pa[u].z * va[u].z;
+            acc = acc + pd[4 * u + 3];
+            pn[4 * u + 3] = pa[u].w * va[u].w;
           }
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int u = 0; u < 4; u++) {
-            acc = acc + pa[u].x * va[u].x;
-            acc = acc + pa[u].y * va[u].y;
-            acc = acc + pa[u].z * va[u].z;
-            acc = acc + pa[u].w * va[u].w;
-          }
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int u = 0; u < 4; u++) {
-            pa[u] = pn[u];
-            va[u] = vn[u];
-          }
+          for (int u = 0; u < 16; u++) pd[u] = pn[u];
         }
       } else {
         for (int r = 0; r < m; r++) acc = acc + pr[t0 + r] * vcol[r];
