@@ -907,6 +907,7 @@ constexpr int kScoreRows = 64;
 constexpr int kPvCols = 32;
 constexpr int kMaxGroup = 8;    // query heads per kv head
 
+
 // Floats per head row of the softmax array: room for every position plus the sum's read-ahead.
 __host__ __device__ inline int pv_row_stride(int ctx) { return ((ctx + 31) & ~31) + 64; }
 // Floats per head row of the scores array (rows start 16-byte aligned).
@@ -966,24 +967,29 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
                                                       float* __restrict__ att, int D, const int* __restrict__ pos,
                                                       size_t seq_stride) {
   extern __shared__ __attribute__((aligned(16))) float lsm[];
-  constexpr int CRS = CR + 4, NV = CR * kPvCols / 4 / 256;      // V rows per chunk (stride), float4 per thread
+  constexpr int CRS = CR + 4, NV = CR * kPvCols / 4 / 256;      // chunk rows (LDS stride), float4 per thread
   constexpr int PB = 2;                   // score float4 per thread and head in one pass (2048 positions)
   const int c0 = blockIdx.x * kPvCols, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, G = H / KVH;
   const int T = pos[b] + 1, TS = pv_row_stride(ctx), nch = (T + CR - 1) / CR, CS = score_stride(ctx);
   const int T4 = (T + 3) >> 2;
-  float* vs = lsm;                        // [2][kPvCols][CRS]: V chunks, column-major
+  float* vs = lsm;                        // [2][kPvCols][CRS]: V chunks, column-major, double buffered
   float* p = vs + 2 * kPvCols * CRS;      // [G][TS]
   float* red = p + G * TS;                // [4 waves][kMaxGroup] maxima, [kMaxGroup] max, [kMaxGroup] sum
   float* rmax = red + 4 * kMaxGroup;
   float* rsum = rmax + kMaxGroup;
   const float* sb = sc + ((size_t)b * H + g * G) * CS;
   const float* vb = vc + (size_t)b * seq_stride + ((size_t)layer * KVH + g) * ctx * HD + c0;
+  // V chunks reach shared memory through registers: register set k holds the chunks ch = k mod 3;
+  // chunk ch + 1 is stored at the end of chunk ch, and its set then loads chunk ch + 4 (the last
+  // chunk again near the end, so that loads and stores stay unconditional)
   auto vload = [&](int ch, float4* r) {
 #pragma unroll
     for (int u = 0; u < NV; u++) {
-      const int i = tid + 256 * u, row = i / (kPvCols / 4), c4 = i - row * (kPvCols / 4), t = ch * CR + row;
-      r[u] = t < T ? *reinterpret_cast<const float4*>(vb + (size_t)t * HD + 4 * c4) : make_float4(0, 0, 0, 0);
+      // rows from T on are never read: they repeat row T - 1, so the loads carry no condition
+      const int i = tid + 256 * u, row = i / (kPvCols / 4), c4 = i - row * (kPvCols / 4);
+      const int t = min(ch * CR + row, T - 1);
+      r[u] = *reinterpret_cast<const float4*>(vb + (size_t)t * HD + 4 * c4);
     }
   };
   auto vstore = [&](int buf, const float4* r) {
@@ -1053,8 +1059,9 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
         }
       }
   };
-  float4 vr[NV];
-  vload(0, vr);                           // the first V chunk loads while the softmax runs
+  // the first V chunk loads while the softmax runs (the score registers leave no room for more)
+  float4 vr[3][NV];
+  vload(0, vr[0]);
   float mxh[kMaxGroup];
 #pragma unroll
   for (int gh = 0; gh < kMaxGroup; gh++) mxh[gh] = -1e30f;
@@ -1076,8 +1083,6 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
       store_exp(q0, v);
     }
   }
-  vstore(0, vr);                          // V work overlaps the sum below
-  if (nch > 1) vload(1, vr);
   __syncthreads();
   if (tid < G) {                          // the sum in position order; the next 32 values load ahead
     const float* e = p + tid * TS;
@@ -1138,53 +1143,58 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
       }
     }
   }
-  __syncthreads();
-  // P.V: thread (head, column); positions in order.  The shared-memory reads of the next 16
-  // positions are issued before the current 16 are added.
+  vstore(0, vr[0]);
+#pragma unroll
+  for (int k = 1; k < 4; k++) vload(min(k, nch - 1), vr[k % 3]);
+  // P.V: thread (head, column); positions in order
   const int gh = tid / kPvCols, c = tid - gh * kPvCols;
   const bool active = gh < G;
   const float* pr = p + (active ? gh : 0) * TS;
   float acc = 0.0f;
-  for (int ch = 0; ch < nch; ch++) {
-    const int buf = ch & 1, t0 = ch * CR, m = min(CR, T - t0);
-    const float* vcol = vs + (buf * kPvCols + c) * CRS;
+  auto pv_chunk = [&](int ch) {           // acc += p[t] * V[t][c] over chunk ch, positions in order
+    const int t0 = ch * CR, m = min(CR, T - t0);
+    const float* vcol = vs + ((ch & 1) * kPvCols + c) * CRS;            // vcol[r]: row r, column c
     if (active) {
       if (m == CR) {
-        // products of the next 16 positions are formed while the current 16 are added (the multiplies
-        // fill the add chain's latency); shared-memory reads run one batch further ahead
-        float4 pa[4], va[4];
-        float pd[16];
+        // products of the next 16 positions are formed while the current 16 are added; the
+        // shared-memory reads run one batch further ahead
+        float4 pa[4];
+        float va[16], pd[16];
+#pragma unroll
+        for (int u = 0; u < 4; u++) pa[u] = *reinterpret_cast<const float4*>(pr + t0 + 4 * u);
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-          pa[u] = *reinterpret_cast<const float4*>(pr + t0 + 4 * u);
-          va[u] = *reinterpret_cast<const float4*>(vcol + 4 * u);
+          const float4 w = *reinterpret_cast<const float4*>(vcol + 4 * u);
+          va[4 * u] = w.x; va[4 * u + 1] = w.y; va[4 * u + 2] = w.z; va[4 * u + 3] = w.w;
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-          pd[4 * u] = pa[u].x * va[u].x;
-          pd[4 * u + 1] = pa[u].y * va[u].y;
-          pd[4 * u + 2] = pa[u].z * va[u].z;
-          pd[4 * u + 3] = pa[u].w * va[u].w;
+          pd[4 * u] = pa[u].x * va[4 * u];
+          pd[4 * u + 1] = pa[u].y * va[4 * u + 1];
+          pd[4 * u + 2] = pa[u].z * va[4 * u + 2];
+          pd[4 * u + 3] = pa[u].w * va[4 * u + 3];
         }
         for (int r0 = 0; r0 < CR; r0 += 16) {
           const int r1 = r0 + 16 < CR ? r0 + 16 : r0;
 #pragma unroll
+          for (int u = 0; u < 4; u++) pa[u] = *reinterpret_cast<const float4*>(pr + t0 + r1 + 4 * u);
+#pragma unroll
           for (int u = 0; u < 4; u++) {
-            pa[u] = *reinterpret_cast<const float4*>(pr + t0 + r1 + 4 * u);
-            va[u] = *reinterpret_cast<const float4*>(vcol + r1 + 4 * u);
+            const float4 w = *reinterpret_cast<const float4*>(vcol + r1 + 4 * u);
+            va[4 * u] = w.x; va[4 * u + 1] = w.y; va[4 * u + 2] = w.z; va[4 * u + 3] = w.w;
           }
           __builtin_amdgcn_sched_barrier(0);
           float pn[16];
 #pragma unroll
           for (int u = 0; u < 4; u++) {
             acc = acc + pd[4 * u];
-            pn[4 * u] = pa[u].x * va[u].x;
+            pn[4 * u] = pa[u].x * va[4 * u];
             acc = acc + pd[4 * u + 1];
-            pn[4 * u + 1] = pa[u].y * va[u].y;
+            pn[4 * u + 1] = pa[u].y * va[4 * u + 1];
             acc = acc + pd[4 * u + 2];
-            pn[4 * u + 2] = pa[u].z * va[u].z;
+            pn[4 * u + 2] = pa[u].z * va[4 * u + 2];
             acc = acc + pd[4 * u + 3];
-            pn[4 * u + 3] = pa[u].w * va[u].w;
+            pn[4 * u + 3] = pa[u].w * va[4 * u + 3];
           }
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1194,11 +1204,27 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
         for (int r = 0; r < m; r++) acc = acc + pr[t0 + r] * vcol[r];
       }
     }
-    if (ch + 1 < nch) {
-      vstore(buf ^ 1, vr);
-      if (ch + 2 < nch) vload(ch + 2, vr);
+  };
+  // Full triples: after chunk ch, chunk ch + 1 goes into the other buffer (read last in chunk ch - 1,
+  // before the barrier) and its register set loads chunk ch + 4.  The loop has no exit but its
+  // head, so the loads in flight are the same on every entry to it.
+  int c3 = 0;
+  for (; c3 + 3 < nch; c3 += 3)
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+      __syncthreads();
+      pv_chunk(c3 + k);
+      vstore((c3 + k + 1) & 1, vr[(k + 1) % 3]);
+      vload(min(c3 + k + 4, nch - 1), vr[(k + 1) % 3]);
     }
-    __syncthreads();
+  // the last one to three chunks, all loaded already
+#pragma unroll
+  for (int k = 0; k < 3; k++) {
+    if (c3 + k < nch) {
+      __syncthreads();
+      pv_chunk(c3 + k);
+      if (c3 + k + 1 < nch) vstore((c3 + k + 1) & 1, vr[(k + 1) % 3]);
+    }
   }
   if (active) att[(size_t)b * D + (g * G + gh) * HD + c0 + c] = acc;
 }
