@@ -73,6 +73,16 @@ constexpr int split_cnt(int ng, int w) {
   return ng - split_g0(ng, w) <= 0 ? 0 : (ng - split_g0(ng, w) < split_per(ng) ? ng - split_g0(ng, w) : split_per(ng));
 }
 
+constexpr int kActStride = 16;    // exchange entries per GU workgroup's 9 activation entries
+
+// Activation entry i (block i / 9, word i % 9) in the exchange area.
+struct ActEntry {
+  __device__ int operator()(int i) const { return (i / 9) * kActStride + i % 9; }
+};
+struct SameEntry {
+  __device__ int operator()(int i) const { return i; }
+};
+
 // The model shape a persistent kernel is compiled for (head_dim 64).
 template <int D_, int F_, int H_, int KVH_>
 struct PShape {
@@ -86,8 +96,11 @@ struct PShape {
   static constexpr int KACT = (NACT + kPThreads - 1) / kPThreads;
   static constexpr int STV = D / 4 + 4;                                // stride of the lane runs
   // exchange area, in 8-byte entries: x after o, x after down, x into the head, attention
-  // output, quantized activation, then two (value, index) argmax buffers used by step parity
-  static constexpr int oX1 = 0, oX2 = D, oXH = 2 * D, oATT = 3 * D, oACT = 4 * D, oARG = 4 * D + NACT;
+  // output, quantized activation, then two (value, index) argmax buffers used by step parity.
+  // Every producer's entries start a 128-byte line; the 9 activation entries of a GU workgroup
+  // get a line of their own (kActStride entries), since lines shared by producers on different
+  // XCDs reach the readers later.
+  static constexpr int oX1 = 0, oX2 = D, oXH = 2 * D, oATT = 3 * D, oACT = 4 * D, oARG = 4 * D + kActStride * nGU;
   static constexpr size_t ll_entries(int G) { return (size_t)oARG + 4 * (size_t)G; }
   static constexpr int RAW = NACT > 2 * kPThreads ? NACT : 2 * kPThreads;   // raw entry words
   static_assert(D % 64 == 0 && F % 32 == 0 && D == H * kHD && H % KVH == 0, "unsupported shape");
@@ -136,20 +149,20 @@ __device__ __forceinline__ uint64_t ll_peek(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Wait for entries base[tid + 256k] (k < K, index < n) to carry epoch ep.  All K loads are in
+// Wait for entries base[at(tid + 256k)] (k < K, tid + 256k < n) to carry epoch ep.  All K loads are in
 // flight together and only the entries still missing are polled again, so a hand-off costs one
 // memory round trip however many entries a thread receives; between polls the wave sleeps
 // `nap` x 64 cycles (polls of every waiting workgroup share the memory system with the weight
 // stream).  Bounded: after kSpinLimit polls the thread raises st->abort; a raised flag makes
 // every waiter give up (`bad`).
-template <int K>
+template <int K, class At = SameEntry>
 __device__ __forceinline__ void ll_recv(const uint64_t* base, int n, uint32_t ep, State* st, bool& bad,
-                                        uint32_t (&out)[K], int nap) {
+                                        uint32_t (&out)[K], int nap, At at = At()) {
   uint64_t w[K];
 #pragma unroll
   for (int k = 0; k < K; k++) {
     const int i = (int)threadIdx.x + kPThreads * k;
-    w[k] = i < n ? ll_peek(base + i) : ((uint64_t)ep << 32);
+    w[k] = i < n ? ll_peek(base + at(i)) : ((uint64_t)ep << 32);
   }
   int spins = 0;
   for (;;) {
@@ -161,7 +174,7 @@ __device__ __forceinline__ void ll_recv(const uint64_t* base, int n, uint32_t ep
 #pragma unroll
     for (int k = 0; k < K; k++) {
       const int i = (int)threadIdx.x + kPThreads * k;
-      if (i < n && (uint32_t)(w[k] >> 32) != ep) w[k] = ll_peek(base + i);
+      if (i < n && (uint32_t)(w[k] >> 32) != ep) w[k] = ll_peek(base + at(i));
     }
     if (++spins > kSpinLimit) {
       bad = true;
@@ -954,7 +967,7 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
     wr_load<S::NGF, S::NB8F, G0d, Cd>(L.down, wg, lane, rd);
     {
       uint32_t v[S::KACT];
-      ll_recv<S::KACT>(a.ll + S::oACT, S::NACT, phase_epoch(ep0, s, E, 4 * l + 2), a.st, bad, v, a.nap);
+      ll_recv<S::KACT>(a.ll + S::oACT, S::NACT, phase_epoch(ep0, s, E, 4 * l + 2), a.st, bad, v, a.nap, ActEntry());
 #pragma unroll
       for (int k = 0; k < S::KACT; k++)
         if (tid + kPThreads * k < S::NACT) m.raw[tid + kPThreads * k] = v[k];
@@ -1372,8 +1385,8 @@ __device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t
       const int w = tid & 7, e0 = ((w >> 2) << 4) + ((w & 3) << 1);
       const int q0 = __shfl(q, e0), q1 = __shfl(q, e0 + 1), q2 = __shfl(q, e0 + 8), q3 = __shfl(q, e0 + 9);
       const uint32_t ep = phase_epoch(ep0, s, E, 4 * l + 2);
-      if (tid < 8) ll_put(a.ll + S::oACT + u * 9 + tid, pack4(q0, q1, q2, q3), ep);
-      else if (tid == 8) ll_put(a.ll + S::oACT + u * 9 + 8, __float_as_uint(dd), ep);
+      if (tid < 8) ll_put(a.ll + S::oACT + u * kActStride + tid, pack4(q0, q1, q2, q3), ep);
+      else if (tid == 8) ll_put(a.ll + S::oACT + u * kActStride + 8, __float_as_uint(dd), ep);
     }
     if (u == 0) prof_mark(a, s, l * 16 + 8);
     prof_wg(a, s, l, 1);
