@@ -57,6 +57,98 @@ __device__ __forceinline__ float fast_exp(float x) {
   return x < -87.0f ? 0.0f : e;
 }
 
+// ---------------------------------------------------------------- cross-lane maxima
+
+// Maximum over each quad of lanes (4k .. 4k+3, all active): two DPP quad permutations.
+__device__ __forceinline__ float quad_max(float v) {
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));
+  return v;
+}
+
+// Maximum over each group of 32 lanes (all active): quads, then the mirror within 8 and within 16
+// lanes (every lane of a quad, then of an 8-group, holds the same value), then lane ^ 16.
+__device__ __forceinline__ float max32(float v) {
+  v = quad_max(v);
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
+  return v;
+}
+
+// Maximum over the whole wave (all 64 lanes active), the same in every lane.
+__device__ __forceinline__ float max64(float v) {
+  v = max32(v);
+  const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  return __builtin_fmaxf(lo, hi);
+}
+
+// ---------------------------------------------------------------- correctly rounded quotients
+//
+// The reference divides in IEEE binary32 (f32.div).  These forms give the same quotients from a
+// product with a reciprocal and fused residual corrections (Markstein's method: P. Markstein,
+// "Computation of elementary functions on the IBM RISC System/6000 processor", IBM J. Res. Dev.
+// 34(1), 1990), each on a domain where it equals the IEEE quotient for every input — checked
+// exhaustively by q4hip_check_division — and fall back to the IEEE division elsewhere.  The
+// fallback sits behind a wave-uniform test, so it costs nothing unless some lane needs it.
+
+// a / 127 for a >= 0 (the block scale d = amax / 127, kernels.c:98): exact for every finite a.
+__device__ __forceinline__ float div_127(float a) {
+  constexpr float c = 1.0f / 127.0f;
+  const float q0 = a * c;
+  const float q = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, a), c, q0);
+  return a == __builtin_inff() ? a : q;
+}
+
+// d ? 1 / d : 0 for d >= 0 (kernels.c:99): the hardware reciprocal estimate and one correction are
+// exact for d in [2^-126, 2^126).
+__device__ __forceinline__ float inv_scale(float d) {
+  const float y0 = __builtin_amdgcn_rcpf(d);
+  const float y = __builtin_fmaf(__builtin_fmaf(-d, y0, 1.0f), y0, y0);
+  const bool fast = d >= 0x1p-126f && d < 0x1p126f;
+  if (__builtin_amdgcn_ballot_w64(!fast && d != 0.0f) == 0) return fast ? y : 0.0f;
+  return fast ? y : (d != 0.0f ? 1.0f / d : 0.0f);
+}
+
+// 1 / d: exact for d in [2^-126, 2^126).
+__device__ __forceinline__ float recip(float d) {
+  const float y0 = __builtin_amdgcn_rcpf(d);
+  const float y = __builtin_fmaf(__builtin_fmaf(-d, y0, 1.0f), y0, y0);
+  const bool fast = d >= 0x1p-126f && d < 0x1p126f;
+  if (__builtin_amdgcn_ballot_w64(!fast) == 0) return y;
+  return fast ? y : 1.0f / d;
+}
+
+// a / N for a >= 0 and a compile-time N (the mean of squares of RMSNorm, kernels.c:84): a power of
+// two is a product; N = 896 takes the corrected product for a in [2^-119, inf), exact there.
+template <int N>
+__device__ __forceinline__ float div_const(float a) {
+  if constexpr ((N & (N - 1)) == 0) {
+    return a * (1.0f / (float)N);
+  } else if constexpr (N == 896) {
+    constexpr float c = 1.0f / (float)N;
+    const float q0 = a * c;
+    const float q = __builtin_fmaf(__builtin_fmaf(-q0, (float)N, a), c, q0);
+    const bool fast = a >= 0x1p-119f && a < __builtin_inff();
+    if (__builtin_amdgcn_ballot_w64(!fast) == 0) return q;
+    return fast ? q : a / (float)N;
+  } else {
+    return a / (float)N;
+  }
+}
+
+// g / y for y = 1 + fast_exp(-g) (SiLU, kernels.c:395): exact for finite g != 0 with y < 2^126.
+__device__ __forceinline__ float div_silu(float g, float y) {
+  const float y0 = __builtin_amdgcn_rcpf(y);
+  const float y1 = __builtin_fmaf(__builtin_fmaf(-y, y0, 1.0f), y0, y0);
+  const float q0 = g * y1;
+  const float q = __builtin_fmaf(__builtin_fmaf(-q0, y, g), y1, q0);
+  const bool fast = y < 0x1p126f && g != 0.0f && __builtin_fabsf(g) < __builtin_inff();
+  if (__builtin_amdgcn_ballot_w64(!fast) == 0) return q;
+  return fast ? q : g / y;
+}
+
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
   return __half2float(__ushort_as_half((unsigned short)h));
 }
@@ -125,7 +217,7 @@ __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, c
         v[k] = (lane_staged(xl, st, i) * rs) * w[i];
       } else if (MODE == QM_SWIGLU) {
         const float g = xr[i];
-        v[k] = g / (1.0f + fast_exp(-g)) * xr[n + i];
+        v[k] = div_silu(g, 1.0f + fast_exp(-g)) * xr[n + i];
       } else {
         v[k] = xr[i];
       }
@@ -133,10 +225,9 @@ __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, c
     float am = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; k++) am = __builtin_fmaxf(am, __builtin_fabsf(v[k]));
-    am = __builtin_fmaxf(am, __shfl_xor(am, 1, 4));
-    am = __builtin_fmaxf(am, __shfl_xor(am, 2, 4));
-    const float dd = am / 127.0f;
-    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    am = quad_max(am);
+    const float dd = div_127(am);
+    const float id = inv_scale(dd);
     int q[8];
     int sum = 0;
 #pragma unroll

@@ -498,10 +498,9 @@ __device__ __forceinline__ uint4 quant_lane(const float (&v)[8]) {
   float am = 0.0f;
 #pragma unroll
   for (int k = 0; k < 8; k++) am = __builtin_fmaxf(am, __builtin_fabsf(v[k]));
-  am = __builtin_fmaxf(am, __shfl_xor(am, 1, 4));
-  am = __builtin_fmaxf(am, __shfl_xor(am, 2, 4));
-  const float dd = am / 127.0f;
-  const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+  am = quad_max(am);
+  const float dd = div_127(am);
+  const float id = inv_scale(dd);
   int q[8];
   int sum = 0;
 #pragma unroll
@@ -646,7 +645,7 @@ __device__ __forceinline__ void norm_quant(const PSmem& m, const float (&nw)[8],
     float s = 0.0f;
     if (tid < 4) s = run_sum<S::D / 4>(m.sq + tid * S::STV);
     const float s0 = __shfl(s, 0), s1 = __shfl(s, 1), s2 = __shfl(s, 2), s3 = __shfl(s, 3);
-    if (tid == 0) m.red[4] = 1.0f / __builtin_sqrtf((((s0 + s1) + s2) + s3) / (float)S::D + eps);
+    if (tid == 0) m.red[4] = recip(__builtin_sqrtf(div_const<S::D>(((s0 + s1) + s2) + s3) + eps));
   }
   __syncthreads();
   const float rs = m.red[4];
@@ -1246,8 +1245,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       if (__syncthreads_or(bad)) return false;
       for (int t = obeg + tid; t < oend; t += kPThreads) lmax = __builtin_fmaxf(lmax, sc[t]);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) lmax = __builtin_fmaxf(lmax, __shfl_xor(lmax, o));
+    lmax = max64(lmax);
     if (lane == 0) m.red[wave] = lmax;
     __syncthreads();
     const float mx = __builtin_fmaxf(__builtin_fmaxf(m.red[0], m.red[1]), __builtin_fmaxf(m.red[2], m.red[3]));
@@ -1375,12 +1373,10 @@ __device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t
     if (tid < 64) {
       const int i = tid & 31;
       const float g = m.gu[i];
-      const float x = g / (1.0f + fast_exp(-g)) * m.gu[32 + i];
-      float am = __builtin_fabsf(x);
-#pragma unroll
-      for (int o = 1; o < 32; o <<= 1) am = __builtin_fmaxf(am, __shfl_xor(am, o));
-      const float dd = am / 127.0f;
-      const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+      const float x = div_silu(g, 1.0f + fast_exp(-g)) * m.gu[32 + i];
+      const float am = max32(__builtin_fabsf(x));
+      const float dd = div_127(am);
+      const float id = inv_scale(dd);
       const int q = quant_one(x * id);
       const int w = tid & 7, e0 = ((w >> 2) << 4) + ((w & 3) << 1);
       const int q0 = __shfl(q, e0), q1 = __shfl(q, e0 + 1), q2 = __shfl(q, e0 + 8), q3 = __shfl(q, e0 + 9);

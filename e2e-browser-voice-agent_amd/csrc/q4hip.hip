@@ -2577,3 +2577,66 @@ int q4hip_mv_time_cold(q4hip_mv* m, int64_t rotate_bytes, int iters, float* us, 
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- quotient self-check
+
+namespace {
+
+// Form `mode` over input bit patterns [lo, hi] against the IEEE division (grid-stride, bounded).
+__global__ __launch_bounds__(256) void k_check_division(int mode, uint32_t lo, uint32_t hi,
+                                                        unsigned long long* bad) {
+  unsigned long long n = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)lo + blockIdx.x * blockDim.x + threadIdx.x; i <= hi; i += stride) {
+    const float a = __uint_as_float((uint32_t)i);
+    float want, got;
+    if (mode == 0) {
+      want = a / 127.0f;
+      got = div_127(a);
+    } else if (mode == 1) {
+      want = a != 0.0f ? 1.0f / a : 0.0f;
+      got = inv_scale(a);
+    } else if (mode == 2) {
+      const float y = 1.0f + fast_exp(-a);
+      want = a / y;
+      got = div_silu(a, y);
+    } else if (mode == 3) {
+      want = a / 896.0f;
+      got = div_const<896>(a);
+    } else {
+      want = 1.0f / a;
+      got = recip(a);
+    }
+    n += __float_as_uint(want) != __float_as_uint(got) && !(want != want && got != got);
+  }
+  if (n) atomicAdd(bad + mode, n);
+}
+
+}  // namespace
+
+extern "C" {
+
+int q4hip_check_division(int device, unsigned long long* mismatches, int n) {
+  if (!mismatches || n < 1 || n > 5) return fail(Q4HIP_EINVAL, "need 1..5 counters");
+  HIPCHK(hipSetDevice(device));
+  unsigned long long* d = nullptr;
+  HIPCHK(hipMalloc(&d, 5 * sizeof(unsigned long long)));
+  hipError_t e = hipMemset(d, 0, 5 * sizeof(unsigned long long));
+  const uint32_t top = 0x7F800000u;   // +inf: every non-negative value
+  for (int mode = 0; mode < n && e == hipSuccess; mode++) {
+    if (mode == 2) {
+      k_check_division<<<8192, 256>>>(mode, 0u, 0x7FFFFFFFu, d);
+      k_check_division<<<8192, 256>>>(mode, 0x80000000u, 0xFFFFFFFFu, d);
+    } else {
+      k_check_division<<<8192, 256>>>(mode, 0u, top, d);
+    }
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(mismatches, d, (size_t)n * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) return fail(Q4HIP_EHIP, "division check: %s", hipGetErrorString(e));
+  return Q4HIP_OK;
+}
+
+}  // extern "C"

@@ -28,7 +28,7 @@ EXPORTS = [
     "q4hip_mv_destroy", "q4hip_set_decode_mode", "q4hip_decode_mode_used", "q4hip_profile_persistent",
     "q4hip_set_kv", "q4hip_profile_pass", "q4hip_batch_create", "q4hip_batch_destroy",
     "q4hip_batch_prefill", "q4hip_batch_set_kv", "q4hip_batch_generate", "q4hip_batch_time_generate",
-    "q4hip_batch_read_logits", "q4hip_mv_time_cold",
+    "q4hip_batch_read_logits", "q4hip_mv_time_cold", "q4hip_check_division",
 ]
 
 _lib = None
@@ -51,6 +51,7 @@ def lib() -> ctypes.CDLL:
     sig = {
         "q4hip_last_error": (ctypes.c_char_p, []),
         "q4hip_device_count": (I, [ctypes.POINTER(I)]),
+        "q4hip_check_division": (I, [I, P, I]),
         "q4hip_create": (I, [ctypes.POINTER(P), I, I, I, I, I, I, I, I, F, I]),
         "q4hip_set_tensor": (I, [P, I, I, I, I, P, I64, ctypes.c_size_t]),
         "q4hip_set_rope": (I, [P, P, I]),
@@ -100,6 +101,17 @@ def device_count() -> int:
     n = ctypes.c_int(0)
     _check(lib().q4hip_device_count(ctypes.byref(n)))
     return n.value
+
+
+DIVISION_FORMS = ["a / 127", "d ? 1/d : 0", "g / (1 + fast_exp(-g))", "a / 896", "1 / d"]
+
+
+def check_division(device: int = 0) -> dict:
+    """Mismatch counts of the device's quotient forms against IEEE division over their whole
+    input domains (q4hip_check_division)."""
+    out = np.zeros(len(DIVISION_FORMS), np.uint64)
+    _check(lib().q4hip_check_division(device, _ptr(out), len(DIVISION_FORMS)))
+    return dict(zip(DIVISION_FORMS, (int(v) for v in out)))
 
 
 class Model:

@@ -195,6 +195,14 @@ int q4hip_mv_time(q4hip_mv* m, int iters, float* us);
 int q4hip_mv_time_cold(q4hip_mv* m, int64_t rotate_bytes, int iters, float* us, int* copies_used);
 void q4hip_mv_destroy(q4hip_mv* m);
 
+/* ---- self-check of the quotient forms ------------------------------------------------------
+ * The kernels compute the reference's IEEE binary32 divisions (engine/kernels.c:84, 98-99, 395)
+ * by reciprocal products with fused corrections on verified domains.  This runs every input of
+ * each form's domain on the device against the IEEE division and writes the mismatch counts:
+ * [0] a / 127 (a >= 0), [1] d ? 1/d : 0 (d >= 0), [2] g / (1 + fast_exp(-g)) (every bit pattern),
+ * [3] a / 896 (a >= 0), [4] 1 / d (d >= 0).  No counterpart in the reference (a diagnostic). */
+int q4hip_check_division(int device, unsigned long long* mismatches, int n);
+
 #ifdef __cplusplus
 }
 #endif
