@@ -1321,7 +1321,9 @@ struct Mat {
   Q4Mat view() const { return Q4Mat{(const uint4*)qs, (const uint4*)d, N, nb, ng, nb8, Np}; }
 };
 
-int mat_alloc(Mat& m, int N, int K, int fmt = Q4HIP_TYPE_Q4_0) {
+// The zeroing is ordered on stream s, the stream every later upload and kernel of m runs on (a
+// non-blocking stream is not ordered after work on the legacy default stream).
+int mat_alloc(Mat& m, int N, int K, hipStream_t s, int fmt = Q4HIP_TYPE_Q4_0) {
   m.fmt = fmt;
   m.N = N;
   m.K = K;
@@ -1334,8 +1336,8 @@ int mat_alloc(Mat& m, int N, int K, int fmt = Q4HIP_TYPE_Q4_0) {
   const size_t qbytes = (size_t)m.Np * m.ng * 64 + kWeightPadQ, dbytes = (size_t)m.Np * m.nb8 * 16 + kWeightPadD;
   HIPCHK(hipMalloc(&m.qs, qbytes));
   HIPCHK(hipMalloc(&m.d, dbytes));
-  HIPCHK(hipMemset(m.qs, 0, qbytes));
-  HIPCHK(hipMemset(m.d, 0, dbytes));
+  HIPCHK(hipMemsetAsync(m.qs, 0, qbytes, s));
+  HIPCHK(hipMemsetAsync(m.d, 0, dbytes, s));
   return Q4HIP_OK;
 }
 
@@ -1702,7 +1704,7 @@ void setup_persistent(q4hip* h) {
   const size_t ll_entries = pi->ll_entries(G);
   if (hipMalloc(&h->d_layers, lv.size() * sizeof(LayerView)) != hipSuccess ||
       hipMemcpy(h->d_layers, lv.data(), lv.size() * sizeof(LayerView), hipMemcpyHostToDevice) != hipSuccess ||
-      hipMalloc(&h->ll, ll_entries * 8) != hipSuccess || hipMemset(h->ll, 0, ll_entries * 8) != hipSuccess) {
+      hipMalloc(&h->ll, ll_entries * 8) != hipSuccess || hipMemsetAsync(h->ll, 0, ll_entries * 8, h->stream) != hipSuccess) {
     (void)hipGetLastError();
     return no("device allocation failed");
   }
@@ -1711,7 +1713,7 @@ void setup_persistent(q4hip* h) {
   // long contexts: two attention workgroups per head when the roles still fit one per CU
   if (pi->nRoles + h->H <= G && h->pers_ring > 0) {
     const size_t lbytes = (size_t)h->H * h->ctx * 8;
-    if (hipMalloc(&h->lsc, lbytes) == hipSuccess && hipMemset(h->lsc, 0, lbytes) == hipSuccess) {
+    if (hipMalloc(&h->lsc, lbytes) == hipSuccess && hipMemsetAsync(h->lsc, 0, lbytes, h->stream) == hipSuccess) {
       h->pers_split_ok = true;
     } else {
       (void)hipGetLastError();
@@ -1888,15 +1890,15 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
   h->L.resize(layers);
   for (int l = 0; l < layers; l++) {
     Layer& y = h->L[l];
-    TRY(mat_alloc(y.qkv, h->QKV, dim));
-    TRY(mat_alloc(y.o, dim, dim));
-    TRY(mat_alloc(y.gu, 2 * ffn, dim));
-    TRY(mat_alloc(y.down, dim, ffn));
+    TRY(mat_alloc(y.qkv, h->QKV, dim, h->stream));
+    TRY(mat_alloc(y.o, dim, dim, h->stream));
+    TRY(mat_alloc(y.gu, 2 * ffn, dim, h->stream));
+    TRY(mat_alloc(y.down, dim, ffn, h->stream));
     TRYHIP(hipMalloc(&y.attn_norm, (size_t)dim * 4));
     TRYHIP(hipMalloc(&y.ffn_norm, (size_t)dim * 4));
     TRYHIP(hipMalloc(&y.bqkv, (size_t)h->QKV * 4));
   }
-  TRY(mat_alloc(h->head, vocab, dim));
+  TRY(mat_alloc(h->head, vocab, dim, h->stream));
   TRYHIP(hipMalloc(&h->embd, (size_t)vocab * (dim / 32) * 18));
   TRYHIP(hipMalloc(&h->out_norm, (size_t)dim * 4));
   TRYHIP(hipMalloc(&h->rope, (size_t)ctx * HD * 4));
@@ -1910,8 +1912,8 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
   const size_t kvbytes = (size_t)layers * kv_heads * ctx * HD * 4;
   TRYHIP(hipMalloc(&h->kc, kvbytes));
   TRYHIP(hipMalloc(&h->vc, kvbytes));
-  TRYHIP(hipMemset(h->kc, 0, kvbytes));
-  TRYHIP(hipMemset(h->vc, 0, kvbytes));
+  TRYHIP(hipMemsetAsync(h->kc, 0, kvbytes, h->stream));
+  TRYHIP(hipMemsetAsync(h->vc, 0, kvbytes, h->stream));
   TRYHIP(hipMalloc(&h->xq, (size_t)M * h->xstride * 64));
   TRYHIP(hipMalloc(&h->xh, (size_t)M * h->xstride * 128));
   TRYHIP(hipMalloc(&h->tpos, (size_t)M * sizeof(int)));
@@ -1919,11 +1921,13 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
   TRYHIP(hipMalloc(&h->am_v, (size_t)h->am_parts * 4));
   TRYHIP(hipMalloc(&h->am_i, (size_t)h->am_parts * 4));
   TRYHIP(hipMalloc(&h->tokens, (size_t)(ctx + 1) * 4));
-  TRYHIP(hipMemset(h->tokens, 0, (size_t)(ctx + 1) * 4));
+  TRYHIP(hipMemsetAsync(h->tokens, 0, (size_t)(ctx + 1) * 4, h->stream));
   TRYHIP(hipMalloc(&h->st, sizeof(State)));
-  TRYHIP(hipMemset(h->st, 0, sizeof(State)));
+  TRYHIP(hipMemsetAsync(h->st, 0, sizeof(State), h->stream));
   TRYHIP(hipHostMalloc(&h->pin_ids, (size_t)(ctx + 1) * 4, hipHostMallocDefault));
   TRYHIP(hipHostMalloc(&h->pin_next, 64, hipHostMallocDefault));
+  // the zeroing above is complete before any later call, whatever stream that call uses
+  TRYHIP(hipStreamSynchronize(h->stream));
 #undef TRY
 #undef TRYHIP
   *out = h;
@@ -1984,7 +1988,7 @@ int q4hip_set_tensor(q4hip* h, int kind, int layer, int row0, int type, const vo
         h->graph = nullptr;
       }
       mat_free(h->head);
-      const int rc = mat_alloc(h->head, h->V, h->D, type);
+      const int rc = mat_alloc(h->head, h->V, h->D, h->stream, type);
       if (rc != Q4HIP_OK) return rc;
     }
     return mat_upload(h->head, row0, rows, data, h->stream);
@@ -2192,7 +2196,7 @@ int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n) {
   unsigned long long* d = nullptr;
   HIPCHK(hipMalloc(&d, (size_t)cnt * 8));
   std::vector<unsigned long long> t(cnt, 0);
-  hipError_t e = hipMemset(d, 0, (size_t)cnt * 8);
+  hipError_t e = hipMemsetAsync(d, 0, (size_t)cnt * 8, h->stream);
   h->pin_ids[0] = token;
   if (e == hipSuccess) e = hipMemcpyAsync(h->tokens + pos, h->pin_ids, 4, hipMemcpyHostToDevice, h->stream);
   if (e == hipSuccess) {
@@ -2325,9 +2329,10 @@ int q4hip_batch_create(q4hip_batch** out, q4hip* h, int B) {
   al((void**)&bt->tok, (size_t)B * 4);
   al((void**)&bt->pos, (size_t)B * 4);
   al((void**)&bt->sc, (size_t)B * h->H * score_stride(h->ctx) * 4);
-  if (e == hipSuccess) e = hipMemset(bt->kc, 0, kvbytes);
-  if (e == hipSuccess) e = hipMemset(bt->vc, 0, kvbytes);
+  if (e == hipSuccess) e = hipMemsetAsync(bt->kc, 0, kvbytes, h->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(bt->vc, 0, kvbytes, h->stream);
   if (e == hipSuccess) e = hipHostMalloc((void**)&bt->pin, (size_t)2 * B * 4, hipHostMallocDefault);
+  if (e == hipSuccess) e = hipStreamSynchronize(h->stream);   // caches zeroed before q4hip_batch_set_kv
   if (e != hipSuccess) {
     const int rc = fail(Q4HIP_EHIP, "batch of %d: %s", B, hipGetErrorString(e));
     q4hip_batch_destroy(bt);
@@ -2488,7 +2493,7 @@ int q4hip_mv_create(q4hip_mv** out, int N, int K, const void* w, int device) {
   if (e == hipSuccess) e = hipMalloc(&m->y, (size_t)N * 4);
   if (e == hipSuccess) e = hipMalloc(&m->xq, (size_t)(K / 32) * 64);
   if (e != hipSuccess) { rc = fail(Q4HIP_EHIP, "matvec alloc: %s", hipGetErrorString(e)); q4hip_mv_destroy(m); return rc; }
-  rc = mat_alloc(m->W, N, K);
+  rc = mat_alloc(m->W, N, K, m->stream);
   if (rc == Q4HIP_OK) rc = mat_upload(m->W, 0, N, w, m->stream);
   if (rc != Q4HIP_OK) { q4hip_mv_destroy(m); return rc; }
   *out = m;
