@@ -3,13 +3,15 @@
 // A kernel-per-operation step is ~245 dependent launches of 2.5-20 us each.  Here every workgroup
 // (one per CU) stays resident and takes one role for the whole launch:
 //   OD  (D/16 WGs)   rows 16w..16w+15 of o and down; owns those rows of the residual x
-//   A   (H WGs)      one attention head: its q rows and its kv group's k, v rows (the k/v rows are
-//                    recomputed by the heads of a group instead of exchanged), RoPE, K/V append,
-//                    attention
+//   A   (H WGs)      one attention head: its q rows, RoPE, the scores over past positions, then
+//                    the current position's from the new K row, softmax and P.V
+//   KV  (2 KVH WGs)  the new K (with RoPE) or V row of one kv group: its 64 qkv rows, the cache
+//                    store, and the row handed to the group's A workgroups, which meanwhile score
+//                    the past positions
 //   GU  (F/32 WGs)   gate and up rows of one 32-value block of the SwiGLU activation, quantized
 //   all              the output head (row groups round-robin), then the greedy argmax
-// Four exchanges per layer (att -> OD, x after o -> GU, act -> OD, x after down -> A) and one per
-// step (argmax).  Each exchanged value is stored together with the epoch of the phase that wrote it
+// Five exchanges per layer (x after down -> A and KV, new K/V -> A, att -> OD, x after o -> GU,
+// act -> OD) and one per step (argmax).  Each exchanged value is stored together with the epoch of the phase that wrote it
 // in one 8-byte agent-scope store ("LL" store): a reader polls the data itself, so a hand-off is
 // one hop, and a thread's entries are all in flight at once.  Every role issues the loads of its
 // next weights, norm weights and biases (and the attention role its past K/V rows) before it
@@ -90,21 +92,23 @@ struct PShape {
   static constexpr int NBD = D / 32, NBF = F / 32, NBM = NBD > NBF ? NBD : NBF;
   static constexpr int NGD = (NBD + 3) / 4, NGF = (NBF + 3) / 4;      // groups of 4 blocks
   static constexpr int NB8D = (NBD + 7) / 8, NB8F = (NBF + 7) / 8;    // uint4 words of 8 scales
-  static constexpr int nOD = D / 16, nA = H, nGU = F / 32, nRoles = nOD + nA + nGU;
+  static constexpr int nOD = D / 16, nA = H, nKV = 2 * KVH, nGU = F / 32, nRoles = nOD + nA + nKV + nGU;
   static constexpr int KD = (D + kPThreads - 1) / kPThreads;           // x entries per thread
   static constexpr int NACT = 9 * nGU;                                 // act entries
   static constexpr int KACT = (NACT + kPThreads - 1) / kPThreads;
   static constexpr int STV = D / 4 + 4;                                // stride of the lane runs
   // exchange area, in 8-byte entries: x after o, x after down, x into the head, attention
-  // output, quantized activation, then two (value, index) argmax buffers used by step parity.
+  // output, quantized activation, the new K and V rows of each kv group ([group][k, v][64]), then
+  // two (value, index) argmax buffers used by step parity.
   // Every producer's entries start a 128-byte line; the 9 activation entries of a GU workgroup
   // get a line of their own (kActStride entries), since lines shared by producers on different
   // XCDs reach the readers later.
-  static constexpr int oX1 = 0, oX2 = D, oXH = 2 * D, oATT = 3 * D, oACT = 4 * D, oARG = 4 * D + kActStride * nGU;
+  static constexpr int oX1 = 0, oX2 = D, oXH = 2 * D, oATT = 3 * D, oACT = 4 * D;
+  static constexpr int oKV = oACT + kActStride * nGU, oARG = oKV + 2 * KVH * kHD;
   static constexpr size_t ll_entries(int G) { return (size_t)oARG + 4 * (size_t)G; }
   static constexpr int RAW = NACT > 2 * kPThreads ? NACT : 2 * kPThreads;   // raw entry words
   static_assert(D % 64 == 0 && F % 32 == 0 && D == H * kHD && H % KVH == 0, "unsupported shape");
-  static_assert(D <= 4 * kPThreads, "norm_quant gives one block lane per thread");
+  static_assert(D <= 4 * kPThreads, "norm_quant gives half a block lane per thread");
 };
 
 // ---------------------------------------------------------------- memory helpers
@@ -491,22 +495,28 @@ __device__ __forceinline__ float embed_value(const uint8_t* emb, int D, int t, i
   return (float)((e < 16 ? (q & 15) : (q >> 4)) - 8) * d;
 }
 
-// Quantize one 32-block lane (quantize_row, kernels.c:90-114): v = the values at elements
-// {2j, 2j+1, 8+2j, 9+2j, 16+2j, 17+2j, 24+2j, 25+2j}; the four lanes of a block are consecutive
-// threads and exchange the block maximum by shuffles.
-__device__ __forceinline__ uint4 quant_lane(const float (&v)[8]) {
+// Quantize one 32-block (quantize_row, kernels.c:90-114) by half block lanes: block lane j of
+// block b owns elements {2j, 2j+1, 8+2j, 9+2j} (word 0) and {16+2j, 17+2j, 24+2j, 25+2j} (word 1);
+// thread 2l + h holds the four values of word h of block lane l = 4b + j, so the eight threads of
+// a block are consecutive.  The block maximum is an 8-lane reduction, and the pair combines its
+// words and sums by a lane swap.  The h = 0 thread gets block lane l's activation entry:
+// {word 0, word 1, -8 * (sum of its 8 values), d}.
+__device__ __forceinline__ uint4 quant_half(const float (&v)[4]) {
   float am = 0.0f;
 #pragma unroll
-  for (int k = 0; k < 8; k++) am = __builtin_fmaxf(am, __builtin_fabsf(v[k]));
+  for (int k = 0; k < 4; k++) am = __builtin_fmaxf(am, __builtin_fabsf(v[k]));
   am = quad_max(am);
+  am = __builtin_fmaxf(am, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(am), 0x141, 0xF, 0xF, true)));
   const float dd = div_127(am);
   const float id = inv_scale(dd);
-  int q[8];
-  int sum = 0;
+  int q[4];
 #pragma unroll
-  for (int k = 0; k < 8; k++) { q[k] = quant_one(v[k] * id); sum += q[k]; }
-  return make_uint4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]), (uint32_t)(-8 * sum),
-                    __float_as_uint(dd));
+  for (int k = 0; k < 4; k++) q[k] = quant_one(v[k] * id);
+  const uint32_t w = pack4(q[0], q[1], q[2], q[3]);
+  const int sum = (q[0] + q[1]) + (q[2] + q[3]);
+  const uint32_t wo = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0xB1, 0xF, 0xF, true);
+  const int so = __builtin_amdgcn_mov_dpp(sum, 0xB1, 0xF, 0xF, true);
+  return make_uint4(w, wo, (uint32_t)(-8 * (sum + so)), __float_as_uint(dd));
 }
 
 // Element k (0..7) of block lane t = (block t/4, lane t%4).
@@ -621,14 +631,15 @@ __device__ __forceinline__ void recv_x(const uint64_t* src, uint32_t ep, State* 
   }
 }
 
-// The 8 norm weights of this thread's block lane, loaded ahead of the wait.
+// The 4 norm weights of this thread's half block lane (thread 2l + h: word h of block lane l),
+// loaded ahead of the wait.
 template <class S>
-__device__ __forceinline__ void normw_load(const float* w, float (&nw)[8]) {
+__device__ __forceinline__ void normw_load(const float* w, float (&nw)[4]) {
   const int t = threadIdx.x;
-  if (t < S::NBD * 4) {
+  if (t < S::NBD * 8) {
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const float2 p = gld2f(w + lane_elem(t, 2 * u));
+    for (int u = 0; u < 2; u++) {
+      const float2 p = gld2f(w + lane_elem(t >> 1, 4 * (t & 1) + 2 * u));
       nw[2 * u] = p.x;
       nw[2 * u + 1] = p.y;
     }
@@ -639,7 +650,7 @@ __device__ __forceinline__ void normw_load(const float* w, float (&nw)[8]) {
 // run the four lane sums of x*x in order, then thread t < NBD*4 quantizes block lane t.
 // The caller has synchronised after staging; returns after a barrier.
 template <class S>
-__device__ __forceinline__ void norm_quant(const PSmem& m, const float (&nw)[8], float eps) {
+__device__ __forceinline__ void norm_quant(const PSmem& m, const float (&nw)[4], float eps) {
   const int tid = threadIdx.x;
   if (tid < 64) {
     float s = 0.0f;
@@ -649,14 +660,15 @@ __device__ __forceinline__ void norm_quant(const PSmem& m, const float (&nw)[8],
   }
   __syncthreads();
   const float rs = m.red[4];
-  if (tid < S::NBD * 4) {
-    float v[8];
+  if (tid < S::NBD * 8) {
+    float v[4];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int i = lane_elem(tid, k);
+    for (int k = 0; k < 4; k++) {
+      const int i = lane_elem(tid >> 1, 4 * (tid & 1) + k);
       v[k] = (m.xl[(i & 3) * S::STV + (i >> 2)] * rs) * nw[k];
     }
-    m.xq[tid] = quant_lane(v);
+    const uint4 q = quant_half(v);
+    if ((tid & 1) == 0) m.xq[tid >> 1] = q;
   }
   __syncthreads();
 }
@@ -688,7 +700,7 @@ __device__ __forceinline__ bool head_scan_q4(const PArgs& a, const PSmem& m, uin
                                              float& bv, int& bi) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int G = gridDim.x, wg = blockIdx.x, nRG = a.head.Np / 16, stride = 4 * G;
-  float nw[8];
+  float nw[4];
   normw_load<S>(a.out_norm, nw);
   int rgi = wg + G * wave;
   WR<S::NGD> R0[1], R1[1], R2[1];
@@ -795,7 +807,7 @@ __device__ __forceinline__ bool head_scan_q8(const PArgs& a, const PSmem& m, uin
   constexpr int NG8 = (S::NBD + 1) / 2;
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int G = gridDim.x, wg = blockIdx.x, nRG = a.head.Np / 16, stride = 4 * G;
-  float nw[8];
+  float nw[4];
   normw_load<S>(a.out_norm, nw);
   int rgi = wg + G * wave;
   WR8<NG8, S::NB8D> R0, R1;
@@ -942,11 +954,12 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
     if (__syncthreads_or(bad)) return false;
     if (wg == 0) prof_mark(a, s, l * 16 + 0);
     prof_wg(a, s, l, 0);
-    if (tid < S::NBD * 4) {
-      float v[8];
+    if (tid < S::NBD * 8) {
+      float v[4];
 #pragma unroll
-      for (int k = 0; k < 8; k++) v[k] = m.xl[lane_elem(tid, k)];
-      m.xq[tid] = quant_lane(v);
+      for (int k = 0; k < 4; k++) v[k] = m.xl[lane_elem(tid >> 1, 4 * (tid & 1) + k)];
+      const uint4 q = quant_half(v);
+      if ((tid & 1) == 0) m.xq[tid >> 1] = q;
     }
     __syncthreads();
     wr_terms<S::NBD, G0o, Co>(ro, m.xq, lane, m.terms);
@@ -1016,10 +1029,8 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
   const int E = 4 * a.NL + 1;
   const int aidx = blockIdx.x - S::nOD, h = aidx % S::H, half = aidx / S::H, kh = h / GRP;
   const bool split = a.asplit > 1;
-  const bool writer = (h % GRP) == 0 && half == 0;
   const bool mark = aidx == 0;
-  const int rq = (h * kHD) / 16 + wave, rk = (S::D + kh * kHD) / 16 + wave;
-  const int rv = (S::D + S::KVH * kHD + kh * kHD) / 16 + wave;
+  const int rq = (h * kHD) / 16 + wave;
   float* qv = m.qv;
   float* kv = m.qv + 64;
   float* vv = m.qv + 128;
@@ -1038,21 +1049,15 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
   const int oend = split ? (half == 0 ? pos : (nall / 2) * kRingRows) : 0;
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
-    WR<S::NGD> w3[3];
-    wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.qkv, rq, lane, w3[0]);
-    wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.qkv, rk, lane, w3[1]);
-    wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.qkv, rv, lane, w3[2]);
-    float nw[8];
+    WR<S::NGD> wq[1];
+    wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.qkv, rq, lane, wq[0]);
+    float nw[4];
     normw_load<S>(L.attn_norm, nw);
-    float bq = 0.0f, bk = 0.0f, bvv = 0.0f;
-    if (j == 0) {
-      bq = gldf(L.bqkv + rq * 16 + r);
-      bk = gldf(L.bqkv + rk * 16 + r);
-      bvv = gldf(L.bqkv + rv * 16 + r);
-    }
+    float bq = 0.0f;
+    if (j == 0) bq = gldf(L.bqkv + rq * 16 + r);
     float rc = 0.0f, rsn = 0.0f;
-    if (tid < 64) {
-      const float2 cs = gld2f(a.rope + (size_t)pos * kHD + 2 * (tid & 31));
+    if (tid < 32) {
+      const float2 cs = gld2f(a.rope + (size_t)pos * kHD + 2 * tid);
       rc = cs.x;
       rsn = cs.y;
     }
@@ -1101,45 +1106,35 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     prof_wg(a, s, l, 0);
     norm_quant<S>(m, nw, a.eps);
     if (mark) prof_mark(a, s, l * 16 + 9);
-    float acc[3] = {0.0f, 0.0f, 0.0f};
-    wr_dot<S::NBD, 0, S::NGD, 3>(w3, m.xq, j, acc);
-    const float q = hsum4(acc[0]), k = hsum4(acc[1]), v = hsum4(acc[2]);
-    if (j == 0) {
-      qv[16 * wave + r] = q + bq;
-      kv[16 * wave + r] = k + bk;
-      vv[16 * wave + r] = v + bvv;
-    }
+    float acc[1] = {0.0f};
+    wr_dot<S::NBD, 0, S::NGD, 1>(wq, m.xq, j, acc);
+    const float q = hsum4(acc[0]);
+    if (j == 0) qv[16 * wave + r] = q + bq;
     __syncthreads();
     if (mark) prof_mark(a, s, l * 16 + 5);
-    // RoPE (kernels.c:340-344): threads 0..31 rotate q pairs, 32..63 k pairs
-    if (tid < 64) {
-      const int i = tid & 31;
-      float* x = tid < 32 ? qv : kv;
-      const float x0 = x[i], x1 = x[i + 32];
-      x[i] = x0 * rc - x1 * rsn;
-      x[i + 32] = x1 * rc + x0 * rsn;
+    // RoPE (kernels.c:340-344) of the q pairs
+    if (tid < 32) {
+      const float x0 = qv[tid], x1 = qv[tid + 32];
+      qv[tid] = x0 * rc - x1 * rsn;
+      qv[tid + 32] = x1 * rc + x0 * rsn;
     }
     __syncthreads();
     if (mark) prof_mark(a, s, l * 16 + 11);
-    if (writer && tid < 64) {
-      st_coherent(a.kc + cbase + (size_t)pos * kHD + tid, kv[tid]);
-      st_coherent(a.vc + cbase + (size_t)pos * kHD + tid, vv[tid]);
-    }
     // scores: four lane sums over i = j mod 4, hsum, scale (kernels.c:362-366)
     const int T = pos + 1;
     const float scale = 1.0f / __builtin_sqrtf((float)kHD);
     float lmax = -1e30f;
-    // staged positions [0, nt) and the current one: one thread per position
-    if (tid < T) {
+    // staged positions [0, nt): one thread per position
+    if (tid < nt) {
       float4 qr[kHD / 4];
 #pragma unroll
       for (int i = 0; i < kHD / 4; i++) qr[i] = reinterpret_cast<const float4*>(qv)[i];
 #pragma unroll
       for (int i = 0; i < kHD / 4; i++) pin(qr[i]);
-      for (int t = tid; t < T; t += kPThreads) {
-        if (t == pos || t < nt) {
+      for (int t = tid; t < nt; t += kPThreads) {
+        {
           float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
-          const float4* kr = reinterpret_cast<const float4*>(t == pos ? kv : kt + t * kKVRow);
+          const float4* kr = reinterpret_cast<const float4*>(kt + t * kKVRow);
           float4 ka[8], kb[8];
 #pragma unroll
           for (int i = 0; i < 8; i++) ka[i] = kr[i];
@@ -1245,6 +1240,35 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       if (__syncthreads_or(bad)) return false;
       for (int t = obeg + tid; t < oend; t += kPThreads) lmax = __builtin_fmaxf(lmax, sc[t]);
     }
+    // the current position: the group's new K and V rows (KV role), then its score
+    {
+      uint32_t knv[1];                   // kv and vv are adjacent: entries 0..63 K, 64..127 V
+      ll_recv<1>(a.ll + S::oKV + 2 * kh * kHD, 2 * kHD, phase_epoch(ep0, s, E, 4 * l + 0), a.st, bad, knv, a.nap);
+      if (tid < 2 * kHD) kv[tid] = __uint_as_float(knv[0]);
+    }
+    if (__syncthreads_or(bad)) return false;
+    if (mark) prof_mark(a, s, l * 16 + 15);
+    if (tid < kHD) {
+      // wave 0 forms the 64 products; lane j < 4 then adds products j, j+4, ... in order (one
+      // read of its 16 products), and the four lane sums combine in hsum order
+      float* pq = m.gu;
+      pq[tid] = qv[tid] * kv[tid];
+      float pj[kHD / 4];
+#pragma unroll
+      for (int i = 0; i < kHD / 4; i++) pj[i] = pq[4 * i + (tid & 3)];
+      float sj = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kHD / 4; i++) sj = sj + pj[i];
+      const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), 0));
+      const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), 1));
+      const float s2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), 2));
+      const float s3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), 3));
+      if (tid == 0) {
+        const float sv = (s0 + s1 + s2 + s3) * scale;
+        sc[pos] = sv;
+        lmax = __builtin_fmaxf(lmax, sv);
+      }
+    }
     lmax = max64(lmax);
     if (lane == 0) m.red[wave] = lmax;
     __syncthreads();
@@ -1345,17 +1369,73 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
 
 // One 32-value block u of the SwiGLU activation: gate rows 32u.., up rows F+32u.. (one 16-row
 // group per wave), then silu(gate)*up and quantize_row of the block (kernels.c:390-397).
+// The new K (with RoPE) or V row of one kv group per layer (kernels.c:333-353): RMSNorm + quantize
+// of x, the group's 64 k or v rows of qkv (one row group per wave) plus bias, RoPE on k
+// (kernels.c:340-344), the cache store at pos, and the row handed to the group's attention
+// workgroups.  Workgroup 2g + c of the role: group g, c = 0 K, 1 V.
+template <class S>
+__device__ __forceinline__ bool kv_step(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int pos, int tok,
+                                        bool& bad) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), r = lane >> 2, j = lane & 3;
+  const int E = 4 * a.NL + 1;
+  const int kidx = blockIdx.x - S::nOD - S::H * a.asplit, kh = kidx >> 1, isv = kidx & 1;
+  const int rg = (S::D + isv * S::KVH * kHD + kh * kHD) / 16 + wave;
+  float* row = m.qv;
+  for (int l = 0; l < a.NL; l++) {
+    const LayerView& L = a.layers[l];
+    WR<S::NGD> w[1];
+    wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.qkv, rg, lane, w[0]);
+    float nw[4];
+    normw_load<S>(L.attn_norm, nw);
+    float b = 0.0f;
+    if (j == 0) b = gldf(L.bqkv + rg * 16 + r);
+    float rc = 0.0f, rsn = 0.0f;
+    if (!isv && tid < 32) {
+      const float2 cs = gld2f(a.rope + (size_t)pos * kHD + 2 * tid);
+      rc = cs.x;
+      rsn = cs.y;
+    }
+    if (l == 0) {
+      for (int i = tid; i < S::D; i += kPThreads) stage_x<S>(m, i, embed_value(a.embd, S::D, tok, i));
+    } else {
+      recv_x<S>(a.ll + S::oX2, phase_epoch(ep0, s, E, 4 * (l - 1) + 3), a.st, m, bad, a.nap);
+    }
+    if (__syncthreads_or(bad)) return false;
+    prof_wg(a, s, l, 0);
+    norm_quant<S>(m, nw, a.eps);
+    prof_wg(a, s, l, 2);
+    float acc[1] = {0.0f};
+    wr_dot<S::NBD, 0, S::NGD, 1>(w, m.xq, j, acc);
+    const float v = hsum4(acc[0]);
+    if (j == 0) row[16 * wave + r] = v + b;
+    __syncthreads();
+    if (!isv && tid < 32) {
+      const float x0 = row[tid], x1 = row[tid + 32];
+      row[tid] = x0 * rc - x1 * rsn;
+      row[tid + 32] = x1 * rc + x0 * rsn;
+    }
+    __syncthreads();
+    if (tid < kHD) {
+      const size_t cbase = ((size_t)l * S::KVH + kh) * a.ctx * kHD;
+      st_coherent((isv ? a.vc : a.kc) + cbase + (size_t)pos * kHD + tid, row[tid]);
+      ll_put(a.ll + S::oKV + kidx * kHD + tid, __float_as_uint(row[tid]), phase_epoch(ep0, s, E, 4 * l + 0));
+    }
+    prof_wg(a, s, l, 1);
+  }
+  return true;
+}
+
 template <class S>
 __device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t ep0, int s, bool& bad) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), r = lane >> 2, j = lane & 3;
   const int E = 4 * a.NL + 1;
-  const int u = blockIdx.x - S::nOD - S::H * a.asplit;
+  const int u = blockIdx.x - S::nOD - S::H * a.asplit - S::nKV;
   const int rg = wave < 2 ? 2 * u + wave : S::F / 16 + 2 * u + (wave - 2);
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
     WR<S::NGD> w[1];
     wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.gu, rg, lane, w[0]);
-    float nw[8];
+    float nw[4];
     normw_load<S>(L.ffn_norm, nw);
     recv_x<S>(a.ll + S::oX1, phase_epoch(ep0, s, E, 4 * l + 1), a.st, m, bad, a.nap);
     if (__syncthreads_or(bad)) return false;
@@ -1412,7 +1492,9 @@ __global__ __launch_bounds__(kPThreads, 1) void k_decode_persistent(PArgs a) {
       }
     } else if (wg < S::nOD + S::H * a.asplit) {
       ok = attn_step<S>(a, m, ep0, s, pos, tok, bad);
-    } else if (wg < S::nOD + S::H * a.asplit + S::nGU) {
+    } else if (wg < S::nOD + S::H * a.asplit + S::nKV) {
+      ok = kv_step<S>(a, m, ep0, s, pos, tok, bad);
+    } else if (wg < S::nOD + S::H * a.asplit + S::nKV + S::nGU) {
       ok = gu_step<S>(a, m, ep0, s, bad);
     }
     if (!ok) return;
