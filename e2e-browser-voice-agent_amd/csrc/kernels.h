@@ -138,13 +138,22 @@ __device__ __forceinline__ float div_const(float a) {
   }
 }
 
-// g / y for y = 1 + fast_exp(-g) (SiLU, kernels.c:395): exact for finite g != 0 with y < 2^126.
-__device__ __forceinline__ float div_silu(float g, float y) {
+// g / y for y = 1 + fast_exp(-g) (SiLU, kernels.c:395): the corrected product is exact for finite
+// g != 0 with y < 2^126 (silu_fast_ok).
+__device__ __forceinline__ float silu_quot(float g, float y) {
   const float y0 = __builtin_amdgcn_rcpf(y);
   const float y1 = __builtin_fmaf(__builtin_fmaf(-y, y0, 1.0f), y0, y0);
   const float q0 = g * y1;
-  const float q = __builtin_fmaf(__builtin_fmaf(-q0, y, g), y1, q0);
-  const bool fast = y < 0x1p126f && g != 0.0f && __builtin_fabsf(g) < __builtin_inff();
+  return __builtin_fmaf(__builtin_fmaf(-q0, y, g), y1, q0);
+}
+
+__device__ __forceinline__ bool silu_fast_ok(float g, float y) {
+  return y < 0x1p126f && g != 0.0f && __builtin_fabsf(g) < __builtin_inff();
+}
+
+__device__ __forceinline__ float div_silu(float g, float y) {
+  const float q = silu_quot(g, y);
+  const bool fast = silu_fast_ok(g, y);
   if (__builtin_amdgcn_ballot_w64(!fast) == 0) return q;
   return fast ? q : g / y;
 }
@@ -210,16 +219,37 @@ __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, c
     const int base = (b << 5) + (j << 1);
     const int e[8] = {base, base + 1, base + 8, base + 9, base + 16, base + 17, base + 24, base + 25};
     float v[8];
+    if (MODE == QM_SWIGLU) {
+      // all 16 inputs are read before any test, and one wave-uniform test covers the 8 quotients
+      float g[8], u[8], y[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int i = e[k];
-      if (MODE == QM_NORM) {
-        v[k] = (lane_staged(xl, st, i) * rs) * w[i];
-      } else if (MODE == QM_SWIGLU) {
-        const float g = xr[i];
-        v[k] = div_silu(g, 1.0f + fast_exp(-g)) * xr[n + i];
-      } else {
-        v[k] = xr[i];
+      for (int k = 0; k < 8; k++) {
+        g[k] = xr[e[k]];
+        u[k] = xr[n + e[k]];
+      }
+      bool fast = true;
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        y[k] = 1.0f + fast_exp(-g[k]);
+        v[k] = silu_quot(g[k], y[k]);
+        fast = fast && silu_fast_ok(g[k], y[k]);
+      }
+      if (__builtin_amdgcn_ballot_w64(!fast) != 0) {
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+          if (!silu_fast_ok(g[k], y[k])) v[k] = g[k] / y[k];
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k] = v[k] * u[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const int i = e[k];
+        if (MODE == QM_NORM) {
+          v[k] = (lane_staged(xl, st, i) * rs) * w[i];
+        } else {
+          v[k] = xr[i];
+        }
       }
     }
     float am = 0.0f;
