@@ -333,7 +333,7 @@ def bench_prefill(args):
         "config": {"workload": "qwen2.5-0.5b-shape Q4_0 prefill of 1024 seeded ids", "global_batch": 1,
                    "seq_len": n, "parallelism": "single-gpu"},
         "profile_us_per_pass": {k: round(v, 1) for k, v in prof.items()},
-        "roofline": {"bound": "mfma", "kernel": "k_gemm_q4 gate+up (exact int8 x q4 dot on VALU)",
+        "roofline": {"bound": "mfma", "kernel": "k_gemm_mfma gate|up (exact int8 x q4 block dots on the matrix cores, fp32 lane chains on the VALU)",
                      "achieved": round(tops, 2), "peak": 5000.0, "unit": "TOP/s (int8)",
                      "frac": round(tops / 5000.0, 5), "traffic": None, "ops_per_launch": 2 * macs,
                      "avg_launch_us": round(gu_us, 1)},
