@@ -11,9 +11,9 @@
 //   GU  (F/32 WGs)   gate and up rows of one 32-value block of the SwiGLU activation, quantized
 //   all              the output head (row groups round-robin), then the greedy argmax
 // Five exchanges per layer (x after down -> A and KV, new K/V -> A, att -> OD, x after o -> GU,
-// act -> OD) and one per step (argmax).  Each exchanged value is stored together with the epoch of the phase that wrote it
-// in one 8-byte agent-scope store ("LL" store): a reader polls the data itself, so a hand-off is
-// one hop, and a thread's entries are all in flight at once.  Every role issues the loads of its
+// act -> OD) and one per step (argmax).  Each exchanged value is stored together with the epoch of
+// the phase that wrote it in one 8-byte agent-scope store ("LL" store): a reader polls the data
+// itself, so a hand-off is one hop, and a thread's entries are all in flight at once.  Every role issues the loads of its
 // next weights, norm weights and biases (and the attention role its past K/V rows) before it
 // waits, so that traffic overlaps the waits.  Waits are bounded: a timeout raises State::abort and
 // every workgroup exits.
