@@ -81,6 +81,13 @@ constexpr int kActStride = 16;    // exchange entries per GU workgroup's 9 activ
 struct ActEntry {
   __device__ int operator()(int i) const { return (i / 9) * kActStride + i % 9; }
 };
+constexpr int kArgStride = 16;    // exchange entries per workgroup's (max, index) pair: a line each
+
+// Entry i of the argmax exchange (workgroup i / 2, word i % 2).
+struct ArgEntry {
+  __device__ int operator()(int i) const { return (i >> 1) * kArgStride + (i & 1); }
+};
+
 struct SameEntry {
   __device__ int operator()(int i) const { return i; }
 };
@@ -105,7 +112,7 @@ struct PShape {
   // XCDs reach the readers later.
   static constexpr int oX1 = 0, oX2 = D, oXH = 2 * D, oATT = 3 * D, oACT = 4 * D;
   static constexpr int oKV = oACT + kActStride * nGU, oARG = oKV + 2 * KVH * kHD;
-  static constexpr size_t ll_entries(int G) { return (size_t)oARG + 4 * (size_t)G; }
+  static constexpr size_t ll_entries(int G) { return (size_t)oARG + 2 * (size_t)kArgStride * G; }
   static constexpr int RAW = NACT > 2 * kPThreads ? NACT : 2 * kPThreads;   // raw entry words
   static_assert(D % 64 == 0 && F % 32 == 0 && D == H * kHD && H % KVH == 0, "unsupported shape");
   static_assert(D <= 4 * kPThreads, "norm_quant gives half a block lane per thread");
@@ -834,7 +841,7 @@ template <class S>
 __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int pos, bool& bad) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int G = gridDim.x, wg = blockIdx.x, E = 4 * a.NL + 1;
-  uint64_t* LARG = a.ll + S::oARG + (size_t)(s & 1) * 2 * G;
+  uint64_t* LARG = a.ll + S::oARG + (size_t)(s & 1) * kArgStride * G;
   const uint32_t epx = phase_epoch(ep0, s, E, 4 * (a.NL - 1) + 3);
   const uint32_t eph = phase_epoch(ep0, s, E, 4 * a.NL);
 
@@ -852,13 +859,13 @@ __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32
   __syncthreads();
   if (tid == 0) {
     for (int w = 1; w < 4; w++) arg_merge(bv, bi, m.argv[w], m.argi[w]);
-    ll_put(LARG + 2 * wg, __float_as_uint(bv), eph);
-    ll_put(LARG + 2 * wg + 1, (uint32_t)bi, eph);
+    ll_put(LARG + kArgStride * wg, __float_as_uint(bv), eph);
+    ll_put(LARG + kArgStride * wg + 1, (uint32_t)bi, eph);
   }
   prof_mark(a, s, a.NL * 16 + 1);
   {
     uint32_t v[2];
-    ll_recv<2>(LARG, 2 * G, eph, a.st, bad, v, a.nap);
+    ll_recv<2>(LARG, 2 * G, eph, a.st, bad, v, a.nap, ArgEntry());
     m.raw[tid] = v[0];
     if (tid + kPThreads < 2 * G) m.raw[tid + kPThreads] = v[1];
   }
