@@ -559,9 +559,13 @@ __host__ __device__ constexpr size_t kv_lds_bytes(int kv_tile) {
 
 // Past K/V rows beyond the staged tile are streamed from HBM through a ring of slots of kRingRows
 // rows in shared memory, filled by asynchronous global-to-LDS loads (each wave instruction moves
-// 4 rows = 1 KB; a slot is 12 instructions, 3 per wave).
+// 4 rows = 1 KB; a slot is 12 instructions, 3 per wave).  A K slot keeps each 4-row group in
+// kGrpFloats (16 floats of padding, see ring_issue_k); V slots use its first kRingRows * kHD
+// floats as plain rows.
 constexpr int kRingRows = 48;
-__host__ __device__ constexpr size_t ring_lds_bytes(int slots) { return (size_t)slots * kRingRows * kHD * 4; }
+constexpr int kGrpFloats = 4 * kHD + 16;
+constexpr int kSlotFloats = kRingRows / 4 * kGrpFloats;
+__host__ __device__ constexpr size_t ring_lds_bytes(int slots) { return (size_t)slots * kSlotFloats * 4; }
 
 template <class S>
 constexpr size_t psmem_terms_offset() {
@@ -898,9 +902,9 @@ __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32
 typedef __attribute__((address_space(3))) void LdsVoid;
 typedef __attribute__((address_space(1))) const void GlobalVoid;
 
-// Issue the asynchronous loads of rows [t0, t0 + kRingRows) of one (layer, kv head) K or V block
-// into `slot`: wave w issues instructions w, w+4, w+8, each moving rows t0+4i .. t0+4i+3.  Rows at
-// or past ctx are read from row ctx-1 (their values are never used).
+// Issue the asynchronous loads of rows [t0, t0 + kRingRows) of one (layer, kv head) V block into
+// `slot` as plain rows: wave w issues instructions w, w+4, w+8, each moving rows t0+4i .. t0+4i+3.
+// Rows at or past ctx are read from row ctx-1 (their values are never used).
 __device__ __forceinline__ void ring_issue(const float* src, int t0, int ctx, float* slot) {
   const int lane = threadIdx.x & 63, wave = wave_id();
 #pragma unroll
@@ -912,17 +916,42 @@ __device__ __forceinline__ void ring_issue(const float* src, int t0, int ctx, fl
   }
 }
 
-// Wait until this wave's loads of the oldest slot in flight have landed: R - 2 newer slots of 3
-// instructions each may still be outstanding (s_waitcnt vmcnt(3 (R - 2)), no other counter waited).
-__device__ __forceinline__ void ring_wait(int slots) {
-  if (slots == 7) __builtin_amdgcn_s_waitcnt(0x0F7F);        // vmcnt(15)
-  else __builtin_amdgcn_s_waitcnt(0x0F73);                    // vmcnt(3)
+// The same rows of a K block for the scores, one 4-row group per instruction at slot + i *
+// kGrpFloats.  An instruction places lane l's 16 bytes at float 4 l of its group, and lane l
+// fetches chunk l >> 2 (elements 4c .. 4c+3) of row l & 3: element 4c + e of group row r lands at
+// float 16 c + 4 r + e.  Four threads per row then read elements 4i + j of their row at immediate
+// offsets 16 i, and with the 16-float padding the 16 rows of a wave cover all 64 banks.
+__device__ __forceinline__ void ring_issue_k(const float* src, int t0, int ctx, float* slot) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+#pragma unroll
+  for (int k = 0; k < 3; k++) {
+    const int i = wave + 4 * k;
+    const int t = t0 + 4 * i + (lane & 3);
+    const float* g = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + 4 * (lane >> 2);
+    __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + i * kGrpFloats), 16, 0, 0);
+  }
+}
+
+// Wait until this wave's loads of the oldest slot in flight have landed (R - 2 newer slots of 3
+// instructions each may still be outstanding: vmcnt(3 (R - 2))) and its LDS accesses are done,
+// then meet the other waves.  Not __syncthreads: its workgroup fence waits for every outstanding
+// load into LDS (vmcnt(0)), which would leave a single slot in flight.  The "memory" clobber keeps
+// the compiler from moving loads or stores across the barrier.
+__device__ __forceinline__ void ring_sync(int slots) {
+  if (slots == 7) asm volatile("s_waitcnt vmcnt(15) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// The same for a ring whose slots are issued one iteration later (R - 3 newer slots in flight).
+__device__ __forceinline__ void ring_sync_lag(int slots) {
+  if (slots == 7) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 __device__ __forceinline__ void ring_drain() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
 
 // Half-width slots for the split attention's P.V: kVRows rows x 32 of the 64 columns (from c0), the
-// footprint of a full slot and, like it, three instructions per wave (ring_wait applies).
+// footprint of a full slot and, like it, three instructions per wave (ring_sync applies).
 constexpr int kVRows = 96;
 __device__ __forceinline__ void ring_issue_half(const float* src, int t0, int ctx, int c0, float* slot) {
   const int lane = threadIdx.x & 63, wave = wave_id();
@@ -1044,7 +1073,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
   float* sc = m.terms;                                     // ctx + kRingRows scores
   float* ring = sc + attn_scores_floats(a.ctx);            // a.ring slots of kRingRows rows
   const int vstride = kv_vstride(a.kv_tile);
-  float* kt = ring + (size_t)a.ring * kRingRows * kHD;     // [kv_tile][kKVRow] K
+  float* kt = ring + (size_t)a.ring * kSlotFloats;        // [kv_tile][kKVRow] K
   float* vT = kt + (size_t)(a.kv_tile + 16) * kKVRow;      // [64][vstride] V transposed
   const int nt = split ? 0 : (pos < a.kv_tile ? pos : a.kv_tile);   // staged past positions
   // K rows streamed for the scores: [kbeg, kend) in chunks of kRingRows -- positions [nt, pos), or
@@ -1102,7 +1131,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     const float* vgl = a.vc + cbase;
     if (nck > 0)
       for (int c = 0; c < a.ring - 1; c++)
-        ring_issue(kgl, kbeg + (c < nck ? c : nck - 1) * kRingRows, a.ctx, ring + (size_t)c * kRingRows * kHD);
+        ring_issue_k(kgl, kbeg + (c < nck ? c : nck - 1) * kRingRows, a.ctx, ring + (size_t)c * kSlotFloats);
     if (l == 0) {
       for (int i = tid; i < S::D; i += kPThreads) stage_x<S>(m, i, embed_value(a.embd, S::D, tok, i));
     } else {
@@ -1176,16 +1205,29 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     if (nck > 0) {
       const int R = a.ring;
       const int pj = tid & 3, pr = tid >> 2;
+      float qj[kHD / 4];                          // this thread's lane of q
+#pragma unroll
+      for (int i = 0; i < kHD / 4; i++) qj[i] = qv[4 * i + pj];
       for (int c = 0; c < nck; c++) {
-        ring_wait(R);
-        __syncthreads();
-        const float* slot = ring + (size_t)(c % R) * kRingRows * kHD;
+        ring_sync(R);
         float sj = 0.0f;
         if (pr < kRingRows) {
+          // element 4i + pj of slot row pr (ring_issue_k's group layout)
+          const float* row = ring + (size_t)(c % R) * kSlotFloats + (pr >> 2) * kGrpFloats + 4 * (pr & 3) + pj;
+          float kr[kHD / 4];
 #pragma unroll
-          for (int i = 0; i < kHD / 4; i++) sj = sj + qv[4 * i + pj] * slot[pr * kHD + 4 * i + pj];
+          for (int i = 0; i < kHD / 4; i++) kr[i] = row[16 * i];
+          // all 16 reads in flight before the first use (else one LDS round trip per step)
+          asm volatile("" : "+v"(kr[0]), "+v"(kr[1]), "+v"(kr[2]), "+v"(kr[3]), "+v"(kr[4]), "+v"(kr[5]),
+                       "+v"(kr[6]), "+v"(kr[7]), "+v"(kr[8]), "+v"(kr[9]), "+v"(kr[10]), "+v"(kr[11]),
+                       "+v"(kr[12]), "+v"(kr[13]), "+v"(kr[14]), "+v"(kr[15]));
+#pragma unroll
+          for (int i = 0; i < kHD / 4; i++) sj = sj + qj[i] * kr[i];
         }
-        const float s1 = __shfl_down(sj, 1, 4), s2 = __shfl_down(sj, 2, 4), s3 = __shfl_down(sj, 3, 4);
+        // lanes pj = 1, 2, 3 of the quad into lane 0 (DPP quad_perm)
+        const float s1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sj), 0xF9, 0xF, 0xF, true));
+        const float s2 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sj), 0xFE, 0xF, 0xF, true));
+        const float s3 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sj), 0xFF, 0xF, 0xF, true));
         const int t = kbeg + c * kRingRows + pr;
         if (pj == 0 && pr < kRingRows && t < kend) {
           const float sv = (((sj + s1) + s2) + s3) * scale;
@@ -1193,14 +1235,15 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
           lmax = __builtin_fmaxf(lmax, sv);
         }
         const int cn = c + R - 1;
-        ring_issue(kgl, kbeg + (cn < nck ? cn : nck - 1) * kRingRows, a.ctx, ring + (size_t)(cn % R) * kRingRows * kHD);
+        ring_issue_k(kgl, kbeg + (cn < nck ? cn : nck - 1) * kRingRows, a.ctx, ring + (size_t)(cn % R) * kSlotFloats);
       }
       ring_drain();
       __syncthreads();
+      prof_wg(a, s, l, 2);
       // the ring is free: the first V slots stream in while exp, sum and division run
       if (!split)
         for (int c = 0; c < R - 1; c++)
-          ring_issue(vgl, nt + (c < nck ? c : nck - 1) * kRingRows, a.ctx, ring + (size_t)c * kRingRows * kHD);
+          ring_issue(vgl, nt + (c < nck ? c : nck - 1) * kRingRows, a.ctx, ring + (size_t)c * kSlotFloats);
     }
     const int nckv = split ? (pos + kVRows - 1) / kVRows : 0;     // split P.V: half-width V slots
     if (split) {
@@ -1210,8 +1253,8 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       uint64_t* ex = a.lsc + (size_t)h * a.ctx;
       for (int t = kbeg + tid; t < kend; t += kPThreads) ll_put(ex + t, __float_as_uint(sc[t]), eps);
       if (nckv > 0)
-        for (int c = 0; c < a.ring - 1; c++)
-          ring_issue_half(vgl, (c < nckv ? c : nckv - 1) * kVRows, a.ctx, 32 * half, ring + (size_t)c * kRingRows * kHD);
+        for (int c = 0; c < a.ring - 2; c++)
+          ring_issue_half(vgl, (c < nckv ? c : nckv - 1) * kVRows, a.ctx, 32 * half, ring + (size_t)c * kSlotFloats);
       for (int b0 = obeg; b0 < oend; b0 += 8 * kPThreads) {
         uint64_t w[8];
 #pragma unroll
@@ -1245,6 +1288,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
         }
       }
       if (__syncthreads_or(bad)) return false;
+      prof_wg(a, s, l, 3);
       for (int t = obeg + tid; t < oend; t += kPThreads) lmax = __builtin_fmaxf(lmax, sc[t]);
     }
     // the current position: the group's new K and V rows (KV role), then its score
@@ -1294,34 +1338,53 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     // streamed ones slot by slot (wave 0 adds while every wave keeps the ring filled), then pos
     float accv = 0.0f;
     if (split) {
-      // this workgroup's 32 output columns, over [0, pos) in half-width slots of kVRows rows
+      // this workgroup's 32 output columns, over [0, pos) in half-width slots of kVRows rows.  In
+      // iteration c waves 1..3 turn slot c into the products p_t * v_t[i] in place while wave 0
+      // adds slot c - 1's in position order (each product rounded, then added, as acc + p * v);
+      // slot c + R - 2 is issued into the one wave 0 finished in iteration c - 1.
       const int R = a.ring;
-      for (int c = 0; c < nckv; c++) {
-        ring_wait(R);
-        __syncthreads();
-        if (tid < 32) {
+      for (int c = 0; nckv > 0 && c <= nckv; c++) {
+        ring_sync_lag(R);
+        if (c < nckv && wave != 0) {
+          float* slot = ring + (size_t)(c % R) * kSlotFloats;
+          const float* pc = sc + c * kVRows;
+          float pv[kVRows * 32 / 192], vx[kVRows * 32 / 192];
 #pragma unroll
-          for (int b = 0; b < kVRows / 48; b++) {
-            const float* slot = ring + (size_t)(c % R) * kRingRows * kHD + b * 48 * 32 + tid;
-            const float* pc = sc + c * kVRows + b * 48;
-            const int n = pos - c * kVRows - b * 48;
-            float pv[48], vx[48];
+          for (int k = 0; k < kVRows * 32 / 192; k++) {
+            const int idx = (tid - 64) + 192 * k;
+            pv[k] = pc[idx >> 5];
+            vx[k] = slot[idx];
+          }
 #pragma unroll
-            for (int u = 0; u < 48; u++) { pv[u] = pc[u]; vx[u] = slot[u * 32]; }
-            if (n >= 48) {                       // a full batch: no select on the chain
+          for (int k = 0; k < kVRows * 32 / 192; k++) slot[(tid - 64) + 192 * k] = pv[k] * vx[k];
+        }
+        if (c > 0 && tid < 32) {
+          const float* slot = ring + (size_t)((c - 1) % R) * kSlotFloats + tid;
+          const int n = pos - (c - 1) * kVRows;
+          float pr[kVRows];
 #pragma unroll
-              for (int u = 0; u < 48; u++) accv = accv + pv[u] * vx[u];
-            } else {
+          for (int u = 0; u < kVRows; u++) pr[u] = slot[u * 32];
 #pragma unroll
-              for (int u = 0; u < 48; u++) {
-                const float t = accv + pv[u] * vx[u];
-                accv = u < n ? t : accv;
-              }
+          for (int u = 0; u < kVRows / 2; u++) pin(pr[u]);
+          if (n >= kVRows) {                   // a full slot: no select on the chain
+#pragma unroll
+            for (int u = 0; u < kVRows / 2; u++) accv = accv + pr[u];
+#pragma unroll
+            for (int u = kVRows / 2; u < kVRows; u++) pin(pr[u]);
+#pragma unroll
+            for (int u = kVRows / 2; u < kVRows; u++) accv = accv + pr[u];
+          } else {
+#pragma unroll
+            for (int u = kVRows / 2; u < kVRows; u++) pin(pr[u]);
+#pragma unroll
+            for (int u = 0; u < kVRows; u++) {
+              const float t = accv + pr[u];
+              accv = u < n ? t : accv;
             }
           }
         }
-        const int cn = c + R - 1;
-        ring_issue_half(vgl, (cn < nckv ? cn : nckv - 1) * kVRows, a.ctx, 32 * half, ring + (size_t)(cn % R) * kRingRows * kHD);
+        const int cn = c + R - 2;
+        ring_issue_half(vgl, (cn < nckv ? cn : nckv - 1) * kVRows, a.ctx, 32 * half, ring + (size_t)(cn % R) * kSlotFloats);
       }
       if (nckv > 0) ring_drain();
       if (tid < 32) {
@@ -1338,10 +1401,9 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     if (nck > 0) {
       const int R = a.ring;
       for (int c = 0; c < nck; c++) {
-        ring_wait(R);
-        __syncthreads();
+        ring_sync(R);
         if (tid < kHD) {
-          const float* slot = ring + (size_t)(c % R) * kRingRows * kHD + tid;
+          const float* slot = ring + (size_t)(c % R) * kSlotFloats + tid;
           const float* pc = sc + nt + c * kRingRows;
           const int n = nstream - c * kRingRows;
           float pv[kRingRows], vx[kRingRows];
@@ -1359,7 +1421,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
           }
         }
         const int cn = c + R - 1;
-        ring_issue(vgl, nt + (cn < nck ? cn : nck - 1) * kRingRows, a.ctx, ring + (size_t)(cn % R) * kRingRows * kHD);
+        ring_issue(vgl, nt + (cn < nck ? cn : nck - 1) * kRingRows, a.ctx, ring + (size_t)(cn % R) * kSlotFloats);
       }
       ring_drain();
     }

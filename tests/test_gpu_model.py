@@ -242,20 +242,22 @@ def _fill_kv(shape, P, seed):
     return k, v
 
 
-@pytest.mark.parametrize("mode,tile,split", [("graph", None, None), ("persistent", None, None), ("persistent", "16", None),
-                                             ("persistent", "0", None), ("persistent", None, "0")])
-def test_prefilled_cache_long_context(mode, tile, split, monkeypatch):
-    """Decode over a cache of 500 positions written through q4hip_set_kv (the reference's host-owned
+@pytest.mark.parametrize("mode,tile,split,P,ctx", [("graph", None, None, 500, 640), ("persistent", None, None, 500, 640),
+                                                    ("persistent", "16", None, 500, 640), ("persistent", "0", None, 500, 640),
+                                                    ("persistent", None, "0", 500, 640), ("persistent", None, None, 1500, 1600),
+                                                    ("persistent", None, "0", 1500, 1600)])
+def test_prefilled_cache_long_context(mode, tile, split, P, ctx, monkeypatch):
+    """Decode over a cache of P positions written through q4hip_set_kv (the reference's host-owned
     kc/vc, kernels.c:433-440): positions past the attention role's staged tile are streamed from
-    HBM; logits and tokens equal the oracle's with the same cache."""
+    HBM (through 3 ring slots up to ctx 1024, 7 beyond); logits and tokens equal the oracle's with
+    the same cache."""
     import q4hip
     if tile is not None:
         monkeypatch.setenv("Q4HIP_KV_TILE", tile)
     if split is not None:                       # two attention workgroups per head from position `split`
         monkeypatch.setenv("Q4HIP_SPLIT_FROM", split)
-    print(f"prefilled cache mode {mode} tile {tile} split {split}", flush=True)
-    P = 500
-    shape, g, o = _pair("small", 31, ctx=640, mode=mode)
+    print(f"prefilled cache mode {mode} tile {tile} split {split} positions {P} ctx {ctx}", flush=True)
+    shape, g, o = _pair("small", 31, ctx=ctx, mode=mode)
     try:
         k, v = _fill_kv(shape, P, 31)
         ok, ov = o.kv()
@@ -274,7 +276,7 @@ def test_prefilled_cache_long_context(mode, tile, split, monkeypatch):
         with pytest.raises(q4hip.Q4Error):
             g.set_kv(0, shape.kv_heads, 0, k[0, 0], v[0, 0])
         with pytest.raises(q4hip.Q4Error):
-            g.set_kv(0, 0, 640 - 3, k[0, 0, :8], v[0, 0, :8])
+            g.set_kv(0, 0, ctx - 3, k[0, 0, :8], v[0, 0, :8])
     finally:
         g.close()
         o.close()
