@@ -559,12 +559,17 @@ __host__ __device__ constexpr size_t kv_lds_bytes(int kv_tile) {
 
 // Past K/V rows beyond the staged tile are streamed from HBM through a ring of slots of kRingRows
 // rows in shared memory, filled by asynchronous global-to-LDS loads (each wave instruction moves
-// 4 rows = 1 KB; a slot is 12 instructions, 3 per wave).  A K slot keeps each 4-row group in
-// kGrpFloats (16 floats of padding, see ring_issue_k); V slots use its first kRingRows * kHD
-// floats as plain rows.
+// 4 rows = 1 KB; a slot is 12 instructions).  V slots hold plain rows.  For the scores the same
+// memory is split into per-wave rings of 16-row K chunks, each 4-row group in kGrpFloats (16
+// floats of padding, see ring_issue_kc): a wave streams and scores its own chunks.
 constexpr int kRingRows = 48;
 constexpr int kGrpFloats = 4 * kHD + 16;
 constexpr int kSlotFloats = kRingRows / 4 * kGrpFloats;
+constexpr int kChunkFloats = 4 * kGrpFloats;
+// K chunk slots per wave in a ring of `slots` slots (5 of 7, 2 of 3)
+__host__ __device__ constexpr int kchunk_slots(int slots) { return 3 * slots / 4; }
+static_assert(4 * kchunk_slots(7) * kChunkFloats <= 7 * kSlotFloats, "per-wave K rings exceed the ring");
+static_assert(4 * kchunk_slots(3) * kChunkFloats <= 3 * kSlotFloats, "per-wave K rings exceed the ring");
 __host__ __device__ constexpr size_t ring_lds_bytes(int slots) { return (size_t)slots * kSlotFloats * 4; }
 
 template <class S>
@@ -916,20 +921,27 @@ __device__ __forceinline__ void ring_issue(const float* src, int t0, int ctx, fl
   }
 }
 
-// The same rows of a K block for the scores, one 4-row group per instruction at slot + i *
-// kGrpFloats.  An instruction places lane l's 16 bytes at float 4 l of its group, and lane l
-// fetches chunk l >> 2 (elements 4c .. 4c+3) of row l & 3: element 4c + e of group row r lands at
-// float 16 c + 4 r + e.  Four threads per row then read elements 4i + j of their row at immediate
-// offsets 16 i, and with the 16-float padding the 16 rows of a wave cover all 64 banks.
-__device__ __forceinline__ void ring_issue_k(const float* src, int t0, int ctx, float* slot) {
-  const int lane = threadIdx.x & 63, wave = wave_id();
+// One wave's loads of K rows [t0, t0 + 16) into a chunk slot, one 4-row group per instruction at
+// slot + g * kGrpFloats.  An instruction places lane l's 16 bytes at float 4 l of its group, and
+// lane l fetches elements 4c .. 4c+3 (c = l >> 2) of row l & 3: element 4c + e of group row r
+// lands at float 16 c + 4 r + e.  Four lanes per row then read elements 4i + j of their row at
+// immediate offsets 16 i, and with the 16-float padding the 16 rows of the wave cover all 64 banks.
+// Rows at or past ctx are read from row ctx-1 (their values are never used).
+__device__ __forceinline__ void ring_issue_kc(const float* src, int t0, int ctx, float* slot) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int k = 0; k < 3; k++) {
-    const int i = wave + 4 * k;
-    const int t = t0 + 4 * i + (lane & 3);
-    const float* g = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + 4 * (lane >> 2);
-    __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + i * kGrpFloats), 16, 0, 0);
+  for (int g = 0; g < 4; g++) {
+    const int t = t0 + 4 * g + (lane & 3);
+    const float* p = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + 4 * (lane >> 2);
+    __builtin_amdgcn_global_load_lds((GlobalVoid*)p, (LdsVoid*)(slot + g * kGrpFloats), 16, 0, 0);
   }
+}
+
+// Wait until this wave's loads of its oldest K chunk in flight have landed (`cs` - 2 newer chunks
+// of 4 instructions may still be outstanding).  Only the issuing wave reads a chunk: no barrier.
+__device__ __forceinline__ void kchunk_wait(int cs) {
+  if (cs == 5) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Wait until this wave's loads of the oldest slot in flight have landed (R - 2 newer slots of 3
@@ -942,27 +954,49 @@ __device__ __forceinline__ void ring_sync(int slots) {
   else asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// The same for a ring whose slots are issued one iteration later (R - 3 newer slots in flight).
-__device__ __forceinline__ void ring_sync_lag(int slots) {
-  if (slots == 7) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 __device__ __forceinline__ void ring_drain() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
 
-// Half-width slots for the split attention's P.V: kVRows rows x 32 of the 64 columns (from c0), the
-// footprint of a full slot and, like it, three instructions per wave (ring_sync applies).
+// Half-width slots for the split attention's P.V: kVRows rows x 32 of the 64 columns (from c0) as
+// plain rows of 32 floats, the footprint of a full slot.  Producer wave pw (waves 1..3) loads rows
+// 32 pw .. 32 pw + 31 of a slot with 4 instructions of 8 rows each and forms their products.
 constexpr int kVRows = 96;
-__device__ __forceinline__ void ring_issue_half(const float* src, int t0, int ctx, int c0, float* slot) {
-  const int lane = threadIdx.x & 63, wave = wave_id();
+__device__ __forceinline__ void ring_issue_vp(const float* src, int t0, int ctx, int c0, int pw, float* slot) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int k = 0; k < 3; k++) {
-    const int i = wave + 4 * k;
+  for (int k = 0; k < 4; k++) {
+    const int i = 4 * pw + k;
     const int t = t0 + 8 * i + (lane >> 3);
     const float* g = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + c0 + 4 * (lane & 7);
     __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + i * 256), 16, 0, 0);
   }
 }
+
+// A producer wave's wait for its own rows of the oldest slot in flight (d - 1 newer slots of 4
+// instructions may still be outstanding).
+__device__ __forceinline__ void vpart_wait(int d) {
+  if (d == 5) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// Hand-off counters of the split P.V in this workgroup's shared memory.  Bounded waits: false
+// after kLdsSpinLimit polls (the caller gives up the step like any other timed-out wait).
+typedef __attribute__((address_space(3))) int LdsInt;
+constexpr int kLdsSpinLimit = 1 << 20;
+__device__ __forceinline__ bool lds_wait_ge(volatile LdsInt* c, int v) {
+  for (int spin = 0; spin < kLdsSpinLimit; spin++) {
+    if (*c >= v) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+__device__ __forceinline__ bool lds_wait_ge3(volatile LdsInt* c, int v) {
+  for (int spin = 0; spin < kLdsSpinLimit; spin++) {
+    const int a0 = c[0], a1 = c[1], a2 = c[2];
+    if (a0 >= v && a1 >= v && a2 >= v) return true;
+  }
+  return false;
+}
+
 
 // ---------------------------------------------------------------- roles (one step each)
 
@@ -1125,13 +1159,18 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
         }
       }
     }
-    // past positions [kbeg, kend) stream through the ring; its first K slots load during the wait
+    // past positions [kbeg, kend) stream through the ring: for the scores in 16-row chunks, wave w
+    // taking chunks w, w + 4, ... through its own ring of cs slots (the first ones load during the
+    // wait for x); for P.V in slots of kRingRows (or kVRows) rows
     const int nstream = kend - kbeg, nck = (nstream + kRingRows - 1) / kRingRows;
+    const int nkc = (nstream + 15) / 16, nloc = nkc > wave ? (nkc - wave + 3) / 4 : 0;
+    const int cs = kchunk_slots(a.ring);
+    float* wring = ring + (size_t)wave * cs * kChunkFloats;
     const float* kgl = a.kc + cbase;
     const float* vgl = a.vc + cbase;
-    if (nck > 0)
-      for (int c = 0; c < a.ring - 1; c++)
-        ring_issue_k(kgl, kbeg + (c < nck ? c : nck - 1) * kRingRows, a.ctx, ring + (size_t)c * kSlotFloats);
+    if (nloc > 0)
+      for (int j = 0; j < cs - 1; j++)
+        ring_issue_kc(kgl, kbeg + 16 * (4 * (j < nloc ? j : nloc - 1) + wave), a.ctx, wring + (size_t)j * kChunkFloats);
     if (l == 0) {
       for (int i = tid; i < S::D; i += kPThreads) stage_x<S>(m, i, embed_value(a.embd, S::D, tok, i));
     } else {
@@ -1204,16 +1243,15 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     // reference's lane j (i = j mod 4), the lanes are combined in hsum order
     if (nck > 0) {
       const int R = a.ring;
-      const int pj = tid & 3, pr = tid >> 2;
-      float qj[kHD / 4];                          // this thread's lane of q
+      const int pj = lane & 3, pr = lane >> 2;   // lane pj of row pr of the wave's chunk
+      if (nloc > 0) {
+        float qj[kHD / 4];                        // this lane's reference lane of q
 #pragma unroll
-      for (int i = 0; i < kHD / 4; i++) qj[i] = qv[4 * i + pj];
-      for (int c = 0; c < nck; c++) {
-        ring_sync(R);
-        float sj = 0.0f;
-        if (pr < kRingRows) {
-          // element 4i + pj of slot row pr (ring_issue_k's group layout)
-          const float* row = ring + (size_t)(c % R) * kSlotFloats + (pr >> 2) * kGrpFloats + 4 * (pr & 3) + pj;
+        for (int i = 0; i < kHD / 4; i++) qj[i] = qv[4 * i + pj];
+        for (int j = 0; j < nloc; j++) {
+          kchunk_wait(cs);
+          // element 4i + pj of chunk row pr (ring_issue_kc's group layout)
+          const float* row = wring + (size_t)(j % cs) * kChunkFloats + (pr >> 2) * kGrpFloats + 4 * (pr & 3) + pj;
           float kr[kHD / 4];
 #pragma unroll
           for (int i = 0; i < kHD / 4; i++) kr[i] = row[16 * i];
@@ -1221,21 +1259,22 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
           asm volatile("" : "+v"(kr[0]), "+v"(kr[1]), "+v"(kr[2]), "+v"(kr[3]), "+v"(kr[4]), "+v"(kr[5]),
                        "+v"(kr[6]), "+v"(kr[7]), "+v"(kr[8]), "+v"(kr[9]), "+v"(kr[10]), "+v"(kr[11]),
                        "+v"(kr[12]), "+v"(kr[13]), "+v"(kr[14]), "+v"(kr[15]));
+          float sj = 0.0f;
 #pragma unroll
           for (int i = 0; i < kHD / 4; i++) sj = sj + qj[i] * kr[i];
+          // lanes pj = 1, 2, 3 of the quad into lane 0 (DPP quad_perm)
+          const float s1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sj), 0xF9, 0xF, 0xF, true));
+          const float s2 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sj), 0xFE, 0xF, 0xF, true));
+          const float s3 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sj), 0xFF, 0xF, 0xF, true));
+          const int t = kbeg + 16 * (4 * j + wave) + pr;
+          if (pj == 0 && t < kend) {
+            const float sv = (((sj + s1) + s2) + s3) * scale;
+            sc[t] = sv;
+            lmax = __builtin_fmaxf(lmax, sv);
+          }
+          const int jn = j + cs - 1;
+          ring_issue_kc(kgl, kbeg + 16 * (4 * (jn < nloc ? jn : nloc - 1) + wave), a.ctx, wring + (size_t)(jn % cs) * kChunkFloats);
         }
-        // lanes pj = 1, 2, 3 of the quad into lane 0 (DPP quad_perm)
-        const float s1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sj), 0xF9, 0xF, 0xF, true));
-        const float s2 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sj), 0xFE, 0xF, 0xF, true));
-        const float s3 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sj), 0xFF, 0xF, 0xF, true));
-        const int t = kbeg + c * kRingRows + pr;
-        if (pj == 0 && pr < kRingRows && t < kend) {
-          const float sv = (((sj + s1) + s2) + s3) * scale;
-          sc[t] = sv;
-          lmax = __builtin_fmaxf(lmax, sv);
-        }
-        const int cn = c + R - 1;
-        ring_issue_k(kgl, kbeg + (cn < nck ? cn : nck - 1) * kRingRows, a.ctx, ring + (size_t)(cn % R) * kSlotFloats);
       }
       ring_drain();
       __syncthreads();
@@ -1252,9 +1291,9 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       const uint32_t eps = phase_epoch(ep0, s, E, 4 * l + 0);
       uint64_t* ex = a.lsc + (size_t)h * a.ctx;
       for (int t = kbeg + tid; t < kend; t += kPThreads) ll_put(ex + t, __float_as_uint(sc[t]), eps);
-      if (nckv > 0)
+      if (nckv > 0 && wave != 0)
         for (int c = 0; c < a.ring - 2; c++)
-          ring_issue_half(vgl, (c < nckv ? c : nckv - 1) * kVRows, a.ctx, 32 * half, ring + (size_t)c * kSlotFloats);
+          ring_issue_vp(vgl, (c < nckv ? c : nckv - 1) * kVRows, a.ctx, 32 * half, wave - 1, ring + (size_t)c * kSlotFloats);
       for (int b0 = obeg; b0 < oend; b0 += 8 * kPThreads) {
         uint64_t w[8];
 #pragma unroll
@@ -1332,35 +1371,55 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     if (mark) prof_mark(a, s, l * 16 + 13);
     const float sum = m.red[8];
     for (int t = tid; t < T; t += kPThreads) sc[t] = sc[t] / sum;
+    volatile LdsInt* cnt = (volatile LdsInt*)(m.red + 12);   // split P.V hand-offs (below)
+    if (tid < 4) cnt[tid] = 0;
     __syncthreads();
     if (mark) prof_mark(a, s, l * 16 + 14);
     // out_i = sum over t in order of p_t * v_t[i] (kernels.c:372-375): staged positions, then the
     // streamed ones slot by slot (wave 0 adds while every wave keeps the ring filled), then pos
     float accv = 0.0f;
     if (split) {
-      // this workgroup's 32 output columns, over [0, pos) in half-width slots of kVRows rows.  In
-      // iteration c waves 1..3 turn slot c into the products p_t * v_t[i] in place while wave 0
-      // adds slot c - 1's in position order (each product rounded, then added, as acc + p * v);
-      // slot c + R - 2 is issued into the one wave 0 finished in iteration c - 1.
-      const int R = a.ring;
-      for (int c = 0; nckv > 0 && c <= nckv; c++) {
-        ring_sync_lag(R);
-        if (c < nckv && wave != 0) {
-          float* slot = ring + (size_t)(c % R) * kSlotFloats;
-          const float* pc = sc + c * kVRows;
-          float pv[kVRows * 32 / 192], vx[kVRows * 32 / 192];
+      // this workgroup's 32 output columns over [0, pos) in half-width slots of kVRows rows.  Each
+      // producer wave (1..3) streams its 32 rows of every slot, turns them into the products
+      // p_t * v_t[i] in place and counts the slot in cnt[pw]; wave 0 waits for all three counts,
+      // reads the slot, counts it in cnt[3] and adds the products in position order (each product
+      // rounded, then added, as acc + p * v).  Slot c + D reuses the buffer of slot c + D - R
+      // once wave 0 has read that; no barrier between the waves.
+      const int R = a.ring, D = R - 2;
+      if (wave != 0) {
+        const int pw = wave - 1;
+        for (int c = 0; c < nckv; c++) {
+          vpart_wait(D);
+          float* part = ring + (size_t)(c % R) * kSlotFloats + pw * 1024;
+          const float* pc = sc + c * kVRows + 32 * pw;
+          float pv[16], vx[16];
 #pragma unroll
-          for (int k = 0; k < kVRows * 32 / 192; k++) {
-            const int idx = (tid - 64) + 192 * k;
-            pv[k] = pc[idx >> 5];
-            vx[k] = slot[idx];
+          for (int k = 0; k < 16; k++) {
+            pv[k] = pc[(lane + 64 * k) >> 5];
+            vx[k] = part[lane + 64 * k];
           }
 #pragma unroll
-          for (int k = 0; k < kVRows * 32 / 192; k++) slot[(tid - 64) + 192 * k] = pv[k] * vx[k];
+          for (int k = 0; k < 16; k++) part[lane + 64 * k] = pv[k] * vx[k];
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (lane == 0) cnt[pw] = c + 1;
+          const int cn = c + D;
+          if (!lds_wait_ge(cnt + 3, cn - R + 1)) {
+            bad = true;
+            break;
+          }
+          asm volatile("" ::: "memory");
+          ring_issue_vp(vgl, (cn < nckv ? cn : nckv - 1) * kVRows, a.ctx, 32 * half, pw, ring + (size_t)(cn % R) * kSlotFloats);
         }
-        if (c > 0 && tid < 32) {
-          const float* slot = ring + (size_t)((c - 1) % R) * kSlotFloats + tid;
-          const int n = pos - (c - 1) * kVRows;
+      } else {
+        for (int c = 0; c < nckv; c++) {
+          if (!lds_wait_ge3(cnt, c + 1)) {
+            bad = true;
+            break;
+          }
+          asm volatile("" ::: "memory");
+          // lanes 0..31 hold this workgroup's columns (lanes 32..63 read the next row, unused)
+          const float* slot = ring + (size_t)(c % R) * kSlotFloats + lane;
+          const int n = pos - c * kVRows;
           float pr[kVRows];
 #pragma unroll
           for (int u = 0; u < kVRows; u++) pr[u] = slot[u * 32];
@@ -1371,11 +1430,15 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
             for (int u = 0; u < kVRows / 2; u++) accv = accv + pr[u];
 #pragma unroll
             for (int u = kVRows / 2; u < kVRows; u++) pin(pr[u]);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0) cnt[3] = c + 1;
 #pragma unroll
             for (int u = kVRows / 2; u < kVRows; u++) accv = accv + pr[u];
           } else {
 #pragma unroll
             for (int u = kVRows / 2; u < kVRows; u++) pin(pr[u]);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0) cnt[3] = c + 1;
 #pragma unroll
             for (int u = 0; u < kVRows; u++) {
               const float t = accv + pr[u];
@@ -1383,10 +1446,12 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
             }
           }
         }
-        const int cn = c + R - 2;
-        ring_issue_half(vgl, (cn < nckv ? cn : nckv - 1) * kVRows, a.ctx, 32 * half, ring + (size_t)(cn % R) * kSlotFloats);
       }
-      if (nckv > 0) ring_drain();
+      ring_drain();
+      if (__syncthreads_or(bad)) {
+        if (tid == 0) __hip_atomic_store(&a.st->abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+      }
       if (tid < 32) {
         const int d = 32 * half + tid;
         accv = accv + sc[pos] * vv[d];
