@@ -111,7 +111,7 @@ def summarize(a) -> None:
     lines = [
         f"# Persistent decode kernel, Qwen2.5-0.5B shape, {steps} greedy steps per launch",
         "",
-        "Commands (repo root on the GPU box, `cd /tmp && export TMPDIR=/tmp` first; paths absolute):",
+        "Commands (repository root on the MI355X host, `cd /tmp && export TMPDIR=/tmp` first; paths absolute):",
         "",
         "```",
         f"rocprofv3 --kernel-trace --stats -d T -o t --output-format csv -- python3 e2e-browser-voice-agent_amd/py/profile_decode.py run --steps {steps}",
@@ -167,7 +167,7 @@ def steps(a) -> None:
         c[1] += d
     busy = sum(v[1] for v in agg.values()) / nsteps
     span = (int(rest[-1]["End_Timestamp"]) - int(rest[0]["Start_Timestamp"])) / 1e3 / nsteps
-    lines = [f"# {a.title}", "", "Commands (repo root on the GPU box, `cd /tmp && export TMPDIR=/tmp` first; paths absolute):",
+    lines = [f"# {a.title}", "", "Commands (repository root on the MI355X host, `cd /tmp && export TMPDIR=/tmp` first; paths absolute):",
              "", "```", a.command,
              f"python3 e2e-browser-voice-agent_amd/py/profile_decode.py steps --trace T --marker {a.marker} --skip {a.skip} "
              f"--title ... --command ... --out <this file>", "```", "",

@@ -1,8 +1,8 @@
 /*
  * oracle.c -- CPU restatement of the reference's Qwen2 Q4_0 token loop.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for tests/, the smoke check and the
- * CPU-baseline leg of bench.py.  The product never links or calls it.
+ * TEST INFRASTRUCTURE ONLY: computes the expected results for tests/, the smoke
+ * check and the CPU-baseline leg of bench.py.  The product never links or calls it.
  *
  * Follows h2-own-inference-engine/engine/kernels.c (plain SIMD128 build) and
  * h2-own-inference-engine/engine/cpu-worker.js.  Each 128-bit SIMD value of the

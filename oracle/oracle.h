@@ -1,9 +1,8 @@
 /*
  * oracle.h -- CPU restatement of the reference's Qwen2 Q4_0 token loop.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: tests/, the smoke
- * check and the CPU-baseline leg of bench.py load it to compute expected
- * results.  The product (the HIP library, the N-API addon and the JavaScript
+ * TEST INFRASTRUCTURE ONLY.  tests/, the smoke check and the CPU-baseline leg
+ * of bench.py load this library to compute expected results.  The product (the HIP library, the N-API addon and the JavaScript
  * backend) never links, loads or calls it.
  *
  * It restates, in scalar C with the same floating-point operation order,

@@ -1,7 +1,7 @@
 """ctypes binding of liboracle.so, the CPU restatement of the reference's token loop.
 
-TEST INFRASTRUCTURE ONLY: imported by tests/, the smoke check and bench.py's CPU-baseline leg as
-the checker.  The product never imports it.
+TEST INFRASTRUCTURE ONLY: imported by tests/, the smoke check and bench.py's CPU-baseline leg to
+compute expected results.  The product never imports it.
 
 Weights are fed the way engine/cpu-worker.js feeds kernels.c: Q4_0 blocks split into 16 value
 bytes + an fp32 scale (copyBlocks, cpu-worker.js:97-104), q|k|v and gate|up fused by rows
