@@ -576,6 +576,11 @@ __global__ void k_set_pos(State* st, int pos0) {
   if (threadIdx.x == 0) st->pos0 = pos0;
 }
 
+// Raises the abort flag (what a timed-out bounded wait does), for the test of the rerun path.
+__global__ void k_raise_abort(State* st) {
+  if (threadIdx.x == 0) st->abort = 1;
+}
+
 // Q4_0 GEMM for few tokens: y[m][n] (+)= W[n] . x[m] for M <= a few dozen tokens, with every
 // output accumulated exactly as matmul_q4 does (four lane chains over the blocks in order, then
 // the lane sum; kernels.c:200-229), so results equal k_matvec's and k_gemm_q4's bit for bit.
@@ -1421,6 +1426,7 @@ struct q4hip {
   int pers_kv_tile = 0;
   size_t pers_lds = 0;
   int pers_ring = 0;
+  int pers_test_abort = 0;   // persistent launches still to start with the abort flag raised
   int pers_nap = 1;
   const void* pers_fn = nullptr;
   uint64_t* lsc = nullptr;     // score exchange of the split attention ([H][ctx] entries)
@@ -1722,6 +1728,7 @@ void setup_persistent(q4hip* h) {
     }
   }
   if (const char* e = getenv("Q4HIP_SPLIT_FROM")) h->pers_split_from = std::max(0, atoi(e));
+  if (const char* e = getenv("Q4HIP_TEST_ABORT")) h->pers_test_abort = std::max(0, atoi(e));
   h->pers_ok = true;
   h->pers_broken = false;
 }
@@ -1778,6 +1785,10 @@ hipError_t launch_persistent(q4hip* h, int pos0, int steps, unsigned long long* 
   a.ring = h->pers_ring;
   a.nap = h->pers_nap;
   a.prof = prof;
+  if (h->pers_test_abort > 0) {          // Q4HIP_TEST_ABORT: the launch finds the flag raised
+    h->pers_test_abort--;
+    k_raise_abort<<<1, 64, 0, h->stream>>>(h->st);
+  }
   void* args[] = {&a};
   return hipLaunchKernel(h->pers_fn, dim3(h->pers_grid), dim3(kPThreads), args, h->pers_lds, h->stream);
 }

@@ -305,3 +305,28 @@ def test_split_attention_decode(name, seed, n_prompt, monkeypatch):
     finally:
         g.close()
         o.close()
+
+
+def test_persistent_timeout_reruns_on_graph_path(monkeypatch):
+    """A persistent launch whose bounded waits give up raises the abort flag; the library then reruns
+    the call on the graph path and keeps the context there.  The flag is raised from the host before
+    the first persistent launch (Q4HIP_TEST_ABORT=1), so every kernel still exits normally: tokens
+    and logits still equal the oracle's, and the mode used afterwards is the graph path."""
+    import q4hip
+    monkeypatch.setenv("Q4HIP_TEST_ABORT", "1")
+    print("persistent abort -> graph rerun", flush=True)
+    shape, g, o = _pair("tiny", 61, ctx=128, mode="persistent")
+    try:
+        ids = synth.prompt_ids(61, 12, shape.vocab)
+        ng, no = g.forward(ids, 0), o.forward(ids, 0)
+        assert ng == no
+        dev = g.generate(ng, len(ids), 16)
+        tok = no
+        for i in range(16):
+            tok = o.forward([tok], len(ids) + i)
+            assert dev[i] == tok, f"step {i}"
+        _compare_logits(g, o, "last step")
+        assert g.decode_mode_used() == q4hip.DECODE_GRAPH
+    finally:
+        g.close()
+        o.close()
