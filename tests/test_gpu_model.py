@@ -330,3 +330,31 @@ def test_persistent_timeout_reruns_on_graph_path(monkeypatch):
     finally:
         g.close()
         o.close()
+
+
+def test_long_context_qwen05b_4096():
+    """The long-context workload itself: Qwen2.5-0.5B shape, 4096 cached fp16-valued positions written
+    through q4hip_set_kv, then single decode steps on the persistent path (two attention workgroups per
+    head, K/V streamed through the ring): tokens and logits equal the oracle's at every step."""
+    import q4hip
+    print("qwen2.5-0.5b long context 4096 positions", flush=True)
+    P = 4096
+    shape, g, o = _pair("qwen2.5-0.5b", 41, ctx=P + 40, threads=16, mode="persistent")
+    try:
+        k, v = _fill_kv(shape, P, 41)
+        ok, ov = o.kv()
+        ok[:, :, :P] = k
+        ov[:, :, :P] = v
+        for l in range(shape.layers):
+            for kh in range(shape.kv_heads):
+                g.set_kv(l, kh, 0, k[l, kh], v[l, kh])
+        tok = 7
+        for step in range(4):
+            ng, no = g.forward([tok], P + step), o.forward([tok], P + step)
+            assert ng == no, f"step {step}"
+            _compare_logits(g, o, f"step {step}")
+            tok = ng
+        assert g.decode_mode_used() == q4hip.DECODE_PERSISTENT
+    finally:
+        g.close()
+        o.close()
