@@ -234,3 +234,45 @@ def test_batch_full_size_matches_single_sequence():
         one.close()
     finally:
         g.close()
+
+
+def test_batch_qwen15b_prefilled_1024():
+    """The batched-decode configuration's shape and cache length (Qwen2.5-1.5B, 1024 cached positions
+    per sequence written through q4hip_batch_set_kv, different contents and positions): every
+    sequence's tokens and last logits equal the oracle's over the same cache."""
+    import q4hip
+    shape = synth.SHAPES["qwen2.5-1.5b"]
+    t = _model("qwen2.5-1.5b", 50)
+    P, B, ctx, steps = 1024, 4, 1040, 2
+    print(f"qwen15b batch of {B}, {P}-position caches", flush=True)
+    g = q4hip.Model(shape, ctx=ctx)
+    g.load(t)
+    o = oracle.Model(shape, t, ctx=ctx, mt=16, threads=16)
+    bt = q4hip.Batch(g, B)
+    try:
+        caches = []
+        for b in range(B):
+            r = np.random.default_rng(200 + b)
+            k = r.standard_normal((shape.layers, shape.kv_heads, P, shape.head_dim)).astype(np.float16).astype(np.float32)
+            v = r.standard_normal((shape.layers, shape.kv_heads, P, shape.head_dim)).astype(np.float16).astype(np.float32)
+            caches.append((k, v))
+            for l in range(shape.layers):
+                for kh in range(shape.kv_heads):
+                    bt.set_kv(b, l, kh, 0, k[l, kh], v[l, kh])
+        first = [5, 17, 900, 4242]
+        pos = [P, P - 1, P - 100, P - 511]
+        out = bt.generate(first, pos, steps)
+        lg = bt.read_logits()
+        for b in range(B):
+            ok, ov = o.kv()
+            ok[:, :, :P] = caches[b][0]
+            ov[:, :, :P] = caches[b][1]
+            tok = first[b]
+            for i in range(steps):
+                tok = o.forward([tok], pos[b] + i)
+                assert out[i, b] == tok, f"sequence {b} step {i}"
+            _same_logits(lg[b], o.logits(), f"sequence {b}")
+    finally:
+        bt.close()
+        g.close()
+        o.close()
