@@ -358,3 +358,22 @@ def test_long_context_qwen05b_4096():
     finally:
         g.close()
         o.close()
+
+
+def test_prefill_qwen05b_1024():
+    """The prefill workload: a 1024-token prompt on the Qwen2.5-0.5B shape in one pass (every projection
+    on the exact matrix-core GEMMs, attention on the list kernels) gives the oracle's next token and
+    logits, and the first decode step after it agrees too."""
+    print("qwen2.5-0.5b prefill 1024", flush=True)
+    shape, g, o = _pair("qwen2.5-0.5b", 42, ctx=1040, threads=16, mode="persistent")
+    try:
+        ids = synth.prompt_ids(42, 1024, shape.vocab)
+        ng, no = g.forward(ids, 0), o.forward(ids, 0)
+        assert ng == no
+        _compare_logits(g, o, "prefill")
+        ng, no = g.forward([ng], 1024), o.forward([no], 1024)
+        assert ng == no
+        _compare_logits(g, o, "step after the prompt")
+    finally:
+        g.close()
+        o.close()
