@@ -208,6 +208,31 @@ enum QuantMode { QM_PLAIN = 0, QM_NORM = 1, QM_SWIGLU = 2 };
 // `outh` (optional): the matrix-core operand of the multi-token GEMM, 32 bytes per (block, lane j):
 // the 8 int8 values as fp16 (exact) in the order of `out`'s two words, then -sum of the 8 values
 // as fp16 (exact, |sum| <= 1016), then 7 zero halves.
+// One work item (block b, lane j) of quantize_row from its 8 values (elements 2j, 2j+1, 2j+8, 2j+9,
+// 2j+16, 2j+17, 2j+24, 2j+25 of the block): the block maximum over the quad of lanes j = 0..3 (four
+// consecutive threads of one wave, all active), the scale, the int8 values and their sum, written as
+// out[b*4 + j] and, when given, the matrix-core operand outh[2 (b*4 + j)], outh[2 (b*4 + j) + 1].
+__device__ __forceinline__ void quantize_item(const float (&v)[8], int b, int j, uint4* __restrict__ out,
+                                              uint4* __restrict__ outh) {
+  float am = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; k++) am = __builtin_fmaxf(am, __builtin_fabsf(v[k]));
+  am = quad_max(am);
+  const float dd = div_127(am);
+  const float id = inv_scale(dd);
+  int q[8];
+  int sum = 0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) { q[k] = quant_one(v[k] * id); sum += q[k]; }
+  out[(b << 2) + j] = make_uint4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]),
+                                 (uint32_t)(-8 * sum), __float_as_uint(dd));
+  if (outh) {
+    outh[2 * ((b << 2) + j)] = make_uint4(pack_f16x2(q[0], q[1]), pack_f16x2(q[2], q[3]), pack_f16x2(q[4], q[5]),
+                                          pack_f16x2(q[6], q[7]));
+    outh[2 * ((b << 2) + j) + 1] = make_uint4(pack_f16x2(-sum, 0), 0u, 0u, 0u);
+  }
+}
+
 template <int MODE>
 __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, const float* xl, int st, int n,
                                                  const float* __restrict__ w, float rs,
@@ -252,23 +277,7 @@ __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, c
         }
       }
     }
-    float am = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; k++) am = __builtin_fmaxf(am, __builtin_fabsf(v[k]));
-    am = quad_max(am);
-    const float dd = div_127(am);
-    const float id = inv_scale(dd);
-    int q[8];
-    int sum = 0;
-#pragma unroll
-    for (int k = 0; k < 8; k++) { q[k] = quant_one(v[k] * id); sum += q[k]; }
-    out[(b << 2) + j] = make_uint4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]),
-                                   (uint32_t)(-8 * sum), __float_as_uint(dd));
-    if (outh) {
-      outh[2 * ((b << 2) + j)] = make_uint4(pack_f16x2(q[0], q[1]), pack_f16x2(q[2], q[3]), pack_f16x2(q[4], q[5]),
-                                            pack_f16x2(q[6], q[7]));
-      outh[2 * ((b << 2) + j) + 1] = make_uint4(pack_f16x2(-sum, 0), 0u, 0u, 0u);
-    }
+    quantize_item(v, b, j, out, outh);
   }
 }
 

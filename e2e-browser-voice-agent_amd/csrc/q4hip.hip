@@ -970,7 +970,8 @@ template <int HD, int CR>
 __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ sc, int H, int KVH,
                                                       const float* __restrict__ vc, int ctx, int layer,
                                                       float* __restrict__ att, int D, const int* __restrict__ pos,
-                                                      size_t seq_stride) {
+                                                      size_t seq_stride, uint4* __restrict__ xq, int xstride,
+                                                      uint4* __restrict__ xh) {
   extern __shared__ __attribute__((aligned(16))) float lsm[];
   constexpr int CRS = CR + 4, NV = CR * kPvCols / 4 / 256;      // chunk rows (LDS stride), float4 per thread
   constexpr int PB = 2;                   // score float4 per thread and head in one pass (2048 positions)
@@ -1232,6 +1233,20 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
     }
   }
   if (active) att[(size_t)b * D + (g * G + gh) * HD + c0 + c] = acc;
+  if (xq) {
+    // the o projection's activation: each head's 32 outputs are one quantize_row block of row b
+    // (what k_quant<QM_PLAIN> would compute from att), quantized here by lanes (head, j) of wave 0
+    __syncthreads();
+    if (active) vs[gh * kPvCols + c] = acc;
+    __syncthreads();
+    if (tid < 4 * G) {
+      const int hh = tid >> 2, j = tid & 3, base = hh * kPvCols + 2 * j;
+      const float v[8] = {vs[base], vs[base + 1], vs[base + 8], vs[base + 9],
+                          vs[base + 16], vs[base + 17], vs[base + 24], vs[base + 25]};
+      const int blk = ((g * G + hh) * HD + c0) >> 5;
+      quantize_item(v, blk, j, xq + (size_t)b * xstride * 4, xh ? xh + (size_t)b * xstride * 8 : nullptr);
+    }
+  }
 }
 
 // Greedy token of every row of logits [B][V] (first maximum, cpu-worker.js:157): partial maxima
@@ -1538,18 +1553,19 @@ size_t attn_pv_lds(int H, int KVH, int ctx) {
   return (size_t)(2 * kPvCols * (kPvRows + 4) + G * pv_row_stride(ctx) + 6 * kMaxGroup) * sizeof(float);
 }
 
+// With xq, the P.V kernel also writes the quantized activation of att (k_quant<QM_PLAIN>'s output).
 void launch_attn_list(hipStream_t s, int HD, int B, int H, int KVH, const float* qkv, int QKV, const float* kc,
                       const float* vc, int ctx, int layer, float* sc, float* att, int D, const int* pos,
-                      size_t seq_stride) {
+                      size_t seq_stride, uint4* xq = nullptr, int xstride = 0, uint4* xh = nullptr) {
   const dim3 sg((unsigned)((ctx + kScoreRows - 1) / kScoreRows), (unsigned)KVH, (unsigned)B);
   const dim3 pg((unsigned)(HD / kPvCols), (unsigned)KVH, (unsigned)B);
   const size_t lds = attn_pv_lds(H, KVH, ctx);
   if (HD == 64) {
     k_attn_scores_list<64><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, seq_stride);
-    k_attn_pv_list<64, kPvRows><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride);
+    k_attn_pv_list<64, kPvRows><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride, xq, xstride, xh);
   } else {
     k_attn_scores_list<128><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, seq_stride);
-    k_attn_pv_list<128, kPvRows><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride);
+    k_attn_pv_list<128, kPvRows><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride, xq, xstride, xh);
   }
 }
 
@@ -1587,8 +1603,11 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
     prof_mark(h, Q4HIP_PROF_ROPE);
     k_rope_kv<<<dim3(h->H + h->KVH, M), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, h->kc, h->vc, h->ctx, l, h->st);
     prof_mark(h, Q4HIP_PROF_ATTN);
+    bool quantized = false;                 // the list P.V kernel wrote xq (and xh) itself
     if (M > 1 && h->ascr && h->list_attn == 1) {
-      launch_attn_list(s, HD, M, h->H, h->KVH, h->qkv, QKV, h->kc, h->vc, h->ctx, l, h->ascr, h->att, D, h->tpos, 0);
+      launch_attn_list(s, HD, M, h->H, h->KVH, h->qkv, QKV, h->kc, h->vc, h->ctx, l, h->ascr, h->att, D, h->tpos, 0,
+                       h->xq, h->xstride, xh);
+      quantized = true;
     } else if (M > 1 && h->ascr) {
       const dim3 ag(h->H, (M + kAttnTokens - 1) / kAttnTokens);
       if (HD == 64)
@@ -1596,14 +1615,16 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
       else
         k_attn_prefill<128><<<ag, 256, 0, s>>>(h->qkv, QKV, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, D, h->st, M, h->ascr);
     } else if (M == 1 && h->ascr && h->list_attn == 1) {
-      launch_attn_list(s, HD, 1, h->H, h->KVH, h->qkv, QKV, h->kc, h->vc, h->ctx, l, h->ascr, h->att, D, &h->st->pos0, 0);
+      launch_attn_list(s, HD, 1, h->H, h->KVH, h->qkv, QKV, h->kc, h->vc, h->ctx, l, h->ascr, h->att, D, &h->st->pos0, 0,
+                       h->xq, h->xstride, xh);
+      quantized = true;
     } else if (HD == 64) {
       k_attn<64><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, h->st);
     } else {
       k_attn<128><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, h->st);
     }
     prof_mark(h, Q4HIP_PROF_QUANT);
-    launch_quant<QM_PLAIN>(s, M, h->att, D, D, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
+    if (!quantized) launch_quant<QM_PLAIN>(s, M, h->att, D, D, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
     prof_mark(h, Q4HIP_PROF_O);
     launch_matvec<OP_ADD>(s, y.o, h->xq, h->xstride, M, h->x, D, nullptr, xh);
     prof_mark(h, Q4HIP_PROF_NORM_Q);
@@ -2282,8 +2303,7 @@ void enqueue_batch_step(q4hip_batch* bt, int* out) {
     k_rope_kv_list<<<dim3(h->H + h->KVH, B), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, bt->kc,
                                                              bt->vc, h->ctx, l, bt->pos, bt->seq_stride);
     launch_attn_list(s, HD, B, h->H, h->KVH, h->qkv, QKV, bt->kc, bt->vc, h->ctx, l, bt->sc, h->att, D, bt->pos,
-                     bt->seq_stride);
-    launch_quant<QM_PLAIN>(s, B, h->att, D, D, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
+                     bt->seq_stride, h->xq, h->xstride, xh);
     launch_matvec<OP_ADD>(s, y.o, h->xq, h->xstride, B, h->x, D, nullptr, xh);
     launch_quant<QM_NORM>(s, B, h->x, D, D, y.ffn_norm, h->eps, h->xq, h->xstride, 0, xh);
     launch_matvec<OP_STORE>(s, y.gu, h->xq, h->xstride, B, h->gu, 2 * F, nullptr, xh);
