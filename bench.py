@@ -72,7 +72,7 @@ def profiled_traffic():
 
 def cpu_baseline(shape, tensors, ids, first_tokens):
     """The oracle on the host cores: prompt with every logical core, decode with ceil(cores/2)
-    threads (the reference's policy, engine/cpu.js:203-205); median ms per decode token."""
+    threads (the reference's policy, engine/cpu.js:21-23); median ms per decode token."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle
     cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()

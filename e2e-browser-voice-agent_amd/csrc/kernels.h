@@ -27,7 +27,7 @@
 namespace q4 {
 
 constexpr int kRowTile = 64;        // rows per weight tile
-constexpr int kMaxChunk = 16;       // the reference's prompt chunk (MT, engine/cpu.js:228): the per-token matvec's tile
+constexpr int kMaxChunk = 16;       // the reference's prompt chunk (MT, engine/cpu.js:46): the per-token matvec's tile
 constexpr int kMaxPass = 1024;      // tokens per device pass; results do not depend on the chunking
 
 // Device-resident step state: pos0 of the current pass, last sampled token.  Kernels read

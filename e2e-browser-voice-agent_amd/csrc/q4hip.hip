@@ -1442,6 +1442,7 @@ struct q4hip {
   size_t pers_lds = 0;
   int pers_ring = 0;
   int pers_test_abort = 0;   // persistent launches still to start with the abort flag raised
+  int pers_last_steps = 0;   // steps of the last persistent launch (the epochs it may have used)
   int pers_nap = 1;
   const void* pers_fn = nullptr;
   uint64_t* lsc = nullptr;     // score exchange of the split attention ([H][ctx] entries)
@@ -1806,6 +1807,7 @@ hipError_t launch_persistent(q4hip* h, int pos0, int steps, unsigned long long* 
   a.ring = h->pers_ring;
   a.nap = h->pers_nap;
   a.prof = prof;
+  h->pers_last_steps = steps;
   if (h->pers_test_abort > 0) {          // Q4HIP_TEST_ABORT: the launch finds the flag raised
     h->pers_test_abort--;
     k_raise_abort<<<1, 64, 0, h->stream>>>(h->st);
@@ -1818,12 +1820,18 @@ hipError_t launch_persistent(q4hip* h, int pos0, int steps, unsigned long long* 
 // example because another process held CUs so not every workgroup could start).  Clears the flag,
 // switches this context to the graph path and returns true: the caller reruns the call, which
 // overwrites everything the aborted launch wrote (K/V from pos on, tokens after pos).
+// An aborted launch returns before it advances the epoch, and some of its roles have already
+// posted exchange entries tagged with epochs of that launch (the KV role posts layer 0's rows
+// without waiting for anything).  The epoch is moved past every epoch the launch could use, so a
+// later persistent launch (after q4hip_set_decode_mode re-enables the path) never takes those
+// entries for its own.
 bool aborted(q4hip* h) {
   State hs;
   if (hipMemcpy(&hs, h->st, sizeof(State), hipMemcpyDeviceToHost) != hipSuccess) return false;
   if (!hs.abort) return false;
   h->pers_broken = true;
   hs.abort = 0;
+  hs.epoch += (uint32_t)h->pers_last_steps * (uint32_t)(4 * h->NL + 1) + 2u;
   (void)hipMemcpy(h->st, &hs, sizeof(State), hipMemcpyHostToDevice);
   return true;
 }
@@ -2028,9 +2036,12 @@ int q4hip_set_tensor(q4hip* h, int kind, int layer, int row0, int type, const vo
   return fail(Q4HIP_EINVAL, "unknown tensor kind %d", kind);
 }
 
-int q4hip_set_rope(q4hip* h, const float* table, int n_pos) {
+int q4hip_set_rope(q4hip* h, const float* table, int64_t n_floats) {
   if (!h || !table) return fail(Q4HIP_EINVAL, "null argument");
-  if (n_pos < h->ctx) return fail(Q4HIP_EINVAL, "RoPE table has %d positions, ctx is %d", n_pos, h->ctx);
+  const int64_t need = (int64_t)h->ctx * h->HD;
+  if (n_floats < need)
+    return fail(Q4HIP_EINVAL, "RoPE table has %lld floats, ctx %d x head_dim %d needs %lld", (long long)n_floats,
+                h->ctx, h->HD, (long long)need);
   HIPCHK(hipSetDevice(h->device));
   HIPCHK(hipMemcpy(h->rope, table, (size_t)h->ctx * h->HD * 4, hipMemcpyHostToDevice));
   h->rope_set = true;

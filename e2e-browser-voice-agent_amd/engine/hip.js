@@ -4,7 +4,7 @@
 //   createHIP(gguf, bytes, cfg, opts) -> Promise<backend>
 //
 // The backend object has the surface the reference engine's LLM class drives
-// (h2-own-inference-engine/engine/cpu.js:234-250, engine/webgpu.js:617-620):
+// (h2-own-inference-engine/engine/cpu.js:52-68, engine/webgpu.js:617-620):
 //   name, ctx, info, forward(ids, pos, {temperature, seed, wantLogits}) -> next id,
 //   readLogits() -> Float32Array(vocab), profile(), destroy()
 // plus generate(first, pos, steps), the greedy loop run on the device.
@@ -62,6 +62,12 @@ function sample(lg, temperature, seed) {
   return best;
 }
 
+// The token forward() returns after a call at position pos: sample() seeded with (seed + pos) >>> 0,
+// as engine/cpu-worker.js:180 seeds it.
+function sampleAt(lg, temperature, seed, pos) {
+  return sample(lg, temperature, (seed + pos) >>> 0);
+}
+
 function check(T, name, types, label) {
   const t = T[name];
   if (!t) throw new Error(`${name}: missing`);
@@ -116,7 +122,7 @@ async function createHIP(gguf, bytes, cfg, opts = {}) {
     up(KIND.EMBD, 0, 0, embd);
     up(KIND.OUTPUT, 0, 0, out);
     up(KIND.OUTPUT_NORM, 0, 0, outNorm);
-    a.setRope(h, ropeTable(ctx, HD, ropeTheta), ctx);
+    a.setRope(h, ropeTable(ctx, HD, ropeTheta));
   } catch (e) {
     a.destroy(h);
     throw e;
@@ -134,7 +140,7 @@ async function createHIP(gguf, bytes, cfg, opts = {}) {
       const next = a.forward(h, Int32Array.from(ids), pos);
       if (!(temperature > 0)) return next;
       a.readLogits(h, logits);
-      return sample(logits, temperature, (seed + pos) >>> 0);
+      return sampleAt(logits, temperature, seed, pos);
     },
     async readLogits() {
       a.readLogits(h, logits);
@@ -158,4 +164,4 @@ async function createHIP(gguf, bytes, cfg, opts = {}) {
   };
 }
 
-module.exports = { createHIP, ropeTable, sample, KIND };
+module.exports = { createHIP, ropeTable, sample, sampleAt, KIND };

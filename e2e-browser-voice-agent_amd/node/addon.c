@@ -4,7 +4,7 @@
  * Thin by design: every function converts JavaScript arguments to the C ABI's plain pointers and
  * sizes, calls it, and turns a non-zero status into a thrown Error whose message is
  * q4hip_last_error() and whose `code` is the status.  Calls are synchronous; the JavaScript layer
- * keeps the reference backend's async surface (engine/cpu.js:237-248) on top.
+ * keeps the reference backend's async surface (engine/cpu.js:55-62) on top.
  */
 #include <node_api.h>
 #include <stdint.h>
@@ -144,22 +144,22 @@ static napi_value js_set_tensor(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
-/* setRope(handle, Float32Array table, nPos) */
+/* setRope(handle, Float32Array table): the library checks the table's float count against
+ * ctx * head_dim and reads nothing from a shorter one. */
 static napi_value js_set_rope(napi_env env, napi_callback_info info) {
-  size_t argc = 3;
-  napi_value a[3];
+  size_t argc = 2;
+  napi_value a[2];
   NAPI_CALL(env, napi_get_cb_info(env, info, &argc, a, NULL, NULL));
-  if (argc < 3) { napi_throw_type_error(env, NULL, "setRope: 3 arguments"); return NULL; }
+  if (argc < 2) { napi_throw_type_error(env, NULL, "setRope: 2 arguments"); return NULL; }
   q4hip* h = get_handle(env, a[0]);
   if (!h) return NULL;
   void* data;
   size_t len;
-  int32_t npos;
-  if (!get_bytes(env, a[1], &data, &len) || !get_i32(env, a[2], &npos)) {
-    napi_throw_type_error(env, NULL, "setRope: bad arguments");
+  if (!get_bytes(env, a[1], &data, &len)) {
+    napi_throw_type_error(env, NULL, "setRope: Float32Array expected");
     return NULL;
   }
-  int rc = q4hip_set_rope(h, (const float*)data, npos);
+  int rc = q4hip_set_rope(h, (const float*)data, (int64_t)(len / 4));
   if (rc) return throw_status(env, rc);
   return NULL;
 }

@@ -54,7 +54,7 @@ def lib() -> ctypes.CDLL:
         "q4hip_check_division": (I, [I, P, I]),
         "q4hip_create": (I, [ctypes.POINTER(P), I, I, I, I, I, I, I, I, F, I]),
         "q4hip_set_tensor": (I, [P, I, I, I, I, P, I64, ctypes.c_size_t]),
-        "q4hip_set_rope": (I, [P, P, I]),
+        "q4hip_set_rope": (I, [P, P, I64]),
         "q4hip_forward": (I, [P, P, I, I, ctypes.POINTER(I)]),
         "q4hip_read_logits": (I, [P, P, I]),
         "q4hip_generate": (I, [P, I, I, I, P]),
@@ -161,7 +161,7 @@ class Model:
         if rope is None:
             rope = synth.rope_table(self.ctx, s.head_dim, s.rope_theta)
         rope = np.ascontiguousarray(rope, dtype=np.float32)
-        _check(lib().q4hip_set_rope(self.h, _ptr(rope), rope.shape[0]))
+        _check(lib().q4hip_set_rope(self.h, _ptr(rope), rope.size))
 
     def set_kv(self, layer: int, kv_head: int, pos0: int, k: np.ndarray, v: np.ndarray) -> None:
         """Write K and V rows [n][head_dim] of one layer and kv head at positions pos0.."""

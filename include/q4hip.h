@@ -3,7 +3,7 @@
  *
  * One opaque context per loaded model, bound to one GPU and one HIP stream.
  * Calls on a context are serialized by the caller (one job at a time, as the
- * reference backend's single `pending` slot does, engine/cpu.js:215-232);
+ * reference backend's single `pending` slot does, engine/cpu.js:33-50);
  * contexts are independent.  Every entry point returns Q4HIP_OK (0) or an
  * error code; q4hip_last_error() gives the message of the calling thread's
  * last failure ("context full", "kind 0: expected Q4_0", a HIP error ...).
@@ -70,9 +70,10 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
 int q4hip_set_tensor(q4hip* h, int kind, int layer, int row0, int ggml_type, const void* data,
                      int64_t rows, size_t nbytes);
 
-/* Upload the RoPE table: fp32 [n_pos][head_dim/2][2] = cos, sin of pos/theta^(2i/head_dim),
- * computed in double by the host as engine/cpu-worker.js:130-135 does.  n_pos >= ctx. */
-int q4hip_set_rope(q4hip* h, const float* table, int n_pos);
+/* Upload the RoPE table: fp32 [pos][head_dim/2][2] = cos, sin of pos/theta^(2i/head_dim),
+ * computed in double by the host as engine/cpu-worker.js:130-135 does.  `n_floats` is the number
+ * of floats `table` holds; fewer than ctx * head_dim is rejected (nothing is read). */
+int q4hip_set_rope(q4hip* h, const float* table, int64_t n_floats);
 
 /* Run tokens ids[0..n) at positions pos..pos+n-1 and return the greedy next token (first
  * maximum wins): replaces forward() of engine/cpu-worker.js:169-182 with temperature 0, i.e.
@@ -86,7 +87,7 @@ int q4hip_forward(q4hip* h, const int* ids, int n, int pos, int* next);
  *   PERSISTENT one launch per call that runs all of the call's steps; fails with
  *              Q4HIP_EINVAL if the model (head_dim 64, D <= 1024, ...) or device does not admit it.
  * Both give bit-identical results.  The reference picks among its kernel builds the same way
- * (engine/cpu.js:199-206); this has no other counterpart there. */
+ * (engine/cpu.js:18-24); this has no other counterpart there. */
 #define Q4HIP_DECODE_AUTO 0
 #define Q4HIP_DECODE_GRAPH 1
 #define Q4HIP_DECODE_PERSISTENT 2
@@ -94,7 +95,7 @@ int q4hip_set_decode_mode(q4hip* h, int mode);
 /* The path the last decode step took (Q4HIP_DECODE_GRAPH or Q4HIP_DECODE_PERSISTENT; 0 before any). */
 int q4hip_decode_mode_used(q4hip* h, int* mode);
 
-/* Copy the last forward's logits (vocab floats) to host memory: readLogits (engine/cpu.js:242). */
+/* Copy the last forward's logits (vocab floats) to host memory: readLogits (engine/cpu.js:60-62). */
 int q4hip_read_logits(q4hip* h, float* out, int n);
 
 /* Greedy continuation on the device: token `first` at position `pos`, then `steps` decode steps,
@@ -155,7 +156,7 @@ void q4hip_destroy(q4hip* h);
 
 /* ---- batched decode -------------------------------------------------------------------------
  * B independent sequences decoded together, one token each per step, with the context's weights.
- * The reference decodes one sequence per backend (engine/cpu.js:215-232, engine/llm.js:86-97); a
+ * The reference decodes one sequence per backend (engine/cpu.js:33-50, engine/llm.js:86-97); a
  * batch runs B such loops at once, and every sequence's tokens and logits are the ones its own
  * loop would give.  Each sequence has its own fp32 K/V cache of the context's ctx positions; the
  * context's activation buffers are shared, so B <= the context's pass size and calls on a batch and

@@ -5,6 +5,7 @@
 //   generate <gguf> <ctx> <ids.json> <steps> <logits.f32>
 //        -> {tokens (per-step forward loop), device (device loop), stats}; last logits written raw
 //   sample <logits.f32> <temperature> <seed>      -> {id}
+//   samples <cases.json>                           -> [id] for [{logits (path to raw f32), temperature, seed, pos}]
 //   tokenize <meta.json> <texts.json>              -> {ids, text, pieces} per text (tokenizer alone)
 //   chat <gguf> <ctx> <turns.json> <maxTokens>     -> per turn {pieces, ids, prompt, stats}
 const fs = require("fs");
@@ -12,7 +13,7 @@ const path = require("path");
 const engine = path.join(__dirname, "..", "..", "e2e-browser-voice-agent_amd", "engine");
 const { parseGGUF, qwen2Config, readModel } = require(path.join(engine, "gguf.js"));
 const { LLM } = require(path.join(engine, "llm.js"));
-const { sample } = require(path.join(engine, "hip.js"));
+const { sample, sampleAt } = require(path.join(engine, "hip.js"));
 const { Tokenizer, chatPrompt } = require(path.join(engine, "tokenizer.js"));
 
 async function main() {
@@ -50,6 +51,14 @@ async function main() {
     const b = fs.readFileSync(args[0]);
     const lg = new Float32Array(b.buffer, b.byteOffset, b.length / 4);
     return { id: sample(lg, Number(args[1]), Number(args[2]) >>> 0) };
+  }
+  if (cmd === "samples") {
+    const cases = JSON.parse(fs.readFileSync(args[0], "utf8"));
+    return cases.map((c) => {
+      const b = fs.readFileSync(c.logits);
+      const lg = new Float32Array(b.buffer, b.byteOffset, b.length / 4);
+      return sampleAt(lg, c.temperature, c.seed, c.pos);
+    });
   }
   if (cmd === "tokenize") {
     const tok = new Tokenizer(JSON.parse(fs.readFileSync(args[0], "utf8")));

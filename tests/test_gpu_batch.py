@@ -276,3 +276,56 @@ def test_batch_qwen15b_prefilled_1024():
         bt.close()
         g.close()
         o.close()
+
+
+def _seq_cache(shape, P, seed):
+    """K and V rows [layers][kv_heads][P][head_dim] of one sequence: fp16-valued N(0, 1)."""
+    r = np.random.default_rng(seed)
+    dims = (shape.layers, shape.kv_heads, P, shape.head_dim)
+    k = r.standard_normal(dims, dtype=np.float32).astype(np.float16).astype(np.float32)
+    v = r.standard_normal(dims, dtype=np.float32).astype(np.float16).astype(np.float32)
+    return k, v
+
+
+def test_batch_qwen15b_b32_ctx1024():
+    """The batched-decode configuration as defined: Qwen2.5-1.5B shape, 32 sequences, each with its
+    own cache of about 1024 positions (different contents, written through q4hip_batch_set_kv) and
+    its own position (ragged: 1024 down to 725), then 3 greedy steps of all 32 together.  Every
+    sequence's tokens and last-step logits equal the oracle's, run one sequence at a time over the
+    same cache (engine/llm.js:86-97, engine/kernels.c:355-377)."""
+    import q4hip
+    shape = synth.SHAPES["qwen2.5-1.5b"]
+    t = _model("qwen2.5-1.5b", 51)
+    P, B, ctx, steps = 1024, 32, 1040, 3
+    pos = [P - (b * 37) % 300 for b in range(B)]
+    first = [int(x) for x in np.random.default_rng(51).integers(0, shape.vocab, B)]
+    print(f"qwen15b batch of {B}, {P}-position caches, positions {min(pos)}..{max(pos)}", flush=True)
+    g = q4hip.Model(shape, ctx=ctx)
+    g.load(t)
+    bt = q4hip.Batch(g, B)
+    o = None
+    try:
+        for b in range(B):
+            k, v = _seq_cache(shape, P, 300 + b)
+            for l in range(shape.layers):
+                for kh in range(shape.kv_heads):
+                    bt.set_kv(b, l, kh, 0, k[l, kh], v[l, kh])
+        out = bt.generate(first, pos, steps)
+        lg = bt.read_logits()
+        print("batch done; oracle per sequence", flush=True)
+        o = oracle.Model(shape, t, ctx=ctx, mt=16, threads=16)
+        for b in range(B):
+            k, v = _seq_cache(shape, P, 300 + b)
+            ok, ov = o.kv()
+            ok[:, :, :P] = k
+            ov[:, :, :P] = v
+            tok = first[b]
+            for i in range(steps):
+                tok = o.forward([tok], pos[b] + i)
+                assert out[i, b] == tok, f"sequence {b} step {i}"
+            _same_logits(lg[b], o.logits(), f"sequence {b}")
+    finally:
+        bt.close()
+        g.close()
+        if o is not None:
+            o.close()

@@ -5,6 +5,8 @@ Bar: identical greedy token sequences and bit-identical logits (a floating-point
 max-abs <= 1e-3 would do for logits; the kernels reproduce the reference's operation order, so
 bit equality is what is asserted).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -327,6 +329,18 @@ def test_persistent_timeout_reruns_on_graph_path(monkeypatch):
             assert dev[i] == tok, f"step {i}"
         _compare_logits(g, o, "last step")
         assert g.decode_mode_used() == q4hip.DECODE_GRAPH
+        # Back on the persistent path: the aborted launch left exchange entries of its own epochs
+        # (the K/V rows of layer 0 for token ng at position 12).  A different token at a new
+        # position must not pick them up.
+        g.set_decode_mode(q4hip.DECODE_PERSISTENT)
+        pos = len(ids) + 16
+        other = (ng + 1) % shape.vocab
+        for i in range(3):
+            nt, nto = g.forward([other], pos + i), o.forward([other], pos + i)
+            assert g.decode_mode_used() == q4hip.DECODE_PERSISTENT
+            assert nt == nto, f"persistent step {i} after the rerun"
+            _compare_logits(g, o, f"persistent step {i} after the rerun")
+            other = nt
     finally:
         g.close()
         o.close()
@@ -377,3 +391,33 @@ def test_prefill_qwen05b_1024():
     finally:
         g.close()
         o.close()
+
+
+def test_short_rope_table_rejected():
+    """q4hip_set_rope takes the table's float count and rejects a table shorter than ctx x head_dim
+    before reading it; the N-API addon passes the typed array's length, so a short Float32Array
+    throws instead of being read past its end."""
+    import ctypes
+    import subprocess
+    import q4hip
+    shape = synth.SHAPES["tiny"]
+    g = q4hip.Model(shape, ctx=64)
+    try:
+        short = np.zeros(64 * shape.head_dim - 1, np.float32)
+        rc = q4hip.lib().q4hip_set_rope(g.h, short.ctypes.data_as(ctypes.c_void_p), short.size)
+        assert rc == q4hip.EINVAL and b"RoPE table" in q4hip.lib().q4hip_last_error()
+    finally:
+        g.close()
+    addon = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                         "e2e-browser-voice-agent_amd", "lib", "q4hip.node")
+    js = f"""
+    const a = require({addon!r});
+    const h = a.create({shape.dim}, {shape.layers}, {shape.ffn}, {shape.heads}, {shape.kv_heads}, {shape.vocab}, 64, 0, 1e-6, 0);
+    let msg = "";
+    try {{ a.setRope(h, new Float32Array(10)); }} catch (e) {{ msg = e.message; }}
+    a.destroy(h);
+    console.log(msg);
+    """
+    r = subprocess.run(["node", "-e", js], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "RoPE table has 10 floats" in r.stdout

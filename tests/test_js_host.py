@@ -70,15 +70,97 @@ def test_not_a_gguf(tmp_path):
     assert node("load", str(p), 64)["error"] == "not a GGUF file"
 
 
+def _mulberry32(state):
+    """Tommy Ettinger's mulberry32 (public domain): a 32-bit state advanced by 0x6D2B79F5, mixed
+    with two xorshift-multiply rounds; uniform floats in [0, 1) as output / 2^32."""
+    M = 0xFFFFFFFF
+    while True:
+        state = (state + 0x6D2B79F5) & M
+        z = state
+        z = ((z ^ (z >> 15)) * (z | 1)) & M
+        z ^= (z + (((z ^ (z >> 7)) * (z | 61)) & M)) & M
+        yield ((z ^ (z >> 14)) & M) / 4294967296.0
+
+
+def _sample_ref(lg, temperature, seed, pos, *, const=0x6D2B79F5, use_pos=True, le=True, reverse=False,
+                last_max=False):
+    """Softmax sampling by an inverse-CDF walk (cpu-worker.js:154-167, seeded as :180), written from
+    the algorithm: greedy = first maximum; else u = first PRNG draw, r = u * sum_i e_i with
+    e_i = exp(l_i / T - l_max / T) in double, and the first i with r - (e_0 + ... + e_i) <= 0.
+    The keyword arguments plant mistakes for the sensitivity check."""
+    import math
+    vals = [float(v) for v in lg]
+    best = 0
+    for i in range(1, len(vals)):
+        if vals[i] > vals[best] or (last_max and vals[i] == vals[best]):
+            best = i
+    if not temperature > 0:
+        return best
+    s = ((seed + pos) if use_pos else seed) & 0xFFFFFFFF
+    u = next(_mulberry32((s + const - 0x6D2B79F5) & 0xFFFFFFFF))
+    mx = vals[best] / temperature
+    e = [math.exp(v / temperature - mx) for v in vals]
+    r = u * sum(e)          # left-to-right sum, as the walk's loop
+    order = range(len(vals) - 1, -1, -1) if reverse else range(len(vals))
+    for i in order:
+        r -= e[i]
+        if (r <= 0) if le else (r < 0):
+            return i
+    return best
+
+
+def _first_draw_multiple_of(step, pos):
+    """A seed whose first draw at position pos is a multiple of step / 2^32 (so r lands exactly on
+    a boundary of an all-equal distribution over 2^32 / step entries)."""
+    for seed in range(1, 1 << 24):
+        s = (seed + pos + 0x6D2B79F5) & 0xFFFFFFFF
+        z = ((s ^ (s >> 15)) * (s | 1)) & 0xFFFFFFFF
+        z ^= (z + (((z ^ (z >> 7)) * (z | 61)) & 0xFFFFFFFF)) & 0xFFFFFFFF
+        if ((z ^ (z >> 14)) & 0xFFFFFFFF) % step == 0:
+            return seed
+    raise AssertionError("no seed found")
+
+
 def test_sampling_follows_reference(tmp_path):
-    """Greedy = first maximum; temperature > 0 is deterministic in the seed (cpu-worker.js:154-167)."""
-    lg = np.random.default_rng(0).standard_normal(5000).astype(np.float32)
-    lg[[10, 20]] = 9.0
-    p = tmp_path / "lg.f32"
-    p.write_bytes(lg.tobytes())
-    assert node("sample", p, 0, 1)["id"] == 10
-    a, b = node("sample", p, 0.8, 42)["id"], node("sample", p, 0.8, 42)["id"]
-    assert a == b and 0 <= a < 5000
+    """hip.js sampleAt (the sampling of forward() at temperature > 0) against an independent
+    implementation of mulberry32 and the inverse-CDF walk, over fixed logits, temperatures, seeds and
+    positions; greedy takes the first maximum.  Planted mistakes in the Python copy (a wrong
+    constant, the seed without the position, '<' for '<=', the walk from the other end, the last
+    maximum) each change at least one result, so the cases pin those details."""
+    rng = np.random.default_rng(0)
+    files = []
+    for k, (n, scale) in enumerate([(5000, 2.0), (300, 0.5), (1000, 6.0)]):
+        lg = (rng.standard_normal(n) * scale).astype(np.float32)
+        p = tmp_path / f"lg{k}.f32"
+        p.write_bytes(lg.tobytes())
+        files.append((str(p), lg))
+    tie = np.zeros(64, np.float32)
+    tie[[10, 20]] = 3.0
+    (tmp_path / "tie.f32").write_bytes(tie.tobytes())
+    flat = np.zeros(1 << 16, np.float32)      # e_i = 1 exactly: r hits 0 exactly at one step
+    (tmp_path / "flat.f32").write_bytes(flat.tobytes())
+    cases, logits = [], []
+    for path, lg in files:
+        for temperature in (0.0, 0.3, 0.7, 1.0, 1.6):
+            for seed, pos in ((1, 0), (42, 5), (0xFFFFFFFF, 777), (2024, 64)):
+                cases.append({"logits": path, "temperature": temperature, "seed": seed, "pos": pos})
+                logits.append(lg)
+    for temperature in (0.0, 1.0):
+        cases.append({"logits": str(tmp_path / "tie.f32"), "temperature": temperature, "seed": 7, "pos": 3})
+        logits.append(tie)
+    seed = _first_draw_multiple_of(1 << 16, 9)
+    cases.append({"logits": str(tmp_path / "flat.f32"), "temperature": 1.0, "seed": seed, "pos": 9})
+    logits.append(flat)
+    cp = tmp_path / "cases.json"
+    cp.write_text(json.dumps(cases))
+    got = node("samples", cp)
+    want = [_sample_ref(lg, c["temperature"], c["seed"], c["pos"]) for c, lg in zip(cases, logits)]
+    assert got == want
+    assert got[-3] == 10                                   # greedy tie: the first maximum
+    for mistake in ({"const": 0x6D2B79F4}, {"use_pos": False}, {"le": False}, {"reverse": True},
+                    {"last_max": True}):
+        planted = [_sample_ref(lg, c["temperature"], c["seed"], c["pos"], **mistake) for c, lg in zip(cases, logits)]
+        assert planted != want, mistake
 
 
 @pytest.mark.gpu
