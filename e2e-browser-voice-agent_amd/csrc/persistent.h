@@ -60,7 +60,16 @@ struct PArgs {
                   // columns for P.V, so each streams half of K and half of V
   uint64_t* lsc;  // [H][ctx] score entries of the pair exchange (asplit 2)
   unsigned long long* prof;   // optional: phase timestamps of step 0, [(NL + 1) * 16]
+  // Delay, in units of 512 cycles, between a role's hand-off and the loads of its next phase's
+  // weights: [0] o/down role before the o weights, [1] before the down weights, [2] attention and
+  // K/V roles, [3] gate/up role.  The weight bursts then stay out of the memory system while the
+  // hand-off they follow is polled for.
+  int pf[4];
 };
+
+__device__ __forceinline__ void pf_delay(int n) {
+  for (int i = 0; i < n; i++) __builtin_amdgcn_s_sleep(8);
+}
 
 constexpr int kPThreads = 256;
 constexpr int kSpinLimit = 1 << 21;
@@ -99,7 +108,7 @@ struct PShape {
   static constexpr int NBD = D / 32, NBF = F / 32, NBM = NBD > NBF ? NBD : NBF;
   static constexpr int NGD = (NBD + 3) / 4, NGF = (NBF + 3) / 4;      // groups of 4 blocks
   static constexpr int NB8D = (NBD + 7) / 8, NB8F = (NBF + 7) / 8;    // uint4 words of 8 scales
-  static constexpr int nOD = D / 16, nA = H, nKV = 2 * KVH, nGU = F / 32, nRoles = nOD + nA + nKV + nGU;
+  static constexpr int nOD = D / 16, nA = H, nKV = 8 * KVH, nGU = F / 32, nRoles = nOD + nA + nKV + nGU;
   static constexpr int KD = (D + kPThreads - 1) / kPThreads;           // x entries per thread
   static constexpr int NACT = 9 * nGU;                                 // act entries
   static constexpr int KACT = (NACT + kPThreads - 1) / kPThreads;
@@ -198,6 +207,26 @@ __device__ __forceinline__ void ll_recv(const uint64_t* base, int n, uint32_t ep
   for (int k = 0; k < K; k++) out[k] = (uint32_t)w[k];
 }
 
+// Complete a wait for one entry whose first poll `w` was issued earlier (ll_recv's loop for K = 1).
+__device__ __forceinline__ void ll_wait1(const uint64_t* p, uint64_t& w, uint32_t ep, State* st, bool& bad, int nap) {
+  int spins = 0;
+  while ((uint32_t)(w >> 32) != ep && !bad) {
+    for (int z = 0; z < nap; z++) __builtin_amdgcn_s_sleep(1);
+    w = ll_peek(p);
+    if (++spins > kSpinLimit) {
+      bad = true;
+      __hip_atomic_store(&st->abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if ((spins & 255) == 0 && __hip_atomic_load(&st->abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+      bad = true;
+    }
+  }
+}
+
+// A workgroup barrier for shared memory only: this wave's LDS accesses are done, then the waves
+// meet.  Outstanding global loads (a poll in flight, ring slots) are not waited for, as the
+// fence of __syncthreads would.  The "memory" clobber keeps loads and stores on their side.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // ---------------------------------------------------------------- register-resident weights
 
 // CNT groups of one 16-row group, lane (r = lane/4, j = lane%4): word j of 4 blocks per group and
@@ -215,6 +244,20 @@ __device__ __forceinline__ void wr_load(const Q4Mat& W, int rg16, int lane, WR<C
   if constexpr (CNT > 0) {
     const int row = rg16 * 16 + (lane >> 2), j = lane & 3;
     const int tile = row >> 6, rr = row & 63;
+    const uint4* wq = W.qs + ((size_t)tile * NG * 64 + rr) * 4 + j + (size_t)G0 * 256;
+    const uint4* wd = W.d + ((size_t)tile * NB8 + G0 / 2) * 64 + rr;
+#pragma unroll
+    for (int g = 0; g < CNT; g++) R.w[g] = gld(wq + (size_t)g * 256);
+#pragma unroll
+    for (int c = 0; c < (CNT + 1) / 2; c++) R.s[c] = gld(wd + (size_t)c * 64);
+  }
+}
+
+// The same for the row `row` of this lane (lane j = lane % 4 of it), any row of a 64-row tile.
+template <int NG, int NB8, int G0, int CNT>
+__device__ __forceinline__ void wr_load_row(const Q4Mat& W, int row, int lane, WR<CNT>& R) {
+  if constexpr (CNT > 0) {
+    const int j = lane & 3, tile = row >> 6, rr = row & 63;
     const uint4* wq = W.qs + ((size_t)tile * NG * 64 + rr) * 4 + j + (size_t)G0 * 256;
     const uint4* wd = W.d + ((size_t)tile * NB8 + G0 / 2) * 64 + rr;
 #pragma unroll
@@ -494,6 +537,74 @@ __device__ __forceinline__ float seq_dot4(float acc, const float* p, const float
   return acc;
 }
 
+// Running sums over values in shared memory with the reads of the next 32 values in flight while
+// the current 32 are added (two register batches; the loop carries one batch of reads across its
+// back edge).  The values past n up to the next multiple of 32 must be +0: the running sums start
+// at +0 and round to nearest, so they never become -0, and adding +0 (or a -0 product) leaves them
+// unchanged -- the result is the reference's n-term sum exactly.
+
+// ((0 + x_0) + x_1) + ... + x_{n-1}, x 16-byte aligned.
+__device__ __forceinline__ float chain_sum(const float* x, int n) {
+  const float4* p = reinterpret_cast<const float4*>(x);
+  const int nb = (n + 31) >> 5;
+  float s = 0.0f;
+  if (nb == 0) return s;
+  float4 A[8], B[8];
+#pragma unroll
+  for (int u = 0; u < 8; u++) A[u] = p[u];
+  for (int c = 0;; c += 2) {
+    const int c1 = c + 1 < nb ? c + 1 : c;
+#pragma unroll
+    for (int u = 0; u < 8; u++) B[u] = p[c1 * 8 + u];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 8; u++) { s = s + A[u].x; s = s + A[u].y; s = s + A[u].z; s = s + A[u].w; }
+    if (c + 1 >= nb) break;
+    const int c2 = c + 2 < nb ? c + 2 : c + 1;
+#pragma unroll
+    for (int u = 0; u < 8; u++) A[u] = p[c2 * 8 + u];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 8; u++) { s = s + B[u].x; s = s + B[u].y; s = s + B[u].z; s = s + B[u].w; }
+    if (c + 2 >= nb) break;
+  }
+  return s;
+}
+
+// ((0 + p_0 * v_0) + p_1 * v_1) + ... over t < n (each product rounded, then added), p and v
+// 16-byte aligned; p (and v) zero past n up to the next multiple of 32.
+__device__ __forceinline__ float chain_dot(const float* pp, const float* vv, int n) {
+  const float4* p = reinterpret_cast<const float4*>(pp);
+  const float4* v = reinterpret_cast<const float4*>(vv);
+  const int nb = (n + 31) >> 5;
+  float s = 0.0f;
+  if (nb == 0) return s;
+  float4 PA[8], VA[8], PB[8], VB[8];
+#pragma unroll
+  for (int u = 0; u < 8; u++) { PA[u] = p[u]; VA[u] = v[u]; }
+  for (int c = 0;; c += 2) {
+    const int c1 = c + 1 < nb ? c + 1 : c;
+#pragma unroll
+    for (int u = 0; u < 8; u++) { PB[u] = p[c1 * 8 + u]; VB[u] = v[c1 * 8 + u]; }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      s = s + PA[u].x * VA[u].x; s = s + PA[u].y * VA[u].y; s = s + PA[u].z * VA[u].z; s = s + PA[u].w * VA[u].w;
+    }
+    if (c + 1 >= nb) break;
+    const int c2 = c + 2 < nb ? c + 2 : c + 1;
+#pragma unroll
+    for (int u = 0; u < 8; u++) { PA[u] = p[c2 * 8 + u]; VA[u] = v[c2 * 8 + u]; }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      s = s + PB[u].x * VB[u].x; s = s + PB[u].y * VB[u].y; s = s + PB[u].z * VB[u].z; s = s + PB[u].w * VB[u].w;
+    }
+    if (c + 2 >= nb) break;
+  }
+  return s;
+}
+
 __device__ __forceinline__ float embed_value(const uint8_t* emb, int D, int t, int i) {
   const uint8_t* bp = emb + ((size_t)t * (D / 32) + (i >> 5)) * 18;
   const float d = half_bits_to_float((uint32_t)bp[0] | ((uint32_t)bp[1] << 8));
@@ -551,8 +662,9 @@ struct PSmem {
 
 // Staged K/V of the attention role: K as rows [kv_tile][kKVRow], V transposed [64][kv_vstride]
 // (a lane reads its dimension of 4 positions at once; the stride is 4 mod 64 floats, so the 16
-// lanes of a 16-byte read hit distinct banks), both readable 16 positions past the tile.
-__host__ __device__ constexpr int kv_vstride(int kv_tile) { return ((kv_tile + 16 + 63) & ~63) + 4; }
+// lanes of a 16-byte read hit distinct banks), K readable 16 positions past the tile, V rows
+// 32 positions past it.
+__host__ __device__ constexpr int kv_vstride(int kv_tile) { return ((kv_tile + 32 + 63) & ~63) + 4; }
 __host__ __device__ constexpr size_t kv_lds_bytes(int kv_tile) {
   return kv_tile == 0 ? 0 : ((size_t)(kv_tile + 16) * kKVRow + (size_t)kHD * kv_vstride(kv_tile)) * 4;
 }
@@ -583,13 +695,14 @@ constexpr size_t psmem_base_bytes() {
   return psmem_terms_offset<S>() + (size_t)64 * S::NBM * 4;
 }
 
-// What the attention role uses: its scores (ctx + kRingRows floats, 16-byte aligned), then the
-// ring and the staged tile.  They overlap the other roles' term buffer, not anything it shares.
-__host__ __device__ constexpr size_t attn_scores_floats(int ctx) { return (size_t)((ctx + kRingRows + 3) & ~3); }
+// What the attention role uses: its scores and their exponentials (ctx + kRingRows floats each,
+// 16-byte aligned), then the ring and the staged tile.  They overlap the other roles' term buffer, not anything it shares.
+__host__ __device__ constexpr size_t attn_scores_floats(int ctx) { return (size_t)((ctx + kRingRows + 32 + 3) & ~3); }
 
 template <class S>
 constexpr size_t psmem_attn_bytes(int ctx, int ring_slots, int kv_tile) {
-  return psmem_terms_offset<S>() + attn_scores_floats(ctx) * 4 + ring_lds_bytes(ring_slots) + kv_lds_bytes(kv_tile);
+  return psmem_terms_offset<S>() + 2 * attn_scores_floats(ctx) * 4 + ring_lds_bytes(ring_slots) +
+         kv_lds_bytes(kv_tile);
 }
 
 template <class S>
@@ -619,10 +732,23 @@ __device__ __forceinline__ void prof_mark(const PArgs& a, int s, int slot) {
   if (a.prof && s == 0 && threadIdx.x == 0) a.prof[slot] = wall_clock64();
 }
 
-// Per-workgroup timestamps of step 0, after the (NL + 1) * 16 phase slots: [layer][workgroup][4].
+// Per-workgroup timestamps of step 0, after the (NL + 1) * 16 phase slots: [layer][workgroup][8].
+constexpr int kProfWG = 8;
+__device__ __forceinline__ unsigned long long* prof_slot(const PArgs& a, int s, int l, int k) {
+  return a.prof && s == 0 ? a.prof + (size_t)(a.NL + 1) * 16 + ((size_t)l * gridDim.x + blockIdx.x) * kProfWG + k
+                          : nullptr;
+}
+// The per-workgroup timestamp k once `v` has been computed (the empty asm consumes v and the
+// timestamp is read after it); outstanding memory operations are not waited for.
+__device__ __forceinline__ void prof_after(const PArgs& a, int s, int l, int k, float v) {
+  if (a.prof && s == 0) {
+    asm volatile("" ::"v"(v));
+    *prof_slot(a, s, l, k) = wall_clock64();
+  }
+}
 __device__ __forceinline__ void prof_wg(const PArgs& a, int s, int l, int k) {
   if (a.prof && s == 0 && threadIdx.x == 0)
-    a.prof[(size_t)(a.NL + 1) * 16 + ((size_t)l * gridDim.x + blockIdx.x) * 4 + k] = wall_clock64();
+    a.prof[(size_t)(a.NL + 1) * 16 + ((size_t)l * gridDim.x + blockIdx.x) * kProfWG + k] = wall_clock64();
 }
 
 // ---------------------------------------------------------------- RMSNorm + quantize
@@ -666,11 +792,15 @@ __device__ __forceinline__ void normw_load(const float* w, float (&nw)[4]) {
 // run the four lane sums of x*x in order, then thread t < NBD*4 quantizes block lane t.
 // The caller has synchronised after staging; returns after a barrier.
 template <class S>
-__device__ __forceinline__ void norm_quant(const PSmem& m, const float (&nw)[4], float eps) {
+__device__ __forceinline__ void norm_quant(const PSmem& m, const float (&nw)[4], float eps, unsigned long long* mark = nullptr) {
   const int tid = threadIdx.x;
   if (tid < 64) {
     float s = 0.0f;
     if (tid < 4) s = run_sum<S::D / 4>(m.sq + tid * S::STV);
+    if (mark && tid == 0) {
+      asm volatile("" ::"v"(s));
+      *mark = wall_clock64();
+    }
     const float s0 = __shfl(s, 0), s1 = __shfl(s, 1), s2 = __shfl(s, 2), s3 = __shfl(s, 3);
     if (tid == 0) m.red[4] = recip(__builtin_sqrtf(div_const<S::D>(((s0 + s1) + s2) + s3) + eps));
   }
@@ -1012,6 +1142,7 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
     // ---- o: x1 = x + W_o . quantize(att)
+    if (l > 0) pf_delay(a.pf[0]);
     WR<Co> ro;
     wr_load<S::NGD, S::NB8D, G0o, Co>(L.o, wg, lane, ro);
     {
@@ -1033,6 +1164,7 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
     }
     __syncthreads();
     wr_terms<S::NBD, G0o, Co>(ro, m.xq, lane, m.terms);
+    prof_wg(a, s, l, 4);
     __syncthreads();
     if constexpr (W == 0) {
       const float v = hsum4(serial_sum<S::NBD>(m.terms, lane));
@@ -1045,6 +1177,7 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
       prof_wg(a, s, l, 1);
     }
     // ---- down: x2 = x1 + W_down . act (act arrives quantized)
+    pf_delay(a.pf[1]);
     WR<Cd> rd;
     wr_load<S::NGF, S::NB8F, G0d, Cd>(L.down, wg, lane, rd);
     {
@@ -1069,7 +1202,9 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
     if (wg == 0) prof_mark(a, s, l * 16 + 2);
     prof_wg(a, s, l, 2);
     wr_terms<S::NBF, G0d, Cd>(rd, m.xq, lane, m.terms);
+    prof_wg(a, s, l, 5);
     __syncthreads();
+    prof_wg(a, s, l, 6);
     if constexpr (W == 0) {
       const float v = hsum4(serial_sum<S::NBF>(m.terms, lane));
       if (j == 0) {
@@ -1105,7 +1240,8 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
   float* kv = m.qv + 64;
   float* vv = m.qv + 128;
   float* sc = m.terms;                                     // ctx + kRingRows scores
-  float* ring = sc + attn_scores_floats(a.ctx);            // a.ring slots of kRingRows rows
+  float* ee = sc + attn_scores_floats(a.ctx);              // their exponentials
+  float* ring = ee + attn_scores_floats(a.ctx);            // a.ring slots of kRingRows rows
   const int vstride = kv_vstride(a.kv_tile);
   float* kt = ring + (size_t)a.ring * kSlotFloats;        // [kv_tile][kKVRow] K
   float* vT = kt + (size_t)(a.kv_tile + 16) * kKVRow;      // [64][vstride] V transposed
@@ -1119,6 +1255,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
   const int oend = split ? (half == 0 ? pos : (nall / 2) * kRingRows) : 0;
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
+    if (l > 0) pf_delay(a.pf[2]);
     WR<S::NGD> wq[1];
     wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.qkv, rq, lane, wq[0]);
     float nw[4];
@@ -1330,14 +1467,33 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       prof_wg(a, s, l, 3);
       for (int t = obeg + tid; t < oend; t += kPThreads) lmax = __builtin_fmaxf(lmax, sc[t]);
     }
-    // the current position: the group's new K and V rows (KV role), then its score
-    {
-      uint32_t knv[1];                   // kv and vv are adjacent: entries 0..63 K, 64..127 V
-      ll_recv<1>(a.ll + S::oKV + 2 * kh * kHD, 2 * kHD, phase_epoch(ep0, s, E, 4 * l + 0), a.st, bad, knv, a.nap);
-      if (tid < 2 * kHD) kv[tid] = __uint_as_float(knv[0]);
+    // The softmax over the past positions, while the new K row is on its way.  The new position
+    // comes last in the reference's running maximum and sum (kernels.c:362-369), so with the past
+    // maximum M the exponentials e_t = fast_exp(s_t - M) and their running sum over t < pos are
+    // already the reference's unless the new score exceeds M; then everything is redone with it.
+    // Waves 1 and 2 poll for the group's new K and V rows (issued first, so the loads are in
+    // flight during the softmax); the barriers in between wait for shared memory only.
+    const bool kpoll = tid >= 64 && tid < 64 + 2 * kHD;
+    const uint64_t* ksrc = a.ll + S::oKV + 2 * kh * kHD + (tid - 64);
+    const uint32_t ekv = phase_epoch(ep0, s, E, 4 * l + 0);
+    uint64_t kw = (uint64_t)ekv << 32;
+    if (kpoll) kw = ll_peek(ksrc);
+    lmax = max64(lmax);
+    if (lane == 0) m.red[wave] = lmax;
+    lds_barrier();
+    const float mpast = __builtin_fmaxf(__builtin_fmaxf(m.red[0], m.red[1]), __builtin_fmaxf(m.red[2], m.red[3]));
+    for (int t = tid; t < ((pos + 31) & ~31); t += kPThreads) ee[t] = t < pos ? fast_exp(sc[t] - mpast) : 0.0f;
+    lds_barrier();
+    if (tid == 0) {
+      m.red[8] = chain_sum(ee, pos);
+      prof_after(a, s, l, 6, m.red[8]);
+    } else if (kpoll) {
+      ll_wait1(ksrc, kw, ekv, a.st, bad, a.nap);
+      kv[tid - 64] = __uint_as_float((uint32_t)kw);    // kv and vv are adjacent: 0..63 K, 64..127 V
     }
     if (__syncthreads_or(bad)) return false;
     if (mark) prof_mark(a, s, l * 16 + 15);
+    prof_wg(a, s, l, 4);
     if (tid < kHD) {
       // wave 0 forms the 64 products; lane j < 4 then adds products j, j+4, ... in order (one
       // read of its 16 products), and the four lane sums combine in hsum order
@@ -1356,25 +1512,33 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       if (tid == 0) {
         const float sv = (s0 + s1 + s2 + s3) * scale;
         sc[pos] = sv;
-        lmax = __builtin_fmaxf(lmax, sv);
+        if (sv > mpast) {
+          m.red[9] = 1.0f;               // the new score is the maximum: redo below
+        } else {
+          const float en = fast_exp(sv - mpast);
+          ee[pos] = en;
+          m.red[8] = m.red[8] + en;
+          m.red[9] = 0.0f;
+        }
       }
     }
-    lmax = max64(lmax);
-    if (lane == 0) m.red[wave] = lmax;
     __syncthreads();
-    const float mx = __builtin_fmaxf(__builtin_fmaxf(m.red[0], m.red[1]), __builtin_fmaxf(m.red[2], m.red[3]));
     if (mark) prof_mark(a, s, l * 16 + 12);
-    for (int t = tid; t < T; t += kPThreads) sc[t] = fast_exp(sc[t] - mx);
-    __syncthreads();
-    if (tid == 0) m.red[8] = seq_sum(sc, T);
-    __syncthreads();
+    if (m.red[9] != 0.0f) {
+      const float mx = sc[pos];
+      for (int t = tid; t < ((T + 31) & ~31); t += kPThreads) ee[t] = t < T ? fast_exp(sc[t] - mx) : 0.0f;
+      __syncthreads();
+      if (tid == 0) m.red[8] = chain_sum(ee, T);
+      __syncthreads();
+    }
     if (mark) prof_mark(a, s, l * 16 + 13);
     const float sum = m.red[8];
-    for (int t = tid; t < T; t += kPThreads) sc[t] = sc[t] / sum;
+    for (int t = tid; t < T; t += kPThreads) sc[t] = ee[t] / sum;
     volatile LdsInt* cnt = (volatile LdsInt*)(m.red + 12);   // split P.V hand-offs (below)
     if (tid < 4) cnt[tid] = 0;
     __syncthreads();
     if (mark) prof_mark(a, s, l * 16 + 14);
+    prof_wg(a, s, l, 5);
     // out_i = sum over t in order of p_t * v_t[i] (kernels.c:372-375): staged positions, then the
     // streamed ones slot by slot (wave 0 adds while every wave keeps the ring filled), then pos
     float accv = 0.0f;
@@ -1503,31 +1667,38 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
 
 // One 32-value block u of the SwiGLU activation: gate rows 32u.., up rows F+32u.. (one 16-row
 // group per wave), then silu(gate)*up and quantize_row of the block (kernels.c:390-397).
-// The new K (with RoPE) or V row of one kv group per layer (kernels.c:333-353): RMSNorm + quantize
-// of x, the group's 64 k or v rows of qkv (one row group per wave) plus bias, RoPE on k
-// (kernels.c:340-344), the cache store at pos, and the row handed to the group's attention
-// workgroups.  Workgroup 2g + c of the role: group g, c = 0 K, 1 V.
-template <class S>
+// The new K (with RoPE) or V rows of one kv group per layer (kernels.c:333-353), 16 rows per
+// workgroup: workgroup 8g + 4c + p of the role takes rows {8p .. 8p+7} and {32+8p .. 32+8p+7} of
+// group g's 64 k (c = 0) or v (c = 1) rows, so the RoPE pairs (i, i+32) stay together.  RMSNorm +
+// quantize of x; each wave forms the terms of its share of the blocks for the 16 rows, wave 0 adds
+// them in the reference's order, adds the bias, applies RoPE to k, stores the rows at pos and hands
+// them to the group's attention workgroups.
+template <class S, int W>
 __device__ __forceinline__ bool kv_step(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int pos, int tok,
                                         bool& bad) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), r = lane >> 2, j = lane & 3;
+  constexpr int G0 = split_g0(S::NGD, W), C = split_cnt(S::NGD, W);
+  const int tid = threadIdx.x, lane = tid & 63, r = lane >> 2, j = lane & 3;
   const int E = 4 * a.NL + 1;
-  const int kidx = blockIdx.x - S::nOD - S::H * a.asplit, kh = kidx >> 1, isv = kidx & 1;
-  const int rg = (S::D + isv * S::KVH * kHD + kh * kHD) / 16 + wave;
-  float* row = m.qv;
+  const int kidx = blockIdx.x - S::nOD - S::H * a.asplit;
+  const int kh = kidx >> 3, isv = (kidx >> 2) & 1, p = kidx & 3;
+  const int pi = 8 * p + (r & 7);                       // RoPE pair index of this lane's row
+  const int li = r < 8 ? pi : 32 + pi;                  // the row within the group's 64
+  const int row = S::D + isv * S::KVH * kHD + kh * kHD + li;
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
-    WR<S::NGD> w[1];
-    wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.qkv, rg, lane, w[0]);
+    if (l > 0) pf_delay(a.pf[2]);
+    WR<C> w;
+    wr_load_row<S::NGD, S::NB8D, G0, C>(L.qkv, row, lane, w);
     float nw[4];
     normw_load<S>(L.attn_norm, nw);
-    float b = 0.0f;
-    if (j == 0) b = gldf(L.bqkv + rg * 16 + r);
-    float rc = 0.0f, rsn = 0.0f;
-    if (!isv && tid < 32) {
-      const float2 cs = gld2f(a.rope + (size_t)pos * kHD + 2 * tid);
-      rc = cs.x;
-      rsn = cs.y;
+    float b = 0.0f, rc = 0.0f, rsn = 0.0f;
+    if (W == 0 && j == 0) {
+      b = gldf(L.bqkv + row);
+      if (!isv) {
+        const float2 cs = gld2f(a.rope + (size_t)pos * kHD + 2 * pi);
+        rc = cs.x;
+        rsn = cs.y;
+      }
     }
     if (l == 0) {
       for (int i = tid; i < S::D; i += kPThreads) stage_x<S>(m, i, embed_value(a.embd, S::D, tok, i));
@@ -1536,25 +1707,25 @@ __device__ __forceinline__ bool kv_step(const PArgs& a, const PSmem& m, uint32_t
     }
     if (__syncthreads_or(bad)) return false;
     prof_wg(a, s, l, 0);
-    norm_quant<S>(m, nw, a.eps);
+    norm_quant<S>(m, nw, a.eps, prof_slot(a, s, l, 7));
     prof_wg(a, s, l, 2);
-    float acc[1] = {0.0f};
-    wr_dot<S::NBD, 0, S::NGD, 1>(w, m.xq, j, acc);
-    const float v = hsum4(acc[0]);
-    if (j == 0) row[16 * wave + r] = v + b;
+    wr_terms<S::NBD, G0, C>(w, m.xq, lane, m.terms);
     __syncthreads();
-    if (!isv && tid < 32) {
-      const float x0 = row[tid], x1 = row[tid + 32];
-      row[tid] = x0 * rc - x1 * rsn;
-      row[tid + 32] = x1 * rc + x0 * rsn;
+    if constexpr (W == 0) {
+      const float v = hsum4(serial_sum<S::NBD>(m.terms, lane)) + b;
+      prof_wg(a, s, l, 3);
+      // RoPE (kernels.c:340-344): lane 4r holds row i = 8p + r (r < 8) or i + 32 (r >= 8); the
+      // partner of the pair sits 32 lanes away
+      const float o = __shfl_xor(v, 32);
+      float y = v;
+      if (!isv) y = r < 8 ? v * rc - o * rsn : v * rc + o * rsn;
+      if (j == 0) {
+        const size_t cbase = ((size_t)l * S::KVH + kh) * a.ctx * kHD;
+        st_coherent((isv ? a.vc : a.kc) + cbase + (size_t)pos * kHD + li, y);
+        ll_put(a.ll + S::oKV + (2 * kh + isv) * kHD + li, __float_as_uint(y), phase_epoch(ep0, s, E, 4 * l + 0));
+      }
+      prof_wg(a, s, l, 1);
     }
-    __syncthreads();
-    if (tid < kHD) {
-      const size_t cbase = ((size_t)l * S::KVH + kh) * a.ctx * kHD;
-      st_coherent((isv ? a.vc : a.kc) + cbase + (size_t)pos * kHD + tid, row[tid]);
-      ll_put(a.ll + S::oKV + kidx * kHD + tid, __float_as_uint(row[tid]), phase_epoch(ep0, s, E, 4 * l + 0));
-    }
-    prof_wg(a, s, l, 1);
   }
   return true;
 }
@@ -1567,6 +1738,7 @@ __device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t
   const int rg = wave < 2 ? 2 * u + wave : S::F / 16 + 2 * u + (wave - 2);
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
+    if (l > 0) pf_delay(a.pf[3]);
     WR<S::NGD> w[1];
     wr_load<S::NGD, S::NB8D, 0, S::NGD>(L.gu, rg, lane, w[0]);
     float nw[4];
@@ -1575,12 +1747,14 @@ __device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t
     if (__syncthreads_or(bad)) return false;
     if (u == 0) prof_mark(a, s, l * 16 + 7);
     prof_wg(a, s, l, 0);
-    norm_quant<S>(m, nw, a.eps);
+    norm_quant<S>(m, nw, a.eps, prof_slot(a, s, l, 7));
     if (u == 0) prof_mark(a, s, l * 16 + 10);
+    prof_wg(a, s, l, 2);
     float acc[1] = {0.0f};
     wr_dot<S::NBD, 0, S::NGD, 1>(w, m.xq, j, acc);
     const float v = hsum4(acc[0]);
     if (j == 0) m.gu[16 * wave + r] = v;
+    prof_wg(a, s, l, 3);
     __syncthreads();
     // silu(gate) * up, one value per lane of wave 0, then quantize_row of the block; word w of the
     // block (A_j for w = j, B_j for w = 4 + j, kernels.h layout) gathers its four int8 by shuffles
@@ -1627,7 +1801,12 @@ __global__ __launch_bounds__(kPThreads, 1) void k_decode_persistent(PArgs a) {
     } else if (wg < S::nOD + S::H * a.asplit) {
       ok = attn_step<S>(a, m, ep0, s, pos, tok, bad);
     } else if (wg < S::nOD + S::H * a.asplit + S::nKV) {
-      ok = kv_step<S>(a, m, ep0, s, pos, tok, bad);
+      switch (wave) {
+        case 0: ok = kv_step<S, 0>(a, m, ep0, s, pos, tok, bad); break;
+        case 1: ok = kv_step<S, 1>(a, m, ep0, s, pos, tok, bad); break;
+        case 2: ok = kv_step<S, 2>(a, m, ep0, s, pos, tok, bad); break;
+        default: ok = kv_step<S, 3>(a, m, ep0, s, pos, tok, bad); break;
+      }
     } else if (wg < S::nOD + S::H * a.asplit + S::nKV + S::nGU) {
       ok = gu_step<S>(a, m, ep0, s, bad);
     }

@@ -1443,6 +1443,7 @@ struct q4hip {
   int pers_ring = 0;
   int pers_test_abort = 0;   // persistent launches still to start with the abort flag raised
   int pers_last_steps = 0;   // steps of the last persistent launch (the epochs it may have used)
+  int pers_pf[4] = {4, 4, 4, 8};   // weight prefetch delays of the roles (PArgs::pf), measured best
   int pers_nap = 1;
   const void* pers_fn = nullptr;
   uint64_t* lsc = nullptr;     // score exchange of the split attention ([H][ctx] entries)
@@ -1751,6 +1752,12 @@ void setup_persistent(q4hip* h) {
   }
   if (const char* e = getenv("Q4HIP_SPLIT_FROM")) h->pers_split_from = std::max(0, atoi(e));
   if (const char* e = getenv("Q4HIP_TEST_ABORT")) h->pers_test_abort = std::max(0, atoi(e));
+  if (const char* e = getenv("Q4HIP_PF")) {   // "o,down,attn,gu" in units of 512 cycles (tuning)
+    int v[4] = {0, 0, 0, 0};
+    if (sscanf(e, "%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3]) == 4)
+      for (int i = 0; i < 4; i++) h->pers_pf[i] = std::max(0, std::min(64, v[i]));
+  }
+
   h->pers_ok = true;
   h->pers_broken = false;
 }
@@ -1807,6 +1814,7 @@ hipError_t launch_persistent(q4hip* h, int pos0, int steps, unsigned long long* 
   a.ring = h->pers_ring;
   a.nap = h->pers_nap;
   a.prof = prof;
+  for (int i = 0; i < 4; i++) a.pf[i] = h->pers_pf[i];
   h->pers_last_steps = steps;
   if (h->pers_test_abort > 0) {          // Q4HIP_TEST_ABORT: the launch finds the flag raised
     h->pers_test_abort--;
@@ -2235,7 +2243,7 @@ int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n) {
   HIPCHK(hipSetDevice(h->device));
   if (!use_persistent(h)) return fail(Q4HIP_EINVAL, "the persistent decode kernel is not in use");
   const int G = h->pers_grid;
-  const int cnt = (h->NL + 1) * 16 + 4 * h->NL * G;
+  const int cnt = (h->NL + 1) * 16 + kProfWG * h->NL * G;
   unsigned long long* d = nullptr;
   HIPCHK(hipMalloc(&d, (size_t)cnt * 8));
   std::vector<unsigned long long> t(cnt, 0);

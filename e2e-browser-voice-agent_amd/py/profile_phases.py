@@ -18,10 +18,13 @@ sys.path.insert(0, HERE)
 
 # per-workgroup timestamp slots k of each role (q4hip_profile_persistent)
 WG_SLOTS = {
-    "OD": {0: "att received", 1: "x1 stored", 2: "act received", 3: "x2 stored"},
-    "A": {0: "x received", 2: "past K scored", 3: "scores exchanged", 1: "att stored"},
-    "KV": {0: "x received", 2: "normalised", 1: "K/V rows stored"},
-    "GU": {0: "x1 received", 1: "act stored"},
+    "OD": {0: "att received", 4: "o terms (wave 0)", 1: "x1 stored", 2: "act received", 5: "down terms (w0)",
+           6: "down terms (all)", 3: "x2 stored"},
+    "A": {0: "x received", 2: "past K scored", 3: "scores exchanged", 6: "past sum done", 4: "new K/V received",
+          5: "p formed",
+          1: "att stored"},
+    "KV": {0: "x received", 7: "norm chain done", 2: "normalised", 3: "rows formed", 1: "K/V rows stored"},
+    "GU": {0: "x1 received", 7: "norm chain done", 2: "normalised", 3: "rows formed", 1: "act stored"},
 }
 # slots of the first attention workgroup's timeline (l * 16 + k)
 A_MARKS = [(9, "normalised"), (5, "q rows"), (11, "RoPE"), (15, "new K/V received"), (12, "maximum"),
@@ -64,13 +67,13 @@ def main() -> None:
     wg = np.median(np.stack([r[1] for r in runs]), axis=0)
     split_from = int(os.environ.get("Q4HIP_SPLIT_FROM", "512"))
     asplit = 2 if P >= split_from else 1
-    nOD, nA, nKV, nGU = shape.dim // 16, shape.heads * asplit, 2 * shape.kv_heads, shape.ffn // 32
+    nOD, nA, nKV, nGU = shape.dim // 16, shape.heads * asplit, 8 * shape.kv_heads, shape.ffn // 32
     roles = {"OD": slice(0, nOD), "A": slice(nOD, nOD + nA), "KV": slice(nOD + nA, nOD + nA + nKV),
              "GU": slice(nOD + nA + nKV, nOD + nA + nKV + nGU)}
     base = wg[:, roles["OD"], 3].max(axis=1)          # last x2 store of each layer
     mid = range(1, L - 1)
     print(f"cached positions {P or 64}, attention workgroups per head {asplit}; per layer "
-          f"{np.median(np.diff(base)):.2f} us; whole step {tl[L, 2]:.2f} us")
+          f"{np.median(np.diff(base)):.2f} us; whole step {tl[L, 2]:.2f} us; shader clock {tl[L, 4]:.0f} MHz")
     for role, slots in WG_SLOTS.items():
         for k, name in slots.items():
             raw = wg[1:L - 1, roles[role], k]
@@ -79,6 +82,10 @@ def main() -> None:
             off = np.stack([wg[l, roles[role], k] - base[l - 1] for l in mid])
             print(f"{role:>3} {name:<18} min {np.median(off.min(1)):7.2f}  median {np.median(np.median(off, 1)):7.2f}"
                   f"  max {np.median(off.max(1)):7.2f}")
+    hb = base[L - 1]
+    print(f"head: x received {tl[L, 0] - hb:.2f}, (value, index) sent {tl[L, 1] - hb:.2f}, token known "
+          f"{tl[L, 2] - hb:.2f} us after the last layer's down stores; layer 0's down stores end {base[0]:.2f} us "
+          f"after the kernel starts")
     marks = np.median(np.stack([[tl[l, k] - base[l - 1] for k, _ in A_MARKS] for l in mid]), axis=0)
     print("first attention workgroup: " + ", ".join(f"{n} {v:.2f}" for (_, n), v in zip(A_MARKS, marks)))
     m.close()

@@ -214,17 +214,17 @@ class Model:
 
     def profile_persistent(self, token: int, pos: int, per_workgroup: bool = False):
         """Timeline of one persistent decode step, microseconds from kernel start,
-        shape (layers + 1, 16); with per_workgroup also the (layers, grid, 4) workgroup
+        shape (layers + 1, 16); with per_workgroup also the (layers, grid, 8) workgroup
         timestamps.  See q4hip_profile_persistent in include/q4hip.h."""
         L = self.shape.layers
-        n = (L + 1) * 16 + 4 * L * 256
+        n = (L + 1) * 16 + 8 * L * 256
         us = np.zeros(n, dtype=np.float32)
         _check(lib().q4hip_profile_persistent(self.h, token, pos, _ptr(us), n))
         tl = us[:(L + 1) * 16].reshape(L + 1, 16)
         if not per_workgroup:
             return tl
         G = int(tl[L, 5])
-        return tl, us[(L + 1) * 16:(L + 1) * 16 + 4 * L * G].reshape(L, G, 4)
+        return tl, us[(L + 1) * 16:(L + 1) * 16 + 8 * L * G].reshape(L, G, 8)
 
     def time_head(self, iters: int) -> float:
         us = ctypes.c_float(0)

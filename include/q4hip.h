@@ -131,10 +131,13 @@ int q4hip_profile_pass(q4hip* h, const int* ids, int ntok, int pos, float* us, i
  * gate/up workgroup); 9 A normalised, 10 gate/up normalised, 11..14 attention after RoPE, max,
  * sum, normalisation (head 0).  Slots 16L + 0..2: head x received, (value, index) sent, token
  * known; slot 16L + 4: the shader clock over the step in MHz; slot 16L + 5: the grid size G.
- * Then, if n allows, 4 * L * G per-workgroup entries [layer][workgroup][k]: o/down workgroups
- * k = 0 att received, 1 x after o sent, 2 act received, 3 x after down sent; attention
- * workgroups 0 x received, 1 att sent; gate/up workgroups 0 x received, 1 act sent.  Measured
- * with the device's constant 100 MHz clock and its shader cycle counter. */
+ * Then, if n allows, 8 * L * G per-workgroup entries [layer][workgroup][k]: o/down workgroups
+ * k = 0 att received, 1 x after o sent, 2 act received, 3 x after down sent, 4 o terms formed
+ * (wave 0), 5 down terms formed (wave 0), 6 down terms of all waves; attention workgroups 0 x
+ * received, 1 att sent, 2 past K scored (streamed), 3 scores exchanged (pair), 4 new K/V received,
+ * 5 probabilities formed; K/V workgroups 0 x received, 2 normalised, 3 rows formed, 1 rows sent;
+ * gate/up workgroups 0 x received, 2 normalised, 3 rows formed, 1 act sent.  Measured with the
+ * device's constant 100 MHz clock and its shader cycle counter. */
 int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n);
 
 /* Write the K and V rows of one layer and kv head at positions [pos0, pos0 + n): `k` and `v` are
