@@ -11,11 +11,14 @@ role per workgroup, the whole greedy loop on the device); its duration comes fro
 library's stream.  Also reported: algorithmic HBM bytes per token / time per token (achieved GB/s),
 the roofline of that kernel (the only kernel in the timed region), the HBM traffic per launch from
 the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, the same K steps on the multi-kernel
-hipGraph path for comparison, and the oracle timed on the host cores as the CPU baseline.
+hipGraph path for comparison, the same greedy decode driven from Node.js through the N-API addon
+(engine/llm.js generateIds, one forward() call per token: node_forward_ms_per_step), and the oracle
+timed on the host cores as the CPU baseline.
 
 Other workloads of the same model (one JSON line each, same keys):
   --workload long-context  batch-1 decode after a 4096-position cache filled with seeded fp16-valued
                            K/V (written through q4hip_set_kv), 256 greedy steps by default
+                           (--kv-cache f16: the cache stored as fp16, half the K/V bytes)
   --workload prefill       one 1024-token seeded prompt per step
   --workload matvec        the isolated Q4_0 matvec at the model's five shapes, 1000 launches each
   --workload batched       32 independent sequences on the Qwen2.5-1.5B shape, each after a
@@ -128,6 +131,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode", choices=["decode", "long-context", "prefill", "matvec", "batched"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-node", action="store_true", help="skip the Node.js host leg of the decode workload")
+    ap.add_argument("--kv-cache", default="f32", choices=["f32", "f16"],
+                    help="K/V cache storage of the long-context and batched workloads: f32 (the "
+                         "reference's cache type, bit-exact) or f16 (half the K/V bytes; parity against "
+                         "the oracle with the same fp16 rounding)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the batch-1 decode loop runs on a single device "
@@ -220,10 +228,39 @@ def bench_decode(args):
         "roofline": roofline,
         "model_gen_s": round(t_gen, 1),
     }
+    m.close()
+    if not args.no_node:
+        out.update(node_host_decode(shape, tensors, ids, args.steps, [first] + toks))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(shape, tensors, ids, [first] + toks)
-    m.close()
     print(json.dumps(out))
+
+
+def node_host_decode(shape, tensors, ids, steps, want):
+    """The same greedy decode driven from Node.js as an application does (engine/llm.js generateIds:
+    one forward() call through the N-API addon per token, each a one-step launch), on a GGUF file of
+    the same model.  Reports the median host-side milliseconds per decode call."""
+    import shutil
+    import subprocess
+    import tempfile
+    import synth
+    d = tempfile.mkdtemp(prefix="q4hip-bench-")
+    try:
+        path = os.path.join(d, "model.gguf")
+        synth.write_gguf(path, shape, tensors)
+        with open(os.path.join(d, "ids.json"), "w") as f:
+            json.dump(list(ids), f)
+        script = os.path.join(REPO, "e2e-browser-voice-agent_amd", "node", "host_decode.js")
+        r = subprocess.run(["node", script, path, str(max(256, len(ids) + steps + 2)), os.path.join(d, "ids.json"),
+                            str(steps + 1)], capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            raise RuntimeError(f"Node host decode failed: {r.stderr.strip()[-2000:]}")
+        res = json.loads(r.stdout.strip().splitlines()[-1])
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    return {"node_forward_ms_per_step": round(res["medianStepMs"], 4),
+            "node_tokens_identical": res["tokens"] == want,
+            "node_decode_path": res["decodePath"]}
 
 
 LONG_CTX = 4096
@@ -249,7 +286,8 @@ def bench_long_context(args):
     P = LONG_CTX
     ctx = P + max(args.steps, args.warmup) + 2
     tensors = synth.make_model(shape, SEED)
-    m = q4hip.Model(shape, ctx=ctx)
+    kv16 = args.kv_cache == "f16"
+    m = q4hip.Model(shape, ctx=ctx, kv_type=q4hip.KV_F16 if kv16 else q4hip.KV_F32)
     m.load(tensors)
     for l, kh, k, v in fill_cache(shape, P):
         m.set_kv(l, kh, 0, k, v)
@@ -258,19 +296,20 @@ def bench_long_context(args):
         m.generate(first, P, args.warmup)
     toks, dev_ms = m.time_generate(first, P, args.steps)
     mode = m.decode_mode_used()
-    # algorithmic bytes with the fp16 cache of the configuration: 12,288 B per position
+    # algorithmic bytes: the step's weights and logits, then every cached position's K and V row at the
+    # byte width of the cache (fp32: 24,576 B per position; fp16: 12,288 B)
     base = algorithmic_bytes(shape, 0)["total"]
-    per_pos = shape.layers * shape.kv_heads * shape.head_dim * 2 * 2
+    per_pos = shape.layers * shape.kv_heads * shape.head_dim * 2 * (2 if kv16 else 4)
     tot = sum(base + per_pos * (P + i + 1) for i in range(args.steps))
     gbps = tot / (dev_ms / 1e3) / 1e9
     out = {
-        "metric": "decode tokens/s at batch 1 (Qwen2.5-0.5B Q4_0 shape) after a 4096-position fp16 KV cache; achieved HBM GB/s",
+        "metric": "decode tokens/s at batch 1 (Qwen2.5-0.5B Q4_0 shape) after a 4096-position KV cache; achieved HBM GB/s",
         "value": round(args.steps / (dev_ms / 1e3), 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(dev_ms / args.steps, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "i8xq4/f32", "data": "synthetic",
         "config": {"workload": "qwen2.5-0.5b-shape Q4_0 greedy decode, batch 1, 4096-position cache + 256 steps",
                    "global_batch": 1, "seq_len": P + args.steps, "cache_positions": P,
-                   "kv_cache": "fp16 values stored fp32", "parallelism": "single-gpu",
+                   "kv_cache": "fp16" if kv16 else "fp32 (fp16-valued rows)", "parallelism": "single-gpu",
                    "decode_path": {2: "persistent", 1: "graph"}.get(mode, str(mode))},
         "achieved_gbps": round(gbps, 1),
         "roofline": {"bound": "hbm", "kernel": "k_decode_persistent" if mode == 2 else "decode graph",
@@ -283,6 +322,8 @@ def bench_long_context(args):
         cores = _cores()
         th = max(1, math.ceil(cores / 2))
         o = oracle.Model(shape, tensors, ctx=ctx, threads=th)
+        if kv16:
+            o.set_variant(oracle.V_KV_F16)
         ok, ov = o.kv()
         for l, kh, k, v in fill_cache(shape, P):
             ok[l, kh, :P] = k
@@ -423,7 +464,8 @@ def bench_batched(args):
     ctx = BATCH_PROMPT + max(args.steps, args.warmup) + 2
     t0 = time.time()
     tensors = synth.make_model(shape, SEED)
-    m = q4hip.Model(shape, ctx=ctx)
+    kv16 = args.kv_cache == "f16"
+    m = q4hip.Model(shape, ctx=ctx, kv_type=q4hip.KV_F16 if kv16 else q4hip.KV_F32)
     m.load(tensors)
     bt = q4hip.Batch(m, BATCH)
     first = [bt.prefill(b, synth.prompt_ids(SEED + 10 + b, BATCH_PROMPT, shape.vocab), 0) for b in range(BATCH)]
@@ -433,11 +475,11 @@ def bench_batched(args):
         bt.generate(first, pos, args.warmup)
     toks, dev_ms = bt.time_generate(first, pos, args.steps)
     tok_s = BATCH * args.steps / (dev_ms / 1e3)
-    # algorithmic bytes per step: the weights once, then every sequence's K/V with the fp16 cache of
-    # the configuration (4 bytes per element pair would be the fp32 storage)
+    # algorithmic bytes per step: the weights once, then every sequence's K/V rows at the byte width
+    # of the cache
     base = algorithmic_bytes(shape, 0)
     weights = base["layers"] + base["head"] + base["other"] - shape.vocab * 4
-    per_pos = shape.layers * shape.kv_heads * shape.head_dim * 2 * 2
+    per_pos = shape.layers * shape.kv_heads * shape.head_dim * 2 * (2 if kv16 else 4)
     logits = BATCH * shape.vocab * 4
     tot = sum(weights + logits + BATCH * per_pos * (BATCH_PROMPT + i + 1) for i in range(args.steps))
     gbps = tot / (dev_ms / 1e3) / 1e9
@@ -448,7 +490,8 @@ def bench_batched(args):
         "scaling": "weak", "vs_baseline": None, "dtype": "i8xq4/f32", "data": "synthetic",
         "config": {"workload": "qwen2.5-1.5b-shape Q4_0 greedy decode, 32 sequences, 1024-token prompts",
                    "global_batch": BATCH, "seq_len": BATCH_PROMPT + args.steps,
-                   "kv_cache": "fp32 (the reference's cache type)", "parallelism": "single-gpu"},
+                   "kv_cache": "fp16" if kv16 else "fp32 (the reference's cache type)",
+                   "parallelism": "single-gpu"},
         "achieved_gbps": round(gbps, 1),
         "roofline": {"bound": "hbm", "kernel": "batched decode step (all kernels)",
                      "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",

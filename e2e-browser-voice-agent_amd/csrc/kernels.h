@@ -162,6 +162,22 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
   return __half2float(__ushort_as_half((unsigned short)h));
 }
 
+// ---- the K/V cache element: fp32 (the reference's cache, kernels.c:347-350) or fp16 (half the
+// bytes: values rounded to nearest, ties to even, when appended, and widened exactly when read)
+typedef _Float16 kvhalf;
+template <class KT>
+__device__ __forceinline__ float4 kv_ld4(const KT* p);
+template <>
+__device__ __forceinline__ float4 kv_ld4<float>(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+template <>
+__device__ __forceinline__ float4 kv_ld4<kvhalf>(const kvhalf* p) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  return make_float4(half_bits_to_float(u.x & 0xffffu), half_bits_to_float(u.x >> 16),
+                     half_bits_to_float(u.y & 0xffffu), half_bits_to_float(u.y >> 16));
+}
+
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }

@@ -45,8 +45,8 @@ struct PArgs {
   int head_q8;
   const LayerView* layers;
   const float* rope;
-  float* kc;
-  float* vc;
+  void* kc;        // the K/V cache: fp32, or fp16 in the kernels instantiated for it
+  void* vc;
   float* logits;
   int* tokens;
   State* st;
@@ -155,6 +155,18 @@ __device__ __forceinline__ float gldf(const float* p) { return *(GlobalF32*)(con
 
 __device__ __forceinline__ void st_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent(kvhalf* p, float v) {
+  const kvhalf hv = (kvhalf)v;
+  __hip_atomic_store((unsigned short*)p, __builtin_bit_cast(unsigned short, hv), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Four consecutive K/V cache elements, widened to fp32.
+__device__ __forceinline__ float4 kv_gld4(const float* p) { return gld4f(p); }
+__device__ __forceinline__ float4 kv_gld4(const kvhalf* p) {
+  typedef __attribute__((address_space(1))) const unsigned int GlobalU32;
+  const unsigned int a = ((GlobalU32*)(const void*)p)[0], b = ((GlobalU32*)(const void*)p)[1];
+  return make_float4(half_bits_to_float(a & 0xffffu), half_bits_to_float(a >> 16), half_bits_to_float(b & 0xffffu),
+                     half_bits_to_float(b >> 16));
 }
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
@@ -1226,14 +1238,17 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
 // K/V of a position are written once per launch (agent-scope stores), by the first head of the
 // group, and are first read by the other heads at least one step later: each position is read only
 // once pos has moved past it.
-template <class S>
+template <class S, class KT>
 __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int pos, int tok,
                                           bool& bad) {
+  // the ring and the pair split stream fp32 rows (fp16 caches are staged whole: the host admits
+  // them only when the context fits the staged tile)
+  constexpr bool kStream = sizeof(KT) == 4;
   constexpr int GRP = S::H / S::KVH;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), r = lane >> 2, j = lane & 3;
   const int E = 4 * a.NL + 1;
   const int aidx = blockIdx.x - S::nOD, h = aidx % S::H, half = aidx / S::H, kh = h / GRP;
-  const bool split = a.asplit > 1;
+  const bool split = kStream && a.asplit > 1;
   const bool mark = aidx == 0;
   const int rq = (h * kHD) / 16 + wave;
   float* qv = m.qv;
@@ -1277,7 +1292,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
         const int idx = i0 + u * kPThreads + tid;
         if (idx < nt * 32) {
           const int which = idx >= nt * 16, rem = idx - which * nt * 16, t = rem >> 4, c4 = (rem & 15) * 4;
-          v4[u] = gld4f((which ? a.vc : a.kc) + cbase + (size_t)t * kHD + c4);
+          v4[u] = kv_gld4((const KT*)(which ? a.vc : a.kc) + cbase + (size_t)t * kHD + c4);
         }
       }
 #pragma unroll
@@ -1299,12 +1314,12 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     // past positions [kbeg, kend) stream through the ring: for the scores in 16-row chunks, wave w
     // taking chunks w, w + 4, ... through its own ring of cs slots (the first ones load during the
     // wait for x); for P.V in slots of kRingRows (or kVRows) rows
-    const int nstream = kend - kbeg, nck = (nstream + kRingRows - 1) / kRingRows;
+    const int nstream = kend - kbeg, nck = kStream ? (nstream + kRingRows - 1) / kRingRows : 0;
     const int nkc = (nstream + 15) / 16, nloc = nkc > wave ? (nkc - wave + 3) / 4 : 0;
     const int cs = kchunk_slots(a.ring);
     float* wring = ring + (size_t)wave * cs * kChunkFloats;
-    const float* kgl = a.kc + cbase;
-    const float* vgl = a.vc + cbase;
+    const float* kgl = (const float*)a.kc + cbase;    // fp32 caches only (kStream)
+    const float* vgl = (const float*)a.vc + cbase;
     if (nloc > 0)
       for (int j = 0; j < cs - 1; j++)
         ring_issue_kc(kgl, kbeg + 16 * (4 * (j < nloc ? j : nloc - 1) + wave), a.ctx, wring + (size_t)j * kChunkFloats);
@@ -1673,7 +1688,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
 // quantize of x; each wave forms the terms of its share of the blocks for the 16 rows, wave 0 adds
 // them in the reference's order, adds the bias, applies RoPE to k, stores the rows at pos and hands
 // them to the group's attention workgroups.
-template <class S, int W>
+template <class S, int W, class KT>
 __device__ __forceinline__ bool kv_step(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int pos, int tok,
                                         bool& bad) {
   constexpr int G0 = split_g0(S::NGD, W), C = split_cnt(S::NGD, W);
@@ -1719,9 +1734,10 @@ __device__ __forceinline__ bool kv_step(const PArgs& a, const PSmem& m, uint32_t
       const float o = __shfl_xor(v, 32);
       float y = v;
       if (!isv) y = r < 8 ? v * rc - o * rsn : v * rc + o * rsn;
+      y = (float)(KT)y;    // the value the cache holds (fp16 caches: rounded), also the one handed over
       if (j == 0) {
         const size_t cbase = ((size_t)l * S::KVH + kh) * a.ctx * kHD;
-        st_coherent((isv ? a.vc : a.kc) + cbase + (size_t)pos * kHD + li, y);
+        st_coherent((KT*)(isv ? a.vc : a.kc) + cbase + (size_t)pos * kHD + li, y);
         ll_put(a.ll + S::oKV + (2 * kh + isv) * kHD + li, __float_as_uint(y), phase_epoch(ep0, s, E, 4 * l + 0));
       }
       prof_wg(a, s, l, 1);
@@ -1778,7 +1794,7 @@ __device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t
   return true;
 }
 
-template <class S>
+template <class S, class KT>
 __global__ __launch_bounds__(kPThreads, 1) void k_decode_persistent(PArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const PSmem m = psmem<S>(smem);
@@ -1799,13 +1815,13 @@ __global__ __launch_bounds__(kPThreads, 1) void k_decode_persistent(PArgs a) {
         default: ok = od_step<S, 3>(a, m, ep0, s, tok, bad); break;
       }
     } else if (wg < S::nOD + S::H * a.asplit) {
-      ok = attn_step<S>(a, m, ep0, s, pos, tok, bad);
+      ok = attn_step<S, KT>(a, m, ep0, s, pos, tok, bad);
     } else if (wg < S::nOD + S::H * a.asplit + S::nKV) {
       switch (wave) {
-        case 0: ok = kv_step<S, 0>(a, m, ep0, s, pos, tok, bad); break;
-        case 1: ok = kv_step<S, 1>(a, m, ep0, s, pos, tok, bad); break;
-        case 2: ok = kv_step<S, 2>(a, m, ep0, s, pos, tok, bad); break;
-        default: ok = kv_step<S, 3>(a, m, ep0, s, pos, tok, bad); break;
+        case 0: ok = kv_step<S, 0, KT>(a, m, ep0, s, pos, tok, bad); break;
+        case 1: ok = kv_step<S, 1, KT>(a, m, ep0, s, pos, tok, bad); break;
+        case 2: ok = kv_step<S, 2, KT>(a, m, ep0, s, pos, tok, bad); break;
+        default: ok = kv_step<S, 3, KT>(a, m, ep0, s, pos, tok, bad); break;
       }
     } else if (wg < S::nOD + S::H * a.asplit + S::nKV + S::nGU) {
       ok = gu_step<S>(a, m, ep0, s, bad);

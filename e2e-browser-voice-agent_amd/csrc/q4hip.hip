@@ -265,10 +265,11 @@ __global__ __launch_bounds__(64) void k_matvec_q8(Q4Mat W, const uint4* __restri
   if (j == 0 && row < W.N) y[row] = v;
 }
 
-// RoPE on the q and k heads, then K (roped) and V appended to the fp32 cache at pos
-// (kernels.c:337-352).  Grid (heads + kv_heads, M), HD/2 threads: thread i owns pair (i, i+HD/2).
+// RoPE on the q and k heads, then K (roped) and V appended to the cache at pos (kernels.c:337-352;
+// fp32, or rounded to fp16).  Grid (heads + kv_heads, M), HD/2 threads: thread i owns pair (i, i+HD/2).
+template <class KT>
 __global__ void k_rope_kv(float* __restrict__ qkv, int QKV, int D, int H, int KVH, int HD,
-                          const float* __restrict__ rope, float* __restrict__ kc, float* __restrict__ vc,
+                          const float* __restrict__ rope, KT* __restrict__ kc, KT* __restrict__ vc,
                           int ctx, int layer, const State* __restrict__ st) {
   const int h = blockIdx.x, m = blockIdx.y, i = threadIdx.x, half = HD / 2;
   const int pos = st->pos0 + m;
@@ -282,10 +283,10 @@ __global__ void k_rope_kv(float* __restrict__ qkv, int QKV, int D, int H, int KV
     const int kh = h - H;
     const size_t off = (((size_t)layer * KVH + kh) * ctx + pos) * HD;
     const float* vs = qkv + (size_t)m * QKV + D + KVH * HD + kh * HD;
-    kc[off + i] = y0;
-    kc[off + i + half] = y1;
-    vc[off + i] = vs[i];
-    vc[off + i + half] = vs[i + half];
+    kc[off + i] = (KT)y0;
+    kc[off + i + half] = (KT)y1;
+    vc[off + i] = (KT)vs[i];
+    vc[off + i + half] = (KT)vs[i + half];
   }
 }
 
@@ -298,9 +299,9 @@ __global__ void k_rope_kv(float* __restrict__ qkv, int QKV, int D, int H, int KV
 // row per (token, head) of ctx floats.  Grid (H, ceil(M/32)).
 constexpr int kAttnTokens = 32, kAttnChunk = 32;
 
-template <int HD>
+template <int HD, class KT>
 __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ qkv, int QKV, int H, int KVH,
-                                                      const float* __restrict__ kc, const float* __restrict__ vc,
+                                                      const KT* __restrict__ kc, const KT* __restrict__ vc,
                                                       int ctx, int layer, float* __restrict__ att, int D,
                                                       const State* __restrict__ st, int M, float* __restrict__ scr) {
   constexpr int RS = HD + 4, DPT = HD / 8;
@@ -313,8 +314,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
   const int m = mb + mi;
   const int Tm = m < M ? pos0 + m + 1 : 0;
   const int Tb = pos0 + (mb + kAttnTokens < M ? mb + kAttnTokens : M);
-  const float* kb = kc + ((size_t)layer * KVH + kh) * ctx * HD;
-  const float* vb = vc + ((size_t)layer * KVH + kh) * ctx * HD;
+  const KT* kb = kc + ((size_t)layer * KVH + kh) * ctx * HD;
+  const KT* vb = vc + ((size_t)layer * KVH + kh) * ctx * HD;
   float* srow = scr + ((size_t)(m < M ? m : 0) * H + h) * ctx;
   for (int i = tid; i < kAttnTokens * HD; i += 256) {
     const int r = i / HD, c = i - r * HD;
@@ -326,7 +327,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
     __syncthreads();
     for (int i = tid; i < kAttnChunk * HD / 4; i += 256) {
       const int r = i / (HD / 4), c4 = i - r * (HD / 4), t = t0 + r;
-      const float4 v = t < Tb ? reinterpret_cast<const float4*>(kb + (size_t)t * HD)[c4] : make_float4(0, 0, 0, 0);
+      const float4 v = t < Tb ? kv_ld4<KT>(kb + (size_t)t * HD + 4 * c4) : make_float4(0, 0, 0, 0);
       *reinterpret_cast<float4*>(&cs[r][4 * c4]) = v;
     }
     __syncthreads();
@@ -375,7 +376,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
     __syncthreads();
     for (int i = tid; i < kAttnChunk * HD / 4; i += 256) {
       const int r = i / (HD / 4), c4 = i - r * (HD / 4), t = t0 + r;
-      const float4 v = t < Tb ? reinterpret_cast<const float4*>(vb + (size_t)t * HD)[c4] : make_float4(0, 0, 0, 0);
+      const float4 v = t < Tb ? kv_ld4<KT>(vb + (size_t)t * HD + 4 * c4) : make_float4(0, 0, 0, 0);
       *reinterpret_cast<float4*>(&cs[r][4 * c4]) = v;
     }
     for (int i = tid; i < kAttnTokens * kAttnChunk; i += 256) {
@@ -407,9 +408,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float* __restrict__ 
 // t order, then out_i = sum over t in order of (e_t/sum)*v_t[i].  Grid (H, M), one wave; thread t
 // scores position t (its K row loaded whole), thread i accumulates output element(s) i over t with
 // V loaded 32 positions ahead.  Shared: HD + T floats.
-template <int HD>
+template <int HD, class KT>
 __global__ __launch_bounds__(64) void k_attn(const float* __restrict__ qkv, int QKV, int D, int H, int KVH,
-                                             const float* __restrict__ kc, const float* __restrict__ vc,
+                                             const KT* __restrict__ kc, const KT* __restrict__ vc,
                                              int ctx, int layer, float* __restrict__ att,
                                              const State* __restrict__ st) {
   extern __shared__ __attribute__((aligned(16))) float sm[];
@@ -417,8 +418,8 @@ __global__ __launch_bounds__(64) void k_attn(const float* __restrict__ qkv, int 
   const int h = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
   const int T = st->pos0 + m + 1, kh = h / (H / KVH);
   const float* q = qkv + (size_t)m * QKV + h * HD;
-  const float* kb = kc + ((size_t)layer * KVH + kh) * ctx * HD;
-  const float* vb = vc + ((size_t)layer * KVH + kh) * ctx * HD;
+  const KT* kb = kc + ((size_t)layer * KVH + kh) * ctx * HD;
+  const KT* vb = vc + ((size_t)layer * KVH + kh) * ctx * HD;
   float* sq = sm;
   float* sc = sm + HD;
   for (int i = tid; i < HD; i += 64) sq[i] = q[i];
@@ -427,10 +428,10 @@ __global__ __launch_bounds__(64) void k_attn(const float* __restrict__ qkv, int 
   float lmax = -1e30f;
   const float4* qr = reinterpret_cast<const float4*>(sq);
   for (int t = tid; t < T; t += 64) {
-    const float4* kr = reinterpret_cast<const float4*>(kb + (size_t)t * HD);
+    const KT* kr = kb + (size_t)t * HD;
     float4 kv[HD / 4];
 #pragma unroll
-    for (int i4 = 0; i4 < HD / 4; i4++) kv[i4] = kr[i4];
+    for (int i4 = 0; i4 < HD / 4; i4++) kv[i4] = kv_ld4<KT>(kr + 4 * i4);
     float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
 #pragma unroll
     for (int i4 = 0; i4 < HD / 4; i4++) {
@@ -475,7 +476,7 @@ __global__ __launch_bounds__(64) void k_attn(const float* __restrict__ qkv, int 
 #pragma unroll
   for (int u = 0; u < TB; u++)
 #pragma unroll
-    for (int e = 0; e < E; e++) vcur[u][e] = u < T ? vb[(size_t)u * HD + tid + 64 * e] : 0.0f;
+    for (int e = 0; e < E; e++) vcur[u][e] = u < T ? (float)vb[(size_t)u * HD + tid + 64 * e] : 0.0f;
   for (int t0 = 0; t0 < T; t0 += TB) {
     float vnext[TB][E];
     const int t1 = t0 + TB;
@@ -483,7 +484,7 @@ __global__ __launch_bounds__(64) void k_attn(const float* __restrict__ qkv, int 
 #pragma unroll
       for (int u = 0; u < TB; u++)
 #pragma unroll
-        for (int e = 0; e < E; e++) vnext[u][e] = t1 + u < T ? vb[(size_t)(t1 + u) * HD + tid + 64 * e] : 0.0f;
+        for (int e = 0; e < E; e++) vnext[u][e] = t1 + u < T ? (float)vb[(size_t)(t1 + u) * HD + tid + 64 * e] : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < TB; u++) {
@@ -876,8 +877,9 @@ __global__ void k_embed_list(const uint8_t* __restrict__ emb, int D, const int* 
 
 // RoPE of token b's q and k heads at position pos[b], then K and V appended to sequence b's cache
 // (kernels.c:337-352).  Grid (H + KVH, B), HD/2 threads.
+template <class KT>
 __global__ void k_rope_kv_list(float* __restrict__ qkv, int QKV, int D, int H, int KVH, int HD,
-                               const float* __restrict__ rope, float* __restrict__ kc, float* __restrict__ vc,
+                               const float* __restrict__ rope, KT* __restrict__ kc, KT* __restrict__ vc,
                                int ctx, int layer, const int* __restrict__ pos, size_t seq_stride) {
   const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x, half = HD / 2;
   const int p = pos[b];
@@ -891,10 +893,10 @@ __global__ void k_rope_kv_list(float* __restrict__ qkv, int QKV, int D, int H, i
     const int kh = h - H;
     const size_t off = (size_t)b * seq_stride + (((size_t)layer * KVH + kh) * ctx + p) * HD;
     const float* vs = qkv + (size_t)b * QKV + D + KVH * HD + kh * HD;
-    kc[off + i] = y0;
-    kc[off + i + half] = y1;
-    vc[off + i] = vs[i];
-    vc[off + i + half] = vs[i + half];
+    kc[off + i] = (KT)y0;
+    kc[off + i + half] = (KT)y1;
+    vc[off + i] = (KT)vs[i];
+    vc[off + i + half] = (KT)vs[i + half];
   }
 }
 
@@ -918,9 +920,9 @@ __host__ __device__ inline int pv_row_stride(int ctx) { return ((ctx + 31) & ~31
 // Floats per head row of the scores array (rows start 16-byte aligned).
 __host__ __device__ inline int score_stride(int ctx) { return (ctx + 3) & ~3; }
 
-template <int HD>
+template <int HD, class KT>
 __global__ __launch_bounds__(64) void k_attn_scores_list(const float* __restrict__ qkv, int QKV, int H, int KVH,
-                                                         const float* __restrict__ kc, int ctx, int layer,
+                                                         const KT* __restrict__ kc, int ctx, int layer,
                                                          float* __restrict__ sc, const int* __restrict__ pos,
                                                          size_t seq_stride) {
   __shared__ __attribute__((aligned(16))) float qs[kMaxGroup * HD];
@@ -941,10 +943,10 @@ __global__ __launch_bounds__(64) void k_attn_scores_list(const float* __restrict
   __syncthreads();
   const int t = t0 + tid;
   if (t >= T) return;
-  const float4* kr = reinterpret_cast<const float4*>(kc + (size_t)b * seq_stride + (((size_t)layer * KVH + g) * ctx + t) * HD);
+  const KT* kr = kc + (size_t)b * seq_stride + (((size_t)layer * KVH + g) * ctx + t) * HD;
   float4 kv[HD / 4];                     // the whole K row: one round trip to memory
 #pragma unroll
-  for (int u = 0; u < HD / 4; u++) kv[u] = kr[u];
+  for (int u = 0; u < HD / 4; u++) kv[u] = kv_ld4<KT>(kr + 4 * u);
   float s[kMaxGroup][4];
 #pragma unroll
   for (int gh = 0; gh < kMaxGroup; gh++) {
@@ -966,9 +968,9 @@ __global__ __launch_bounds__(64) void k_attn_scores_list(const float* __restrict
     if (gh < G) sc[((size_t)b * H + g * G + gh) * score_stride(ctx) + t] = (s[gh][0] + s[gh][1] + s[gh][2] + s[gh][3]) * scale;
 }
 
-template <int HD, int CR>
+template <int HD, int CR, class KT>
 __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ sc, int H, int KVH,
-                                                      const float* __restrict__ vc, int ctx, int layer,
+                                                      const KT* __restrict__ vc, int ctx, int layer,
                                                       float* __restrict__ att, int D, const int* __restrict__ pos,
                                                       size_t seq_stride, uint4* __restrict__ xq, int xstride,
                                                       uint4* __restrict__ xh) {
@@ -985,7 +987,7 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
   float* rmax = red + 4 * kMaxGroup;
   float* rsum = rmax + kMaxGroup;
   const float* sb = sc + ((size_t)b * H + g * G) * CS;
-  const float* vb = vc + (size_t)b * seq_stride + ((size_t)layer * KVH + g) * ctx * HD + c0;
+  const KT* vb = vc + (size_t)b * seq_stride + ((size_t)layer * KVH + g) * ctx * HD + c0;
   // V chunks reach shared memory through registers: register set k holds the chunks ch = k mod 3;
   // chunk ch + 1 is stored at the end of chunk ch, and its set then loads chunk ch + 4 (the last
   // chunk again near the end, so that loads and stores stay unconditional)
@@ -995,7 +997,7 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
       // rows from T on are never read: they repeat row T - 1, so the loads carry no condition
       const int i = tid + 256 * u, row = i / (kPvCols / 4), c4 = i - row * (kPvCols / 4);
       const int t = min(ch * CR + row, T - 1);
-      r[u] = *reinterpret_cast<const float4*>(vb + (size_t)t * HD + 4 * c4);
+      r[u] = kv_ld4<KT>(vb + (size_t)t * HD + 4 * c4);
     }
   };
   auto vstore = [&](int buf, const float4* r) {
@@ -1413,7 +1415,9 @@ struct q4hip {
   float* rope = nullptr;
   bool rope_set = false;
   float *x = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *logits = nullptr;
-  float *kc = nullptr, *vc = nullptr;
+  void *kc = nullptr, *vc = nullptr;   // K/V cache [layer][kv_head][ctx][head_dim]: fp32, or fp16 when kv16
+  bool kv16 = false;
+  int kvb = 4;                         // bytes per cache element
   uint4* xq = nullptr;
   uint4* xh = nullptr;     // the same activations as fp16 matrix-core operands (multi-token passes)
   int xstride = 0;   // activation blocks per token row of xq
@@ -1556,19 +1560,32 @@ size_t attn_pv_lds(int H, int KVH, int ctx) {
 }
 
 // With xq, the P.V kernel also writes the quantized activation of att (k_quant<QM_PLAIN>'s output).
-void launch_attn_list(hipStream_t s, int HD, int B, int H, int KVH, const float* qkv, int QKV, const float* kc,
-                      const float* vc, int ctx, int layer, float* sc, float* att, int D, const int* pos,
-                      size_t seq_stride, uint4* xq = nullptr, int xstride = 0, uint4* xh = nullptr) {
+template <class KT>
+void launch_attn_list_t(hipStream_t s, int HD, int B, int H, int KVH, const float* qkv, int QKV, const KT* kc,
+                        const KT* vc, int ctx, int layer, float* sc, float* att, int D, const int* pos,
+                        size_t seq_stride, uint4* xq, int xstride, uint4* xh) {
   const dim3 sg((unsigned)((ctx + kScoreRows - 1) / kScoreRows), (unsigned)KVH, (unsigned)B);
   const dim3 pg((unsigned)(HD / kPvCols), (unsigned)KVH, (unsigned)B);
   const size_t lds = attn_pv_lds(H, KVH, ctx);
   if (HD == 64) {
-    k_attn_scores_list<64><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, seq_stride);
-    k_attn_pv_list<64, kPvRows><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride, xq, xstride, xh);
+    k_attn_scores_list<64, KT><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, seq_stride);
+    k_attn_pv_list<64, kPvRows, KT><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride, xq, xstride, xh);
   } else {
-    k_attn_scores_list<128><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, seq_stride);
-    k_attn_pv_list<128, kPvRows><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride, xq, xstride, xh);
+    k_attn_scores_list<128, KT><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, seq_stride);
+    k_attn_pv_list<128, kPvRows, KT><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride, xq, xstride, xh);
   }
+}
+
+// kc, vc: fp32 caches, or fp16 ones when kv16.
+void launch_attn_list(hipStream_t s, int HD, int B, int H, int KVH, const float* qkv, int QKV, const void* kc,
+                      const void* vc, bool kv16, int ctx, int layer, float* sc, float* att, int D, const int* pos,
+                      size_t seq_stride, uint4* xq = nullptr, int xstride = 0, uint4* xh = nullptr) {
+  if (kv16)
+    launch_attn_list_t<kvhalf>(s, HD, B, H, KVH, qkv, QKV, (const kvhalf*)kc, (const kvhalf*)vc, ctx, layer, sc, att,
+                               D, pos, seq_stride, xq, xstride, xh);
+  else
+    launch_attn_list_t<float>(s, HD, B, H, KVH, qkv, QKV, (const float*)kc, (const float*)vc, ctx, layer, sc, att, D,
+                              pos, seq_stride, xq, xstride, xh);
 }
 
 // Whether the list attention kernels take this shape (query heads per kv head, LDS), and their LDS
@@ -1578,11 +1595,13 @@ bool attn_list_ok(int H, int KVH, int HD, int ctx) {
   const size_t lds = attn_pv_lds(H, KVH, ctx);
   if (lds > 160 * 1024) return false;
   if (lds > 64 * 1024) {
-    const void* fn = HD == 64 ? (const void*)k_attn_pv_list<64, kPvRows> : (const void*)k_attn_pv_list<128, kPvRows>;
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-      (void)hipGetLastError();
-      return false;
-    }
+    const void* fns[2] = {HD == 64 ? (const void*)k_attn_pv_list<64, kPvRows, float> : (const void*)k_attn_pv_list<128, kPvRows, float>,
+                          HD == 64 ? (const void*)k_attn_pv_list<64, kPvRows, kvhalf> : (const void*)k_attn_pv_list<128, kPvRows, kvhalf>};
+    for (const void* fn : fns)
+      if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+      }
   }
   return true;
 }
@@ -1603,27 +1622,48 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
     prof_mark(h, Q4HIP_PROF_QKV);
     launch_matvec<OP_BIAS>(s, y.qkv, h->xq, h->xstride, M, h->qkv, QKV, y.bqkv, xh);
     prof_mark(h, Q4HIP_PROF_ROPE);
-    k_rope_kv<<<dim3(h->H + h->KVH, M), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, h->kc, h->vc, h->ctx, l, h->st);
+    if (h->kv16)
+      k_rope_kv<kvhalf><<<dim3(h->H + h->KVH, M), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, (kvhalf*)h->kc,
+                                                                  (kvhalf*)h->vc, h->ctx, l, h->st);
+    else
+      k_rope_kv<float><<<dim3(h->H + h->KVH, M), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, (float*)h->kc,
+                                                                 (float*)h->vc, h->ctx, l, h->st);
     prof_mark(h, Q4HIP_PROF_ATTN);
     bool quantized = false;                 // the list P.V kernel wrote xq (and xh) itself
     if (M > 1 && h->ascr && h->list_attn == 1) {
-      launch_attn_list(s, HD, M, h->H, h->KVH, h->qkv, QKV, h->kc, h->vc, h->ctx, l, h->ascr, h->att, D, h->tpos, 0,
+      launch_attn_list(s, HD, M, h->H, h->KVH, h->qkv, QKV, h->kc, h->vc, h->kv16, h->ctx, l, h->ascr, h->att, D, h->tpos, 0,
                        h->xq, h->xstride, xh);
       quantized = true;
     } else if (M > 1 && h->ascr) {
       const dim3 ag(h->H, (M + kAttnTokens - 1) / kAttnTokens);
-      if (HD == 64)
-        k_attn_prefill<64><<<ag, 256, 0, s>>>(h->qkv, QKV, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, D, h->st, M, h->ascr);
+      if (HD == 64 && h->kv16)
+        k_attn_prefill<64, kvhalf><<<ag, 256, 0, s>>>(h->qkv, QKV, h->H, h->KVH, (const kvhalf*)h->kc, (const kvhalf*)h->vc, h->ctx, l,
+                                                      h->att, D, h->st, M, h->ascr);
+      else if (HD == 64)
+        k_attn_prefill<64, float><<<ag, 256, 0, s>>>(h->qkv, QKV, h->H, h->KVH, (const float*)h->kc, (const float*)h->vc, h->ctx, l,
+                                                     h->att, D, h->st, M, h->ascr);
+      else if (h->kv16)
+        k_attn_prefill<128, kvhalf><<<ag, 256, 0, s>>>(h->qkv, QKV, h->H, h->KVH, (const kvhalf*)h->kc, (const kvhalf*)h->vc, h->ctx,
+                                                       l, h->att, D, h->st, M, h->ascr);
       else
-        k_attn_prefill<128><<<ag, 256, 0, s>>>(h->qkv, QKV, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, D, h->st, M, h->ascr);
+        k_attn_prefill<128, float><<<ag, 256, 0, s>>>(h->qkv, QKV, h->H, h->KVH, (const float*)h->kc, (const float*)h->vc, h->ctx, l,
+                                                      h->att, D, h->st, M, h->ascr);
     } else if (M == 1 && h->ascr && h->list_attn == 1) {
-      launch_attn_list(s, HD, 1, h->H, h->KVH, h->qkv, QKV, h->kc, h->vc, h->ctx, l, h->ascr, h->att, D, &h->st->pos0, 0,
+      launch_attn_list(s, HD, 1, h->H, h->KVH, h->qkv, QKV, h->kc, h->vc, h->kv16, h->ctx, l, h->ascr, h->att, D, &h->st->pos0, 0,
                        h->xq, h->xstride, xh);
       quantized = true;
+    } else if (HD == 64 && h->kv16) {
+      k_attn<64, kvhalf><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, (const kvhalf*)h->kc,
+                                                             (const kvhalf*)h->vc, h->ctx, l, h->att, h->st);
     } else if (HD == 64) {
-      k_attn<64><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, h->st);
+      k_attn<64, float><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, (const float*)h->kc,
+                                                            (const float*)h->vc, h->ctx, l, h->att, h->st);
+    } else if (h->kv16) {
+      k_attn<128, kvhalf><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, (const kvhalf*)h->kc,
+                                                              (const kvhalf*)h->vc, h->ctx, l, h->att, h->st);
     } else {
-      k_attn<128><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, h->kc, h->vc, h->ctx, l, h->att, h->st);
+      k_attn<128, float><<<dim3(h->H, M), 64, attn_lds, s>>>(h->qkv, QKV, D, h->H, h->KVH, (const float*)h->kc,
+                                                             (const float*)h->vc, h->ctx, l, h->att, h->st);
     }
     prof_mark(h, Q4HIP_PROF_QUANT);
     if (!quantized) launch_quant<QM_PLAIN>(s, M, h->att, D, D, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
@@ -1654,7 +1694,8 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
 // shapes of the parity tests.  Any other shape decodes through the graph path.
 struct PersInstance {
   int D, F, H, KVH;
-  const void* fn;
+  const void* fn;       // fp32 cache
+  const void* fn16;     // fp16 cache
   size_t lds_base;
   size_t (*attn_bytes)(int ctx, int ring_slots, int kv_tile);
   size_t (*ll_entries)(int);
@@ -1663,8 +1704,9 @@ struct PersInstance {
 
 template <class S>
 PersInstance pers_instance() {
-  return PersInstance{S::D, S::F, S::H, S::KVH, (const void*)k_decode_persistent<S>, psmem_base_bytes<S>(),
-                      &psmem_attn_bytes<S>, &S::ll_entries, S::nRoles, S::NBM};
+  return PersInstance{S::D, S::F, S::H, S::KVH, (const void*)k_decode_persistent<S, float>,
+                      (const void*)k_decode_persistent<S, kvhalf>, psmem_base_bytes<S>(), &psmem_attn_bytes<S>,
+                      &S::ll_entries, S::nRoles, S::NBM};
 }
 
 const PersInstance* find_pers_instance(int D, int F, int H, int KVH) {
@@ -1687,7 +1729,7 @@ void setup_persistent(q4hip* h) {
   if (h->HD != kHD) return no("head_dim is not 64");
   const PersInstance* pi = find_pers_instance(h->D, h->F, h->H, h->KVH);
   if (!pi) return no("no kernel instance for this model shape");
-  h->pers_fn = pi->fn;
+  h->pers_fn = h->kv16 ? pi->fn16 : pi->fn;
   int lds_max = 0;
   if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, h->device) != hipSuccess)
     return no("cannot query shared memory size");
@@ -1707,6 +1749,7 @@ void setup_persistent(q4hip* h) {
     if (need(ring, 0) > budget) return no("shared memory too small for the K/V ring");
     while (kv_tile > 0 && need(ring, kv_tile) > budget) kv_tile--;
   }
+  if (h->kv16 && ring > 0) return no("an fp16 K/V cache longer than the staged tile");
   h->pers_kv_tile = kv_tile;
   h->pers_ring = ring;
   h->pers_lds = need(ring, kv_tile);
@@ -1911,9 +1954,10 @@ void q4hip_destroy(q4hip* h) {
 }
 
 int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_heads, int vocab, int ctx,
-                 int mt, float eps, int device) {
+                 int mt, float eps, int device, int kv_type) {
   if (!out) return fail(Q4HIP_EINVAL, "null argument");
   *out = nullptr;
+  if (kv_type != Q4HIP_KV_F32 && kv_type != Q4HIP_KV_F16) return fail(Q4HIP_EINVAL, "unknown K/V cache type %d", kv_type);
   if (dim <= 0 || layers <= 0 || ffn <= 0 || heads <= 0 || kv_heads <= 0 || vocab <= 0 || ctx <= 1)
     return fail(Q4HIP_EINVAL, "bad configuration");
   if (dim % 32 || ffn % 32 || dim % heads || heads % kv_heads)
@@ -1931,6 +1975,8 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
   q4hip* h = new q4hip();
   h->D = dim; h->NL = layers; h->F = ffn; h->H = heads; h->KVH = kv_heads; h->HD = HD;
   h->QKV = dim + 2 * kv_heads * HD; h->V = vocab; h->ctx = ctx; h->MT = mt; h->device = device; h->eps = eps;
+  h->kv16 = kv_type == Q4HIP_KV_F16;
+  h->kvb = h->kv16 ? 2 : 4;
   int rc = Q4HIP_OK;
 #define TRY(x) do { rc = (x); if (rc != Q4HIP_OK) { q4hip_destroy(h); return rc; } } while (0)
 #define TRYHIP(call) do { hipError_t e_ = (call); if (e_ != hipSuccess) { rc = fail(Q4HIP_EHIP, "%s: %s", #call, hipGetErrorString(e_)); q4hip_destroy(h); return rc; } } while (0)
@@ -1957,7 +2003,7 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
   TRYHIP(hipMalloc(&h->att, (size_t)M * dim * 4));
   TRYHIP(hipMalloc(&h->gu, (size_t)M * 2 * ffn * 4));
   TRYHIP(hipMalloc(&h->logits, (size_t)vocab * 4));
-  const size_t kvbytes = (size_t)layers * kv_heads * ctx * HD * 4;
+  const size_t kvbytes = (size_t)layers * kv_heads * ctx * HD * h->kvb;
   TRYHIP(hipMalloc(&h->kc, kvbytes));
   TRYHIP(hipMalloc(&h->vc, kvbytes));
   TRYHIP(hipMemsetAsync(h->kc, 0, kvbytes, h->stream));
@@ -2099,6 +2145,22 @@ int q4hip_forward(q4hip* h, const int* ids, int n, int pos, int* next) {
   return Q4HIP_OK;
 }
 
+// Copy n fp32 values of K and of V from the host into the cache at dk, dv: as they are, or rounded to
+// fp16 (nearest, ties to even: the conversion of the append kernels) for an fp16 cache.
+static int upload_kv(q4hip* h, void* dk, void* dv, const float* k, const float* v, size_t n) {
+  if (!h->kv16) {
+    HIPCHK(hipMemcpy(dk, k, n * 4, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(dv, v, n * 4, hipMemcpyHostToDevice));
+    return Q4HIP_OK;
+  }
+  std::vector<_Float16> t(n);
+  for (size_t i = 0; i < n; i++) t[i] = (_Float16)k[i];
+  HIPCHK(hipMemcpy(dk, t.data(), n * 2, hipMemcpyHostToDevice));
+  for (size_t i = 0; i < n; i++) t[i] = (_Float16)v[i];
+  HIPCHK(hipMemcpy(dv, t.data(), n * 2, hipMemcpyHostToDevice));
+  return Q4HIP_OK;
+}
+
 int q4hip_set_kv(q4hip* h, int layer, int kv_head, int pos0, int n, const float* k, const float* v) {
   if (!h || !k || !v) return fail(Q4HIP_EINVAL, "null argument");
   if (layer < 0 || layer >= h->NL) return fail(Q4HIP_EINVAL, "layer %d of %d", layer, h->NL);
@@ -2106,10 +2168,8 @@ int q4hip_set_kv(q4hip* h, int layer, int kv_head, int pos0, int n, const float*
   if (n <= 0 || pos0 < 0 || (int64_t)pos0 + n > h->ctx) return fail(Q4HIP_ECONTEXT, "positions %d..%lld outside 0..%d", pos0, (long long)pos0 + n, h->ctx);
   HIPCHK(hipSetDevice(h->device));
   HIPCHK(hipStreamSynchronize(h->stream));
-  const size_t off = (((size_t)layer * h->KVH + kv_head) * h->ctx + pos0) * h->HD, bytes = (size_t)n * h->HD * 4;
-  HIPCHK(hipMemcpy(h->kc + off, k, bytes, hipMemcpyHostToDevice));
-  HIPCHK(hipMemcpy(h->vc + off, v, bytes, hipMemcpyHostToDevice));
-  return Q4HIP_OK;
+  const size_t off = (((size_t)layer * h->KVH + kv_head) * h->ctx + pos0) * h->HD;
+  return upload_kv(h, (char*)h->kc + off * h->kvb, (char*)h->vc + off * h->kvb, k, v, (size_t)n * h->HD);
 }
 
 int q4hip_set_decode_mode(q4hip* h, int mode) {
@@ -2298,7 +2358,8 @@ struct q4hip_batch {
   int B = 0, P = 0;
   size_t seq_stride = 0;     // floats of one sequence's K (or V) cache: layers * kv_heads * ctx * head_dim
   size_t attn_lds = 0;
-  float *kc = nullptr, *vc = nullptr, *logits = nullptr, *am_v = nullptr;
+  void *kc = nullptr, *vc = nullptr;   // the sequences' caches, elements of the context's type
+  float *logits = nullptr, *am_v = nullptr;
   float* sc = nullptr;       // attention scores [B][heads][ctx]
   int *am_i = nullptr, *tok = nullptr, *pos = nullptr, *out = nullptr;
   int out_cap = 0;           // ints of `out`
@@ -2319,9 +2380,15 @@ void enqueue_batch_step(q4hip_batch* bt, int* out) {
     Layer& y = h->L[l];
     launch_quant<QM_NORM>(s, B, h->x, D, D, y.attn_norm, h->eps, h->xq, h->xstride, 0, xh);
     launch_matvec<OP_BIAS>(s, y.qkv, h->xq, h->xstride, B, h->qkv, QKV, y.bqkv, xh);
-    k_rope_kv_list<<<dim3(h->H + h->KVH, B), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope, bt->kc,
-                                                             bt->vc, h->ctx, l, bt->pos, bt->seq_stride);
-    launch_attn_list(s, HD, B, h->H, h->KVH, h->qkv, QKV, bt->kc, bt->vc, h->ctx, l, bt->sc, h->att, D, bt->pos,
+    if (h->kv16)
+      k_rope_kv_list<kvhalf><<<dim3(h->H + h->KVH, B), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope,
+                                                                       (kvhalf*)bt->kc, (kvhalf*)bt->vc, h->ctx, l, bt->pos,
+                                                                       bt->seq_stride);
+    else
+      k_rope_kv_list<float><<<dim3(h->H + h->KVH, B), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope,
+                                                                      (float*)bt->kc, (float*)bt->vc, h->ctx, l, bt->pos,
+                                                                      bt->seq_stride);
+    launch_attn_list(s, HD, B, h->H, h->KVH, h->qkv, QKV, bt->kc, bt->vc, h->kv16, h->ctx, l, bt->sc, h->att, D, bt->pos,
                      bt->seq_stride, h->xq, h->xstride, xh);
     launch_matvec<OP_ADD>(s, y.o, h->xq, h->xstride, B, h->x, D, nullptr, xh);
     launch_quant<QM_NORM>(s, B, h->x, D, D, y.ffn_norm, h->eps, h->xq, h->xstride, 0, xh);
@@ -2368,7 +2435,7 @@ int q4hip_batch_create(q4hip_batch** out, q4hip* h, int B) {
   bt->P = (h->V + 4095) / 4096;
   bt->seq_stride = (size_t)h->NL * h->KVH * h->ctx * h->HD;
   bt->attn_lds = lds;
-  const size_t kvbytes = (size_t)B * bt->seq_stride * 4;
+  const size_t kvbytes = (size_t)B * bt->seq_stride * h->kvb;
   hipError_t e = hipSuccess;
   auto al = [&](void** p, size_t bytes) { if (e == hipSuccess) e = hipMalloc(p, bytes); };
   al((void**)&bt->kc, kvbytes);
@@ -2403,10 +2470,7 @@ int q4hip_batch_set_kv(q4hip_batch* bt, int seq, int layer, int kv_head, int pos
   HIPCHK(hipSetDevice(h->device));
   HIPCHK(hipStreamSynchronize(h->stream));
   const size_t off = (size_t)seq * bt->seq_stride + (((size_t)layer * h->KVH + kv_head) * h->ctx + pos0) * h->HD;
-  const size_t bytes = (size_t)n * h->HD * 4;
-  HIPCHK(hipMemcpy(bt->kc + off, k, bytes, hipMemcpyHostToDevice));
-  HIPCHK(hipMemcpy(bt->vc + off, v, bytes, hipMemcpyHostToDevice));
-  return Q4HIP_OK;
+  return upload_kv(h, (char*)bt->kc + off * h->kvb, (char*)bt->vc + off * h->kvb, k, v, (size_t)n * h->HD);
 }
 
 int q4hip_batch_prefill(q4hip_batch* bt, int seq, const int* ids, int n, int pos, int* next) {
@@ -2422,10 +2486,10 @@ int q4hip_batch_prefill(q4hip_batch* bt, int seq, const int* ids, int n, int pos
   HIPCHK(hipSetDevice(h->device));
   prepare_attention(h);
   // the passes run eagerly against this sequence's cache; the context's own cache is untouched
-  float* kc = h->kc;
-  float* vc = h->vc;
-  h->kc = bt->kc + (size_t)seq * bt->seq_stride;
-  h->vc = bt->vc + (size_t)seq * bt->seq_stride;
+  void* kc = h->kc;
+  void* vc = h->vc;
+  h->kc = (char*)bt->kc + (size_t)seq * bt->seq_stride * h->kvb;
+  h->vc = (char*)bt->vc + (size_t)seq * bt->seq_stride * h->kvb;
   memcpy(h->pin_ids, ids, (size_t)n * 4);
   hipError_t e = hipMemcpyAsync(h->tokens + pos, h->pin_ids, (size_t)n * 4, hipMemcpyHostToDevice, h->stream);
   for (int c = 0; e == hipSuccess && c < n; c += h->MT) {

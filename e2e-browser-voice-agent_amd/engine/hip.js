@@ -7,7 +7,10 @@
 // (h2-own-inference-engine/engine/cpu.js:52-68, engine/webgpu.js:617-620):
 //   name, ctx, info, forward(ids, pos, {temperature, seed, wantLogits}) -> next id,
 //   readLogits() -> Float32Array(vocab), profile(), destroy()
-// plus generate(first, pos, steps), the greedy loop run on the device.
+// plus generate(first, pos, steps), the greedy loop run on the device; setKv(layer, kvHead, pos0,
+// k, v), rows written straight into the K/V cache; setDecodeMode / decodeModeUsed, the choice
+// between the persistent decode kernel and the captured graph; and createBatch(B), B sequences
+// decoded together with this backend's weights (see makeBatch).
 //
 // Below it is the N-API addon lib/q4hip.node over the C ABI of include/q4hip.h.  The addon is
 // required, not optional: without it (or without a GPU) createHIP throws.
@@ -68,6 +71,52 @@ function sampleAt(lg, temperature, seed, pos) {
   return sample(lg, temperature, (seed + pos) >>> 0);
 }
 
+const DECODE_MODES = { auto: 0, graph: 1, persistent: 2 };
+const DECODE_NAMES = { 0: null, 1: "graph", 2: "persistent" };
+
+// B independent sequences on the weights of context h, each with its own K/V cache (the reference
+// runs one sequence per backend; a batch runs B such loops in one pass per step):
+//   prefill(seq, ids, pos) -> next id of that sequence after ids at positions pos..
+//   setKv(seq, layer, kvHead, pos0, k, v)   K/V rows of one sequence, as the backend's setKv
+//   generate(first, pos, steps) -> B arrays of steps greedy tokens; sequence b starts with first[b]
+//                                  at position pos[b]
+//   readLogits() -> Float32Array(B * vocab), the last step's logits, sequence by sequence
+//   destroy()
+// Calls on a batch and on its backend share the backend's buffers and run one at a time.
+function makeBatch(a, h, B, vocab, ctx) {
+  const bt = a.batchCreate(h, B);
+  const ints = (xs, what) => {
+    if (xs.length !== B) throw new Error(`${what}: ${B} entries expected, got ${xs.length}`);
+    return Int32Array.from(xs);
+  };
+  return {
+    B,
+    async prefill(seq, ids, pos = 0) {
+      if (!ids.length) throw new Error("prefill: no token ids");
+      if (pos + ids.length >= ctx) throw new Error("context full");
+      return a.batchPrefill(bt, seq, Int32Array.from(ids), pos);
+    },
+    setKv(seq, layer, kvHead, pos0, k, v) { a.batchSetKv(bt, seq, layer, kvHead, pos0, k, v); },
+    async generate(first, pos, steps) {
+      const o = new Int32Array(steps * B);
+      a.batchGenerate(bt, ints(first, "first"), ints(pos, "pos"), o);
+      const per = [];
+      for (let b = 0; b < B; b++) {
+        const t = new Array(steps);
+        for (let i = 0; i < steps; i++) t[i] = o[i * B + b];
+        per.push(t);
+      }
+      return per;
+    },
+    async readLogits() {
+      const lg = new Float32Array(B * vocab);
+      a.batchReadLogits(bt, lg);
+      return lg;
+    },
+    destroy() { a.batchDestroy(bt); },
+  };
+}
+
 function check(T, name, types, label) {
   const t = T[name];
   if (!t) throw new Error(`${name}: missing`);
@@ -103,8 +152,10 @@ async function createHIP(gguf, bytes, cfg, opts = {}) {
   const out = check(T, "output.weight", [TYPE.Q4_0, TYPE.Q8_0], "Q4_0 or Q8_0");
   const outNorm = check(T, "output_norm.weight", F32, "F32");
 
+  const kvDtype = opts.kvDtype || "f32";
+  if (kvDtype !== "f32" && kvDtype !== "f16") throw new Error(`kvDtype must be "f32" or "f16", not ${kvDtype}`);
   const a = loadAddon();
-  const h = a.create(D, NL, F, H, KVH, vocab, ctx, opts.prefillChunk || 0, eps, device);
+  const h = a.create(D, NL, F, H, KVH, vocab, ctx, opts.prefillChunk || 0, eps, device, kvDtype === "f16" ? 1 : 0);
   const rows = (t) => (t.type === TYPE.F32 ? t.count : t.count / t.shape[0]);
   const up = (kind, layer, row0, t) =>
     a.setTensor(h, kind, layer, row0, t.type, src.subarray(t.start, t.start + t.bytes), rows(t));
@@ -133,7 +184,8 @@ async function createHIP(gguf, bytes, cfg, opts = {}) {
     name: "hip",
     ctx,
     device,
-    info: `HIP device ${device}, Q4_0 x int8 kernels, ${out.type === TYPE.Q8_0 ? "Q8_0" : "Q4_0"} head, fp32 KV cache, persistent decode kernel`,
+    kvDtype,
+    info: `HIP device ${device}, Q4_0 x int8 kernels, ${out.type === TYPE.Q8_0 ? "Q8_0" : "Q4_0"} head, ${kvDtype === "f16" ? "fp16" : "fp32"} KV cache, persistent decode kernel`,
     // Run ids at positions pos.. and return the next token (engine/cpu-worker.js:169-182).
     async forward(ids, pos, { temperature = 0, seed = 1, wantLogits = false } = {}) {
       if (pos + ids.length >= ctx) throw new Error("context full");
@@ -160,8 +212,20 @@ async function createHIP(gguf, bytes, cfg, opts = {}) {
       PROFILE_NAMES.forEach((n, i) => { by[n] = us[i]; });
       return by;
     },
+    // K and V rows [n][head_dim] (Float32Array each) of one layer and kv head at positions pos0..,
+    // e.g. a cache prefilled from stored activations (rounded to fp16 in an fp16 cache).
+    setKv(layer, kvHead, pos0, k, v) { a.setKv(h, layer, kvHead, pos0, k, v); },
+    // "auto" (persistent kernel where the model and device admit it), "graph" or "persistent";
+    // both paths give identical tokens.
+    setDecodeMode(mode) {
+      if (!(mode in DECODE_MODES)) throw new Error(`decode mode must be auto, graph or persistent, not ${mode}`);
+      a.setDecodeMode(h, DECODE_MODES[mode]);
+    },
+    // The path of the last decode step: "persistent", "graph", or null before any.
+    decodeModeUsed() { return DECODE_NAMES[a.decodeModeUsed(h)]; },
+    createBatch(B) { return makeBatch(a, h, B, vocab, ctx); },
     destroy() { a.destroy(h); },
   };
 }
 
-module.exports = { createHIP, ropeTable, sample, sampleAt, KIND };
+module.exports = { createHIP, ropeTable, sample, sampleAt, KIND, DECODE_MODES };

@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libq4hip.so")
 
 OK, EINVAL, ECONTEXT, ETYPE, EHIP, ESTATE = 0, 1, 2, 3, 4, 5
 DECODE_AUTO, DECODE_GRAPH, DECODE_PERSISTENT = 0, 1, 2
+KV_F32, KV_F16 = 0, 1
 PROF_NAMES = ["embed", "norm+quantize", "matvec qkv", "rope+kv", "attention", "quantize", "matvec o",
               "matvec gate+up", "swiglu+quantize", "matvec down", "matvec output", "sample"]
 
@@ -52,7 +53,7 @@ def lib() -> ctypes.CDLL:
         "q4hip_last_error": (ctypes.c_char_p, []),
         "q4hip_device_count": (I, [ctypes.POINTER(I)]),
         "q4hip_check_division": (I, [I, P, I]),
-        "q4hip_create": (I, [ctypes.POINTER(P), I, I, I, I, I, I, I, I, F, I]),
+        "q4hip_create": (I, [ctypes.POINTER(P), I, I, I, I, I, I, I, I, F, I, I]),
         "q4hip_set_tensor": (I, [P, I, I, I, I, P, I64, ctypes.c_size_t]),
         "q4hip_set_rope": (I, [P, P, I64]),
         "q4hip_forward": (I, [P, P, I, I, ctypes.POINTER(I)]),
@@ -117,11 +118,11 @@ def check_division(device: int = 0) -> dict:
 class Model:
     """One loaded model on one GPU: the backend object's C side."""
 
-    def __init__(self, shape: synth.Shape, ctx: int = 2048, mt: int = 0, device: int = 0):
-        self.shape, self.ctx = shape, ctx
+    def __init__(self, shape: synth.Shape, ctx: int = 2048, mt: int = 0, device: int = 0, kv_type: int = KV_F32):
+        self.shape, self.ctx, self.kv_type = shape, ctx, kv_type
         h = ctypes.c_void_p()
         _check(lib().q4hip_create(ctypes.byref(h), shape.dim, shape.layers, shape.ffn, shape.heads,
-                                  shape.kv_heads, shape.vocab, ctx, mt, ctypes.c_float(shape.eps), device))
+                                  shape.kv_heads, shape.vocab, ctx, mt, ctypes.c_float(shape.eps), device, kv_type))
         self.h = h
 
     def close(self) -> None:

@@ -53,13 +53,23 @@ const char* q4hip_last_error(void);
 /* Number of visible HIP devices. */
 int q4hip_device_count(int* count);
 
+/* K/V cache element types (q4hip_create's kv_type):
+ *   Q4HIP_KV_F32  the reference's fp32 cache (kc/vc of engine/cpu-worker.js:71): results bit-identical
+ *                 to the reference's arithmetic
+ *   Q4HIP_KV_F16  half the cache bytes: K and V rounded to fp16 (nearest, ties to even) when appended
+ *                 or written by q4hip_set_kv, and read back exactly; results bit-identical to the
+ *                 reference's arithmetic over a cache holding those rounded values.  Decode steps use
+ *                 the persistent kernel while the context fits its staged tile, else the graph path. */
+#define Q4HIP_KV_F32 0
+#define Q4HIP_KV_F16 1
+
 /* Create a context: replaces set_config (engine/kernels.c:418-421) and the memory plan of
  * engine/cpu-worker.js:52-88.  Allocates weights, activations for device passes of up to `mt`
  * tokens (1..1024, capped at ctx; 0 or out of range = 1024: a prompt runs as passes of that many
- * tokens, with results identical to the reference's 16-token chunks), the fp32 KV cache for `ctx`
- * positions and the token array on `device`.  head_dim = dim/heads. */
+ * tokens, with results identical to the reference's 16-token chunks), the K/V cache of `kv_type`
+ * for `ctx` positions and the token array on `device`.  head_dim = dim/heads. */
 int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_heads, int vocab,
-                 int ctx, int mt, float eps, int device);
+                 int ctx, int mt, float eps, int device, int kv_type);
 
 /* Upload one GGUF tensor (or a part of a fused one): replaces set_tensor (engine/kernels.c:423-431)
  * together with copyBlocks (engine/cpu-worker.js:97-124).  `data` holds `rows` rows in GGUF
@@ -141,7 +151,7 @@ int q4hip_profile_pass(q4hip* h, const int* ids, int ntok, int pos, float* us, i
 int q4hip_profile_persistent(q4hip* h, int token, int pos, float* us, int n);
 
 /* Write the K and V rows of one layer and kv head at positions [pos0, pos0 + n): `k` and `v` are
- * [n][head_dim] fp32.  The reference's cache is memory its host owns and hands to the kernels
+ * [n][head_dim] fp32 (rounded to fp16 for an fp16 cache).  The reference's cache is memory its host owns and hands to the kernels
  * (kc/vc of set_buffers, engine/kernels.c:433-440); this fills ours directly, e.g. with a cache
  * prefilled from stored activations.  Positions must lie below ctx. */
 int q4hip_set_kv(q4hip* h, int layer, int kv_head, int pos0, int n, const float* k, const float* v);

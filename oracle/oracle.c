@@ -243,12 +243,94 @@ void orc_rope_table(float* rope, int ctx, int hd, double theta) {
 
 /* ------------------------------------------------------------------ the model (kernels.c:26-41) */
 
+/* ---- numerics variants (not the reference's arithmetic; see oracle.h) ---- */
+
+/* Round to the nearest binary16 value, ties to even, and widen back (IEEE 754 conversion). */
+float orc_round_f16(float x) {
+  union { float f; uint32_t u; } v = { .f = x };
+  const uint32_t sign = v.u & 0x80000000u, a = v.u & 0x7fffffffu;
+  if (a >= 0x7f800000u) return x;                          /* inf and NaN stay */
+  if (a >= 0x477ff000u) { v.u = sign | 0x7f800000u; return v.f; }   /* >= 65520: to infinity */
+  if (a < 0x38800000u) {                                   /* below 2^-14: multiples of 2^-24 */
+    union { float f; uint32_t u; } m = { .u = a };
+    float q = nearbyintf(m.f * 16777216.0f) * 5.9604644775390625e-8f;
+    union { float f; uint32_t u; } r = { .f = q };
+    r.u |= sign;
+    return r.f;
+  }
+  uint32_t u = a + 0x0fffu + ((a >> 13) & 1u);              /* round off 13 mantissa bits, ties to even */
+  v.u = sign | (u & ~0x1fffu);
+  return v.f;
+}
+
+/* RMSNorm with the sum of squares reassociated as a GPU block reduction would: 32 strided
+ * partial sums (i mod 32), then a pairwise tree. */
+static void rmsnorm_tree(float* out, const float* x, const float* w, int n, float eps) {
+  float p[32];
+  for (int k = 0; k < 32; k++) p[k] = 0.0f;
+  for (int i = 0; i < n; i++) p[i & 31] = p[i & 31] + x[i] * x[i];
+  for (int w2 = 16; w2 > 0; w2 >>= 1)
+    for (int k = 0; k < w2; k++) p[k] = p[k] + p[k + w2];
+  float r = 1.0f / sqrtf(p[0] / (float)n + eps);
+  for (int i = 0; i < n; i++) out[i] = (x[i] * r) * w[i];
+}
+
+/* dot_q4_q8 with each lane's chain over blocks split into 4 contiguous parts (as 4 waves would
+ * split the blocks), the parts added in order, then hsum. */
+static float dot_q4_q8_splitk(const uint8_t* wq, const float* wd, const int8_t* xq, const float* xd, int nb) {
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int per = (nb + 3) / 4;
+  for (int part = 0; part < 4; part++) {
+    float pa[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = part * per; b < nb && b < (part + 1) * per; b++) {
+      int32_t p[4];
+      orc_block_lanes_q4(wq + 16 * b, xq + 32 * b, p);
+      float sc = wd[b] * xd[b];
+      for (int j = 0; j < 4; j++) pa[j] = pa[j] + (float)p[j] * sc;
+    }
+    for (int j = 0; j < 4; j++) acc[j] = acc[j] + pa[j];
+  }
+  return acc[0] + acc[1] + acc[2] + acc[3];
+}
+
+/* Attention split over chunks of 256 positions (flash-decoding): per chunk its own maximum, sum and
+ * P.V; the chunks merged with the log-sum-exp rule using expf. */
+static void attend_split(const float* q, const float* kb, const float* vb, int T, int hd, float* sc, float* out) {
+  enum { CH = 256 };
+  float scale = 1.0f / sqrtf((float)hd), M = -1e30f, S = 0.0f;
+  float acc[256];
+  for (int i = 0; i < hd; i++) acc[i] = 0.0f;
+  for (int t = 0; t < T; t++) {
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < hd; i += 4)
+      for (int j = 0; j < 4; j++) s[j] = s[j] + q[i + j] * kb[(size_t)t * hd + i + j];
+    sc[t] = (s[0] + s[1] + s[2] + s[3]) * scale;
+  }
+  for (int c0 = 0; c0 < T; c0 += CH) {
+    int c1 = c0 + CH < T ? c0 + CH : T;
+    float m = -1e30f, sum = 0.0f, o[256];
+    for (int t = c0; t < c1; t++) if (sc[t] > m) m = sc[t];
+    for (int i = 0; i < hd; i++) o[i] = 0.0f;
+    for (int t = c0; t < c1; t++) {
+      float e = orc_fast_exp(sc[t] - m);
+      sum += e;
+      for (int i = 0; i < hd; i++) o[i] = o[i] + e * vb[(size_t)t * hd + i];
+    }
+    float nm = m > M ? m : M, a = expf(M - nm), b = expf(m - nm);
+    for (int i = 0; i < hd; i++) acc[i] = acc[i] * a + o[i] * b;
+    S = S * a + sum * b;
+    M = nm;
+  }
+  for (int i = 0; i < hd; i++) out[i] = acc[i] / S;
+}
+
 typedef struct { const uint8_t* qs; const float* d; } Q4;
 typedef struct { const int8_t* qs; const float* d; } Q8;
 typedef struct { const float *attn_norm, *ffn_norm, *bqkv; Q4 qkv, o, gu, down; } Layer;
 
 struct orc_model {
   int dim, layers, ffn, heads, kvh, hd, vocab, ctx, mt, threads;
+  int variant;     /* ORC_V_* bits; 0 = the reference's arithmetic */
   float eps;
   Q4 embd; Q8 out; const float* out_norm;
   Layer L[ORC_MAXL];
@@ -311,12 +393,26 @@ void orc_set_tensor(orc_model* g, int kind, int layer, const void* qs, const flo
 
 static void matmul_mt(orc_model* g, Q4 W, int K, int N, int M, float* y, int op, const float* bias) {
   const int nth = g->threads;
+  if (g->variant & ORC_V_DOT_SPLITK) {
+    const int nb = K / 32;
+    #pragma omp parallel for schedule(static) num_threads(nth)
+    for (int n = 0; n < N; n++)
+      for (int m = 0; m < M; m++)
+        put(y, N, m, n, dot_q4_q8_splitk(W.qs + (size_t)n * nb * 16, W.d + (size_t)n * nb, g->aq + (size_t)m * K,
+                                         g->ad + (size_t)m * nb, nb), op, bias);
+    return;
+  }
   /* rows split in contiguous ranges, like split() (kernels.c:63-66) */
   #pragma omp parallel for schedule(static) num_threads(nth)
   for (int t = 0; t < nth; t++) {
     int per = (N + nth - 1) / nth, a = t * per, b = a + per > N ? N : a + per;
     if (a < b) orc_matmul_q4(W.qs, W.d, K, N, a, b, M, g->aq, g->ad, y, op, bias);
   }
+}
+
+static void rmsnorm_v(const orc_model* g, float* out, const float* x, const float* w, int n) {
+  if (g->variant & ORC_V_NORM_TREE) rmsnorm_tree(out, x, w, n, g->eps);
+  else orc_rmsnorm(out, x, w, n, g->eps);
 }
 
 /* kernels.c:306-415 */
@@ -333,7 +429,7 @@ void orc_run(orc_model* g, int pos0, int M, int want_logits) {
   for (int l = 0; l < g->layers; l++) {
     const Layer* L = &g->L[l];
     for (int m = 0; m < M; m++) {                                          /* :328-331 */
-      orc_rmsnorm(g->xn + (size_t)m * D, g->x + (size_t)m * D, L->attn_norm, D, g->eps);
+      rmsnorm_v(g, g->xn + (size_t)m * D, g->x + (size_t)m * D, L->attn_norm, D);
       orc_quantize_row(g->aq + (size_t)m * D, g->ad + (size_t)m * (D / 32), g->as + (size_t)m * (D / 32),
                        g->xn + (size_t)m * D, D);
     }
@@ -348,7 +444,10 @@ void orc_run(orc_model* g, int pos0, int M, int want_logits) {
         float* kd = g->kc + (((size_t)l * KVH + kh) * g->ctx + pos) * HD;
         float* vd = g->vc + (((size_t)l * KVH + kh) * g->ctx + pos) * HD;
         const float* vs = g->qkv + (size_t)m * QKV + D + KVH * HD + kh * HD;
-        for (int i = 0; i < HD; i++) { kd[i] = v[i]; vd[i] = vs[i]; }
+        if (g->variant & ORC_V_KV_F16)
+          for (int i = 0; i < HD; i++) { kd[i] = orc_round_f16(v[i]); vd[i] = orc_round_f16(vs[i]); }
+        else
+          for (int i = 0; i < HD; i++) { kd[i] = v[i]; vd[i] = vs[i]; }
       }
     }
     #pragma omp parallel for schedule(static) num_threads(nth)
@@ -357,15 +456,18 @@ void orc_run(orc_model* g, int pos0, int M, int want_logits) {
       const float* q = g->qkv + (size_t)m * QKV + h * HD;
       const float* kb = g->kc + ((size_t)l * KVH + kh) * g->ctx * HD;
       const float* vb = g->vc + ((size_t)l * KVH + kh) * g->ctx * HD;
-      orc_attend(q, kb, vb, T, HD, g->scores + (size_t)omp_get_thread_num() * g->ctx,
-                 g->att + (size_t)m * D + h * HD);
+      if (g->variant & ORC_V_ATTN_SPLIT)
+        attend_split(q, kb, vb, T, HD, g->scores + (size_t)omp_get_thread_num() * g->ctx, g->att + (size_t)m * D + h * HD);
+      else
+        orc_attend(q, kb, vb, T, HD, g->scores + (size_t)omp_get_thread_num() * g->ctx,
+                   g->att + (size_t)m * D + h * HD);
     }
     for (int m = 0; m < M; m++)                                            /* :379, quantize_tokens :275-277 */
       orc_quantize_row(g->aq + (size_t)m * D, g->ad + (size_t)m * (D / 32), g->as + (size_t)m * (D / 32),
                        g->att + (size_t)m * D, D);
     matmul_mt(g, L->o, D, D, M, g->x, 2, NULL);                             /* :381-382 */
     for (int m = 0; m < M; m++) {                                          /* :385-388 */
-      orc_rmsnorm(g->xn + (size_t)m * D, g->x + (size_t)m * D, L->ffn_norm, D, g->eps);
+      rmsnorm_v(g, g->xn + (size_t)m * D, g->x + (size_t)m * D, L->ffn_norm, D);
       orc_quantize_row(g->aq + (size_t)m * D, g->ad + (size_t)m * (D / 32), g->as + (size_t)m * (D / 32),
                        g->xn + (size_t)m * D, D);
     }
@@ -380,7 +482,7 @@ void orc_run(orc_model* g, int pos0, int M, int want_logits) {
   }
 
   if (want_logits) {                                                       /* :404-414 */
-    orc_rmsnorm(g->xn, g->x + (size_t)(M - 1) * D, g->out_norm, D, g->eps);
+    rmsnorm_v(g, g->xn, g->x + (size_t)(M - 1) * D, g->out_norm, D);
     orc_quantize_row(g->aq, g->ad, g->as, g->xn, D);
     const int nb = D / 32, V = g->vocab;
     #pragma omp parallel for schedule(static) num_threads(nth)
@@ -401,6 +503,7 @@ int orc_forward(orc_model* g, const int* ids, int n, int pos) {
 }
 
 const float* orc_logits(const orc_model* g) { return g->logits; }
+void orc_set_variant(orc_model* g, int flags) { g->variant = flags; }
 float* orc_kcache(orc_model* g) { return g->kc; }
 float* orc_vcache(orc_model* g) { return g->vc; }
 float* orc_hidden(orc_model* g) { return g->x; }

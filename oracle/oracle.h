@@ -71,6 +71,21 @@ void orc_run(orc_model* m, int pos0, int M, int want_logits);
 int orc_forward(orc_model* m, const int* ids, int n, int pos);
 void orc_set_threads(orc_model* m, int threads);
 const float* orc_logits(const orc_model* m);
+
+/* Numerics variants, for measuring how far other operation orders or a half-precision cache move
+ * the results (none is the reference's arithmetic; 0, the default, is):
+ *   ORC_V_NORM_TREE   RMSNorm sums of squares as 32 strided partial sums and a pairwise tree
+ *   ORC_V_DOT_SPLITK  each projection lane chain split into 4 contiguous block ranges, then added
+ *   ORC_V_ATTN_SPLIT  attention over chunks of 256 positions merged by the log-sum-exp rule
+ *   ORC_V_KV_F16      K and V rounded to binary16 (ties to even) when appended to the cache: the
+ *                     arithmetic of a half-precision KV cache read back exactly into fp32 */
+#define ORC_V_NORM_TREE 1
+#define ORC_V_DOT_SPLITK 2
+#define ORC_V_ATTN_SPLIT 4
+#define ORC_V_KV_F16 8
+void orc_set_variant(orc_model* m, int flags);
+/* Round to the nearest binary16 value (ties to even) and widen back to fp32. */
+float orc_round_f16(float x);
 float* orc_kcache(orc_model* m);   /* [layers][kvh][ctx][hd] fp32 */
 float* orc_vcache(orc_model* m);
 float* orc_hidden(orc_model* m);   /* x [mt][dim] */

@@ -60,6 +60,8 @@ def lib() -> ctypes.CDLL:
         "orc_vcache": (P, [P]),
         "orc_hidden": (P, [P]),
         "orc_tokens": (P, [P]),
+        "orc_set_variant": (None, [P, I]),
+        "orc_round_f16": (F, [F]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -158,6 +160,13 @@ def f16_to_f32(h: int) -> float:
     return lib().orc_f16_to_f32(h)
 
 
+V_NORM_TREE, V_DOT_SPLITK, V_ATTN_SPLIT, V_KV_F16 = 1, 2, 4, 8
+
+
+def round_f16(x: float) -> float:
+    return lib().orc_round_f16(ctypes.c_float(x))
+
+
 def rope_table(ctx: int, hd: int, theta: float) -> np.ndarray:
     out = np.empty((ctx, hd // 2, 2), np.float32)
     lib().orc_rope_table(ptr(out), ctx, hd, ctypes.c_double(theta))
@@ -223,6 +232,10 @@ class Model:
 
     def set_threads(self, n: int):
         lib().orc_set_threads(self.h, n)
+
+    def set_variant(self, flags: int):
+        """ORC_V_* bits of oracle.h: other operation orders, or a half-precision KV cache."""
+        lib().orc_set_variant(self.h, flags)
 
     def forward(self, ids, pos: int) -> int:
         a = np.ascontiguousarray(ids, np.int32)

@@ -8,6 +8,11 @@
 //   samples <cases.json>                           -> [id] for [{logits (path to raw f32), temperature, seed, pos}]
 //   tokenize <meta.json> <texts.json>              -> {ids, text, pieces} per text (tokenizer alone)
 //   chat <gguf> <ctx> <turns.json> <maxTokens>     -> per turn {pieces, ids, prompt, stats}
+//   batch <gguf> <ctx> <prompts.json> <steps> <logits.f32> <kvDtype>
+//        -> {first, tokens (per sequence), afterDestroy}; the batch's last logits written raw
+//   setkv <gguf> <ctx> <kv.f32> <positions> <first> <steps> <kvDtype>
+//        -> {modes: {graph|persistent: {tokens, used}}} after the cache [K|V][layer][kvHead][pos][hd]
+//           is written through setKv
 const fs = require("fs");
 const path = require("path");
 const engine = path.join(__dirname, "..", "..", "e2e-browser-voice-agent_amd", "engine");
@@ -85,6 +90,43 @@ async function main() {
     }
     llm.destroy();
     return out;
+  }
+  if (cmd === "batch") {
+    const prompts = JSON.parse(fs.readFileSync(args[2], "utf8"));
+    const steps = Number(args[3]);
+    const llm = await LLM.load({ path: args[0], ctx: Number(args[1]), kvDtype: args[5] });
+    const bt = llm.be.createBatch(prompts.length);
+    const first = [];
+    for (let b = 0; b < prompts.length; b++) first.push(await bt.prefill(b, prompts[b], 0));
+    const tokens = await bt.generate(first, prompts.map((p) => p.length), steps);
+    const lg = await bt.readLogits();
+    fs.writeFileSync(args[4], Buffer.from(lg.buffer));
+    llm.destroy();                     // releases the batch too
+    let afterDestroy = null;
+    try { await bt.generate(first, prompts.map((p) => p.length), 1); } catch (e) { afterDestroy = e.message; }
+    return { first, tokens, afterDestroy };
+  }
+  if (cmd === "setkv") {
+    const b = fs.readFileSync(args[2]);
+    const kv = new Float32Array(b.buffer, b.byteOffset, b.length / 4);
+    const P = Number(args[3]), first = Number(args[4]), steps = Number(args[5]);
+    const llm = await LLM.load({ path: args[0], ctx: Number(args[1]), kvDtype: args[6] });
+    const { layers, kvHeads, dim, heads } = llm.cfg;
+    const hd = dim / heads, block = P * hd, half = layers * kvHeads * block;
+    for (let l = 0; l < layers; l++) {
+      for (let kh = 0; kh < kvHeads; kh++) {
+        const at = (l * kvHeads + kh) * block;
+        llm.be.setKv(l, kh, 0, kv.subarray(at, at + block), kv.subarray(half + at, half + at + block));
+      }
+    }
+    const modes = {};
+    for (const mode of ["graph", "persistent"]) {
+      llm.be.setDecodeMode(mode);
+      const tokens = await llm.be.generate(first, P, steps);
+      modes[mode] = { tokens, used: llm.be.decodeModeUsed() };
+    }
+    llm.destroy();
+    return { modes };
   }
   throw new Error(`unknown command ${cmd}`);
 }

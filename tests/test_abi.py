@@ -50,7 +50,9 @@ def test_addon_loads_and_exports():
                          capture_output=True, text=True, timeout=60)
     assert out.returncode == 0, out.stderr
     keys = out.stdout.strip().split(",")
-    for k in ["create", "destroy", "setTensor", "setRope", "forward", "readLogits", "generate", "profile", "deviceCount"]:
+    for k in ["create", "destroy", "setTensor", "setRope", "forward", "readLogits", "generate", "profile", "deviceCount",
+              "setKv", "setDecodeMode", "decodeModeUsed", "batchCreate", "batchDestroy", "batchPrefill", "batchSetKv",
+              "batchGenerate", "batchReadLogits"]:
         assert k in keys
 
 

@@ -329,3 +329,47 @@ def test_batch_qwen15b_b32_ctx1024():
         g.close()
         if o is not None:
             o.close()
+
+
+def test_batch_qwen15b_b32_ctx1024_fp16():
+    """The batched-decode configuration with the fp16 cache: Qwen2.5-1.5B shape, 32 sequences with
+    their own ~1024-position caches (written through q4hip_batch_set_kv), 3 steps of all 32.  Every
+    sequence's tokens and last logits equal, bit for bit, the oracle's over a cache holding the same
+    fp16-rounded values (ORC_V_KV_F16), run one sequence at a time."""
+    import q4hip
+    shape = synth.SHAPES["qwen2.5-1.5b"]
+    t = _model("qwen2.5-1.5b", 51)
+    P, B, ctx, steps = 1024, 32, 1040, 3
+    pos = [P - (b * 37) % 300 for b in range(B)]
+    first = [int(x) for x in np.random.default_rng(52).integers(0, shape.vocab, B)]
+    print(f"qwen15b batch of {B}, {P}-position fp16 caches", flush=True)
+    g = q4hip.Model(shape, ctx=ctx, kv_type=q4hip.KV_F16)
+    g.load(t)
+    bt = q4hip.Batch(g, B)
+    o = None
+    try:
+        for b in range(B):
+            k, v = _seq_cache(shape, P, 400 + b)
+            for l in range(shape.layers):
+                for kh in range(shape.kv_heads):
+                    bt.set_kv(b, l, kh, 0, k[l, kh], v[l, kh])
+        out = bt.generate(first, pos, steps)
+        lg = bt.read_logits()
+        print("batch done; oracle per sequence", flush=True)
+        o = oracle.Model(shape, t, ctx=ctx, mt=16, threads=16)
+        o.set_variant(oracle.V_KV_F16)
+        for b in range(B):
+            k, v = _seq_cache(shape, P, 400 + b)
+            ok, ov = o.kv()
+            ok[:, :, :P] = k
+            ov[:, :, :P] = v
+            tok = first[b]
+            for i in range(steps):
+                tok = o.forward([tok], pos[b] + i)
+                assert out[i, b] == tok, f"sequence {b} step {i}"
+            _same_logits(lg[b], o.logits(), f"sequence {b}")
+    finally:
+        bt.close()
+        g.close()
+        if o is not None:
+            o.close()

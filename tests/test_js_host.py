@@ -199,6 +199,60 @@ def test_q8_head_through_napi_matches_oracle(tmp_path):
     o.close()
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_batch_through_napi_matches_oracle(tiny_gguf, tmp_path, kv):
+    """createBatch through the addon: four sequences with prompts of different lengths, prefilled
+    one by one, then decoded together; each sequence's tokens and last logits are its own oracle
+    loop's.  Destroying the backend releases the batch, whose next call throws."""
+    import oracle
+    shape, t, p = tiny_gguf
+    prompts = [synth.prompt_ids(90 + b, n, shape.vocab) for b, n in enumerate([9, 23, 1, 40])]
+    (tmp_path / "prompts.json").write_text(json.dumps(prompts))
+    steps = 12
+    out = node("batch", p, 128, tmp_path / "prompts.json", steps, tmp_path / "lg.f32", kv)
+    lg = np.frombuffer((tmp_path / "lg.f32").read_bytes(), np.float32).reshape(len(prompts), shape.vocab)
+    o = oracle.Model(shape, t, ctx=128)
+    if kv == "f16":
+        o.set_variant(oracle.V_KV_F16)
+    for b, ids in enumerate(prompts):
+        ref = o.generate(ids, steps + 1)
+        assert [out["first"][b]] + out["tokens"][b] == ref, b
+        assert np.array_equal(lg[b].view(np.uint32), o.logits().view(np.uint32)), b
+    o.close()
+    assert "destroyed" in out["afterDestroy"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_set_kv_through_napi_matches_oracle(tiny_gguf, tmp_path, kv):
+    """setKv fills 48 cached positions of every layer and kv head from the host; decoding from
+    there on the graph path and on the persistent kernel (setDecodeMode, decodeModeUsed) gives the
+    oracle's tokens after the same cache."""
+    import oracle
+    shape, t, p = tiny_gguf
+    P, first, steps = 48, 5, 10
+    rng = np.random.default_rng(91)
+    kvs = rng.standard_normal((2, shape.layers, shape.kv_heads, P, shape.head_dim), dtype=np.float32)
+    (tmp_path / "kv.f32").write_bytes(kvs.tobytes())
+    out = node("setkv", p, 128, tmp_path / "kv.f32", P, first, steps, kv)
+    o = oracle.Model(shape, t, ctx=128)
+    if kv == "f16":
+        o.set_variant(oracle.V_KV_F16)
+    ok, ov = o.kv()
+    # an fp16 cache holds each value rounded to nearest-even fp16 (numpy's conversion)
+    cached = kvs.astype(np.float16).astype(np.float32) if kv == "f16" else kvs
+    ok[:, :, :P] = cached[0]
+    ov[:, :, :P] = cached[1]
+    ref, tok = [], first
+    for i in range(steps):
+        tok = o.forward([tok], P + i)
+        ref.append(tok)
+    o.close()
+    for mode in ("graph", "persistent"):
+        assert out["modes"][mode] == {"tokens": ref, "used": mode}, mode
+
+
 # ---------------------------------------------------------------------------- tokenizer and chat
 
 TEXTS = [

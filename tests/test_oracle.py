@@ -451,3 +451,44 @@ def _float64_model(shape, t, ids):
             x[i] = x[i] + Wd @ qz(g / (1 + np.exp(-g)) * u)
     head = synth.dequantize_q4_0(t["output.weight"].data).reshape(shape.vocab, D).astype(np.float64)
     return head @ qz(norm(x[-1], t["output_norm.weight"].data))
+
+
+def test_round_f16_matches_ieee_conversion():
+    """orc_round_f16 (the oracle's half-precision KV cache rounding) against numpy's IEEE 754
+    float32 -> float16 conversion (round to nearest, ties to even): 2^20 bit patterns spread over
+    the whole float32 range, every float16 tie point (the midpoints between neighbouring halves)
+    and their neighbours, the overflow and subnormal boundaries, signed zeros, inf and NaN."""
+    import ctypes
+    f = oracle.lib().orc_round_f16
+    pats = np.arange(0, 1 << 32, 1 << 12, dtype=np.uint64).astype(np.uint32)
+    h = np.arange(0, 0x7c00, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    mids = ((h[:-1].astype(np.float64) + h[1:].astype(np.float64)) / 2).astype(np.float32)
+    extra = np.array([65504.0, 65519.0, 65519.99, 65520.0, 65536.0, 6.1035156e-05, 6.097555e-05, 5.9604645e-08,
+                      2.9802322e-08, 2.9802326e-08, 0.0, -0.0, np.inf, -np.inf], np.float32)
+    vals = np.concatenate([pats.view(np.float32), mids, np.nextafter(mids, np.float32(np.inf)),
+                           np.nextafter(mids, np.float32(-np.inf)), extra, -mids, -extra])
+    vals = vals[np.isfinite(vals) | np.isinf(vals)]
+    got = np.array([f(ctypes.c_float(v)) for v in vals], np.float32)
+    want = vals.astype(np.float16).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.isnan(f(ctypes.c_float(float("nan"))))
+
+
+def test_variant_zero_is_the_reference_arithmetic():
+    """orc_set_variant(0) leaves every result as before; each variant changes the logits of a tiny
+    model (the variants are measuring tools, so they must actually differ from the reference)."""
+    shape = synth.SHAPES["tiny"]
+    t = synth.make_model(shape, 5)
+    ids = synth.prompt_ids(5, 300, shape.vocab)
+    base = oracle.Model(shape, t, ctx=512)
+    n0 = base.forward(ids, 0)
+    l0 = base.logits()
+    for flags in (oracle.V_NORM_TREE, oracle.V_DOT_SPLITK, oracle.V_ATTN_SPLIT, oracle.V_KV_F16):
+        m = oracle.Model(shape, t, ctx=512)
+        m.set_variant(0)
+        assert m.forward(ids, 0) == n0 and np.array_equal(m.logits().view(np.uint32), l0.view(np.uint32))
+        m.set_variant(flags)
+        m.forward(ids, 0)
+        assert not np.array_equal(m.logits().view(np.uint32), l0.view(np.uint32)), flags
+        m.close()
+    base.close()
