@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -2692,6 +2693,83 @@ int q4hip_mv_time_cold(q4hip_mv* m, int64_t rotate_bytes, int iters, float* us, 
   if (e != hipSuccess) return fail(Q4HIP_EHIP, "cold matvec timing: %s", hipGetErrorString(e));
   *us = ms * 1000.0f / iters;
   if (copies_used) *copies_used = copies;
+  return Q4HIP_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- matvec without allocation
+
+// The int8 activation blocks of q4hip_mv_run_noalloc (64 bytes per 32 values, the layout
+// k_quant writes): one copy per device, held until the process ends and shared by every call on
+// that device.  Each call quantizes its whole input into it before the matvec reads it, so
+// nothing in it has to start at zero.
+constexpr int kNoAllocBlocks = Q4HIP_NOALLOC_MAX_K / 32;
+static __device__ __align__(256) uint4 scratch[kNoAllocBlocks * 4];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint4* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of `scratch` on `device` (current), looked up once per device.  In host code the
+// array's name is only a stand-in: kernels get this address.
+int scratch_on(int device, uint4** out) {
+  if (device < 0 || device >= kMaxDevices) return fail(Q4HIP_EINVAL, "device %d beyond %d", device, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[device]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail(Q4HIP_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_dev[device] = (uint4*)p;
+  }
+  *out = g_scratch_dev[device];
+  return Q4HIP_OK;
+}
+
+// `bytes` of device memory of `device` start at p (checked before any launch, so a host pointer or
+// a short buffer is an error, not a memory fault).
+int check_device_span(const void* p, size_t bytes, int device, const char* what) {
+  hipPointerAttribute_t a;
+  if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(Q4HIP_EINVAL, "%s: not device memory", what);
+  }
+  if (a.type != hipMemoryTypeDevice || a.device != device)
+    return fail(Q4HIP_EINVAL, "%s: not device memory of device %d", what, device);
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(Q4HIP_EINVAL, "%s: no device allocation holds it", what);
+  }
+  if ((const char*)p + bytes > (const char*)base + size)
+    return fail(Q4HIP_EINVAL, "%s: %zu bytes needed, the allocation ends %zu bytes after it", what, bytes,
+                (size_t)((const char*)base + size - (const char*)p));
+  return Q4HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q4hip_mv_run_noalloc(q4hip_mv* m, const float* x, float* y, void* stream) {
+  if (!m || !x || !y) return fail(Q4HIP_EINVAL, "null argument");
+  const int K = m->W.K, N = m->W.N;
+  if (K > Q4HIP_NOALLOC_MAX_K)
+    return fail(Q4HIP_EINVAL, "K = %d exceeds the no-allocation limit of %d", K, Q4HIP_NOALLOC_MAX_K);
+  HIPCHK(hipSetDevice(m->device));
+  uint4* xq = nullptr;
+  int rc = scratch_on(m->device, &xq);
+  if (rc == Q4HIP_OK) rc = check_device_span(x, (size_t)K * 4, m->device, "x");
+  if (rc == Q4HIP_OK) rc = check_device_span(y, (size_t)N * 4, m->device, "y");
+  if (rc != Q4HIP_OK) return rc;
+  hipStream_t s = stream ? (hipStream_t)stream : m->stream;
+  launch_quant<QM_PLAIN>(s, 1, x, K, K, nullptr, 0.0f, xq, K / 32, 0);
+  launch_matvec<OP_STORE>(s, m->W, xq, m->W.nb, 1, y, N, nullptr);
+  HIPCHK(hipGetLastError());
+  if (!stream) HIPCHK(hipStreamSynchronize(s));
   return Q4HIP_OK;
 }
 

@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libq4hip.so")
 OK, EINVAL, ECONTEXT, ETYPE, EHIP, ESTATE = 0, 1, 2, 3, 4, 5
 DECODE_AUTO, DECODE_GRAPH, DECODE_PERSISTENT = 0, 1, 2
 KV_F32, KV_F16 = 0, 1
+NOALLOC_MAX_K = 65536          # include/q4hip.h Q4HIP_NOALLOC_MAX_K
 PROF_NAMES = ["embed", "norm+quantize", "matvec qkv", "rope+kv", "attention", "quantize", "matvec o",
               "matvec gate+up", "swiglu+quantize", "matvec down", "matvec output", "sample"]
 
@@ -29,7 +30,7 @@ EXPORTS = [
     "q4hip_mv_destroy", "q4hip_set_decode_mode", "q4hip_decode_mode_used", "q4hip_profile_persistent",
     "q4hip_set_kv", "q4hip_profile_pass", "q4hip_batch_create", "q4hip_batch_destroy",
     "q4hip_batch_prefill", "q4hip_batch_set_kv", "q4hip_batch_generate", "q4hip_batch_time_generate",
-    "q4hip_batch_read_logits", "q4hip_mv_time_cold", "q4hip_check_division",
+    "q4hip_batch_read_logits", "q4hip_mv_time_cold", "q4hip_check_division", "q4hip_mv_run_noalloc",
 ]
 
 _lib = None
@@ -80,6 +81,7 @@ def lib() -> ctypes.CDLL:
         "q4hip_batch_time_generate": (I, [P, P, P, I, P, ctypes.POINTER(F)]),
         "q4hip_batch_read_logits": (I, [P, P, I64]),
         "q4hip_mv_time_cold": (I, [P, I64, I, ctypes.POINTER(F), ctypes.POINTER(I)]),
+        "q4hip_mv_run_noalloc": (I, [P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -310,6 +312,11 @@ class Matvec:
         y = np.empty(self.N, dtype=np.float32)
         _check(lib().q4hip_mv_run(self.h, _ptr(x), _ptr(y)))
         return y
+
+    def run_device(self, x_dev: int, y_dev: int, stream: int = 0) -> None:
+        """y = W x on device buffers (addresses), allocating nothing; waits unless `stream` is given."""
+        _check(lib().q4hip_mv_run_noalloc(self.h, ctypes.c_void_p(x_dev), ctypes.c_void_p(y_dev),
+                                          ctypes.c_void_p(stream or None)))
 
     def time(self, iters: int) -> float:
         us = ctypes.c_float(0)

@@ -209,6 +209,18 @@ int q4hip_mv_time(q4hip_mv* m, int iters, float* us);
 int q4hip_mv_time_cold(q4hip_mv* m, int64_t rotate_bytes, int iters, float* us, int* copies_used);
 void q4hip_mv_destroy(q4hip_mv* m);
 
+/* The matvec of q4hip_mv_run with nothing allocated: no counterpart in the reference.  It is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc).  x (K floats) and y (N floats) are device memory of the
+ * handle's device, checked before anything is launched.  The int8 activation blocks go to a
+ * library-owned static device buffer of Q4HIP_NOALLOC_MAX_K / 32 blocks (128 KB per device, held
+ * until the process ends); K above Q4HIP_NOALLOC_MAX_K is rejected.  `stream` (a hipStream_t)
+ * NULL: the handle's stream, and the call waits for the result; otherwise the work is enqueued
+ * on that stream and the call returns at once.  Every call on one device shares the buffer:
+ * calls that overlap on one GPU (other streams, other threads, other handles) race. */
+#define Q4HIP_NOALLOC_MAX_K 65536
+int q4hip_mv_run_noalloc(q4hip_mv* m, const float* x, float* y, void* stream);
+
 /* ---- self-check of the quotient forms ------------------------------------------------------
  * The kernels compute the reference's IEEE binary32 divisions (engine/kernels.c:84, 98-99, 395)
  * by reciprocal products with fused corrections on verified domains.  This runs every input of
