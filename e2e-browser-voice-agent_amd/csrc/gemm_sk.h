@@ -1,0 +1,258 @@
+// gemm_sk.h -- the Q4_0 projection of a few tokens (batched decode) on the matrix cores.
+//
+// y[m][n] (op)= W[n] . x[m] for up to a few dozen tokens, every output accumulated exactly as
+// matmul_q4 does (engine/kernels.c:200-229): four lane chains acc_j += f32(p_j) * (dw * dx) over
+// the blocks in order, then ((a0 + a1) + a2) + a3.  p_j, the integer dot of reference lane j's 8
+// nibbles (as n - 8) with its 8 int8 activations, is one v_mfma_f32_16x16x16_f16 per 16 rows x 16
+// tokens: k = 0..7 carry x_k * (1024 + n_k) (the nibble becomes fp16 0x6400 | n by a byte
+// permute), k = 8 carries (-sum x) * 1032, k = 9..15 are zero; every product and partial sum is an
+// integer below 2^22, so the fp32 result is exactly p_j.  The chain updates stay on the vector
+// ALUs in block order.
+//
+// Layout of a workgroup (16 tokens, 256 threads):
+//   JS = 4  16 weight rows; wave w runs lane chain w of all 16 rows (for matrices with few rows:
+//           four times the workgroups); the chains are added in the reference's order at the end
+//   JS = 1  64 weight rows; wave w runs rows 16w .. 16w + 15 with all four chains
+// What one group of 4 blocks needs -- the 16 tokens' fp16 operands (8 KB, contiguous in the
+// tiled operand layout), their block scales dx, the weight words and the fp16 weight scales of the
+// workgroup's rows -- streams through an R-slot ring in shared memory by asynchronous
+// global -> LDS loads, R - 1 groups ahead of the group being computed.  Every wave issues the same
+// five load instructions per group, so the wait for the oldest slot is a single vmcnt; one barrier
+// per group.  Loads past the last group or block are clamped to it (valid memory, never used).
+#pragma once
+#include "kernels.h"
+
+namespace q4 {
+
+typedef __attribute__((address_space(3))) void SkLds;
+typedef _Float16 sk_h4 __attribute__((ext_vector_type(4)));
+typedef float sk_f4 __attribute__((ext_vector_type(4)));
+
+// Bytes of one ring slot.
+template <int JS>
+struct SkSlot {
+  static constexpr int ACT = 8192;                 // [block 4][chain 4][quarter 4][token 16][8 B]
+  static constexpr int DX = 256;                   // [block 4][token 16] f32
+  static constexpr int QS = JS == 4 ? 1024 : 4096; // [chain 4][row 16 or 64] uint4
+  static constexpr int SC = JS == 4 ? 128 : 512;   // [row][2 dwords]: the 4 fp16 scales of the group
+  static constexpr int oDX = ACT, oQS = ACT + DX, oSC = ACT + DX + QS, BYTES = ACT + DX + QS + SC;
+};
+
+// Wait until at most n of this wave's load instructions are outstanding, and this wave's LDS
+// accesses are done, then meet the other waves.  (Not __syncthreads: its workgroup fence would wait
+// for every outstanding load into LDS.)
+template <int N>
+__device__ __forceinline__ void sk_sync() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Asynchronous global -> LDS loads (global_load_lds): lane l's 16 (or 4) bytes from `src` land at
+// LDS address lds + 16 l (4 l); `lds` is wave-uniform and goes to M0.  Written as inline assembly so
+// that the compiler does not treat every later shared-memory read as dependent on every load in
+// flight (it would wait for all of them): the ring's own vmcnt waits order the reads.  The s_nop
+// covers the wait state the hardware needs between writing M0 and the load that reads it.
+#ifdef SK_EMULATE_DMA
+__device__ __forceinline__ void sk_dma16(const void* src, const void* lds) {
+  reinterpret_cast<uint4*>(const_cast<void*>(lds))[threadIdx.x & 63] = *reinterpret_cast<const uint4*>(src);
+}
+__device__ __forceinline__ void sk_dma4(const void* src, const void* lds) {
+  reinterpret_cast<uint32_t*>(const_cast<void*>(lds))[threadIdx.x & 63] = *reinterpret_cast<const uint32_t*>(src);
+}
+#else
+__device__ __forceinline__ void sk_dma16(const void* src, const void* lds) {
+  const uint32_t a = (uint32_t)(uintptr_t)(SkLds*)lds;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(a) : "memory");
+}
+__device__ __forceinline__ void sk_dma4(const void* src, const void* lds) {
+  const uint32_t a = (uint32_t)(uintptr_t)(SkLds*)lds;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "{m0}"(a) : "memory");
+}
+#endif
+
+// Per-lane sources of a workgroup's loads, computed once; group g adds g times a stride.
+//   act  this wave's block (4g + wave) of the 16-token tile: 2 KB, two instructions of 1 KB
+//   dx   the same block's 16 block scales (lanes 0..15)
+//   qs   JS 4: row lane (0..15) of the workgroup, chain `wave`; JS 1: row lane (0..63), chain `wave`
+//   sc   the 8 bytes of the group's 4 fp16 scales of one row, as two dwords (JS 4: lanes 0..7 take
+//        rows 4 wave .. 4 wave + 3; JS 1: lanes 0..31 take rows 16 wave .. 16 wave + 15)
+// Blocks past nb and groups past ng are clamped to the last ones.
+template <int JS>
+struct SkSrc {
+  const uint4* act;      // block `wave` of group 0 of the tile
+  const uint4* qs;       // group 0
+  const uint32_t* sc;    // group 0 (dword 0 of the row's 4-scale half of a uint4)
+  int nb, ng, wave, lane;
+  __device__ __forceinline__ SkSrc(const Q4Mat& W, const uint4* xt, int xstride, int T, int R0) {
+    lane = threadIdx.x & 63;
+    wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    nb = W.nb;
+    ng = W.ng;
+    act = xt + (size_t)T * xstride * kXhBlock;
+    const int tile = R0 >> 6, rr0 = R0 & 63;
+    if (JS == 4) {
+      qs = W.qs + ((size_t)tile * ng * 64 + rr0 + (lane & 15)) * 4 + wave;
+      sc = reinterpret_cast<const uint32_t*>(W.d + (size_t)tile * W.nb8 * 64 + rr0 + 4 * wave + ((lane >> 1) & 3)) +
+           (lane & 1);
+    } else {
+      qs = W.qs + ((size_t)tile * ng * 64 + lane) * 4 + wave;
+      sc = reinterpret_cast<const uint32_t*>(W.d + (size_t)tile * W.nb8 * 64 + 16 * wave + ((lane >> 1) & 15)) +
+           (lane & 1);
+    }
+  }
+};
+
+// Issue the loads of group g into ring slot `slot`: five instructions per wave, whatever g.
+template <int JS>
+__device__ __forceinline__ void sk_issue(const unsigned char* slot, const SkSrc<JS>& src, int g) {
+  using S = SkSlot<JS>;
+  const int lane = src.lane, wave = src.wave;
+  g = g < src.ng ? g : src.ng - 1;
+  int b = 4 * g + wave;
+  b = b < src.nb ? b : src.nb - 1;
+  const uint4* a = src.act + (size_t)b * kXhBlock;
+  sk_dma16(a + lane, slot + wave * 2048);
+  sk_dma16(a + 64 + lane, slot + wave * 2048 + 1024);
+  if (lane < 16) sk_dma4(reinterpret_cast<const float*>(a + 128) + lane, slot + S::oDX + wave * 64);
+  const uint32_t* scg = src.sc + (size_t)(g >> 1) * 256 + ((g & 1) << 1);   // 64 rows x 4 dwords per uint4 group
+  if (JS == 4) {
+    if (lane < 16) sk_dma16(src.qs + (size_t)g * 256, slot + S::oQS + wave * 256);
+    if (lane < 8) sk_dma4(scg, slot + S::oSC + wave * 32);
+  } else {
+    sk_dma16(src.qs + (size_t)g * 256, slot + S::oQS + wave * 1024);
+    if (lane < 32) sk_dma4(scg, slot + S::oSC + wave * 128);
+  }
+}
+
+// The B operand of lane quarter kg for one weight word (4 nibble pairs of one block and chain):
+// kg 0 low nibbles, kg 1 high nibbles, each as fp16 1024 + n; kg 2 (1032, 0, 0, 0); kg 3 zero.
+struct SkB {
+  uint32_t sh, mask, orv, sel0, sel1;
+  __device__ __forceinline__ explicit SkB(int kg) {
+    sh = (kg & 1) << 2;
+    mask = kg < 2 ? 0x0F0F0F0Fu : 0u;
+    orv = kg < 2 ? 0u : 0x08080808u;
+    sel0 = kg < 2 ? 0x04010400u : kg == 2 ? 0x0C0C0400u : 0x0C0C0C0Cu;
+    sel1 = kg < 2 ? 0x04030402u : 0x0C0C0C0Cu;
+  }
+  __device__ __forceinline__ sk_h4 operator()(uint32_t wv) const {
+    const uint32_t v = ((wv >> sh) & mask) | orv;
+    return __builtin_bit_cast(sk_h4, make_uint2(__builtin_amdgcn_perm(0x64646464u, v, sel0),
+                                                __builtin_amdgcn_perm(0x64646464u, v, sel1)));
+  }
+};
+
+template <int OP>
+__device__ __forceinline__ void sk_put(float* y, int ldy, const float* bias, int M, int N, int m, int n, float v) {
+  if (m < M && n < N) {
+    float* o = y + (size_t)m * ldy + n;
+    if (OP == 2) *o = *o + v;          // OP_ADD
+    else if (OP == 1) *o = v + bias[n];   // OP_BIAS
+    else *o = v;                        // OP_STORE
+  }
+}
+
+// Grid (Np / (JS == 4 ? 16 : 64), ceil(M / 16)); R * SkSlot<JS>::BYTES of static shared memory.
+// xt: the fp16 operands and block scales in the 16-token tiles of quantize_item (kXhBlock).
+// The ring slots are R distinct shared arrays and the group loop is unrolled by R, so every slot
+// address is a constant.
+template <int OP, int JS, int R>
+__global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restrict__ xt, int xstride, int M,
+                                                float* __restrict__ y, int ldy, const float* __restrict__ bias) {
+  using S = SkSlot<JS>;
+  static_assert(R >= 3 && R <= 8, "ring depth");
+  __shared__ __align__(16) unsigned char q0[S::BYTES], q1[S::BYTES], q2[S::BYTES], q3[S::BYTES], q4[S::BYTES],
+      q5[S::BYTES], q6[S::BYTES], q7[S::BYTES];
+  unsigned char* const ring[8] = {q0, q1, q2, q3, q4, q5, q6, q7};
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, kg = lane >> 4;
+  const int T = blockIdx.y;
+  const int R0 = JS == 4 ? blockIdx.x * 16 : blockIdx.x * 64;
+  const int ng = W.ng, nb = W.nb;
+  const SkB bop(kg);
+  const SkSrc<JS> src(W, xt, xstride, T, R0);
+  constexpr int NJ = JS == 4 ? 1 : 4;
+  const int wrow = JS == 4 ? li : 16 * wave + li;            // this lane's weight row in the workgroup
+  float acc[NJ][4];
+#pragma unroll
+  for (int c = 0; c < NJ; c++) acc[c][0] = acc[c][1] = acc[c][2] = acc[c][3] = 0.0f;
+
+  auto compute = [&](const unsigned char* slot, int g) {
+    const uint4* acts = reinterpret_cast<const uint4*>(slot);
+    const float* dxs = reinterpret_cast<const float*>(slot + S::oDX);
+    const uint4* qss = reinterpret_cast<const uint4*>(slot + S::oQS);
+    const uint2* scs = reinterpret_cast<const uint2*>(slot + S::oSC);
+    const uint2 sc = scs[wrow];
+    uint4 wq[NJ];
+    if (JS == 4) wq[0] = qss[wave * 16 + li];
+    else {
+#pragma unroll
+      for (int c = 0; c < 4; c++) wq[c] = qss[c * 64 + wrow];
+    }
+    auto block = [&](int k) {
+      const uint32_t sw = (k >> 1) == 0 ? sc.x : sc.y;
+      const float dw = half_bits_to_float((k & 1) ? (sw >> 16) : (sw & 0xffffu));
+      const float4 dx = *reinterpret_cast<const float4*>(dxs + k * 16 + 4 * kg);
+      sk_f4 d[NJ];
+#pragma unroll
+      for (int c = 0; c < NJ; c++) {
+        const int j = JS == 4 ? wave : c;
+        const uint32_t wv = k == 0 ? wq[c].x : k == 1 ? wq[c].y : k == 2 ? wq[c].z : wq[c].w;
+        const uint2 aw = reinterpret_cast<const uint2*>(acts)[((k * 4 + j) * 4 + kg) * 16 + li];
+        d[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(sk_h4, aw), bop(wv),
+                                                     (sk_f4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+      }
+      const float s0 = dw * dx.x, s1 = dw * dx.y, s2 = dw * dx.z, s3 = dw * dx.w;
+#pragma unroll
+      for (int c = 0; c < NJ; c++) {
+        acc[c][0] = acc[c][0] + d[c][0] * s0;
+        acc[c][1] = acc[c][1] + d[c][1] * s1;
+        acc[c][2] = acc[c][2] + d[c][2] * s2;
+        acc[c][3] = acc[c][3] + d[c][3] * s3;
+      }
+    };
+    const int nbk = nb - 4 * g;                              // blocks of this group that exist (uniform)
+    if (nbk >= 4) {                                          // straight-line code for whole groups
+#pragma unroll
+      for (int k = 0; k < 4; k++) block(k);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 3; k++)
+        if (k < nbk) block(k);
+    }
+  };
+
+#pragma unroll
+  for (int p = 0; p < R - 1; p++) sk_issue<JS>(ring[p], src, p);
+  for (int g0 = 0; g0 < ng; g0 += R) {
+#pragma unroll
+    for (int u = 0; u < R; u++) {
+      const int g = g0 + u;
+      if (g < ng) {
+        // group g's loads were followed by those of R - 2 groups
+        sk_sync<5 * (R - 2)>();
+        // the slot of group g - 1 is free: every wave has passed the barrier after computing it
+        sk_issue<JS>(ring[(u + R - 1) % R], src, g + R - 1);
+        compute(ring[u], g);
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");          // no load into shared memory outlives the loop
+  // lane (li, kg) holds tokens 16 T + 4 kg + r of weight row R0 + wrow
+  const int m0 = T * 16 + 4 * kg;
+  if (JS == 1) {
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      sk_put<OP>(y, ldy, bias, M, W.N, m0 + r, R0 + 16 * wave + li,
+                 ((acc[0][r] + acc[1][r]) + acc[2][r]) + acc[3][r]);
+  } else {
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(q0);               // [chain][token][row] (S::BYTES >= 4 KB)
+#pragma unroll
+    for (int r = 0; r < 4; r++) red[(wave * 16 + 4 * kg + r) * 16 + li] = acc[0][r];
+    __syncthreads();
+    const float v = ((red[tid] + red[256 + tid]) + red[512 + tid]) + red[768 + tid];
+    sk_put<OP>(y, ldy, bias, M, W.N, T * 16 + (tid >> 4), R0 + (tid & 15), v);
+  }
+}
+
+}  // namespace q4

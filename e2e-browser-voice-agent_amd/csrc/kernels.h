@@ -228,8 +228,22 @@ enum QuantMode { QM_PLAIN = 0, QM_NORM = 1, QM_SWIGLU = 2 };
 // 2j+16, 2j+17, 2j+24, 2j+25 of the block): the block maximum over the quad of lanes j = 0..3 (four
 // consecutive threads of one wave, all active), the scale, the int8 values and their sum, written as
 // out[b*4 + j] and, when given, the matrix-core operand outh[2 (b*4 + j)], outh[2 (b*4 + j) + 1].
+// The fp16 matrix-core operands of a token's activation blocks, tiled by 16 tokens: per (tile,
+// block) 132 uint4 -- [lane chain 4][quarter 4][token 16][8 bytes] (the 16 fp16 values x_0..x_7,
+// -sum x, 0 x 7 of a chain in four 8-byte quarters), then the 16 tokens' block scales dx as fp32 --
+// so a group of blocks of 16 tokens is contiguous memory, and 16 tokens' quarter of one chain are
+// 128 contiguous bytes (one matrix-core operand read by 16 lanes).
+constexpr int kXhBlock = 132;   // uint4 per (tile, block)
+__host__ __device__ inline size_t xh_tile(int m, int xstride) { return (size_t)(m >> 4) * xstride * kXhBlock; }
+__host__ __device__ inline size_t xh_bytes(int tokens, int xstride) {
+  return (size_t)((tokens + 15) >> 4) * xstride * kXhBlock * 16;
+}
+
+// Quantize the 8 values of reference lane j of block b (quantize_row, kernels.c:90-114) into
+// out[4b + j] = {A_j, B_j, -8 sum q, d}; with outh (the token's tile, xh_tile) also the fp16
+// operand of token t = m % 16 and, for j = 0, its block scale.
 __device__ __forceinline__ void quantize_item(const float (&v)[8], int b, int j, uint4* __restrict__ out,
-                                              uint4* __restrict__ outh) {
+                                              uint4* __restrict__ outh, int t = 0) {
   float am = 0.0f;
 #pragma unroll
   for (int k = 0; k < 8; k++) am = __builtin_fmaxf(am, __builtin_fabsf(v[k]));
@@ -243,9 +257,13 @@ __device__ __forceinline__ void quantize_item(const float (&v)[8], int b, int j,
   out[(b << 2) + j] = make_uint4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]),
                                  (uint32_t)(-8 * sum), __float_as_uint(dd));
   if (outh) {
-    outh[2 * ((b << 2) + j)] = make_uint4(pack_f16x2(q[0], q[1]), pack_f16x2(q[2], q[3]), pack_f16x2(q[4], q[5]),
-                                          pack_f16x2(q[6], q[7]));
-    outh[2 * ((b << 2) + j) + 1] = make_uint4(pack_f16x2(-sum, 0), 0u, 0u, 0u);
+    uint4* o = outh + (size_t)b * kXhBlock;
+    uint2* oq = reinterpret_cast<uint2*>(o) + j * 64 + t;       // quarter q of (chain j, token t): oq[16 q]
+    oq[0] = make_uint2(pack_f16x2(q[0], q[1]), pack_f16x2(q[2], q[3]));
+    oq[16] = make_uint2(pack_f16x2(q[4], q[5]), pack_f16x2(q[6], q[7]));
+    oq[32] = make_uint2(pack_f16x2(-sum, 0), 0u);
+    oq[48] = make_uint2(0u, 0u);
+    if (j == 0) reinterpret_cast<float*>(o + 128)[t] = dd;
   }
 }
 
@@ -253,7 +271,7 @@ template <int MODE>
 __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, const float* xl, int st, int n,
                                                  const float* __restrict__ w, float rs,
                                                  uint4* __restrict__ out, int tid, int nthreads,
-                                                 uint4* __restrict__ outh = nullptr) {
+                                                 uint4* __restrict__ outh = nullptr, int tok = 0) {
   const int nb = n >> 5;
   for (int t = tid; t < (nb << 2); t += nthreads) {
     const int b = t >> 2, j = t & 3;
@@ -293,7 +311,7 @@ __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, c
         }
       }
     }
-    quantize_item(v, b, j, out, outh);
+    quantize_item(v, b, j, out, outh, tok);
   }
 }
 

@@ -16,6 +16,7 @@
 #include <string>
 #include <vector>
 
+#include "gemm_sk.h"
 #include "kernels.h"
 #include "persistent.h"
 #include "q4hip.h"
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(256) void k_quant(const float* __restrict__ in, int
     rs = rms_scale_staged(xl, n, st, eps, red);
   }
   quantize_row_dev<MODE>(xr, xl, st, n, w, rs, xq + (size_t)blockIdx.x * xstride * 4, threadIdx.x, blockDim.x,
-                         xh ? xh + (size_t)blockIdx.x * xstride * 8 : nullptr);
+                         xh ? xh + xh_tile(blockIdx.x, xstride) : nullptr, blockIdx.x & 15);
 }
 
 enum { OP_STORE = 0, OP_BIAS = 1, OP_ADD = 2 };   // put() of kernels.c:190-194
@@ -729,8 +730,14 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(Q4Mat W, const uint4* __restr
 #pragma unroll
     for (int u = 0; u < NX; u++) {
       const int i = tid + 256 * u, t = i >> 5, k = i & 31, m = T0 + t, blk = g * 4 + (k >> 3);
-      v[u] = (m < M && blk < nb) ? xh[((size_t)m * xstride * 4 + blk * 4 + ((k >> 1) & 3)) * 2 + (k & 1)]
-                                 : make_uint4(0, 0, 0, 0);
+      if (m < M && blk < nb) {
+        const uint2* q = reinterpret_cast<const uint2*>(xh + xh_tile(m, xstride) + (size_t)blk * kXhBlock) +
+                         (((k >> 1) & 3) * 4 + 2 * (k & 1)) * 16 + (m & 15);
+        const uint2 lo = q[0], hi = q[16];
+        v[u] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      } else {
+        v[u] = make_uint4(0, 0, 0, 0);
+      }
     }
     const int t = tid >> 2, kb = tid & 3, m = T0 + t, blk = g * 4 + kb;
     d = (tid < 4 * TOK && m < M && blk < nb) ? __uint_as_float(xq[(size_t)m * xstride * 4 + blk * 4].w) : 0.0f;
@@ -1247,7 +1254,7 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
       const float v[8] = {vs[base], vs[base + 1], vs[base + 8], vs[base + 9],
                           vs[base + 16], vs[base + 17], vs[base + 24], vs[base + 25]};
       const int blk = ((g * G + hh) * HD + c0) >> 5;
-      quantize_item(v, blk, j, xq + (size_t)b * xstride * 4, xh ? xh + (size_t)b * xstride * 8 : nullptr);
+      quantize_item(v, blk, j, xq + (size_t)b * xstride * 4, xh ? xh + xh_tile(b, xstride) : nullptr, b & 15);
     }
   }
 }
@@ -1489,11 +1496,28 @@ int check_ready(q4hip* h) {
 //   M > 64: k_gemm_mfma, 32 tokens per wave when K > 2048 (down), else 16
 //   M <= 64, fewer rows: k_gemm_rows with 2 tokens per wave (1 below 16 tokens)
 // Q4HIP_GEMM=valu keeps the matrix cores out (k_gemm_rows up to 64 tokens, else k_gemm_q4).
-enum { GK_ROWS2, GK_ROWS1, GK_MFMA_T2J1, GK_MFMA_T1J1, GK_TILED };
+//   M <= 64 with fp16 operands: k_gemm_sk (ring-fed matrix cores), one chain per wave (JS 4) when
+//   the matrix has too few rows to give 512 workgroups of 64 rows
+// Q4HIP_GEMM=mfma keeps k_gemm_sk out (the earlier choice; same bits, for comparison).
+enum { GK_ROWS2, GK_ROWS1, GK_MFMA_T2J1, GK_MFMA_T1J1, GK_TILED, GK_SK4, GK_SK1 };
+
+constexpr int kSkR4 = 4, kSkR1 = 4;    // ring slots of k_gemm_sk (JS 4: 38.4 KB, JS 1: 52.2 KB)
+
+// Q4HIP_SK_RING=6 or 8 (JS 4), 6 (JS 1): a deeper k_gemm_sk ring (same results; for measurements).
+int sk_ring() {
+  static const int r = [] { const char* e = getenv("Q4HIP_SK_RING"); return e ? atoi(e) : 0; }();
+  return r;
+}
 
 int pick_gemm(const Mat& W, int M, bool have_xh) {
   static const bool no_mfma = [] { const char* e = getenv("Q4HIP_GEMM"); return e && strcmp(e, "valu") == 0; }();
+  static const bool no_sk = [] { const char* e = getenv("Q4HIP_GEMM"); return e && strcmp(e, "mfma") == 0; }();
   if (have_xh && !no_mfma) {
+    static const int force_js = [] { const char* e = getenv("Q4HIP_SK_JS"); return e ? atoi(e) : 0; }();
+    if (M <= 64 && !no_sk) {
+      if (force_js == 1 || force_js == 4) return force_js == 1 ? GK_SK1 : GK_SK4;
+      return (W.Np / 64) * ((M + 15) / 16) >= 512 ? GK_SK1 : GK_SK4;
+    }
     if (W.Np >= 16384) return GK_MFMA_T1J1;
     if (M > 64) return W.nb > 64 ? GK_MFMA_T2J1 : GK_MFMA_T1J1;
   }
@@ -1506,6 +1530,12 @@ void launch_mfma(hipStream_t s, const Mat& W, const uint4* xq, const uint4* xh, 
                  const float* bias) {
   k_gemm_mfma<OP, TT, JS><<<dim3((unsigned)(W.Np / (JS == 1 ? 64 : 16)), (unsigned)((M + 16 * TT - 1) / (16 * TT))), 256, 0, s>>>(
       W.view(), xq, xh, xstride, M, y, ldy, bias);
+}
+
+template <int OP, int JS, int R>
+void launch_sk(hipStream_t s, const Mat& W, const uint4* xh, int xstride, int M, float* y, int ldy, const float* bias) {
+  k_gemm_sk<OP, JS, R><<<dim3((unsigned)(W.Np / (JS == 4 ? 16 : 64)), (unsigned)((M + 15) / 16)), 256, 0, s>>>(
+      W.view(), xh, xstride, M, y, ldy, bias);
 }
 
 template <int OP, int TPW>
@@ -1531,6 +1561,15 @@ void launch_matvec(hipStream_t s, const Mat& W, const uint4* xq, int xstride, in
     case GK_ROWS1: launch_rows<OP, 1>(s, W, xq, xstride, M, y, ldy, bias); break;
     case GK_MFMA_T2J1: launch_mfma<OP, 2, 1>(s, W, xq, xh, xstride, M, y, ldy, bias); break;
     case GK_MFMA_T1J1: launch_mfma<OP, 1, 1>(s, W, xq, xh, xstride, M, y, ldy, bias); break;
+    case GK_SK4:
+      if (sk_ring() == 8) launch_sk<OP, 4, 8>(s, W, xh, xstride, M, y, ldy, bias);
+      else if (sk_ring() == 6) launch_sk<OP, 4, 6>(s, W, xh, xstride, M, y, ldy, bias);
+      else launch_sk<OP, 4, kSkR4>(s, W, xh, xstride, M, y, ldy, bias);
+      break;
+    case GK_SK1:
+      if (sk_ring() == 6) launch_sk<OP, 1, 6>(s, W, xh, xstride, M, y, ldy, bias);
+      else launch_sk<OP, 1, kSkR1>(s, W, xh, xstride, M, y, ldy, bias);
+      break;
     default:
       k_gemm_q4<OP><<<dim3((unsigned)(W.Np / kGemmRows), (unsigned)((M + kGemmTokens - 1) / kGemmTokens)), 256, 0, s>>>(
           W.view(), xq, xstride, M, y, ldy, bias);
@@ -2010,7 +2049,8 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
   TRYHIP(hipMemsetAsync(h->kc, 0, kvbytes, h->stream));
   TRYHIP(hipMemsetAsync(h->vc, 0, kvbytes, h->stream));
   TRYHIP(hipMalloc(&h->xq, (size_t)M * h->xstride * 64));
-  TRYHIP(hipMalloc(&h->xh, (size_t)M * h->xstride * 128));
+  TRYHIP(hipMalloc(&h->xh, xh_bytes(M, h->xstride)));
+  TRYHIP(hipMemsetAsync(h->xh, 0, xh_bytes(M, h->xstride), h->stream));
   TRYHIP(hipMalloc(&h->tpos, (size_t)M * sizeof(int)));
   h->am_parts = (vocab + 4095) / 4096;
   TRYHIP(hipMalloc(&h->am_v, (size_t)h->am_parts * 4));
