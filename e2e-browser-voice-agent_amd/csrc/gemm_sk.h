@@ -83,7 +83,12 @@ struct SkSrc {
   const uint4* qs;       // group 0
   const uint32_t* sc;    // group 0 (dword 0 of the row's 4-scale half of a uint4)
   int nb, ng, wave, lane;
-  __device__ __forceinline__ SkSrc(const Q4Mat& W, const uint4* xt, int xstride, int T, int R0) {
+  // JS 1 local row l (0..63) of the workgroup -> matrix row: R0 + l, or with ffn > 0 (the fused
+  // gate|up matrix, R0 = 32 b) gate rows 32 b + l for l < 32 and up rows ffn + 32 b + l - 32.
+  static __device__ __forceinline__ int row_of(int R0, int ffn, int l) {
+    return ffn > 0 ? (l < 32 ? R0 + l : ffn + R0 + l - 32) : R0 + l;
+  }
+  __device__ __forceinline__ SkSrc(const Q4Mat& W, const uint4* xt, int xstride, int T, int R0, int ffn = 0) {
     lane = threadIdx.x & 63;
     wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     nb = W.nb;
@@ -95,9 +100,9 @@ struct SkSrc {
       sc = reinterpret_cast<const uint32_t*>(W.d + (size_t)tile * W.nb8 * 64 + rr0 + 4 * wave + ((lane >> 1) & 3)) +
            (lane & 1);
     } else {
-      qs = W.qs + ((size_t)tile * ng * 64 + lane) * 4 + wave;
-      sc = reinterpret_cast<const uint32_t*>(W.d + (size_t)tile * W.nb8 * 64 + 16 * wave + ((lane >> 1) & 15)) +
-           (lane & 1);
+      const int rq = row_of(R0, ffn, lane), rs = row_of(R0, ffn, 16 * wave + ((lane >> 1) & 15));
+      qs = W.qs + ((size_t)(rq >> 6) * ng * 64 + (rq & 63)) * 4 + wave;
+      sc = reinterpret_cast<const uint32_t*>(W.d + (size_t)(rs >> 6) * W.nb8 * 64 + (rs & 63)) + (lane & 1);
     }
   }
 };
@@ -156,9 +161,16 @@ __device__ __forceinline__ void sk_put(float* y, int ldy, const float* bias, int
 // xt: the fp16 operands and block scales in the 16-token tiles of quantize_item (kXhBlock).
 // The ring slots are R distinct shared arrays and the group loop is unrolled by R, so every slot
 // address is a constant.
-template <int OP, int JS, int R>
+// EPI = 1 (with JS 1): W is the fused gate|up matrix of ffn rows each, blockIdx.x = block b of the
+// SwiGLU activation; the workgroup's waves 0, 1 take gate rows 32 b .. 32 b + 31 and waves 2, 3 the
+// matching up rows, and the epilogue writes act = SwiGLU(gate, up) quantized (block b of xq_out
+// and xh_out, what k_quant<QM_SWIGLU> writes) instead of y.
+template <int OP, int JS, int R, int EPI = 0>
 __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restrict__ xt, int xstride, int M,
-                                                float* __restrict__ y, int ldy, const float* __restrict__ bias) {
+                                                float* __restrict__ y, int ldy, const float* __restrict__ bias,
+                                                uint4* __restrict__ xq_out = nullptr, uint4* __restrict__ xh_out = nullptr,
+                                                int ffn = 0) {
+  static_assert(EPI == 0 || JS == 1, "the SwiGLU epilogue needs the 64-row layout");
   using S = SkSlot<JS>;
   static_assert(R >= 3 && R <= 8, "ring depth");
   __shared__ __align__(16) unsigned char q0[S::BYTES], q1[S::BYTES], q2[S::BYTES], q3[S::BYTES], q4[S::BYTES],
@@ -166,19 +178,22 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
   unsigned char* const ring[8] = {q0, q1, q2, q3, q4, q5, q6, q7};
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, kg = lane >> 4;
   const int T = blockIdx.y;
-  const int R0 = JS == 4 ? blockIdx.x * 16 : blockIdx.x * 64;
+  const int R0 = EPI == 1 ? blockIdx.x * 32 : JS == 4 ? blockIdx.x * 16 : blockIdx.x * 64;
   const int ng = W.ng, nb = W.nb;
   const SkB bop(kg);
-  const SkSrc<JS> src(W, xt, xstride, T, R0);
+  const SkSrc<JS> src(W, xt, xstride, T, R0, EPI == 1 ? ffn : 0);
   constexpr int NJ = JS == 4 ? 1 : 4;
   const int wrow = JS == 4 ? li : 16 * wave + li;            // this lane's weight row in the workgroup
   float acc[NJ][4];
 #pragma unroll
   for (int c = 0; c < NJ; c++) acc[c][0] = acc[c][1] = acc[c][2] = acc[c][3] = 0.0f;
 
+  // One group: every shared-memory read of the group first, then its 4 NJ matrix-core products,
+  // then the chain updates in block order (a wave pays the read and product latencies once per
+  // group, not once per block).
   auto compute = [&](const unsigned char* slot, int g) {
-    const uint4* acts = reinterpret_cast<const uint4*>(slot);
-    const float* dxs = reinterpret_cast<const float*>(slot + S::oDX);
+    const uint2* acts = reinterpret_cast<const uint2*>(slot);
+    const float4* dxs = reinterpret_cast<const float4*>(slot + S::oDX);
     const uint4* qss = reinterpret_cast<const uint4*>(slot + S::oQS);
     const uint2* scs = reinterpret_cast<const uint2*>(slot + S::oSC);
     const uint2 sc = scs[wrow];
@@ -188,20 +203,18 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
 #pragma unroll
       for (int c = 0; c < 4; c++) wq[c] = qss[c * 64 + wrow];
     }
-    auto block = [&](int k) {
+    uint2 aw[4][NJ];
+    float4 dx[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      dx[k] = dxs[k * 4 + kg];
+#pragma unroll
+      for (int c = 0; c < NJ; c++) aw[k][c] = acts[((k * 4 + (JS == 4 ? wave : c)) * 4 + kg) * 16 + li];
+    }
+    auto update = [&](int k, const sk_f4 (&d)[NJ]) {
       const uint32_t sw = (k >> 1) == 0 ? sc.x : sc.y;
       const float dw = half_bits_to_float((k & 1) ? (sw >> 16) : (sw & 0xffffu));
-      const float4 dx = *reinterpret_cast<const float4*>(dxs + k * 16 + 4 * kg);
-      sk_f4 d[NJ];
-#pragma unroll
-      for (int c = 0; c < NJ; c++) {
-        const int j = JS == 4 ? wave : c;
-        const uint32_t wv = k == 0 ? wq[c].x : k == 1 ? wq[c].y : k == 2 ? wq[c].z : wq[c].w;
-        const uint2 aw = reinterpret_cast<const uint2*>(acts)[((k * 4 + j) * 4 + kg) * 16 + li];
-        d[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(sk_h4, aw), bop(wv),
-                                                     (sk_f4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-      }
-      const float s0 = dw * dx.x, s1 = dw * dx.y, s2 = dw * dx.z, s3 = dw * dx.w;
+      const float s0 = dw * dx[k].x, s1 = dw * dx[k].y, s2 = dw * dx[k].z, s3 = dw * dx[k].w;
 #pragma unroll
       for (int c = 0; c < NJ; c++) {
         acc[c][0] = acc[c][0] + d[c][0] * s0;
@@ -210,14 +223,29 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
         acc[c][3] = acc[c][3] + d[c][3] * s3;
       }
     };
+    auto product = [&](int k, sk_f4 (&d)[NJ]) {
+#pragma unroll
+      for (int c = 0; c < NJ; c++) {
+        const uint32_t wv = k == 0 ? wq[c].x : k == 1 ? wq[c].y : k == 2 ? wq[c].z : wq[c].w;
+        d[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(sk_h4, aw[k][c]), bop(wv),
+                                                     (sk_f4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+      }
+    };
     const int nbk = nb - 4 * g;                              // blocks of this group that exist (uniform)
     if (nbk >= 4) {                                          // straight-line code for whole groups
+      sk_f4 d[4][NJ];
 #pragma unroll
-      for (int k = 0; k < 4; k++) block(k);
+      for (int k = 0; k < 4; k++) product(k, d[k]);
+#pragma unroll
+      for (int k = 0; k < 4; k++) update(k, d[k]);
     } else {
 #pragma unroll
       for (int k = 0; k < 3; k++)
-        if (k < nbk) block(k);
+        if (k < nbk) {
+          sk_f4 d[NJ];
+          product(k, d);
+          update(k, d);
+        }
     }
   };
 
@@ -239,7 +267,26 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");          // no load into shared memory outlives the loop
   // lane (li, kg) holds tokens 16 T + 4 kg + r of weight row R0 + wrow
   const int m0 = T * 16 + 4 * kg;
-  if (JS == 1) {
+  if (EPI == 1) {
+    __syncthreads();
+    float* gus = reinterpret_cast<float*>(q0);               // [token 16][local row 64]: gate 0..31, up 32..63
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      gus[(4 * kg + r) * 64 + 16 * wave + li] = ((acc[0][r] + acc[1][r]) + acc[2][r]) + acc[3][r];
+    __syncthreads();
+    if (tid < 64) {                                          // wave 0: lane (token t, reference lane j)
+      const int t = tid >> 2, j = tid & 3, m = T * 16 + t;
+      const int e[8] = {2 * j, 2 * j + 1, 8 + 2 * j, 9 + 2 * j, 16 + 2 * j, 17 + 2 * j, 24 + 2 * j, 25 + 2 * j};
+      float g[8], u[8], v[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        g[k] = gus[t * 64 + e[k]];
+        u[k] = gus[t * 64 + 32 + e[k]];
+      }
+      swiglu8(g, u, v);
+      if (m < M) quantize_item(v, blockIdx.x, j, xq_out + (size_t)m * xstride * 4, xh_out + xh_tile(m, xstride), m & 15);
+    }
+  } else if (JS == 1) {
 #pragma unroll
     for (int r = 0; r < 4; r++)
       sk_put<OP>(y, ldy, bias, M, W.N, m0 + r, R0 + 16 * wave + li,

@@ -215,6 +215,27 @@ __device__ __forceinline__ float lane_staged(const float* xl, int st, int i) {
 
 enum QuantMode { QM_PLAIN = 0, QM_NORM = 1, QM_SWIGLU = 2 };
 
+// v = (g / (1 + fast_exp(-g))) * u for 8 values (kernels.c:395).  All 16 inputs are in hand before
+// any test, and one wave-uniform test covers the 8 quotients (the exact fallback division only
+// where a quotient leaves the domain of the fast form).
+__device__ __forceinline__ void swiglu8(const float (&g)[8], const float (&u)[8], float (&v)[8]) {
+  float y[8];
+  bool fast = true;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    y[k] = 1.0f + fast_exp(-g[k]);
+    v[k] = silu_quot(g[k], y[k]);
+    fast = fast && silu_fast_ok(g[k], y[k]);
+  }
+  if (__builtin_amdgcn_ballot_w64(!fast) != 0) {
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      if (!silu_fast_ok(g[k], y[k])) v[k] = g[k] / y[k];
+  }
+#pragma unroll
+  for (int k = 0; k < 8; k++) v[k] = v[k] * u[k];
+}
+
 // Quantize one token row of n values into n/32 activation blocks (quantize_row, kernels.c:90-114),
 // with the value transform of the caller fused in: plain, RMSNorm (x*r)*w (kernels.c:85), or
 // SwiGLU g/(1+e^-g)*u (kernels.c:395).  Work item t = (block b, lane j); the four lanes of a
@@ -279,27 +300,13 @@ __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, c
     const int e[8] = {base, base + 1, base + 8, base + 9, base + 16, base + 17, base + 24, base + 25};
     float v[8];
     if (MODE == QM_SWIGLU) {
-      // all 16 inputs are read before any test, and one wave-uniform test covers the 8 quotients
-      float g[8], u[8], y[8];
+      float g[8], u[8];
 #pragma unroll
       for (int k = 0; k < 8; k++) {
         g[k] = xr[e[k]];
         u[k] = xr[n + e[k]];
       }
-      bool fast = true;
-#pragma unroll
-      for (int k = 0; k < 8; k++) {
-        y[k] = 1.0f + fast_exp(-g[k]);
-        v[k] = silu_quot(g[k], y[k]);
-        fast = fast && silu_fast_ok(g[k], y[k]);
-      }
-      if (__builtin_amdgcn_ballot_w64(!fast) != 0) {
-#pragma unroll
-        for (int k = 0; k < 8; k++)
-          if (!silu_fast_ok(g[k], y[k])) v[k] = g[k] / y[k];
-      }
-#pragma unroll
-      for (int k = 0; k < 8; k++) v[k] = v[k] * u[k];
+      swiglu8(g, u, v);
     } else {
 #pragma unroll
       for (int k = 0; k < 8; k++) {

@@ -1428,6 +1428,8 @@ struct q4hip {
   int kvb = 4;                         // bytes per cache element
   uint4* xq = nullptr;
   uint4* xh = nullptr;     // the same activations as fp16 matrix-core operands (multi-token passes)
+  uint4* xh2 = nullptr;    // the SwiGLU activation's operands when written by the gate|up projection
+                           // itself (that kernel still reads xh)
   int xstride = 0;   // activation blocks per token row of xq
   float* ascr = nullptr;   // attention scores of multi-token passes: [MT][H][score_stride(ctx)], allocated on first use
   int* tpos = nullptr;     // positions of the tokens of a pass
@@ -1509,9 +1511,20 @@ int sk_ring() {
   return r;
 }
 
+bool gemm_env(const char* v) {
+  const char* e = getenv("Q4HIP_GEMM");
+  return e && strcmp(e, v) == 0;
+}
+
+// Whether few-token projections may use k_gemm_sk (not under Q4HIP_GEMM=valu or =mfma).
+bool sk_enabled() {
+  static const bool on = !gemm_env("valu") && !gemm_env("mfma");
+  return on;
+}
+
 int pick_gemm(const Mat& W, int M, bool have_xh) {
-  static const bool no_mfma = [] { const char* e = getenv("Q4HIP_GEMM"); return e && strcmp(e, "valu") == 0; }();
-  static const bool no_sk = [] { const char* e = getenv("Q4HIP_GEMM"); return e && strcmp(e, "mfma") == 0; }();
+  static const bool no_mfma = gemm_env("valu");
+  static const bool no_sk = !sk_enabled();
   if (have_xh && !no_mfma) {
     static const int force_js = [] { const char* e = getenv("Q4HIP_SK_JS"); return e ? atoi(e) : 0; }();
     if (M <= 64 && !no_sk) {
@@ -1536,6 +1549,18 @@ template <int OP, int JS, int R>
 void launch_sk(hipStream_t s, const Mat& W, const uint4* xh, int xstride, int M, float* y, int ldy, const float* bias) {
   k_gemm_sk<OP, JS, R><<<dim3((unsigned)(W.Np / (JS == 4 ? 16 : 64)), (unsigned)((M + 15) / 16)), 256, 0, s>>>(
       W.view(), xh, xstride, M, y, ldy, bias);
+}
+
+// gate|up projection with the SwiGLU + quantize of its output fused (k_gemm_sk, EPI 1): act of the M
+// tokens into xq and xh_out, exactly what the projection followed by k_quant<QM_SWIGLU> writes.
+// xh_out must not be xh_in (other workgroups still read their input blocks).  False (nothing
+// launched) where that path does not apply; the caller then runs the two launches.
+bool launch_gu_swiglu(hipStream_t s, const Mat& W, const uint4* xh_in, int xstride, int M, uint4* xq_out,
+                      uint4* xh_out, int F) {
+  if (!xh_in || M > 64 || F % 32 || !sk_enabled()) return false;
+  k_gemm_sk<OP_STORE, 1, kSkR1, 1><<<dim3((unsigned)(F / 32), (unsigned)((M + 15) / 16)), 256, 0, s>>>(
+      W.view(), xh_in, xstride, M, nullptr, 0, nullptr, xq_out, xh_out, F);
+  return true;
 }
 
 template <int OP, int TPW>
@@ -1712,11 +1737,16 @@ void enqueue_pass(q4hip* h, int M, bool want_logits) {
     prof_mark(h, Q4HIP_PROF_NORM_Q);
     launch_quant<QM_NORM>(s, M, h->x, D, D, y.ffn_norm, h->eps, h->xq, h->xstride, 0, xh);
     prof_mark(h, Q4HIP_PROF_GU);
-    launch_matvec<OP_STORE>(s, y.gu, h->xq, h->xstride, M, h->gu, 2 * F, nullptr, xh);
-    prof_mark(h, Q4HIP_PROF_SWIGLU);
-    launch_quant<QM_SWIGLU>(s, M, h->gu, 2 * F, F, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
+    uint4* xh_act = xh;      // where the down projection finds the activation's fp16 operands
+    if (launch_gu_swiglu(s, y.gu, xh, h->xstride, M, h->xq, h->xh2, F)) {
+      xh_act = h->xh2;
+    } else {
+      launch_matvec<OP_STORE>(s, y.gu, h->xq, h->xstride, M, h->gu, 2 * F, nullptr, xh);
+      prof_mark(h, Q4HIP_PROF_SWIGLU);
+      launch_quant<QM_SWIGLU>(s, M, h->gu, 2 * F, F, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
+    }
     prof_mark(h, Q4HIP_PROF_DOWN);
-    launch_matvec<OP_ADD>(s, y.down, h->xq, h->xstride, M, h->x, D, nullptr, xh);
+    launch_matvec<OP_ADD>(s, y.down, h->xq, h->xstride, M, h->x, D, nullptr, xh_act);
   }
   if (want_logits) {
     prof_mark(h, Q4HIP_PROF_NORM_Q);
@@ -1984,7 +2014,7 @@ void q4hip_destroy(q4hip* h) {
   }
   mat_free(h->head);
   void* bufs[] = {h->embd, h->out_norm, h->rope, h->x, h->qkv, h->att, h->gu, h->logits, h->kc, h->vc,
-                  h->xq, h->am_v, h->am_i, h->tokens, h->st, h->d_layers, h->ll, h->ascr, h->xh, h->tpos,
+                  h->xq, h->am_v, h->am_i, h->tokens, h->st, h->d_layers, h->ll, h->ascr, h->xh, h->xh2, h->tpos,
                   h->lsc};
   for (void* p : bufs) if (p) (void)hipFree(p);
   if (h->pin_ids) (void)hipHostFree(h->pin_ids);
@@ -2051,6 +2081,8 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
   TRYHIP(hipMalloc(&h->xq, (size_t)M * h->xstride * 64));
   TRYHIP(hipMalloc(&h->xh, xh_bytes(M, h->xstride)));
   TRYHIP(hipMemsetAsync(h->xh, 0, xh_bytes(M, h->xstride), h->stream));
+  TRYHIP(hipMalloc(&h->xh2, xh_bytes(M, h->xstride)));
+  TRYHIP(hipMemsetAsync(h->xh2, 0, xh_bytes(M, h->xstride), h->stream));
   TRYHIP(hipMalloc(&h->tpos, (size_t)M * sizeof(int)));
   h->am_parts = (vocab + 4095) / 4096;
   TRYHIP(hipMalloc(&h->am_v, (size_t)h->am_parts * 4));
@@ -2433,9 +2465,14 @@ void enqueue_batch_step(q4hip_batch* bt, int* out) {
                      bt->seq_stride, h->xq, h->xstride, xh);
     launch_matvec<OP_ADD>(s, y.o, h->xq, h->xstride, B, h->x, D, nullptr, xh);
     launch_quant<QM_NORM>(s, B, h->x, D, D, y.ffn_norm, h->eps, h->xq, h->xstride, 0, xh);
-    launch_matvec<OP_STORE>(s, y.gu, h->xq, h->xstride, B, h->gu, 2 * F, nullptr, xh);
-    launch_quant<QM_SWIGLU>(s, B, h->gu, 2 * F, F, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
-    launch_matvec<OP_ADD>(s, y.down, h->xq, h->xstride, B, h->x, D, nullptr, xh);
+    uint4* xh_act = xh;
+    if (launch_gu_swiglu(s, y.gu, xh, h->xstride, B, h->xq, h->xh2, F)) {
+      xh_act = h->xh2;
+    } else {
+      launch_matvec<OP_STORE>(s, y.gu, h->xq, h->xstride, B, h->gu, 2 * F, nullptr, xh);
+      launch_quant<QM_SWIGLU>(s, B, h->gu, 2 * F, F, nullptr, 0.0f, h->xq, h->xstride, 0, xh);
+    }
+    launch_matvec<OP_ADD>(s, y.down, h->xq, h->xstride, B, h->x, D, nullptr, xh_act);
   }
   launch_quant<QM_NORM>(s, B, h->x, D, D, h->out_norm, h->eps, h->xq, h->xstride, 0, xh);
   if (h->head.fmt == Q4HIP_TYPE_Q8_0) {

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 
 import numpy as np
 
@@ -129,6 +130,8 @@ class Model:
 
     def close(self) -> None:
         if self.h:
+            for bt in list(getattr(self, "_batches", ())):   # batches go before their context
+                bt.close()
             lib().q4hip_destroy(self.h)
             self.h = None
 
@@ -244,6 +247,9 @@ class Batch:
         h = ctypes.c_void_p()
         _check(lib().q4hip_batch_create(ctypes.byref(h), model.h, B))
         self.h = h
+        if not hasattr(model, "_batches"):
+            model._batches = weakref.WeakSet()
+        model._batches.add(self)
 
     def prefill(self, seq: int, ids, pos: int) -> int:
         """Prompt of sequence `seq` at positions pos..; returns its greedy next token."""
