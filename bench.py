@@ -18,7 +18,8 @@ timed on the host cores as the CPU baseline.
 Other workloads of the same model (one JSON line each, same keys):
   --workload long-context  batch-1 decode after a 4096-position cache filled with seeded fp16-valued
                            K/V (written through q4hip_set_kv), 256 greedy steps by default
-                           (--kv-cache f16: the cache stored as fp16, half the K/V bytes)
+                           (the cache stored as fp16, as the configuration names; --kv-cache f32: the
+                           reference's fp32 cache)
   --workload prefill       one 1024-token seeded prompt per step
   --workload matvec        the isolated Q4_0 matvec at the model's five shapes, 1000 launches each
   --workload batched       32 independent sequences on the Qwen2.5-1.5B shape, each after a
@@ -132,10 +133,10 @@ def main():
     ap.add_argument("--workload", default="decode", choices=["decode", "long-context", "prefill", "matvec", "batched"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-node", action="store_true", help="skip the Node.js host leg of the decode workload")
-    ap.add_argument("--kv-cache", default="f32", choices=["f32", "f16"],
-                    help="K/V cache storage of the long-context and batched workloads: f32 (the "
-                         "reference's cache type, bit-exact) or f16 (half the K/V bytes; parity against "
-                         "the oracle with the same fp16 rounding)")
+    ap.add_argument("--kv-cache", default="f16", choices=["f32", "f16"],
+                    help="K/V cache storage of the long-context and batched workloads: f16 (what those "
+                         "configurations name; half the K/V bytes; parity against the oracle with the "
+                         "same fp16 rounding, default) or f32 (the reference's cache type)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the batch-1 decode loop runs on a single device "
