@@ -682,185 +682,6 @@ __global__ __launch_bounds__(256) void k_gemm_rows(Q4Mat W, const uint4* __restr
   }
 }
 
-// Q4_0 GEMM on the matrix cores, exact: y[m][n] (+)= W[n] . x[m] with the same lane chains as
-// matmul_q4 (kernels.c:200-229).  For lane chain j of block b, the integer dot p of its 8 nibbles
-// n_k (as n_k - 8) with the 8 int8 activations x_k is one v_mfma_f32_16x16x16_f16:
-//   k = 0..7: x_k * (1024 + n_k)      (the nibble as fp16 0x6400 | n, made by a byte permute)
-//   k = 8:    (-sum_k x_k) * 1032     (takes the -8 offset and the 1024 back out)
-//   k = 9..15: 0
-// Every product and partial sum is an integer of magnitude below 2^22, so the fp32 result is
-// exactly p whatever the order of the sums inside the instruction.  The chain update
-// acc_j += p * (dw * dx) then runs on the vector ALUs in block order, as in the other kernels.
-// Operands: A = 16 tokens (32 bytes per token, block and chain, written by the quantizer), B = 16
-// weight rows; D[token][row], lane = row + 16 * (token / 4).
-// A wave takes 16 rows x 16 TT tokens and NJ = 4 / JS chains: JS = 1, all four chains, the four
-// waves of a workgroup on consecutive rows; JS = 4, one chain per wave, the four waves on the same
-// rows (for matrices with few rows), summed through shared memory at the end.  Within a group of
-// 4 blocks the (block, chain) steps are software pipelined: the products of step s + 1 are issued
-// before the chain updates of step s.  Activations and scales of a group are staged in shared
-// memory, loaded two groups ahead; weights run 4 groups ahead in registers.
-// Grid (Np / (JS == 1 ? 64 : 16), ceil(M / (16 TT))).
-typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
-typedef float f4_t __attribute__((ext_vector_type(4)));
-constexpr int kMfmaPD = 2;       // weight groups in flight
-
-template <int OP, int TT, int JS>
-__global__ __launch_bounds__(256) void k_gemm_mfma(Q4Mat W, const uint4* __restrict__ xq, const uint4* __restrict__ xh,
-                                                  int xstride, int M, float* __restrict__ y, int ldy,
-                                                  const float* __restrict__ bias) {
-  constexpr int PD = kMfmaPD, TOK = 16 * TT, NJ = 4 / JS, NX = 2 * TT, NS = 4 * NJ;
-  __shared__ uint4 xs[2][4][4][TOK][2];               // [buf][block][j][token][half]: 16 fp16 operand values
-  __shared__ float dxs[2][4][TOK];                    // [buf][block][token]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, kg = lane >> 4;
-  const int T0 = blockIdx.y * TOK;
-  const int R0 = JS == 1 ? blockIdx.x * 64 + wave * 16 : blockIdx.x * 16;
-  const int j0 = JS == 1 ? 0 : wave;
-  const int row = R0 + li, tile = row >> 6, rr = row & 63;
-  const uint4* wq = W.qs + ((size_t)tile * W.ng * 64 + rr) * 4 + j0;
-  const uint4* wd = W.d + (size_t)tile * W.nb8 * 64 + rr;
-  const int ng = W.ng, nb = W.nb;
-  // weight operand of this lane: k = 4 kg .. 4 kg + 3.  kg 0: low nibbles, 1: high nibbles, each
-  // as fp16 1024 + n (bytes n, 0x64 by permute); kg 2: (1032, 0, 0, 0) -- the nibbles are forced
-  // to 8 and the permute keeps byte 0 only; kg 3: zeros.
-  const uint32_t sh = (kg & 1) << 2;
-  const uint32_t mask = kg < 2 ? 0x0F0F0F0Fu : 0u, orv = kg < 2 ? 0u : 0x08080808u;
-  const uint32_t sel0 = kg < 2 ? 0x04010400u : kg == 2 ? 0x0C0C0400u : 0x0C0C0C0Cu;
-  const uint32_t sel1 = kg < 2 ? 0x04030402u : 0x0C0C0C0Cu;
-  auto xload = [&](int g, uint4* v, float& d) {      // group g: 4 blocks x 4 chains x TOK tokens x 2 halves
-#pragma unroll
-    for (int u = 0; u < NX; u++) {
-      const int i = tid + 256 * u, t = i >> 5, k = i & 31, m = T0 + t, blk = g * 4 + (k >> 3);
-      if (m < M && blk < nb) {
-        const uint2* q = reinterpret_cast<const uint2*>(xh + xh_tile(m, xstride) + (size_t)blk * kXhBlock) +
-                         (((k >> 1) & 3) * 4 + 2 * (k & 1)) * 16 + (m & 15);
-        const uint2 lo = q[0], hi = q[16];
-        v[u] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-      } else {
-        v[u] = make_uint4(0, 0, 0, 0);
-      }
-    }
-    const int t = tid >> 2, kb = tid & 3, m = T0 + t, blk = g * 4 + kb;
-    d = (tid < 4 * TOK && m < M && blk < nb) ? __uint_as_float(xq[(size_t)m * xstride * 4 + blk * 4].w) : 0.0f;
-  };
-  auto xstore = [&](int buf, const uint4* v, float d) {
-#pragma unroll
-    for (int u = 0; u < NX; u++) {
-      const int i = tid + 256 * u, t = i >> 5, k = i & 31;
-      xs[buf][k >> 3][(k >> 1) & 3][t][k & 1] = v[u];
-    }
-    if (tid < 4 * TOK) dxs[buf][tid & 3][tid >> 2] = d;
-  };
-  uint4 wr[PD][NJ], sr[PD / 2];
-#pragma unroll
-  for (int u = 0; u < PD; u++)
-#pragma unroll
-    for (int jj = 0; jj < NJ; jj++) wr[u][jj] = wq[(size_t)u * 256 + jj];   // past the end: the zeroed tail
-#pragma unroll
-  for (int u = 0; u < PD / 2; u++) sr[u] = wd[(size_t)u * 64];
-  uint4 xr[2][NX];
-  float dr[2];
-  xload(0, xr[0], dr[0]);
-  xstore(0, xr[0], dr[0]);
-  if (ng > 1) xload(1, xr[1], dr[1]);
-  __syncthreads();
-  float acc[NJ][TT][4];
-#pragma unroll
-  for (int jj = 0; jj < NJ; jj++)
-#pragma unroll
-    for (int tt = 0; tt < TT; tt++) acc[jj][tt][0] = acc[jj][tt][1] = acc[jj][tt][2] = acc[jj][tt][3] = 0.0f;
-  const uint2* xs2 = reinterpret_cast<const uint2*>(&xs[0][0][0][0][0]);
-  for (int g0 = 0; g0 < ng; g0 += PD) {
-#pragma unroll
-    for (int u = 0; u < PD; u++) {
-      const int g = g0 + u, buf = g & 1;
-      if (g < ng) {
-        if (g + 2 < ng) xload(g + 2, xr[u & 1], dr[u & 1]);   // u & 1 == g & 1 (PD is even)
-        uint4 w[NJ];
-#pragma unroll
-        for (int jj = 0; jj < NJ; jj++) {
-          w[jj] = wr[u][jj];
-          wr[u][jj] = wq[(size_t)(g + PD) * 256 + jj];
-        }
-        const uint4 sc = sr[u >> 1];
-        if (u & 1) sr[u >> 1] = wd[(size_t)((g + PD) >> 1) * 64];
-        f4_t d[2][TT];
-        float s4[TT][4];
-        auto issue = [&](int st) {
-          const int k = st / NJ, jj = st - k * NJ;
-          const uint32_t wv = k == 0 ? w[jj].x : k == 1 ? w[jj].y : k == 2 ? w[jj].z : w[jj].w;
-          const uint32_t v = ((wv >> sh) & mask) | orv;
-          const h4_t bw = __builtin_bit_cast(h4_t, make_uint2(__builtin_amdgcn_perm(0x64646464u, v, sel0),
-                                                              __builtin_amdgcn_perm(0x64646464u, v, sel1)));
-#pragma unroll
-          for (int tt = 0; tt < TT; tt++) {
-            // 8 bytes at quarter kg of the 32-byte operand of token 16 tt + li
-            const uint2 aw = xs2[((((buf * 4 + k) * 4 + j0 + jj) * TOK + tt * 16 + li) * 2) * 2 + kg];
-            d[st & 1][tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4_t, aw), bw,
-                                                                  (f4_t){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-          }
-        };
-        const int nbk = nb - g * 4;                   // blocks of this group that exist (uniform)
-        issue(0);
-#pragma unroll
-        for (int st = 0; st < NS; st++) {
-          const int k = st / NJ, jj = st - k * NJ;
-          if (st + 1 < NS && (st + 1) / NJ < nbk) issue(st + 1);
-          __builtin_amdgcn_sched_barrier(0);
-          if (k < nbk) {
-            if (jj == 0) {
-              const int hb = ((u & 1) << 2) + k;
-              const uint32_t sw = (hb >> 1) == 0 ? sc.x : (hb >> 1) == 1 ? sc.y : (hb >> 1) == 2 ? sc.z : sc.w;
-              const float dw = half_bits_to_float((hb & 1) ? (sw >> 16) : (sw & 0xffffu));
-#pragma unroll
-              for (int tt = 0; tt < TT; tt++) {
-                const float4 dx = *reinterpret_cast<const float4*>(&dxs[buf][k][tt * 16 + 4 * kg]);
-                s4[tt][0] = dw * dx.x;
-                s4[tt][1] = dw * dx.y;
-                s4[tt][2] = dw * dx.z;
-                s4[tt][3] = dw * dx.w;
-              }
-            }
-#pragma unroll
-            for (int tt = 0; tt < TT; tt++)
-#pragma unroll
-              for (int r = 0; r < 4; r++) acc[jj][tt][r] = acc[jj][tt][r] + d[st & 1][tt][r] * s4[tt][r];
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        if (g + 1 < ng) xstore(buf ^ 1, xr[(u + 1) & 1], dr[(u + 1) & 1]);
-        __syncthreads();
-      }
-    }
-  }
-  // lane holds tokens T0 + 16 tt + 4 kg + r of row R0 + li; chains combine as ((a0 + a1) + a2) + a3
-  auto put = [&](int m, int n, float v) {
-    if (m < M && n < W.N) {
-      float* o = y + (size_t)m * ldy + n;
-      if (OP == OP_ADD) *o = *o + v;
-      else if (OP == OP_BIAS) *o = v + bias[n];
-      else *o = v;
-    }
-  };
-  if (JS == 1) {
-#pragma unroll
-    for (int tt = 0; tt < TT; tt++)
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        put(T0 + tt * 16 + 4 * kg + r, row, ((acc[0][tt][r] + acc[1][tt][r]) + acc[2][tt][r]) + acc[3][tt][r]);
-  } else {
-    float* red = reinterpret_cast<float*>(&xs[0][0][0][0][0]);   // [chain][token][row], after the loop's last barrier
-#pragma unroll
-    for (int tt = 0; tt < TT; tt++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) red[(wave * TOK + tt * 16 + 4 * kg + r) * 16 + li] = acc[0][tt][r];
-    __syncthreads();
-    for (int i = tid; i < TOK * 16; i += 256) {
-      const float v = ((red[i] + red[TOK * 16 + i]) + red[2 * TOK * 16 + i]) + red[3 * TOK * 16 + i];
-      put(T0 + (i >> 4), R0 + (i & 15), v);
-    }
-  }
-}
-
 // ================================================================ batched decode kernels
 //
 // B independent sequences decode one token each per step.  Sequence b has its own fp32 cache
@@ -1492,57 +1313,26 @@ int check_ready(q4hip* h) {
   return Q4HIP_OK;
 }
 
-// Kernel choice for passes of M > 8 tokens (every candidate gives the same bits), from timings of
-// all candidates at the Qwen2.5 shapes on MI355X:
-//   matrices with >= 16K rows (gate/up, output head), any M: k_gemm_mfma, 16 tokens per wave
-//   M > 64: k_gemm_mfma, 32 tokens per wave when K > 2048 (down), else 16
-//   M <= 64, fewer rows: k_gemm_rows with 2 tokens per wave (1 below 16 tokens)
+// Kernel choice for passes of M > 8 tokens (every candidate gives the same bits):
+//   k_gemm_sk (matrix cores, operands streamed through a shared-memory ring), one lane chain per
+//   wave (JS 4) when the matrix has too few rows to give 512 workgroups of 64 rows, else all four
+//   chains per wave (JS 1).  Measured on MI355X against the earlier matrix-core GEMM with register
+//   prefetch: 1024-token prefill 15.0 -> 10.5 ms, 32-sequence batched step 4.3 -> 3.7 ms.
 // Q4HIP_GEMM=valu keeps the matrix cores out (k_gemm_rows up to 64 tokens, else k_gemm_q4).
-//   M <= 64 with fp16 operands: k_gemm_sk (ring-fed matrix cores), one chain per wave (JS 4) when
-//   the matrix has too few rows to give 512 workgroups of 64 rows
-// Q4HIP_GEMM=mfma keeps k_gemm_sk out (the earlier choice; same bits, for comparison).
-enum { GK_ROWS2, GK_ROWS1, GK_MFMA_T2J1, GK_MFMA_T1J1, GK_TILED, GK_SK4, GK_SK1 };
+enum { GK_ROWS2, GK_ROWS1, GK_TILED, GK_SK4, GK_SK1 };
 
 constexpr int kSkR4 = 4, kSkR1 = 4;    // ring slots of k_gemm_sk (JS 4: 38.4 KB, JS 1: 52.2 KB)
 
-// Q4HIP_SK_RING=6 or 8 (JS 4), 6 (JS 1): a deeper k_gemm_sk ring (same results; for measurements).
-int sk_ring() {
-  static const int r = [] { const char* e = getenv("Q4HIP_SK_RING"); return e ? atoi(e) : 0; }();
-  return r;
-}
-
-bool gemm_env(const char* v) {
-  const char* e = getenv("Q4HIP_GEMM");
-  return e && strcmp(e, v) == 0;
-}
-
-// Whether few-token projections may use k_gemm_sk (not under Q4HIP_GEMM=valu or =mfma).
+// Whether multi-token projections use the matrix cores (not under Q4HIP_GEMM=valu).
 bool sk_enabled() {
-  static const bool on = !gemm_env("valu") && !gemm_env("mfma");
+  static const bool on = [] { const char* e = getenv("Q4HIP_GEMM"); return !(e && strcmp(e, "valu") == 0); }();
   return on;
 }
 
 int pick_gemm(const Mat& W, int M, bool have_xh) {
-  static const bool no_mfma = gemm_env("valu");
-  static const bool no_sk = !sk_enabled();
-  if (have_xh && !no_mfma) {
-    static const int force_js = [] { const char* e = getenv("Q4HIP_SK_JS"); return e ? atoi(e) : 0; }();
-    if (M <= 64 && !no_sk) {
-      if (force_js == 1 || force_js == 4) return force_js == 1 ? GK_SK1 : GK_SK4;
-      return (W.Np / 64) * ((M + 15) / 16) >= 512 ? GK_SK1 : GK_SK4;
-    }
-    if (W.Np >= 16384) return GK_MFMA_T1J1;
-    if (M > 64) return W.nb > 64 ? GK_MFMA_T2J1 : GK_MFMA_T1J1;
-  }
+  if (have_xh && sk_enabled()) return (W.Np / 64) * ((M + 15) / 16) >= 512 ? GK_SK1 : GK_SK4;
   if (M <= 64) return M >= 16 ? GK_ROWS2 : GK_ROWS1;
   return GK_TILED;
-}
-
-template <int OP, int TT, int JS>
-void launch_mfma(hipStream_t s, const Mat& W, const uint4* xq, const uint4* xh, int xstride, int M, float* y, int ldy,
-                 const float* bias) {
-  k_gemm_mfma<OP, TT, JS><<<dim3((unsigned)(W.Np / (JS == 1 ? 64 : 16)), (unsigned)((M + 16 * TT - 1) / (16 * TT))), 256, 0, s>>>(
-      W.view(), xq, xh, xstride, M, y, ldy, bias);
 }
 
 template <int OP, int JS, int R>
@@ -1557,7 +1347,7 @@ void launch_sk(hipStream_t s, const Mat& W, const uint4* xh, int xstride, int M,
 // launched) where that path does not apply; the caller then runs the two launches.
 bool launch_gu_swiglu(hipStream_t s, const Mat& W, const uint4* xh_in, int xstride, int M, uint4* xq_out,
                       uint4* xh_out, int F) {
-  if (!xh_in || M > 64 || F % 32 || !sk_enabled()) return false;
+  if (!xh_in || F % 32 || !sk_enabled()) return false;
   k_gemm_sk<OP_STORE, 1, kSkR1, 1><<<dim3((unsigned)(F / 32), (unsigned)((M + 15) / 16)), 256, 0, s>>>(
       W.view(), xh_in, xstride, M, nullptr, 0, nullptr, xq_out, xh_out, F);
   return true;
@@ -1584,17 +1374,8 @@ void launch_matvec(hipStream_t s, const Mat& W, const uint4* xq, int xstride, in
   switch (pick_gemm(W, M, xh != nullptr)) {
     case GK_ROWS2: launch_rows<OP, 2>(s, W, xq, xstride, M, y, ldy, bias); break;
     case GK_ROWS1: launch_rows<OP, 1>(s, W, xq, xstride, M, y, ldy, bias); break;
-    case GK_MFMA_T2J1: launch_mfma<OP, 2, 1>(s, W, xq, xh, xstride, M, y, ldy, bias); break;
-    case GK_MFMA_T1J1: launch_mfma<OP, 1, 1>(s, W, xq, xh, xstride, M, y, ldy, bias); break;
-    case GK_SK4:
-      if (sk_ring() == 8) launch_sk<OP, 4, 8>(s, W, xh, xstride, M, y, ldy, bias);
-      else if (sk_ring() == 6) launch_sk<OP, 4, 6>(s, W, xh, xstride, M, y, ldy, bias);
-      else launch_sk<OP, 4, kSkR4>(s, W, xh, xstride, M, y, ldy, bias);
-      break;
-    case GK_SK1:
-      if (sk_ring() == 6) launch_sk<OP, 1, 6>(s, W, xh, xstride, M, y, ldy, bias);
-      else launch_sk<OP, 1, kSkR1>(s, W, xh, xstride, M, y, ldy, bias);
-      break;
+    case GK_SK4: launch_sk<OP, 4, kSkR4>(s, W, xh, xstride, M, y, ldy, bias); break;
+    case GK_SK1: launch_sk<OP, 1, kSkR1>(s, W, xh, xstride, M, y, ldy, bias); break;
     default:
       k_gemm_q4<OP><<<dim3((unsigned)(W.Np / kGemmRows), (unsigned)((M + kGemmTokens - 1) / kGemmTokens)), 256, 0, s>>>(
           W.view(), xq, xstride, M, y, ldy, bias);
