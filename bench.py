@@ -18,12 +18,12 @@ timed on the host cores as the CPU baseline.
 Other workloads of the same model (one JSON line each, same keys):
   --workload long-context  batch-1 decode after a 4096-position cache filled with seeded fp16-valued
                            K/V (written through q4hip_set_kv), 256 greedy steps by default
-                           (the cache stored as fp16, as the configuration names; --kv-cache f32: the
-                           reference's fp32 cache)
+                           (stored fp32 by default; --kv-cache f16 stores it as fp16)
   --workload prefill       one 1024-token seeded prompt per step
   --workload matvec        the isolated Q4_0 matvec at the model's five shapes, 1000 launches each
   --workload batched       32 independent sequences on the Qwen2.5-1.5B shape, each after a
                            1024-token seeded prompt, decoded together; one step = 32 tokens
+                           (fp16 K/V cache by default; --kv-cache f32 for the reference's cache type)
 
 Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 8] [--workload decode]
 """
@@ -133,11 +133,15 @@ def main():
     ap.add_argument("--workload", default="decode", choices=["decode", "long-context", "prefill", "matvec", "batched"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-node", action="store_true", help="skip the Node.js host leg of the decode workload")
-    ap.add_argument("--kv-cache", default="f16", choices=["f32", "f16"],
-                    help="K/V cache storage of the long-context and batched workloads: f16 (what those "
-                         "configurations name; half the K/V bytes; parity against the oracle with the "
-                         "same fp16 rounding, default) or f32 (the reference's cache type)")
+    ap.add_argument("--kv-cache", default=None, choices=["f32", "f16"],
+                    help="K/V cache storage of the long-context and batched workloads: f16 (half the K/V "
+                         "bytes; parity against the oracle with the same fp16 rounding; the batched "
+                         "default) or f32 (the reference's cache type; the long-context default, since "
+                         "the persistent kernel streams fp32 rows past its staged tile and an fp16 cache "
+                         "of 4096 positions decodes on the graph path)")
     args = ap.parse_args()
+    if args.kv_cache is None:
+        args.kv_cache = "f16" if args.workload == "batched" else "f32"
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the batch-1 decode loop runs on a single device "
               "(multi-GPU sharding is not run)", file=sys.stderr)

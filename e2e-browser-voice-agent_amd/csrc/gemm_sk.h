@@ -147,6 +147,49 @@ struct SkB {
   }
 };
 
+// Workgroups are dispatched to the 8 XCDs (each with its own L2) round robin: workgroup L runs on
+// XCD L % 8.  The grid is one-dimensional.  With `by_tile` it maps L to (row group, token tile) so
+// that the workgroups sharing a token tile -- and so its activation stream -- run on as few XCDs
+// as the balance allows: with a multiple of 8 tiles each tile on one XCD, with 1, 2 or 4 tiles
+// each on 8 / tiles XCDs; otherwise row groups run fastest (consecutive workgroups on one tile,
+// spread over the XCDs), which keeps a weight matrix larger than an L2 shared by the tiles in
+// flight.  Measured on the 1024-token prefill: o/down fetch 5.5 -> 1.4 GB per pass with it, but
+// gate/up (4.9 MB of weights) 0.85 -> 7.5 GB, at unchanged kernel times; the host chooses per
+// matrix.  Returns false for the padding workgroups of the second case (row group past the last).
+constexpr int kXcds = 8;
+
+__host__ __device__ inline int sk_grid(int nrg, int ntiles, bool by_tile) {
+  if (!by_tile || ntiles % kXcds == 0) return nrg * ntiles;
+  if (kXcds % ntiles == 0) {
+    const int per = kXcds / ntiles;                 // XCDs per tile
+    return (nrg + per - 1) / per * kXcds;
+  }
+  return nrg * ntiles;
+}
+
+__device__ __forceinline__ bool sk_place(int L, int nrg, int ntiles, bool by_tile, int& rg, int& T) {
+  const int x = L % kXcds, q = L / kXcds;
+  if (!by_tile) {
+    rg = L % nrg;
+    T = L / nrg;
+    return true;
+  }
+  if (ntiles % kXcds == 0) {
+    T = x + kXcds * (q / nrg);
+    rg = q % nrg;
+    return true;
+  }
+  if (kXcds % ntiles == 0) {
+    const int per = kXcds / ntiles;
+    T = x % ntiles;
+    rg = q * per + x / ntiles;
+    return rg < nrg;
+  }
+  rg = L % nrg;
+  T = L / nrg;
+  return true;
+}
+
 template <int OP>
 __device__ __forceinline__ void sk_put(float* y, int ldy, const float* bias, int M, int N, int m, int n, float v) {
   if (m < M && n < N) {
@@ -157,19 +200,19 @@ __device__ __forceinline__ void sk_put(float* y, int ldy, const float* bias, int
   }
 }
 
-// Grid (Np / (JS == 4 ? 16 : 64), ceil(M / 16)); R * SkSlot<JS>::BYTES of static shared memory.
+// Grid sk_grid(row groups, ceil(M / 16)) (one-dimensional); R * SkSlot<JS>::BYTES of static shared memory.
 // xt: the fp16 operands and block scales in the 16-token tiles of quantize_item (kXhBlock).
 // The ring slots are R distinct shared arrays and the group loop is unrolled by R, so every slot
 // address is a constant.
-// EPI = 1 (with JS 1): W is the fused gate|up matrix of ffn rows each, blockIdx.x = block b of the
+// EPI = 1 (with JS 1): W is the fused gate|up matrix of ffn rows each, row group = block b of the
 // SwiGLU activation; the workgroup's waves 0, 1 take gate rows 32 b .. 32 b + 31 and waves 2, 3 the
 // matching up rows, and the epilogue writes act = SwiGLU(gate, up) quantized (block b of xq_out
 // and xh_out, what k_quant<QM_SWIGLU> writes) instead of y.
 template <int OP, int JS, int R, int EPI = 0>
 __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restrict__ xt, int xstride, int M,
                                                 float* __restrict__ y, int ldy, const float* __restrict__ bias,
-                                                uint4* __restrict__ xq_out = nullptr, uint4* __restrict__ xh_out = nullptr,
-                                                int ffn = 0) {
+                                                bool by_tile, uint4* __restrict__ xq_out = nullptr,
+                                                uint4* __restrict__ xh_out = nullptr, int ffn = 0) {
   static_assert(EPI == 0 || JS == 1, "the SwiGLU epilogue needs the 64-row layout");
   using S = SkSlot<JS>;
   static_assert(R >= 3 && R <= 8, "ring depth");
@@ -177,8 +220,12 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
       q5[S::BYTES], q6[S::BYTES], q7[S::BYTES];
   unsigned char* const ring[8] = {q0, q1, q2, q3, q4, q5, q6, q7};
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, kg = lane >> 4;
-  const int T = blockIdx.y;
-  const int R0 = EPI == 1 ? blockIdx.x * 32 : JS == 4 ? blockIdx.x * 16 : blockIdx.x * 64;
+  // nrg row groups (16 rows for JS 4, 64 for JS 1, one 32-value block of gate and up for EPI 1)
+  // times ceil(M / 16) token tiles, placed by sk_place
+  const int nrg = EPI == 1 ? ffn / 32 : JS == 4 ? W.Np / 16 : W.Np / 64;
+  int rgi, T;
+  if (!sk_place(blockIdx.x, nrg, (M + 15) / 16, by_tile, rgi, T)) return;
+  const int R0 = EPI == 1 ? rgi * 32 : JS == 4 ? rgi * 16 : rgi * 64;
   const int ng = W.ng, nb = W.nb;
   const SkB bop(kg);
   const SkSrc<JS> src(W, xt, xstride, T, R0, EPI == 1 ? ffn : 0);
@@ -284,7 +331,7 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
         u[k] = gus[t * 64 + 32 + e[k]];
       }
       swiglu8(g, u, v);
-      if (m < M) quantize_item(v, blockIdx.x, j, xq_out + (size_t)m * xstride * 4, xh_out + xh_tile(m, xstride), m & 15);
+      if (m < M) quantize_item(v, rgi, j, xq_out + (size_t)m * xstride * 4, xh_out + xh_tile(m, xstride), m & 15);
     }
   } else if (JS == 1) {
 #pragma unroll

@@ -6,10 +6,11 @@
         one warmup launch and one timed launch of `steps` greedy steps of the persistent decode
         kernel.  Prints the HIP-event time of the timed launch.
 
-    python profile_decode.py summarize --trace DIR --fetch DIR --write DIR --steps K --out FILE
+    python profile_decode.py summarize --trace DIR --fetch DIR --write DIR [--dram DIR] --steps K --out FILE
         Reads the rocprofv3 CSV outputs (kernel trace with --stats; one --pmc FETCH_SIZE pass; one
-        --pmc WRITE_SIZE pass), scales each counter by what it reads for the copy kernel, and
-        writes a short markdown summary with per-launch and per-step figures.
+        --pmc WRITE_SIZE pass; optionally one --pmc TCC_EA0_RDREQ_DRAM_sum TCC_EA0_RDREQ_sum pass),
+        scales each byte counter by what it reads for the copy kernel, and writes a short markdown
+        summary with per-launch and per-step figures.
 
     python profile_decode.py steps --trace DIR --marker KERNEL --skip N --title T --command C --out FILE
         Per-step kernel times of a multi-kernel workload from a rocprofv3 kernel trace: the dispatches
@@ -117,7 +118,8 @@ def summarize(a) -> None:
         f"rocprofv3 --kernel-trace --stats -d T -o t --output-format csv -- python3 e2e-browser-voice-agent_amd/py/profile_decode.py run --steps {steps}",
         f"rocprofv3 --pmc FETCH_SIZE -d F -o f --output-format csv -- python3 e2e-browser-voice-agent_amd/py/profile_decode.py run --steps {steps}",
         f"rocprofv3 --pmc WRITE_SIZE -d W -o w --output-format csv -- python3 e2e-browser-voice-agent_amd/py/profile_decode.py run --steps {steps}",
-        f"python3 e2e-browser-voice-agent_amd/py/profile_decode.py summarize --trace T --fetch F --write W --steps {steps} --out <this file>",
+        f"rocprofv3 --pmc TCC_EA0_RDREQ_DRAM_sum TCC_EA0_RDREQ_sum -d D -o d --output-format csv -- python3 e2e-browser-voice-agent_amd/py/profile_decode.py run --steps {steps}",
+        f"python3 e2e-browser-voice-agent_amd/py/profile_decode.py summarize --trace T --fetch F --write W --dram D --steps {steps} --out <this file>",
         "```",
         "",
         "| | value |",
@@ -143,6 +145,25 @@ def summarize(a) -> None:
     traffic = {"steps": steps, "launch_us": avg_ns / 1e3, "fetch_bytes_per_step": fetch_b / steps,
                "write_bytes_per_step": write_b / steps, "algorithmic_bytes_per_step": alg / steps,
                "fetch_calibration": f_cal, "write_calibration": w_cal}
+    if a.dram:
+        dram = _counter(a.dram, "TCC_EA0_RDREQ_DRAM_sum")
+        req = _counter(a.dram, "TCC_EA0_RDREQ_sum")
+        _, cd = _find(dram, "copyBuffer")
+        _, pdr = _find(dram, "k_decode_persistent")
+        _, prq = _find(req, "k_decode_persistent")
+        bytes_per_req = COPY_BYTES / max(cd)            # the 256 MiB copy reads COPY_BYTES
+        dram_b = sum(pdr) / len(pdr) * bytes_per_req
+        traffic["dram_read_bytes_per_step"] = dram_b / steps
+        traffic["dram_read_share_of_requests"] = sum(pdr) / sum(prq)
+        lines[-1:-1] = [
+            "",
+            f"`TCC_EA0_RDREQ_DRAM_sum` (L2 read requests sent to the memory side) per launch: {sum(pdr) / len(pdr):.4g}, "
+            f"{sum(pdr) / sum(prq):.4f} of all L2 read requests (`TCC_EA0_RDREQ_sum`); the 256 MiB copy reads "
+            f"{max(cd):.0f} requests = {bytes_per_req:.1f} bytes each, so {dram_b / steps / 1e6:.2f} MB per step go to the "
+            f"memory side. That path includes the 256 MB last-level cache (MALL): hits there are counted too, so this "
+            f"counter bounds the DRAM reads from above and does not split them (the MALL share is measured by weight "
+            f"rotation, `profiles/mall_weight_rotation_head.md`).",
+        ]
     lines += ["", "```json", json.dumps(traffic, indent=1), "```", ""]
     with open(a.out, "w") as f:
         f.write("\n".join(lines))
@@ -190,6 +211,7 @@ def main() -> None:
     s.add_argument("--trace", required=True)
     s.add_argument("--fetch", required=True)
     s.add_argument("--write", required=True)
+    s.add_argument("--dram", default=None)
     s.add_argument("--steps", type=int, default=64)
     s.add_argument("--out", required=True)
     t = sub.add_parser("steps")

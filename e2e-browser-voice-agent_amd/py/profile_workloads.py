@@ -28,6 +28,8 @@ import csv
 import glob
 import json
 import os
+import re
+import subprocess
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -91,6 +93,17 @@ def _rows(d: str, pattern: str):
 
 
 def _short(name: str) -> str:
+    if name.startswith("_Z"):                 # some trace names come mangled
+        try:
+            name = subprocess.run(["c++filt", name], capture_output=True, text=True, timeout=10).stdout.strip() or name
+        except (OSError, subprocess.SubprocessError):
+            pass
+    if name.startswith("_Z"):                 # c++filt without _Float16 support: the bare name
+        m = re.match(r"_Z(\d+)", name)
+        if m:
+            n = int(m.group(1))
+            base = name[m.end():m.end() + n]
+            name = base + ("<..., _Float16>" if "DF16_" in name else "<...>")
     return name.split("(")[0].replace("void ", "")
 
 
@@ -107,20 +120,44 @@ def _dispatches(rows, id_key: str, name_key: str, marker: str, skip: int):
 
 
 def _grid(r) -> str:
-    """Total threads of a dispatch (the counter files give Grid_Size, the trace its x, y, z)."""
+    """Total threads of a dispatch (the counter files give Grid_Size, the trace its x, y, z), with the
+    shared memory it was given (two launches of one kernel on different shapes may share a grid)."""
     if r.get("Grid_Size"):
-        return str(int(float(r["Grid_Size"])))
-    return str(int(r.get("Grid_Size_X", 1)) * int(r.get("Grid_Size_Y", 1)) * int(r.get("Grid_Size_Z", 1)))
+        g = int(float(r["Grid_Size"]))
+    else:
+        g = int(r.get("Grid_Size_X", 1)) * int(r.get("Grid_Size_Y", 1)) * int(r.get("Grid_Size_Z", 1))
+    lds = r.get("LDS_Block_Size") or r.get("Lds_Size") or ""
+    return f"{g}" + (f", LDS {int(float(lds))}" if lds not in ("", "0") else "")
+
+
+def _run_index(rows):
+    """{dispatch id: k} where k numbers the runs of consecutive launches of the same (kernel, grid) in
+    launch order; two shapes of the matvec sweep can share a grid, and their launches form separate
+    runs (the same numbering in the trace and in the counter files, whose launch order is the same)."""
+    order = sorted({(int(r["Dispatch_Id"]), (_short(r["Kernel_Name"]), _grid(r))) for r in rows})
+    out, runs, prev = {}, {}, None
+    for i, key in order:
+        if key != prev:
+            runs[key] = runs.get(key, -1) + 1
+            prev = key
+        out[i] = runs[key]
+    return out
+
+
+def _key(r, marker: str, runs):
+    k = (_short(r["Kernel_Name"]), _grid(r))
+    return k if marker else k + (runs[int(r["Dispatch_Id"])],)
 
 
 def _counter_by_kernel(d: str, counter: str, marker: str, skip: int):
     rows = [r for r in _rows(d, "*counter_collection.csv") if r["Counter_Name"] == counter]
     ids, nsteps = _dispatches(rows, "Dispatch_Id", "Kernel_Name", marker, skip)
     keep = set(ids)
+    runs = _run_index(rows)
     per = {}
     for r in rows:
         if int(r["Dispatch_Id"]) in keep:
-            key = (_short(r["Kernel_Name"]), _grid(r))
+            key = _key(r, marker, runs)
             per.setdefault(key, {}).setdefault(r["Dispatch_Id"], 0.0)
             per[key][r["Dispatch_Id"]] += float(r["Counter_Value"])
     return per, nsteps
@@ -146,16 +183,21 @@ def summarize(a) -> None:
     trace = _rows(a.trace, "*kernel_trace.csv")
     ids, nsteps = _dispatches(trace, "Dispatch_Id", "Kernel_Name", a.marker, a.skip)
     keep = set(ids)
+    runs = _run_index(trace)
     times = {}
     for r in trace:
         if int(r["Dispatch_Id"]) in keep:
-            key = (_short(r["Kernel_Name"]), _grid(r))
+            key = _key(r, a.marker, runs)
             c = times.setdefault(key, [0, 0.0])
             c[0] += 1
             c[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-    f_cal, w_cal = _calibration(a.fetch, "FETCH_SIZE"), _calibration(a.write, "WRITE_SIZE")
-    fetch, _ = _counter_by_kernel(a.fetch, "FETCH_SIZE", a.marker, a.skip)
-    write, _ = _counter_by_kernel(a.write, "WRITE_SIZE", a.marker, a.skip)
+    if a.fetch and a.write:
+        f_cal, w_cal = _calibration(a.fetch, "FETCH_SIZE"), _calibration(a.write, "WRITE_SIZE")
+        fetch, _ = _counter_by_kernel(a.fetch, "FETCH_SIZE", a.marker, a.skip)
+        write, _ = _counter_by_kernel(a.write, "WRITE_SIZE", a.marker, a.skip)
+    else:                                     # kernel trace only
+        f_cal = w_cal = None
+        fetch, write = {}, {}
 
     def per_step(d, key, cal):
         """Bytes per step, or per launch of this kernel with no marker (the matvec sweep)."""
@@ -166,33 +208,55 @@ def summarize(a) -> None:
 
     lines = [f"# {a.title}", "", "Commands (repository root on the MI355X host, `cd /tmp && export TMPDIR=/tmp` "
              "first; paths absolute):", "", "```"]
-    for tool in ("--kernel-trace --stats -d T -o t", "--pmc FETCH_SIZE -d F -o f", "--pmc WRITE_SIZE -d W -o w"):
+    tools = ["--kernel-trace --stats -d T -o t"]
+    if f_cal is not None:
+        tools += ["--pmc FETCH_SIZE -d F -o f", "--pmc WRITE_SIZE -d W -o w"]
+    for tool in tools:
         lines.append(f"rocprofv3 {tool} --output-format csv -- python3 e2e-browser-voice-agent_amd/py/"
                      f"profile_workloads.py run {a.command}")
-    lines += [f"python3 e2e-browser-voice-agent_amd/py/profile_workloads.py summarize --trace T --fetch F --write W "
-              f"--marker '{a.marker}' --skip {a.skip} --title ... --command '{a.command}' --out <this file>", "```", ""]
+    counters = "--fetch F --write W " if f_cal is not None else ""
+    lines += [f"python3 e2e-browser-voice-agent_amd/py/profile_workloads.py summarize --trace T {counters}"
+              f"--marker '{a.marker}' --skip {a.skip}" + (f" --only '{a.only}'" if a.only else "") +
+              f" --title ... --command '{a.command}' --out <this file>", "```", ""]
     unit = "step" if a.marker else "launch"
-    lines += [f"{nsteps} {unit}s counted. Byte counters scaled by the 256 MiB copy kernel: FETCH_SIZE reads "
-              f"{f_cal:.3f} x, WRITE_SIZE {w_cal:.3f} x the bytes copied.", "",
-              f"| kernel | grid | launches per {unit} | us per {unit} | us per launch | fetch MB per {unit} | "
-              f"write MB per {unit} |", "|---|---|---|---|---|---|---|"]
+    cal = (f" Byte counters scaled by the 256 MiB copy kernel: FETCH_SIZE reads {f_cal:.3f} x, WRITE_SIZE "
+           f"{w_cal:.3f} x the bytes copied." if f_cal is not None else " Kernel trace only.")
+    if a.marker:
+        lines += [f"{nsteps} steps counted.{cal}", "",
+                  "| kernel | grid (threads) | launches per step | us per step | us per launch | fetch MB per step | "
+                  "write MB per step |", "|---|---|---|---|---|---|---|"]
+    else:
+        lines += [f"Every launch counted.{cal}", "",
+                  "| kernel | grid (threads) | launches | us per launch | fetch MB per launch | write MB per launch |",
+                  "|---|---|---|---|---|---|"]
     tot_us = tot_f = tot_w = 0.0
-    kernels = []
+    only = re.compile(a.only) if a.only else None
     for key, (n, t) in sorted(times.items(), key=lambda kv: -kv[1][1]):
+        if only and not only.search(key[0]):
+            continue
         fb, wb = per_step(fetch, key, f_cal), per_step(write, key, w_cal)
         per = nsteps if a.marker else n            # no marker: every figure per launch of the kernel
         tot_us += t / per
         tot_f += fb or 0.0
         tot_w += wb or 0.0
-        kernels.append({"kernel": key[0], "grid": key[1], "launches": n / per, "us": t / per,
-                        "fetch_bytes": fb, "write_bytes": wb})
+        if not a.marker:
+            if n < 2:                         # a lone launch (the sweep's first run of a shape)
+                continue
+            lines.append(f"| {key[0]} | {key[1]} | {n} | {t / n:.2f} | "
+                         f"{'-' if fb is None else f'{fb / 1e6:.3f}'} | {'-' if wb is None else f'{wb / 1e6:.3f}'} |")
+            continue
         lines.append(f"| {key[0]} | {key[1]} | {n / per:g} | {t / per:.1f} | {t / n:.1f} | "
                      f"{'-' if fb is None else f'{fb / 1e6:.2f}'} | {'-' if wb is None else f'{wb / 1e6:.2f}'} |")
-    lines += ["", f"Per {unit}: kernel time {tot_us:.1f} us, HBM traffic {(tot_f + tot_w) / 1e6:.2f} MB "
-              f"(fetch {tot_f / 1e6:.2f}, write {tot_w / 1e6:.2f}).", ""]
-    blob = {"unit": unit, "count": nsteps, "kernel_us": tot_us, "fetch_bytes": tot_f, "write_bytes": tot_w,
-            "traffic_bytes": tot_f + tot_w, "fetch_calibration": f_cal, "write_calibration": w_cal,
-            "kernels": kernels}
+    traffic = tot_f + tot_w if f_cal is not None else None
+    if a.marker:
+        lines += ["", f"Per step: kernel time {tot_us:.1f} us" +
+                  (f", HBM traffic {traffic / 1e6:.2f} MB (fetch {tot_f / 1e6:.2f}, write {tot_w / 1e6:.2f})."
+                   if traffic is not None else "."), ""]
+    else:
+        lines += [""]
+    blob = {"unit": unit, "count": nsteps, "kernel_us": tot_us, "fetch_bytes": tot_f if traffic else None,
+            "write_bytes": tot_w if traffic else None, "traffic_bytes": traffic, "fetch_calibration": f_cal,
+            "write_calibration": w_cal}
     lines += ["```json", json.dumps(blob, indent=1), "```", ""]
     with open(a.out, "w") as f:
         f.write("\n".join(lines))
@@ -249,9 +313,12 @@ def main() -> None:
     r.add_argument("--steps", type=int, default=None)
     r.add_argument("--warmup", type=int, default=None)
     s = sub.add_parser("summarize")
-    for k in ("--trace", "--fetch", "--write", "--title", "--command", "--out"):
+    for k in ("--trace", "--title", "--command", "--out"):
         s.add_argument(k, required=True)
+    s.add_argument("--fetch", default=None)
+    s.add_argument("--write", default=None)
     s.add_argument("--marker", default="")
+    s.add_argument("--only", default="", help="regular expression: list only the kernels it matches")
     s.add_argument("--skip", type=int, default=0)
     m = sub.add_parser("mall")
     m.add_argument("--iters", type=int, default=200)
