@@ -59,19 +59,55 @@ def algorithmic_bytes(shape, T):
             "total": layers + head + norms + bias + emb + logits + kv}
 
 
+def repacked_weight_bytes(shape):
+    """Device bytes of the layers' and the head's Q4_0 matrices in the library's layout: per row,
+    16 bytes of nibbles per 4 blocks (64-byte words of 4 lanes) and 16 bytes of fp16 scales per 8
+    blocks, the block counts rounded up to whole groups; rows in tiles of 64."""
+    def mat(n, k):
+        nb = k // 32
+        return (n + 63) // 64 * 64 * (((nb + 3) // 4) * 64 + ((nb + 7) // 8) * 16)
+    D, F = shape.dim, shape.ffn
+    return shape.layers * (mat(shape.qkv, D) + mat(D, D) + mat(2 * F, D) + mat(D, F)) + mat(shape.vocab, D)
+
+
 PROFILE = os.path.join(REPO, "profiles", "decode_persistent_qwen05b_prompt64_steps64.md")
+
+
+def profile_blob(name):
+    """The JSON block at the end of a committed rocprofv3 summary profiles/<name>, or None."""
+    try:
+        text = open(os.path.join(REPO, "profiles", name)).read()
+        blob = text[text.index("```json") + 7:]
+        return json.loads(blob[:blob.index("```")])
+    except (OSError, ValueError):
+        return None
 
 
 def profiled_traffic():
     """Per-step HBM bytes (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration) from
-    the committed rocprofv3 summary of this workload, or None."""
+    the committed rocprofv3 summary of the headline workload, or None."""
+    data = profile_blob(os.path.basename(PROFILE))
     try:
-        text = open(PROFILE).read()
-        blob = text[text.index("```json") + 7:]
-        data = json.loads(blob[:blob.index("```")])
         return data["fetch_bytes_per_step"] + data["write_bytes_per_step"]
-    except (OSError, ValueError, KeyError):
+    except (TypeError, KeyError):
         return None
+
+
+MALL_PROFILE = "mall_weight_rotation_head.md"
+
+
+def mall_share(footprint_bytes):
+    """Fraction of a weight stream of this footprint, read in the same order every pass, that the
+    256 MB last-level cache serves: the committed rotation sweep's row of the smallest footprint
+    at or above it (None without the summary)."""
+    rows = profile_blob(MALL_PROFILE)
+    if not rows:
+        return None
+    above = [r for r in rows if r["footprint_mb"] * 1e6 >= footprint_bytes]
+    row = min(above, key=lambda r: r["footprint_mb"]) if above else rows[-1]
+    return {"served_fraction": row["served_fraction"], "footprint_mb": round(footprint_bytes / 1e6, 1),
+            "measured_at_mb": row["footprint_mb"], "method": "weight-copy rotation of the head matvec",
+            "profile": "profiles/" + MALL_PROFILE}
 
 
 def cpu_baseline(shape, tensors, ids, first_tokens):
@@ -207,6 +243,10 @@ def bench_decode(args):
                 "traffic": round(per_step_traffic * args.steps) if per_step_traffic and mode == 2 else None,
                 "bytes_per_launch": tot, "avg_launch_us": round(dev_ms * 1e3, 1), "steps_per_launch": args.steps,
                 "profile": os.path.relpath(PROFILE, REPO)}
+    # how much of the weight set the 256 MB last-level cache can serve when it is read once per token
+    share = mall_share(repacked_weight_bytes(shape))
+    if share:
+        roofline["infinity_cache_share"] = share
 
     # the same K steps on the multi-kernel path (hipGraph replay per step), for comparison
     m.set_decode_mode(q4hip.DECODE_GRAPH)
@@ -320,7 +360,9 @@ def bench_long_context(args):
         "roofline": {"bound": "hbm", "kernel": "k_decode_persistent" if mode == 2 else "decode graph",
                      "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "bytes_per_launch": tot,
-                     "avg_launch_us": round(dev_ms * 1e3, 1), "steps_per_launch": args.steps},
+                     "avg_launch_us": round(dev_ms * 1e3, 1), "steps_per_launch": args.steps,
+                     "profile": "profiles/decode_long_context_qwen05b_ctx4096.md (kernel trace; the byte-counter "
+                                "pass of this workload ended the profiled process, so traffic is not measured)"},
     }
     if not args.no_cpu:
         oracle = _oracle()
@@ -371,6 +413,14 @@ def bench_prefill(args):
     gu_us = prof["matvec gate+up"] / shape.layers
     macs = n * 2 * shape.ffn * shape.dim
     tops = 2 * macs / (gu_us * 1e-6) / 1e12
+    # the pass's FLOPs: every projection over the n tokens, causal attention (q.k and p.v over
+    # t = 1..n positions per head), the head for the last token
+    D, F, L, H, HD, QKV = shape.dim, shape.ffn, shape.layers, shape.heads, shape.head_dim, shape.qkv
+    gemm = 2 * n * L * (QKV * D + D * D + 2 * F * D + D * F)
+    attn = 4 * L * H * HD * n * (n + 1) // 2
+    flops = gemm + attn + 2 * shape.vocab * D
+    pass_tflops = flops / (ms * 1e-3) / 1e12
+    pf = profile_blob("prefill_qwen05b_1024.md")
     out = {
         "metric": "prefill tokens/s of a 1024-token prompt (Qwen2.5-0.5B Q4_0 shape)",
         "value": round(n / (ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -379,10 +429,15 @@ def bench_prefill(args):
         "config": {"workload": "qwen2.5-0.5b-shape Q4_0 prefill of 1024 seeded ids", "global_batch": 1,
                    "seq_len": n, "parallelism": "single-gpu"},
         "profile_us_per_pass": {k: round(v, 1) for k, v in prof.items()},
-        "roofline": {"bound": "mfma", "kernel": "k_gemm_mfma gate|up (exact int8 x q4 block dots on the matrix cores, fp32 lane chains on the VALU)",
-                     "achieved": round(tops, 2), "peak": 5000.0, "unit": "TOP/s (int8)",
-                     "frac": round(tops / 5000.0, 5), "traffic": None, "ops_per_launch": 2 * macs,
-                     "avg_launch_us": round(gu_us, 1)},
+        "roofline": {"bound": "mfma", "kernel": "whole prefill pass (projections on k_gemm_sk: exact block dots on the "
+                                                 "matrix cores, fp32 lane chains on the VALU)",
+                     "achieved": round(pass_tflops, 2), "peak": 2500.0, "unit": "TFLOP/s (dense bf16 MFMA peak)",
+                     "frac": round(pass_tflops / 2500.0, 5),
+                     "traffic": round(pf["traffic_bytes"] * args.steps) if pf and pf.get("traffic_bytes") else None,
+                     "flops_per_pass": flops, "ops_per_launch": flops * args.steps,
+                     "avg_launch_us": round(ms * 1e3, 1), "profile": "profiles/prefill_qwen05b_1024.md"},
+        "gate_up_int8_dot_tops": {"achieved": round(tops, 2), "peak": 5000.0, "frac": round(tops / 5000.0, 5),
+                                  "us_per_layer": round(gu_us, 1)},
         "next_token": nxt,
     }
     if not args.no_cpu:
@@ -433,7 +488,8 @@ def bench_matvec(args):
         "per_shape": rows,
         "roofline": {"bound": "hbm", "kernel": "k_matvec<1> 151936x896", "achieved": head["gbps"],
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "avg_launch_us": head["us"]},
+                     "traffic": _matvec_head_traffic(), "avg_launch_us": head["us"],
+                     "profile": "profiles/matvec_sweep_qwen05b.md"},
     }
     if not args.no_cpu:
         oracle = _oracle()
@@ -451,6 +507,15 @@ def bench_matvec(args):
                                                           f"{sec * 1e3:.1f} ms each, one thread"}
     print(json.dumps(out))
 
+
+
+def _matvec_head_traffic():
+    """HBM bytes of one head-shape matvec launch from the committed sweep profile, or None."""
+    pm = profile_blob("matvec_sweep_qwen05b.md")
+    for r in (pm or {}).get("per_launch", []):
+        if r["grid"].split(",")[0] == "607744" and r.get("fetch_bytes") is not None:
+            return round(r["fetch_bytes"] + r["write_bytes"])
+    return None
 
 
 BATCH = 32
@@ -488,6 +553,7 @@ def bench_batched(args):
     logits = BATCH * shape.vocab * 4
     tot = sum(weights + logits + BATCH * per_pos * (BATCH_PROMPT + i + 1) for i in range(args.steps))
     gbps = tot / (dev_ms / 1e3) / 1e9
+    pb = profile_blob("batched_decode_qwen15b_b32_ctx1024.md")   # measured with the fp16 cache
     out = {
         "metric": "batched decode tokens/s, 32 sequences at 1024-token context (Qwen2.5-1.5B Q4_0 shape)",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -500,8 +566,10 @@ def bench_batched(args):
         "achieved_gbps": round(gbps, 1),
         "roofline": {"bound": "hbm", "kernel": "batched decode step (all kernels)",
                      "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "bytes_per_launch": tot,
-                     "avg_launch_us": round(dev_ms * 1e3, 1), "steps_per_launch": args.steps},
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": round(pb["traffic_bytes"] * args.steps) if pb and kv16 else None,
+                     "bytes_per_launch": tot, "avg_launch_us": round(dev_ms * 1e3, 1), "steps_per_launch": args.steps,
+                     "profile": "profiles/batched_decode_qwen15b_b32_ctx1024.md"},
         "first_tokens": toks[0, :4].tolist(),
     }
     bt.close()

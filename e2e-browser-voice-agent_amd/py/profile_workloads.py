@@ -231,6 +231,7 @@ def summarize(a) -> None:
                   "|---|---|---|---|---|---|"]
     tot_us = tot_f = tot_w = 0.0
     only = re.compile(a.only) if a.only else None
+    per_launch = []
     for key, (n, t) in sorted(times.items(), key=lambda kv: -kv[1][1]):
         if only and not only.search(key[0]):
             continue
@@ -242,6 +243,8 @@ def summarize(a) -> None:
         if not a.marker:
             if n < 2:                         # a lone launch (the sweep's first run of a shape)
                 continue
+            per_launch.append({"kernel": key[0], "grid": key[1], "launches": n, "us": t / n,
+                               "fetch_bytes": fb, "write_bytes": wb})
             lines.append(f"| {key[0]} | {key[1]} | {n} | {t / n:.2f} | "
                          f"{'-' if fb is None else f'{fb / 1e6:.3f}'} | {'-' if wb is None else f'{wb / 1e6:.3f}'} |")
             continue
@@ -257,6 +260,8 @@ def summarize(a) -> None:
     blob = {"unit": unit, "count": nsteps, "kernel_us": tot_us, "fetch_bytes": tot_f if traffic else None,
             "write_bytes": tot_w if traffic else None, "traffic_bytes": traffic, "fetch_calibration": f_cal,
             "write_calibration": w_cal}
+    if not a.marker:
+        blob["per_launch"] = per_launch
     lines += ["```json", json.dumps(blob, indent=1), "```", ""]
     with open(a.out, "w") as f:
         f.write("\n".join(lines))
