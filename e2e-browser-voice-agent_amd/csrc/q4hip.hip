@@ -2106,13 +2106,14 @@ static int run_generate(q4hip* h, int first, int pos, int steps, int* out, float
   HIPCHK(hipGetLastError());
   HIPCHK(hipMemcpyAsync(h->pin_ids, h->tokens + pos + 1, (size_t)steps * 4, hipMemcpyDeviceToHost, h->stream));
   HIPCHK(hipStreamSynchronize(h->stream));
-  if (pers && aborted(h)) return run_generate(h, first, pos, steps, out, ms);
-  memcpy(out, h->pin_ids, (size_t)steps * 4);
+  const hipError_t te = ms ? hipEventElapsedTime(ms, e0, e1) : hipSuccess;
   if (ms) {
-    HIPCHK(hipEventElapsedTime(ms, e0, e1));
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
   }
+  if (pers && aborted(h)) return run_generate(h, first, pos, steps, out, ms);
+  HIPCHK(te);
+  memcpy(out, h->pin_ids, (size_t)steps * 4);
   return Q4HIP_OK;
 }
 

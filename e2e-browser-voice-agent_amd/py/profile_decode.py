@@ -155,7 +155,7 @@ def summarize(a) -> None:
         dram_b = sum(pdr) / len(pdr) * bytes_per_req
         traffic["dram_read_bytes_per_step"] = dram_b / steps
         traffic["dram_read_share_of_requests"] = sum(pdr) / sum(prq)
-        lines[-1:-1] = [
+        lines += [
             "",
             f"`TCC_EA0_RDREQ_DRAM_sum` (L2 read requests sent to the memory side) per launch: {sum(pdr) / len(pdr):.4g}, "
             f"{sum(pdr) / sum(prq):.4f} of all L2 read requests (`TCC_EA0_RDREQ_sum`); the 256 MiB copy reads "
