@@ -235,33 +235,37 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
 #pragma unroll
   for (int c = 0; c < NJ; c++) acc[c][0] = acc[c][1] = acc[c][2] = acc[c][3] = 0.0f;
 
-  // One group: every shared-memory read of the group first, then its 4 NJ matrix-core products,
-  // then the chain updates in block order (a wave pays the read and product latencies once per
-  // group, not once per block).
-  auto compute = [&](const unsigned char* slot, int g) {
+  // What one group needs from its ring slot, in registers.
+  struct Regs {
+    uint2 sc;              // the 4 fp16 weight scales of this lane's row
+    uint4 wq[NJ];          // weight words of the 4 blocks, per chain
+    uint2 aw[4][NJ];       // fp16 operands, per block and chain
+    float4 dx[4];          // the 4 tokens' block scales, per block
+  };
+  auto read = [&](const unsigned char* slot, Regs& G) {
     const uint2* acts = reinterpret_cast<const uint2*>(slot);
     const float4* dxs = reinterpret_cast<const float4*>(slot + S::oDX);
     const uint4* qss = reinterpret_cast<const uint4*>(slot + S::oQS);
     const uint2* scs = reinterpret_cast<const uint2*>(slot + S::oSC);
-    const uint2 sc = scs[wrow];
-    uint4 wq[NJ];
-    if (JS == 4) wq[0] = qss[wave * 16 + li];
+    G.sc = scs[wrow];
+    if (JS == 4) G.wq[0] = qss[wave * 16 + li];
     else {
 #pragma unroll
-      for (int c = 0; c < 4; c++) wq[c] = qss[c * 64 + wrow];
+      for (int c = 0; c < 4; c++) G.wq[c] = qss[c * 64 + wrow];
     }
-    uint2 aw[4][NJ];
-    float4 dx[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      dx[k] = dxs[k * 4 + kg];
+      G.dx[k] = dxs[k * 4 + kg];
 #pragma unroll
-      for (int c = 0; c < NJ; c++) aw[k][c] = acts[((k * 4 + (JS == 4 ? wave : c)) * 4 + kg) * 16 + li];
+      for (int c = 0; c < NJ; c++) G.aw[k][c] = acts[((k * 4 + (JS == 4 ? wave : c)) * 4 + kg) * 16 + li];
     }
+  };
+  // The 4 NJ matrix-core products of group g, then the chain updates in block order.
+  auto compute = [&](const Regs& G, int g) {
     auto update = [&](int k, const sk_f4 (&d)[NJ]) {
-      const uint32_t sw = (k >> 1) == 0 ? sc.x : sc.y;
+      const uint32_t sw = (k >> 1) == 0 ? G.sc.x : G.sc.y;
       const float dw = half_bits_to_float((k & 1) ? (sw >> 16) : (sw & 0xffffu));
-      const float s0 = dw * dx[k].x, s1 = dw * dx[k].y, s2 = dw * dx[k].z, s3 = dw * dx[k].w;
+      const float s0 = dw * G.dx[k].x, s1 = dw * G.dx[k].y, s2 = dw * G.dx[k].z, s3 = dw * G.dx[k].w;
 #pragma unroll
       for (int c = 0; c < NJ; c++) {
         acc[c][0] = acc[c][0] + d[c][0] * s0;
@@ -273,8 +277,8 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
     auto product = [&](int k, sk_f4 (&d)[NJ]) {
 #pragma unroll
       for (int c = 0; c < NJ; c++) {
-        const uint32_t wv = k == 0 ? wq[c].x : k == 1 ? wq[c].y : k == 2 ? wq[c].z : wq[c].w;
-        d[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(sk_h4, aw[k][c]), bop(wv),
+        const uint32_t wv = k == 0 ? G.wq[c].x : k == 1 ? G.wq[c].y : k == 2 ? G.wq[c].z : G.wq[c].w;
+        d[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(sk_h4, G.aw[k][c]), bop(wv),
                                                      (sk_f4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
       }
     };
@@ -298,16 +302,47 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
 
 #pragma unroll
   for (int p = 0; p < R - 1; p++) sk_issue<JS>(ring[p], src, p);
-  for (int g0 = 0; g0 < ng; g0 += R) {
+  if (JS == 4) {
+    // Software pipeline over groups (JS 4; the 64-row layout has no registers to spare for it):
+    // after the barrier that frees group g's slot, a wave reads group g + 1's operands from shared
+    // memory, then computes group g from registers read one step earlier.  R is even, so group g
+    // uses register set g & 1 in every pass of the unrolled loop.
+    static_assert(R % 2 == 0, "register sets alternate with the group parity");
+    Regs G[2];
+    sk_sync<5 * (R - 2)>();                                  // group 0 has landed
+    sk_issue<JS>(ring[R - 1], src, R - 1);
+    read(ring[0], G[0]);
+    for (int g0 = 0; g0 < ng; g0 += R) {
 #pragma unroll
-    for (int u = 0; u < R; u++) {
-      const int g = g0 + u;
-      if (g < ng) {
-        // group g's loads were followed by those of R - 2 groups
-        sk_sync<5 * (R - 2)>();
-        // the slot of group g - 1 is free: every wave has passed the barrier after computing it
-        sk_issue<JS>(ring[(u + R - 1) % R], src, g + R - 1);
-        compute(ring[u], g);
+      for (int u = 0; u < R; u++) {
+        const int g = g0 + u;
+        if (g < ng) {
+          // groups g + 1 .. g + R - 1 are in flight: wait for g + 1; after the barrier every wave
+          // has read group g's slot, which then takes group g + R
+          sk_sync<5 * (R - 2)>();
+          // the same wait in a form the compiler's wait tracking sees: the registers read in the
+          // previous step are ready, so computing from them does not wait for the reads below
+          __builtin_amdgcn_s_waitcnt(0xC07F);                // lgkmcnt(0)
+          sk_issue<JS>(ring[u], src, g + R);
+          read(ring[(u + 1) % R], G[(u + 1) & 1]);
+          compute(G[u & 1], g);
+        }
+      }
+    }
+  } else {
+    for (int g0 = 0; g0 < ng; g0 += R) {
+#pragma unroll
+      for (int u = 0; u < R; u++) {
+        const int g = g0 + u;
+        if (g < ng) {
+          // group g's loads were followed by those of R - 2 groups
+          sk_sync<5 * (R - 2)>();
+          // the slot of group g - 1 is free: every wave has passed the barrier after computing it
+          sk_issue<JS>(ring[(u + R - 1) % R], src, g + R - 1);
+          Regs G;
+          read(ring[u], G);
+          compute(G, g);
+        }
       }
     }
   }

@@ -802,11 +802,25 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
                                                       const KT* __restrict__ vc, int ctx, int layer,
                                                       float* __restrict__ att, int D, const int* __restrict__ pos,
                                                       size_t seq_stride, uint4* __restrict__ xq, int xstride,
-                                                      uint4* __restrict__ xh) {
+                                                      uint4* __restrict__ xh, bool xcd_group) {
   extern __shared__ __attribute__((aligned(16))) float lsm[];
   constexpr int CRS = CR + 4, NV = CR * kPvCols / 4 / 256;      // chunk rows (LDS stride), float4 per thread
   constexpr int PB = 2;                   // score float4 per thread and head in one pass (2048 positions)
-  const int c0 = blockIdx.x * kPvCols, g = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  constexpr int S = HD / kPvCols;         // column slices of a (sequence, kv head)
+  // Workgroup L runs on XCD L mod 8.  With xcd_group the S slices of one (sequence, kv head) get
+  // ids of one residue, so they share that XCD's L2: a V row's cache lines are fetched once, not
+  // once per slice that touches them (fp16 slices are half a line).
+  const int L = blockIdx.x;
+  int slice, unit;
+  if (xcd_group) {
+    const int x = L % kXcds, k = L / kXcds;
+    unit = (k / S) * kXcds + x;
+    slice = k % S;
+  } else {
+    unit = L / S;
+    slice = L % S;
+  }
+  const int c0 = slice * kPvCols, g = unit % KVH, b = unit / KVH, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, G = H / KVH;
   const int T = pos[b] + 1, TS = pv_row_stride(ctx), nch = (T + CR - 1) / CR, CS = score_stride(ctx);
   const int T4 = (T + 3) >> 2;
@@ -1425,14 +1439,17 @@ void launch_attn_list_t(hipStream_t s, int HD, int B, int H, int KVH, const floa
                         const KT* vc, int ctx, int layer, float* sc, float* att, int D, const int* pos,
                         size_t seq_stride, uint4* xq, int xstride, uint4* xh) {
   const dim3 sg((unsigned)((ctx + kScoreRows - 1) / kScoreRows), (unsigned)KVH, (unsigned)B);
-  const dim3 pg((unsigned)(HD / kPvCols), (unsigned)KVH, (unsigned)B);
+  const unsigned units = (unsigned)KVH * (unsigned)B, pg = units * (unsigned)(HD / kPvCols);
+  const bool xcd_group = units % kXcds == 0;
   const size_t lds = attn_pv_lds(H, KVH, ctx);
   if (HD == 64) {
     k_attn_scores_list<64, KT><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, seq_stride);
-    k_attn_pv_list<64, kPvRows, KT><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride, xq, xstride, xh);
+    k_attn_pv_list<64, kPvRows, KT><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride, xq, xstride, xh,
+                                                         xcd_group);
   } else {
     k_attn_scores_list<128, KT><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, seq_stride);
-    k_attn_pv_list<128, kPvRows, KT><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride, xq, xstride, xh);
+    k_attn_pv_list<128, kPvRows, KT><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride, xq, xstride, xh,
+                                                          xcd_group);
   }
 }
 
