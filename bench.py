@@ -18,7 +18,7 @@ timed on the host cores as the CPU baseline.
 Other workloads of the same model (one JSON line each, same keys):
   --workload long-context  batch-1 decode after a 4096-position cache filled with seeded fp16-valued
                            K/V (written through q4hip_set_kv), 256 greedy steps by default
-                           (stored fp32 by default; --kv-cache f16 stores it as fp16)
+                           (fp16 K/V cache by default; --kv-cache f32 for the reference's cache type)
   --workload prefill       one 1024-token seeded prompt per step
   --workload matvec        the isolated Q4_0 matvec at the model's five shapes, 1000 launches each
   --workload batched       32 independent sequences on the Qwen2.5-1.5B shape, each after a
@@ -171,13 +171,11 @@ def main():
     ap.add_argument("--no-node", action="store_true", help="skip the Node.js host leg of the decode workload")
     ap.add_argument("--kv-cache", default=None, choices=["f32", "f16"],
                     help="K/V cache storage of the long-context and batched workloads: f16 (half the K/V "
-                         "bytes; parity against the oracle with the same fp16 rounding; the batched "
-                         "default) or f32 (the reference's cache type; the long-context default, since "
-                         "the persistent kernel streams fp32 rows past its staged tile and an fp16 cache "
-                         "of 4096 positions decodes on the graph path)")
+                         "bytes; parity against the oracle with the same fp16 rounding; the default, as "
+                         "both configurations name an fp16 cache) or f32 (the reference's cache type)")
     args = ap.parse_args()
     if args.kv_cache is None:
-        args.kv_cache = "f16" if args.workload == "batched" else "f32"
+        args.kv_cache = "f16" if args.workload in ("batched", "long-context") else "f32"
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the batch-1 decode loop runs on a single device "
               "(multi-GPU sharding is not run)", file=sys.stderr)
@@ -323,8 +321,8 @@ def fill_cache(shape, P, seed=SEED):
 
 
 def bench_long_context(args):
-    """Decode after a 4096-position cache of seeded fp16-valued K/V (stored fp32, as the reference's
-    cache is): the attention role streams past rows through its LDS ring."""
+    """Decode after a 4096-position cache of seeded fp16 K/V (an fp16 cache by default, fp32 with
+    --kv-cache f32): the attention role streams past rows through its LDS ring."""
     import q4hip
     import synth
     shape = synth.SHAPES["qwen2.5-0.5b"]

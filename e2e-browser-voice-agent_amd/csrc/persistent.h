@@ -668,7 +668,7 @@ struct PSmem {
   float* argv;    // 8
   int* argi;      // 8
   uint32_t* raw;  // RAW words: exchange entries
-  float* terms;   // last: 64 * NBM per-block terms (OD); for the attention role its ctx + kRingRows
+  float* terms;   // last: 64 * NBM per-block terms (OD); for the attention role its ctx + 2 kRingRows
                   // scores, then its K/V ring and staged tile
 };
 
@@ -707,9 +707,9 @@ constexpr size_t psmem_base_bytes() {
   return psmem_terms_offset<S>() + (size_t)64 * S::NBM * 4;
 }
 
-// What the attention role uses: its scores and their exponentials (ctx + kRingRows floats each,
+// What the attention role uses: its scores and their exponentials (ctx + 2 kRingRows floats each,
 // 16-byte aligned), then the ring and the staged tile.  They overlap the other roles' term buffer, not anything it shares.
-__host__ __device__ constexpr size_t attn_scores_floats(int ctx) { return (size_t)((ctx + kRingRows + 32 + 3) & ~3); }
+__host__ __device__ constexpr size_t attn_scores_floats(int ctx) { return (size_t)((ctx + 2 * kRingRows + 32 + 3) & ~3); }
 
 template <class S>
 constexpr size_t psmem_attn_bytes(int ctx, int ring_slots, int kv_tile) {
@@ -1062,6 +1062,21 @@ __device__ __forceinline__ void ring_issue(const float* src, int t0, int ctx, fl
     __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + i * 256), 16, 0, 0);
   }
 }
+// fp16 rows: a slot holds 2 kRingRows rows (the same 12 instructions, 8 rows each), row r at
+// half 64 r of the slot.
+__device__ __forceinline__ void ring_issue(const kvhalf* src, int t0, int ctx, float* slot) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+#pragma unroll
+  for (int k = 0; k < 3; k++) {
+    const int i = wave + 4 * k;
+    const int t = t0 + 8 * i + (lane >> 3);
+    const kvhalf* g = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + 8 * (lane & 7);
+    __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + i * 256), 16, 0, 0);
+  }
+}
+// Rows of a P.V ring slot: kRingRows fp32 rows or twice as many fp16 rows in the same bytes.
+template <class KT>
+__host__ __device__ constexpr int vslot_rows() { return sizeof(KT) == 4 ? kRingRows : 2 * kRingRows; }
 
 // One wave's loads of K rows [t0, t0 + 16) into a chunk slot, one 4-row group per instruction at
 // slot + g * kGrpFloats.  An instruction places lane l's 16 bytes at float 4 l of its group, and
@@ -1079,10 +1094,44 @@ __device__ __forceinline__ void ring_issue_kc(const float* src, int t0, int ctx,
   }
 }
 
+// The same for an fp16 cache: 16 rows of 128 bytes in two instructions of 8 rows.  Lane l of
+// instruction h fetches bytes 16 c .. 16 c + 15 (c = l >> 3) of row 8 h + (l & 7); instruction h
+// lands at byte 1152 h of the chunk (a 128-byte pad between the two), lane l at 16 l.  Row r's
+// piece c then sits at byte 1152 (r >> 3) + 128 c + 16 (r & 7): for one c the 16 rows start in 16
+// distinct 16-byte bank groups, so the reads below (element 4i + j of a row by lane j) are free of
+// conflicts.  2304 bytes of the chunk's kChunkFloats.
+constexpr int kChunk16Bytes = 2304;
+static_assert(kChunk16Bytes <= kChunkFloats * 4, "fp16 chunk exceeds the chunk slot");
+__device__ __forceinline__ void ring_issue_kc(const kvhalf* src, int t0, int ctx, float* slot) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int t = t0 + 8 * h + (lane & 7);
+    const kvhalf* p = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + 8 * (lane >> 3);
+    __builtin_amdgcn_global_load_lds((GlobalVoid*)p, (LdsVoid*)((char*)slot + 1152 * h), 16, 0, 0);
+  }
+}
+
+// Element 4i + pj (i = 0..15) of row pr of a chunk, as fp32: fp32 chunks in ring_issue_kc's group
+// layout, fp16 chunks in the layout above.
+__device__ __forceinline__ void kchunk_row(const float* chunk, int pr, int pj, float (&kr)[kHD / 4]) {
+  const float* row = chunk + (pr >> 2) * kGrpFloats + 4 * (pr & 3) + pj;
+#pragma unroll
+  for (int i = 0; i < kHD / 4; i++) kr[i] = row[16 * i];
+}
+__device__ __forceinline__ void kchunk_row16(const float* chunk, int pr, int pj, float (&kr)[kHD / 4]) {
+  const unsigned short* hb = reinterpret_cast<const unsigned short*>(
+      reinterpret_cast<const char*>(chunk) + 1152 * (pr >> 3) + 16 * (pr & 7) + 2 * pj);
+#pragma unroll
+  for (int i = 0; i < kHD / 4; i++) kr[i] = half_bits_to_float(hb[64 * (i >> 1) + 4 * (i & 1)]);
+}
+
 // Wait until this wave's loads of its oldest K chunk in flight have landed (`cs` - 2 newer chunks
-// of 4 instructions may still be outstanding).  Only the issuing wave reads a chunk: no barrier.
+// of N instructions -- 4 for fp32 rows, 2 for fp16 -- may still be outstanding).  Only the
+// issuing wave reads a chunk: no barrier.
+template <int N>
 __device__ __forceinline__ void kchunk_wait(int cs) {
-  if (cs == 5) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  if (cs == 5) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * N) : "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
@@ -1113,10 +1162,24 @@ __device__ __forceinline__ void ring_issue_vp(const float* src, int t0, int ctx,
   }
 }
 
-// A producer wave's wait for its own rows of the oldest slot in flight (d - 1 newer slots of 4
-// instructions may still be outstanding).
+// fp16 rows: producer pw's 32 rows x 32 halves (2 KB) in 2 instructions of 16 rows, landing in
+// the upper half of its 4 KB part (byte 2048 + 64 r + 2 col); it reads them all before it writes
+// the fp32 products over the part.
+__device__ __forceinline__ void ring_issue_vp(const kvhalf* src, int t0, int ctx, int c0, int pw, float* slot) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int t = t0 + 32 * pw + 16 * k + (lane >> 2);
+    const kvhalf* g = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + c0 + 8 * (lane & 3);
+    __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + pw * 1024 + 512 + k * 256), 16, 0, 0);
+  }
+}
+
+// A producer wave's wait for its own rows of the oldest slot in flight (d - 1 newer slots of N
+// instructions -- 4 for fp32 rows, 2 for fp16 -- may still be outstanding).
+template <int N>
 __device__ __forceinline__ void vpart_wait(int d) {
-  if (d == 5) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  if (d == 5) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * N) : "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
@@ -1241,20 +1304,21 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
 template <class S, class KT>
 __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int pos, int tok,
                                           bool& bad) {
-  // the ring and the pair split stream fp32 rows (fp16 caches are staged whole: the host admits
-  // them only when the context fits the staged tile)
-  constexpr bool kStream = sizeof(KT) == 4;
+  constexpr bool kF16 = sizeof(KT) == 2;   // fp16 rows stream in half the bytes (same ring memory)
+  constexpr int VR = vslot_rows<KT>();       // rows of a P.V ring slot
+  constexpr int NKC = kF16 ? 2 : 4;          // load instructions per K chunk
+  constexpr int NVP = kF16 ? 2 : 4;          // per producer and half-width V slot
   constexpr int GRP = S::H / S::KVH;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), r = lane >> 2, j = lane & 3;
   const int E = 4 * a.NL + 1;
   const int aidx = blockIdx.x - S::nOD, h = aidx % S::H, half = aidx / S::H, kh = h / GRP;
-  const bool split = kStream && a.asplit > 1;
+  const bool split = a.asplit > 1;
   const bool mark = aidx == 0;
   const int rq = (h * kHD) / 16 + wave;
   float* qv = m.qv;
   float* kv = m.qv + 64;
   float* vv = m.qv + 128;
-  float* sc = m.terms;                                     // ctx + kRingRows scores
+  float* sc = m.terms;                                     // ctx + 2 kRingRows scores
   float* ee = sc + attn_scores_floats(a.ctx);              // their exponentials
   float* ring = ee + attn_scores_floats(a.ctx);            // a.ring slots of kRingRows rows
   const int vstride = kv_vstride(a.kv_tile);
@@ -1314,12 +1378,12 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     // past positions [kbeg, kend) stream through the ring: for the scores in 16-row chunks, wave w
     // taking chunks w, w + 4, ... through its own ring of cs slots (the first ones load during the
     // wait for x); for P.V in slots of kRingRows (or kVRows) rows
-    const int nstream = kend - kbeg, nck = kStream ? (nstream + kRingRows - 1) / kRingRows : 0;
+    const int nstream = kend - kbeg, nck = (nstream + VR - 1) / VR;
     const int nkc = (nstream + 15) / 16, nloc = nkc > wave ? (nkc - wave + 3) / 4 : 0;
     const int cs = kchunk_slots(a.ring);
     float* wring = ring + (size_t)wave * cs * kChunkFloats;
-    const float* kgl = (const float*)a.kc + cbase;    // fp32 caches only (kStream)
-    const float* vgl = (const float*)a.vc + cbase;
+    const KT* kgl = (const KT*)a.kc + cbase;
+    const KT* vgl = (const KT*)a.vc + cbase;
     if (nloc > 0)
       for (int j = 0; j < cs - 1; j++)
         ring_issue_kc(kgl, kbeg + 16 * (4 * (j < nloc ? j : nloc - 1) + wave), a.ctx, wring + (size_t)j * kChunkFloats);
@@ -1401,12 +1465,12 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
 #pragma unroll
         for (int i = 0; i < kHD / 4; i++) qj[i] = qv[4 * i + pj];
         for (int j = 0; j < nloc; j++) {
-          kchunk_wait(cs);
-          // element 4i + pj of chunk row pr (ring_issue_kc's group layout)
-          const float* row = wring + (size_t)(j % cs) * kChunkFloats + (pr >> 2) * kGrpFloats + 4 * (pr & 3) + pj;
+          kchunk_wait<NKC>(cs);
+          // element 4i + pj of chunk row pr
+          const float* chunk = wring + (size_t)(j % cs) * kChunkFloats;
           float kr[kHD / 4];
-#pragma unroll
-          for (int i = 0; i < kHD / 4; i++) kr[i] = row[16 * i];
+          if (kF16) kchunk_row16(chunk, pr, pj, kr);
+          else kchunk_row(chunk, pr, pj, kr);
           // all 16 reads in flight before the first use (else one LDS round trip per step)
           asm volatile("" : "+v"(kr[0]), "+v"(kr[1]), "+v"(kr[2]), "+v"(kr[3]), "+v"(kr[4]), "+v"(kr[5]),
                        "+v"(kr[6]), "+v"(kr[7]), "+v"(kr[8]), "+v"(kr[9]), "+v"(kr[10]), "+v"(kr[11]),
@@ -1434,7 +1498,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       // the ring is free: the first V slots stream in while exp, sum and division run
       if (!split)
         for (int c = 0; c < R - 1; c++)
-          ring_issue(vgl, nt + (c < nck ? c : nck - 1) * kRingRows, a.ctx, ring + (size_t)c * kSlotFloats);
+          ring_issue(vgl, nt + (c < nck ? c : nck - 1) * VR, a.ctx, ring + (size_t)c * kSlotFloats);
     }
     const int nckv = split ? (pos + kVRows - 1) / kVRows : 0;     // split P.V: half-width V slots
     if (split) {
@@ -1568,15 +1632,17 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       if (wave != 0) {
         const int pw = wave - 1;
         for (int c = 0; c < nckv; c++) {
-          vpart_wait(D);
+          vpart_wait<NVP>(D);
           float* part = ring + (size_t)(c % R) * kSlotFloats + pw * 1024;
           const float* pc = sc + c * kVRows + 32 * pw;
+          const unsigned short* ph = reinterpret_cast<const unsigned short*>(part + 512);   // fp16 rows
           float pv[16], vx[16];
 #pragma unroll
           for (int k = 0; k < 16; k++) {
             pv[k] = pc[(lane + 64 * k) >> 5];
-            vx[k] = part[lane + 64 * k];
+            vx[k] = kF16 ? half_bits_to_float(ph[lane + 64 * k]) : part[lane + 64 * k];
           }
+          asm volatile("" ::: "memory");     // every read of the part (fp16 rows included) before any write
 #pragma unroll
           for (int k = 0; k < 16; k++) part[lane + 64 * k] = pv[k] * vx[k];
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1648,24 +1714,32 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
         ring_sync(R);
         if (tid < kHD) {
           const float* slot = ring + (size_t)(c % R) * kSlotFloats + tid;
-          const float* pc = sc + nt + c * kRingRows;
-          const int n = nstream - c * kRingRows;
-          float pv[kRingRows], vx[kRingRows];
+          const unsigned short* slot16 = reinterpret_cast<const unsigned short*>(ring + (size_t)(c % R) * kSlotFloats) + tid;
 #pragma unroll
-          for (int u = 0; u < kRingRows; u++) { pv[u] = pc[u]; vx[u] = slot[u * kHD]; }
-          if (n >= kRingRows) {                // a full slot: no select on the chain
-#pragma unroll
-            for (int u = 0; u < kRingRows; u++) accv = accv + pv[u] * vx[u];
-          } else {
+          for (int hf = 0; hf < VR / kRingRows; hf++) {    // kRingRows rows at a time
+            const int r0 = hf * kRingRows;
+            const float* pc = sc + nt + c * VR + r0;
+            const int n = nstream - c * VR - r0;
+            float pv[kRingRows], vx[kRingRows];
 #pragma unroll
             for (int u = 0; u < kRingRows; u++) {
-              const float t = accv + pv[u] * vx[u];
-              accv = u < n ? t : accv;
+              pv[u] = pc[u];
+              vx[u] = kF16 ? half_bits_to_float(slot16[(r0 + u) * kHD]) : slot[(r0 + u) * kHD];
+            }
+            if (n >= kRingRows) {                // full rows: no select on the chain
+#pragma unroll
+              for (int u = 0; u < kRingRows; u++) accv = accv + pv[u] * vx[u];
+            } else {
+#pragma unroll
+              for (int u = 0; u < kRingRows; u++) {
+                const float t = accv + pv[u] * vx[u];
+                accv = u < n ? t : accv;
+              }
             }
           }
         }
         const int cn = c + R - 1;
-        ring_issue(vgl, nt + (cn < nck ? cn : nck - 1) * kRingRows, a.ctx, ring + (size_t)(cn % R) * kSlotFloats);
+        ring_issue(vgl, nt + (cn < nck ? cn : nck - 1) * VR, a.ctx, ring + (size_t)(cn % R) * kSlotFloats);
       }
       ring_drain();
     }

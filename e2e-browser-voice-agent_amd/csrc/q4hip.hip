@@ -1631,7 +1631,6 @@ void setup_persistent(q4hip* h) {
     if (need(ring, 0) > budget) return no("shared memory too small for the K/V ring");
     while (kv_tile > 0 && need(ring, kv_tile) > budget) kv_tile--;
   }
-  if (h->kv16 && ring > 0) return no("an fp16 K/V cache longer than the staged tile");
   h->pers_kv_tile = kv_tile;
   h->pers_ring = ring;
   h->pers_lds = need(ring, kv_tile);

@@ -32,16 +32,18 @@ def _bits(a):
 MODES = ["graph", "persistent"]
 
 
-def _pair(name, seed, ctx, mt=0, threads=8, mode="graph", head_type=synth.GGML_Q4_0):
+def _pair(name, seed, ctx, mt=0, threads=8, mode="graph", head_type=synth.GGML_Q4_0, kv="f32"):
     """The library with passes of `mt` tokens (0: its default, whole prompts up to 1024) and the
-    oracle with the reference's 16-token chunks."""
+    oracle with the reference's 16-token chunks; kv "f16": both with the fp16 K/V cache."""
     import q4hip
     shape = synth.SHAPES[name]
     t = _model(name, seed, head_type)
-    g = q4hip.Model(shape, ctx=ctx, mt=mt)
+    g = q4hip.Model(shape, ctx=ctx, mt=mt, kv_type=q4hip.KV_F16 if kv == "f16" else q4hip.KV_F32)
     g.load(t)
     g.set_decode_mode(q4hip.DECODE_PERSISTENT if mode == "persistent" else q4hip.DECODE_GRAPH)
     o = oracle.Model(shape, t, ctx=ctx, mt=16, threads=threads)
+    if kv == "f16":
+        o.set_variant(oracle.V_KV_F16)
     return shape, g, o
 
 
@@ -244,22 +246,24 @@ def _fill_kv(shape, P, seed):
     return k, v
 
 
+@pytest.mark.parametrize("kv", ["f32", "f16"])
 @pytest.mark.parametrize("mode,tile,split,P,ctx", [("graph", None, None, 500, 640), ("persistent", None, None, 500, 640),
                                                     ("persistent", "16", None, 500, 640), ("persistent", "0", None, 500, 640),
                                                     ("persistent", None, "0", 500, 640), ("persistent", None, None, 1500, 1600),
-                                                    ("persistent", None, "0", 1500, 1600)])
-def test_prefilled_cache_long_context(mode, tile, split, P, ctx, monkeypatch):
+                                                    ("persistent", None, "0", 1500, 1600), ("persistent", "0", "100000", 1500, 1600)])
+def test_prefilled_cache_long_context(mode, tile, split, P, ctx, kv, monkeypatch):
     """Decode over a cache of P positions written through q4hip_set_kv (the reference's host-owned
     kc/vc, kernels.c:433-440): positions past the attention role's staged tile are streamed from
-    HBM (through 3 ring slots up to ctx 1024, 7 beyond); logits and tokens equal the oracle's with
-    the same cache."""
+    HBM (through 3 ring slots up to ctx 1024, 7 beyond), as fp32 rows or as fp16 rows (half the
+    bytes, their own chunk and slot layouts); logits and tokens equal the oracle's with the same
+    cache."""
     import q4hip
     if tile is not None:
         monkeypatch.setenv("Q4HIP_KV_TILE", tile)
     if split is not None:                       # two attention workgroups per head from position `split`
         monkeypatch.setenv("Q4HIP_SPLIT_FROM", split)
-    print(f"prefilled cache mode {mode} tile {tile} split {split} positions {P} ctx {ctx}", flush=True)
-    shape, g, o = _pair("small", 31, ctx=ctx, mode=mode)
+    print(f"prefilled cache mode {mode} kv {kv} tile {tile} split {split} positions {P} ctx {ctx}", flush=True)
+    shape, g, o = _pair("small", 31, ctx=ctx, mode=mode, kv=kv)
     try:
         k, v = _fill_kv(shape, P, 31)
         ok, ov = o.kv()
@@ -465,8 +469,8 @@ def test_fp16_kv_matches_oracle(name, seed, n_prompt, mode):
 
 def test_fp16_kv_long_context_qwen05b_4096():
     """The long-context workload with the fp16 cache: Qwen2.5-0.5B shape, 4096 cached fp16 K/V
-    positions (seeded N(0, 1), written through q4hip_set_kv), then 16 decode steps (the cache is
-    longer than the persistent kernel's staged tile, so they run on the graph path).  Tokens and
+    positions (seeded N(0, 1), written through q4hip_set_kv), then 16 decode steps on the persistent
+    kernel (two attention workgroups per head, fp16 rows streamed through the ring).  Tokens and
     logits equal the fp16-cache oracle's at every step; the distance from the fp32-cache oracle
     (whose new rows are not rounded) is printed, not asserted: a rounded row flips int8
     activation roundings downstream, so it exceeds 1e-3 (oracle/reassoc_study.py measures it)."""
@@ -498,6 +502,7 @@ def test_fp16_kv_long_context_qwen05b_4096():
             worst = max(worst, float(np.max(np.abs(g.read_logits() - o32.logits()))))
             tok = ng
         print(f"max-abs logit distance from the fp32-cache oracle over {steps} steps: {worst:.4g}", flush=True)
+        assert g.decode_mode_used() == q4hip.DECODE_PERSISTENT
     finally:
         g.close()
         o.close()
