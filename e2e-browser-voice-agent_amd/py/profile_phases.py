@@ -2,6 +2,7 @@
 
     python profile_phases.py                   # Qwen2.5-0.5B shape, 64-token prompt, steps from position 64
     python profile_phases.py --positions 4096  # the same after a 4096-position cache of seeded fp16-valued K/V
+    python profile_phases.py --positions 4096 --kv-cache f16   # ... stored as an fp16 cache
 
 Prints, for the middle layers (median over layers 1 .. L-2), when each role's phases end, in microseconds after
 the last down-projection store of the previous layer: the per-workgroup timestamps (min / median / max over the
@@ -48,11 +49,12 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--positions", type=int, default=0, help="cached positions (0: the 64-token prompt)")
     ap.add_argument("--runs", type=int, default=5)
+    ap.add_argument("--kv-cache", default="f32", choices=["f32", "f16"], help="K/V cache storage")
     args = ap.parse_args()
     shape = synth.SHAPES["qwen2.5-0.5b"]
     L = shape.layers
     P = args.positions
-    m = q4hip.Model(shape, ctx=max(256, P + 40))
+    m = q4hip.Model(shape, ctx=max(256, P + 40), kv_type=q4hip.KV_F16 if args.kv_cache == "f16" else q4hip.KV_F32)
     m.load(synth.make_model(shape, 1))
     m.set_decode_mode(q4hip.DECODE_PERSISTENT)
     if P:

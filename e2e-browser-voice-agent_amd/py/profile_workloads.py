@@ -95,7 +95,11 @@ def _rows(d: str, pattern: str):
 def _short(name: str) -> str:
     if name.startswith("_Z"):                 # some trace names come mangled
         try:
-            name = subprocess.run(["c++filt", name], capture_output=True, text=True, timeout=10).stdout.strip() or name
+            # c++filt may not know _Float16 (DF16_): demangle it as half (Dh) and rename that back
+            alias = name.replace("DF16_", "Dh")
+            out = subprocess.run(["c++filt", alias], capture_output=True, text=True, timeout=10).stdout.strip()
+            if out and not out.startswith("_Z"):
+                name = out.replace("half", "_Float16") if alias != name else out
         except (OSError, subprocess.SubprocessError):
             pass
     if name.startswith("_Z"):                 # c++filt without _Float16 support: the bare name
