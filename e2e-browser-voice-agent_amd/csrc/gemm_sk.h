@@ -88,14 +88,26 @@ struct SkSrc {
   static __device__ __forceinline__ int row_of(int R0, int ffn, int l) {
     return ffn > 0 ? (l < 32 ? R0 + l : ffn + R0 + l - 32) : R0 + l;
   }
-  __device__ __forceinline__ SkSrc(const Q4Mat& W, const uint4* xt, int xstride, int T, int R0, int ffn = 0) {
+  // JS 4 with RoPE pairs (hd > 0, the fused qkv projection): row group rg of a head of hd rows
+  // holds rows 8p .. 8p + 7 of the head's first half (local rows 0..7) and the matching rows of its
+  // second half (local rows 8..15), so each RoPE pair (i, i + hd/2) meets in one workgroup.
+  static __device__ __forceinline__ int rope_row(int rg, int hd, int l) {
+    const int gpr = hd >> 4, head = rg / gpr, p = rg - head * gpr;
+    return head * hd + (l < 8 ? 8 * p + l : (hd >> 1) + 8 * p + l - 8);
+  }
+  __device__ __forceinline__ SkSrc(const Q4Mat& W, const uint4* xt, int xstride, int T, int R0, int ffn = 0,
+                                   int hd = 0) {
     lane = threadIdx.x & 63;
     wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     nb = W.nb;
     ng = W.ng;
     act = xt + (size_t)T * xstride * kXhBlock;
     const int tile = R0 >> 6, rr0 = R0 & 63;
-    if (JS == 4) {
+    if (JS == 4 && hd > 0) {
+      const int rq = rope_row(R0 >> 4, hd, lane & 15), rs = rope_row(R0 >> 4, hd, 4 * wave + ((lane >> 1) & 3));
+      qs = W.qs + ((size_t)(rq >> 6) * ng * 64 + (rq & 63)) * 4 + wave;
+      sc = reinterpret_cast<const uint32_t*>(W.d + (size_t)(rs >> 6) * W.nb8 * 64 + (rs & 63)) + (lane & 1);
+    } else if (JS == 4) {
       qs = W.qs + ((size_t)tile * ng * 64 + rr0 + (lane & 15)) * 4 + wave;
       sc = reinterpret_cast<const uint32_t*>(W.d + (size_t)tile * W.nb8 * 64 + rr0 + 4 * wave + ((lane >> 1) & 3)) +
            (lane & 1);
@@ -200,6 +212,18 @@ __device__ __forceinline__ void sk_put(float* y, int ldy, const float* bias, int
   }
 }
 
+// What the fused qkv epilogue (EPI 2) needs besides the projection: RoPE table, the caches and the
+// per-token positions of a batch of sequences (token m is sequence m).
+struct SkRope {
+  const float* rope = nullptr;   // [ctx][hd / 2][2] cos, sin
+  void* kc = nullptr;            // sequence m's cache at m * seq_stride: [layer][kv head][ctx][hd]
+  void* vc = nullptr;
+  const int* pos = nullptr;      // position of token m
+  size_t seq_stride = 0;
+  int ctx = 0, layer = 0, H = 0, KVH = 0, hd = 0;
+  bool kv16 = false;             // fp16 caches (else fp32)
+};
+
 // Grid sk_grid(row groups, ceil(M / 16)) (one-dimensional); R * SkSlot<JS>::BYTES of static shared memory.
 // xt: the fp16 operands and block scales in the 16-token tiles of quantize_item (kXhBlock).
 // The ring slots are R distinct shared arrays and the group loop is unrolled by R, so every slot
@@ -208,12 +232,18 @@ __device__ __forceinline__ void sk_put(float* y, int ldy, const float* bias, int
 // SwiGLU activation; the workgroup's waves 0, 1 take gate rows 32 b .. 32 b + 31 and waves 2, 3 the
 // matching up rows, and the epilogue writes act = SwiGLU(gate, up) quantized (block b of xq_out
 // and xh_out, what k_quant<QM_SWIGLU> writes) instead of y.
+// EPI = 2 (with JS 4): W is the q|k|v matrix of a batch step (OP_BIAS); row groups hold RoPE pairs
+// (SkSrc::rope_row) and the epilogue applies RoPE to the q and k heads at each token's position,
+// writes q to y and appends k and v to the token's sequence cache (what the bias projection
+// followed by k_rope_kv_list writes).
 template <int OP, int JS, int R, int EPI = 0>
 __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restrict__ xt, int xstride, int M,
                                                 float* __restrict__ y, int ldy, const float* __restrict__ bias,
                                                 bool by_tile, uint4* __restrict__ xq_out = nullptr,
-                                                uint4* __restrict__ xh_out = nullptr, int ffn = 0) {
-  static_assert(EPI == 0 || JS == 1, "the SwiGLU epilogue needs the 64-row layout");
+                                                uint4* __restrict__ xh_out = nullptr, int ffn = 0,
+                                                SkRope rp = SkRope()) {
+  static_assert(EPI != 1 || JS == 1, "the SwiGLU epilogue needs the 64-row layout");
+  static_assert(EPI != 2 || (JS == 4 && OP == 1), "the RoPE epilogue is the 16-row bias projection");
   using S = SkSlot<JS>;
   static_assert(R >= 3 && R <= 8, "ring depth");
   __shared__ __align__(16) unsigned char q0[S::BYTES], q1[S::BYTES], q2[S::BYTES], q3[S::BYTES], q4[S::BYTES],
@@ -228,7 +258,7 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
   const int R0 = EPI == 1 ? rgi * 32 : JS == 4 ? rgi * 16 : rgi * 64;
   const int ng = W.ng, nb = W.nb;
   const SkB bop(kg);
-  const SkSrc<JS> src(W, xt, xstride, T, R0, EPI == 1 ? ffn : 0);
+  const SkSrc<JS> src(W, xt, xstride, T, R0, EPI == 1 ? ffn : 0, EPI == 2 ? rp.hd : 0);
   constexpr int NJ = JS == 4 ? 1 : 4;
   const int wrow = JS == 4 ? li : 16 * wave + li;            // this lane's weight row in the workgroup
   float acc[NJ][4];
@@ -380,7 +410,35 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
     for (int r = 0; r < 4; r++) red[(wave * 16 + 4 * kg + r) * 16 + li] = acc[0][r];
     __syncthreads();
     const float v = ((red[tid] + red[256 + tid]) + red[512 + tid]) + red[768 + tid];
-    sk_put<OP>(y, ldy, bias, M, W.N, T * 16 + (tid >> 4), R0 + (tid & 15), v);
+    if (EPI == 2) {
+      // thread tid: token m = 16 T + tid / 16, local row l = tid % 16; rows l and l ^ 8 are a RoPE
+      // pair (kernels.c:337-352)
+      const int l = tid & 15, m = T * 16 + (tid >> 4), hd = rp.hd, half = hd >> 1;
+      const int row = SkSrc<4>::rope_row(rgi, hd, l);
+      const float x = v + (row < W.N ? bias[row] : 0.0f);
+      const float xo = __shfl_xor(x, 8);                     // the pair's other value, same token
+      if (m < M && row < W.N) {
+        const int head = row / hd, e = row - head * hd, i = e < half ? e : e - half;
+        const int p = rp.pos[m];
+        float out = x;
+        if (head < rp.H + rp.KVH) {
+          const float c = rp.rope[(size_t)p * hd + 2 * i], sn = rp.rope[(size_t)p * hd + 2 * i + 1];
+          out = e < half ? x * c - xo * sn : x * c + xo * sn;
+        }
+        if (head < rp.H) {
+          y[(size_t)m * ldy + row] = out;
+        } else {
+          const bool isv = head >= rp.H + rp.KVH;
+          const int kh = head - rp.H - (isv ? rp.KVH : 0);
+          const size_t off = (size_t)m * rp.seq_stride + (((size_t)rp.layer * rp.KVH + kh) * rp.ctx + p) * hd + e;
+          void* cache = isv ? rp.vc : rp.kc;
+          if (rp.kv16) reinterpret_cast<_Float16*>(cache)[off] = (_Float16)out;
+          else reinterpret_cast<float*>(cache)[off] = out;
+        }
+      }
+    } else {
+      sk_put<OP>(y, ldy, bias, M, W.N, T * 16 + (tid >> 4), R0 + (tid & 15), v);
+    }
   }
 }
 

@@ -1381,6 +1381,19 @@ bool launch_gu_swiglu(hipStream_t s, const Mat& W, const uint4* xh_in, int xstri
   return true;
 }
 
+// q|k|v projection of a batch step with RoPE and the cache append fused (k_gemm_sk, EPI 2): q of the
+// B tokens into qkv, k and v into each sequence's cache at its position -- what the bias projection
+// followed by k_rope_kv_list writes.  False (nothing launched) where that path does not apply.
+bool launch_qkv_rope(hipStream_t s, const Mat& W, const uint4* xh, int xstride, int M, float* qkv, int QKV,
+                     const float* bias, const SkRope& rp) {
+  if (!xh || rp.hd % 16 || pick_gemm(W, M, true) != GK_SK4) return false;
+  const int nt = (M + 15) / 16;
+  const bool by_tile = sk_by_tile(W, nt);
+  k_gemm_sk<OP_BIAS, 4, kSkR4, 2><<<(unsigned)sk_grid(W.Np / 16, nt, by_tile), 256, 0, s>>>(
+      W.view(), xh, xstride, M, qkv, QKV, bias, by_tile, nullptr, nullptr, 0, rp);
+  return true;
+}
+
 template <int OP, int TPW>
 void launch_rows(hipStream_t s, const Mat& W, const uint4* xq, int xstride, int M, float* y, int ldy, const float* bias) {
   k_gemm_rows<OP, TPW><<<dim3((unsigned)(W.Np / 64), (unsigned)((M + TPW - 1) / TPW)), 256, 0, s>>>(
@@ -2264,15 +2277,20 @@ void enqueue_batch_step(q4hip_batch* bt, int* out) {
   for (int l = 0; l < h->NL; l++) {
     Layer& y = h->L[l];
     launch_quant<QM_NORM>(s, B, h->x, D, D, y.attn_norm, h->eps, h->xq, h->xstride, 0, xh);
-    launch_matvec<OP_BIAS>(s, y.qkv, h->xq, h->xstride, B, h->qkv, QKV, y.bqkv, xh);
-    if (h->kv16)
-      k_rope_kv_list<kvhalf><<<dim3(h->H + h->KVH, B), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope,
-                                                                       (kvhalf*)bt->kc, (kvhalf*)bt->vc, h->ctx, l, bt->pos,
-                                                                       bt->seq_stride);
-    else
-      k_rope_kv_list<float><<<dim3(h->H + h->KVH, B), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope,
-                                                                      (float*)bt->kc, (float*)bt->vc, h->ctx, l, bt->pos,
-                                                                      bt->seq_stride);
+    SkRope rp;
+    rp.rope = h->rope; rp.kc = bt->kc; rp.vc = bt->vc; rp.pos = bt->pos; rp.seq_stride = bt->seq_stride;
+    rp.ctx = h->ctx; rp.layer = l; rp.H = h->H; rp.KVH = h->KVH; rp.hd = HD; rp.kv16 = h->kv16;
+    if (!launch_qkv_rope(s, y.qkv, xh, h->xstride, B, h->qkv, QKV, y.bqkv, rp)) {
+      launch_matvec<OP_BIAS>(s, y.qkv, h->xq, h->xstride, B, h->qkv, QKV, y.bqkv, xh);
+      if (h->kv16)
+        k_rope_kv_list<kvhalf><<<dim3(h->H + h->KVH, B), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope,
+                                                                         (kvhalf*)bt->kc, (kvhalf*)bt->vc, h->ctx, l,
+                                                                         bt->pos, bt->seq_stride);
+      else
+        k_rope_kv_list<float><<<dim3(h->H + h->KVH, B), HD / 2, 0, s>>>(h->qkv, QKV, D, h->H, h->KVH, HD, h->rope,
+                                                                        (float*)bt->kc, (float*)bt->vc, h->ctx, l,
+                                                                        bt->pos, bt->seq_stride);
+    }
     launch_attn_list(s, HD, B, h->H, h->KVH, h->qkv, QKV, bt->kc, bt->vc, h->kv16, h->ctx, l, bt->sc, h->att, D, bt->pos,
                      bt->seq_stride, h->xq, h->xstride, xh);
     launch_matvec<OP_ADD>(s, y.o, h->xq, h->xstride, B, h->x, D, nullptr, xh);

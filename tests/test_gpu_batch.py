@@ -175,20 +175,25 @@ def test_batch_errors():
         g.close()
 
 
-def test_batch_qwen05b_sixteen_sequences():
-    """16 sequences of the Qwen2.5-0.5B shape: the output head (151,936 rows) runs as a 16-token
-    matrix-core GEMM; every sequence's tokens and last logits equal the oracle's."""
+@pytest.mark.parametrize("B,kv", [(16, "f32"), (12, "f16")])
+def test_batch_qwen05b_sixteen_sequences(B, kv):
+    """16 (or 12: a partial 16-token tile) sequences of the Qwen2.5-0.5B shape: the output head
+    (151,936 rows) runs as a matrix-core GEMM and the q|k|v projection with RoPE and the cache
+    append fused; every sequence's tokens and last logits equal the oracle's (with an fp16 cache,
+    the oracle over the same fp16 rounding)."""
     import q4hip
     shape = synth.SHAPES["qwen2.5-0.5b"]
     t = _model("qwen2.5-0.5b", 48)
-    B, steps, ctx = 16, 3, 64
+    steps, ctx = 3, 64
     rng = np.random.default_rng(48)
     lens = [int(n) for n in rng.integers(1, 12, B)]
     prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in lens]
-    print(f"qwen05b batch of {B}, prompt lengths {lens}", flush=True)
-    g = q4hip.Model(shape, ctx=ctx)
+    print(f"qwen05b batch of {B}, kv {kv}, prompt lengths {lens}", flush=True)
+    g = q4hip.Model(shape, ctx=ctx, kv_type=q4hip.KV_F16 if kv == "f16" else q4hip.KV_F32)
     g.load(t)
     o = oracle.Model(shape, t, ctx=ctx, mt=16, threads=8)
+    if kv == "f16":
+        o.set_variant(oracle.V_KV_F16)
     bt = q4hip.Batch(g, B)
     try:
         first = [bt.prefill(b, prompts[b], 0) for b in range(B)]
