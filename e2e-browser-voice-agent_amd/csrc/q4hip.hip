@@ -149,6 +149,127 @@ __global__ __launch_bounds__(64) void k_matvec(Q4Mat W, const uint4* __restrict_
   }
 }
 
+// One token, matrices with many blocks per row (down: 896 x 4864): the same sums as k_matvec<1>,
+// with the blocks of a 16-row group spread over four waves.  Wave w forms the terms
+// f32(p_j) * (dw * dx) of block groups w, w + 4, ... (every term is independent of the others) into
+// shared memory; then wave 0 adds each lane's terms in block order, acc = acc + t, as
+// matvec_rows16 does (kernels.c:200-229), and the four lanes of a row combine in hsum order.
+// Dynamic shared memory: nb * 64 bytes of activation blocks, then nb * 256 bytes of terms.
+constexpr int kSplitWaves = 8, kSplitThreads = 64 * kSplitWaves;
+template <int OP>
+__global__ __launch_bounds__(kSplitThreads) void k_matvec_split(Q4Mat W, const uint4* __restrict__ xq, float* __restrict__ y,
+                                                     const float* __restrict__ bias) {
+  extern __shared__ uint4 xs[];
+  float* tm = reinterpret_cast<float*>(xs + W.nb * 4);     // [block][lane (r, j)]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane >> 2, j = lane & 3;
+  const int wv = blockIdx.x, tile = wv >> 2, rr = ((wv & 3) << 4) + r;
+  const int row = (tile << 6) + rr;
+  for (int i = tid; i < W.nb * 4; i += kSplitThreads) xs[i] = xq[i];
+  const uint4* wq = W.qs + ((size_t)tile * W.ng * 64 + rr) * 4 + j;
+  const uint4* wd = W.d + (size_t)tile * W.nb8 * 64 + rr;
+  constexpr int CG = 8;                                     // this wave's groups in flight
+  const int mine = (W.ng - wave + kSplitWaves - 1) / kSplitWaves;   // groups wave, wave + waves, ...
+  uint4 w[CG], sc[CG];
+#pragma unroll
+  for (int c = 0; c < CG; c++) {
+    const int g = wave + kSplitWaves * c;
+    w[c] = c < mine ? wq[(size_t)g * 256] : make_uint4(0, 0, 0, 0);
+    sc[c] = c < mine ? wd[(size_t)(g >> 1) * 64] : make_uint4(0, 0, 0, 0);
+  }
+  __syncthreads();
+  for (int c0 = 0; c0 < mine; c0 += CG) {
+    uint4 wn[CG], sn[CG];
+    const bool more = c0 + CG < mine;
+    if (more) {
+#pragma unroll
+      for (int c = 0; c < CG; c++) {
+        const int cc = c0 + CG + c, g = wave + kSplitWaves * cc;
+        wn[c] = cc < mine ? wq[(size_t)g * 256] : make_uint4(0, 0, 0, 0);
+        sn[c] = cc < mine ? wd[(size_t)(g >> 1) * 64] : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CG; c++) {
+      if (c0 + c < mine) {
+        const int g = wave + kSplitWaves * (c0 + c);
+        const uint32_t ww[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+        const uint32_t sh[4] = {sc[c].x, sc[c].y, sc[c].z, sc[c].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const int b = 4 * g + k;
+          if (b < W.nb) {
+            const int hb = ((g & 1) << 2) + k;                  // half index within the 8 scales
+            const uint32_t hbits = (hb & 1) ? (sh[hb >> 1] >> 16) : (sh[hb >> 1] & 0xffffu);
+            const float dw = half_bits_to_float(hbits);
+            const uint32_t lo = ww[k] & 0x0F0F0F0Fu, hi = (ww[k] >> 4) & 0x0F0F0F0Fu;
+            const uint4 xv = xs[b * 4 + j];
+            int p = sdot4(lo, xv.x, (int)xv.z);
+            p = sdot4(hi, xv.y, p);
+            tm[b * 64 + lane] = (float)p * (dw * __uint_as_float(xv.w));
+          }
+        }
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int c = 0; c < CG; c++) { w[c] = wn[c]; sc[c] = sn[c]; }
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // this lane's chain in block order; the next 8 terms are read while the current 8 are added
+  float acc = 0.0f;
+  int b = 0;
+  if (W.nb >= 16) {
+    float a[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) a[u] = tm[u * 64 + lane];
+    for (; b + 16 <= W.nb; b += 8) {
+      float n8[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) n8[u] = tm[(b + 8 + u) * 64 + lane];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 8; u++) acc = acc + a[u];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 8; u++) a[u] = n8[u];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) acc = acc + a[u];
+    b += 8;
+  }
+  for (; b < W.nb; b++) acc = acc + tm[b * 64 + lane];
+  const float v = hsum4(acc);
+  if (j == 0 && row < W.N) {
+    float* o = y + row;
+    if (OP == OP_ADD) *o = *o + v;
+    else if (OP == OP_BIAS) *o = v + bias[row];
+    else *o = v;
+  }
+}
+
+// Blocks per row from which one-token projections use k_matvec_split.
+constexpr int kSplitMinBlocks = 64;
+// The widest row it takes: activation blocks and terms in shared memory.
+constexpr int kSplitMaxBlocks = 480;
+inline size_t split_lds(int nb) { return (size_t)nb * 320; }
+
+// Raise k_matvec_split's shared-memory limit once per device, with that device current (before
+// any graph capture: the handle and matvec constructors call it).
+void matvec_split_setup(int device) {
+  static std::mutex mu;
+  static uint64_t done = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (device < 0 || device >= 64 || (done >> device) & 1) return;
+  const int lds = (int)split_lds(kSplitMaxBlocks);
+  (void)hipFuncSetAttribute((const void*)k_matvec_split<0>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  (void)hipFuncSetAttribute((const void*)k_matvec_split<1>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  (void)hipFuncSetAttribute((const void*)k_matvec_split<2>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  (void)hipGetLastError();
+  done |= (uint64_t)1 << device;
+}
+
 // y[m][n] (op)= W[n] . x[m] for a pass of M tokens (matmul_q4, kernels.c:200-273): the prefill
 // projections.  A workgroup computes 16 rows x 32 tokens: lane (r, j) of wave w owns reference lane
 // j of row r for tokens 8w..8w+7 of the tile, so every output is acc_j = acc_j + f32(p_j) * (dw * dx)
@@ -1405,7 +1526,10 @@ void launch_matvec(hipStream_t s, const Mat& W, const uint4* xq, int xstride, in
                    const float* bias, const uint4* xh = nullptr) {
   const unsigned grid = (unsigned)(W.Np / 16);
   if (M == 1) {
-    k_matvec<1, OP><<<grid, 64, (size_t)W.nb * 64, s>>>(W.view(), xq, xstride, 1, y, ldy, bias);
+    if (W.nb >= kSplitMinBlocks && W.nb <= kSplitMaxBlocks)
+      k_matvec_split<OP><<<grid, kSplitThreads, split_lds(W.nb), s>>>(W.view(), xq, y, bias);
+    else
+      k_matvec<1, OP><<<grid, 64, (size_t)W.nb * 64, s>>>(W.view(), xq, xstride, 1, y, ldy, bias);
     return;
   }
   if (M <= 8) {
@@ -1865,6 +1989,7 @@ int q4hip_create(q4hip** out, int dim, int layers, int ffn, int heads, int kv_he
   HIPCHK(hipGetDeviceCount(&ndev));
   if (device < 0 || device >= ndev) return fail(Q4HIP_EINVAL, "device %d of %d", device, ndev);
   HIPCHK(hipSetDevice(device));
+  matvec_split_setup(device);
 
   q4hip* h = new q4hip();
   h->D = dim; h->NL = layers; h->F = ffn; h->H = heads; h->KVH = kv_heads; h->HD = HD;
@@ -2518,6 +2643,7 @@ int q4hip_mv_create(q4hip_mv** out, int N, int K, const void* w, int device) {
   rc = mat_alloc(m->W, N, K, m->stream);
   if (rc == Q4HIP_OK) rc = mat_upload(m->W, 0, N, w, m->stream);
   if (rc != Q4HIP_OK) { q4hip_mv_destroy(m); return rc; }
+  matvec_split_setup(device);
   *out = m;
   return Q4HIP_OK;
 }
