@@ -144,7 +144,8 @@ def cpu_baseline(shape, tensors, ids, first_tokens):
     med1 = statistics.median(one)
     return {"value": round(1.0 / med, 3), "unit": "tokens/s", "cores": decode_threads, "kind": "port",
             "sample": f"oracle (C restatement of kernels.c) decode of {len(times)} greedy tokens after the same "
-                      f"64-token prompt, median ms/token {med * 1e3:.1f}, {decode_threads} of {cores} threads",
+                      f"64-token prompt, median ms/token {med * 1e3:.1f}, {decode_threads} of {cores} threads "
+                      f"(logical cores capped at 16, this host's CPU share per GPU)",
             "tokens_agree_with_gpu": bool(agree),
             "one_thread": {"value": round(1.0 / med1, 3), "unit": "tokens/s", "tokens": len(one)},
             "cpu_model": cpu_model()}
