@@ -65,7 +65,15 @@ struct PArgs {
   // K/V roles, [3] gate/up role.  The weight bursts then stay out of the memory system while the
   // hand-off they follow is polled for.
   int pf[4];
+  const int* wgmap;   // physical workgroup -> logical one (the role order below); identity when null
 };
+
+// This workgroup's logical index.  The host places the attention workgroups of one kv group on one
+// XCD (workgroup L runs on XCD L mod 8), so the past K/V rows they all stage come from that XCD's L2
+// after the first of them has fetched them.
+__device__ __forceinline__ int lwg(const PArgs& a) {
+  return a.wgmap ? __builtin_amdgcn_readfirstlane(a.wgmap[blockIdx.x]) : (int)blockIdx.x;
+}
 
 __device__ __forceinline__ void pf_delay(int n) {
   for (int i = 0; i < n; i++) __builtin_amdgcn_s_sleep(8);
@@ -747,7 +755,7 @@ __device__ __forceinline__ void prof_mark(const PArgs& a, int s, int slot) {
 // Per-workgroup timestamps of step 0, after the (NL + 1) * 16 phase slots: [layer][workgroup][8].
 constexpr int kProfWG = 8;
 __device__ __forceinline__ unsigned long long* prof_slot(const PArgs& a, int s, int l, int k) {
-  return a.prof && s == 0 ? a.prof + (size_t)(a.NL + 1) * 16 + ((size_t)l * gridDim.x + blockIdx.x) * kProfWG + k
+  return a.prof && s == 0 ? a.prof + (size_t)(a.NL + 1) * 16 + ((size_t)l * gridDim.x + lwg(a)) * kProfWG + k
                           : nullptr;
 }
 // The per-workgroup timestamp k once `v` has been computed (the empty asm consumes v and the
@@ -760,7 +768,7 @@ __device__ __forceinline__ void prof_after(const PArgs& a, int s, int l, int k, 
 }
 __device__ __forceinline__ void prof_wg(const PArgs& a, int s, int l, int k) {
   if (a.prof && s == 0 && threadIdx.x == 0)
-    a.prof[(size_t)(a.NL + 1) * 16 + ((size_t)l * gridDim.x + blockIdx.x) * kProfWG + k] = wall_clock64();
+    a.prof[(size_t)(a.NL + 1) * 16 + ((size_t)l * gridDim.x + lwg(a)) * kProfWG + k] = wall_clock64();
 }
 
 // ---------------------------------------------------------------- RMSNorm + quantize
@@ -857,7 +865,7 @@ template <class S>
 __device__ __forceinline__ bool head_scan_q4(const PArgs& a, const PSmem& m, uint32_t epx, int s, bool& bad,
                                              float& bv, int& bi) {
   const int lane = threadIdx.x & 63, wave = wave_id();
-  const int G = gridDim.x, wg = blockIdx.x, nRG = a.head.Np / 16, stride = 4 * G;
+  const int G = gridDim.x, wg = lwg(a), nRG = a.head.Np / 16, stride = 4 * G;
   float nw[4];
   normw_load<S>(a.out_norm, nw);
   int rgi = wg + G * wave;
@@ -964,7 +972,7 @@ __device__ __forceinline__ bool head_scan_q8(const PArgs& a, const PSmem& m, uin
                                              float& bv, int& bi) {
   constexpr int NG8 = (S::NBD + 1) / 2;
   const int lane = threadIdx.x & 63, wave = wave_id();
-  const int G = gridDim.x, wg = blockIdx.x, nRG = a.head.Np / 16, stride = 4 * G;
+  const int G = gridDim.x, wg = lwg(a), nRG = a.head.Np / 16, stride = 4 * G;
   float nw[4];
   normw_load<S>(a.out_norm, nw);
   int rgi = wg + G * wave;
@@ -991,7 +999,7 @@ __device__ __forceinline__ bool head_scan_q8(const PArgs& a, const PSmem& m, uin
 template <class S>
 __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int pos, bool& bad) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int G = gridDim.x, wg = blockIdx.x, E = 4 * a.NL + 1;
+  const int G = gridDim.x, wg = lwg(a), E = 4 * a.NL + 1;
   uint64_t* LARG = a.ll + S::oARG + (size_t)(s & 1) * kArgStride * G;
   const uint32_t epx = phase_epoch(ep0, s, E, 4 * (a.NL - 1) + 3);
   const uint32_t eph = phase_epoch(ep0, s, E, 4 * a.NL);
@@ -1212,7 +1220,7 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
   constexpr int G0o = split_g0(S::NGD, W), Co = split_cnt(S::NGD, W);
   constexpr int G0d = split_g0(S::NGF, W), Cd = split_cnt(S::NGF, W);
   const int tid = threadIdx.x, lane = tid & 63, r = lane >> 2, j = lane & 3;
-  const int wg = blockIdx.x, row = wg * 16 + r, E = 4 * a.NL + 1;
+  const int wg = lwg(a), row = wg * 16 + r, E = 4 * a.NL + 1;
   if (tid < 16) m.own[tid] = embed_value(a.embd, S::D, tok, wg * 16 + tid);
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
@@ -1311,7 +1319,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
   constexpr int GRP = S::H / S::KVH;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), r = lane >> 2, j = lane & 3;
   const int E = 4 * a.NL + 1;
-  const int aidx = blockIdx.x - S::nOD, h = aidx % S::H, half = aidx / S::H, kh = h / GRP;
+  const int aidx = lwg(a) - S::nOD, h = aidx % S::H, half = aidx / S::H, kh = h / GRP;
   const bool split = a.asplit > 1;
   const bool mark = aidx == 0;
   const int rq = (h * kHD) / 16 + wave;
@@ -1768,7 +1776,7 @@ __device__ __forceinline__ bool kv_step(const PArgs& a, const PSmem& m, uint32_t
   constexpr int G0 = split_g0(S::NGD, W), C = split_cnt(S::NGD, W);
   const int tid = threadIdx.x, lane = tid & 63, r = lane >> 2, j = lane & 3;
   const int E = 4 * a.NL + 1;
-  const int kidx = blockIdx.x - S::nOD - S::H * a.asplit;
+  const int kidx = lwg(a) - S::nOD - S::H * a.asplit;
   const int kh = kidx >> 3, isv = (kidx >> 2) & 1, p = kidx & 3;
   const int pi = 8 * p + (r & 7);                       // RoPE pair index of this lane's row
   const int li = r < 8 ? pi : 32 + pi;                  // the row within the group's 64
@@ -1824,7 +1832,7 @@ template <class S>
 __device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t ep0, int s, bool& bad) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), r = lane >> 2, j = lane & 3;
   const int E = 4 * a.NL + 1;
-  const int u = blockIdx.x - S::nOD - S::H * a.asplit - S::nKV;
+  const int u = lwg(a) - S::nOD - S::H * a.asplit - S::nKV;
   const int rg = wave < 2 ? 2 * u + wave : S::F / 16 + 2 * u + (wave - 2);
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
@@ -1875,7 +1883,7 @@ __global__ __launch_bounds__(kPThreads, 1) void k_decode_persistent(PArgs a) {
   const uint32_t ep0 = a.st->epoch;
   int pos = a.st->pos0;
   int tok = a.tokens[pos];
-  const int wg = blockIdx.x, wave = wave_id();
+  const int wg = lwg(a), wave = wave_id();
   if (wg == 0) prof_mark(a, 0, a.NL * 16 + 3);
   if (a.prof && wg == 0 && threadIdx.x == 0) a.prof[a.NL * 16 + 4] = clock64();
   bool bad = false;

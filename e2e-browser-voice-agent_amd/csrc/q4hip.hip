@@ -1407,6 +1407,7 @@ struct q4hip {
   LayerView* d_layers = nullptr;
   uint64_t* ll = nullptr;
   int pers_grid = 0;
+  int* pers_wgmap[2] = {nullptr, nullptr};   // physical -> logical workgroup, one attention workgroup per head or two
   const char* pers_why = "";
   int pers_kv_tile = 0;
   size_t pers_lds = 0;
@@ -1739,6 +1740,33 @@ const PersInstance* find_pers_instance(int D, int F, int H, int KVH) {
   return nullptr;
 }
 
+// Placement of the persistent kernel's workgroups: physical workgroup p runs on XCD p mod 8, and
+// the logical index (the role order: o/down, attention, K/V, gate/up, head only) comes from this
+// map.  The attention workgroups of kv group g take physical slots on XCD g mod 8, so the past K/V
+// rows they all stage each layer come from one L2; every other role keeps its order in the
+// remaining slots.  Empty when the slots do not suffice (identity placement).
+std::vector<int> persistent_wgmap(int G, int nOD, int H, int KVH, int asplit) {
+  std::vector<int> map(G, -1);
+  std::vector<char> used(G, 0);
+  const int grp = H / KVH, nA = H * asplit;
+  for (int aidx = 0; aidx < nA; aidx++) {
+    int p = (aidx % H) / grp % 8;
+    while (p < G && used[p]) p += 8;
+    if (p >= G) return {};
+    used[p] = 1;
+    map[p] = nOD + aidx;
+  }
+  int p = 0;
+  for (int lid = 0; lid < G; lid++) {
+    if (lid >= nOD && lid < nOD + nA) continue;
+    while (p < G && used[p]) p++;
+    if (p >= G) return {};
+    used[p] = 1;
+    map[p] = lid;
+  }
+  return map;
+}
+
 // Decide once whether this model and device admit the persistent decode kernel, and set it up.
 // On refusal h->pers_why says which requirement failed.
 void setup_persistent(q4hip* h) {
@@ -1799,6 +1827,16 @@ void setup_persistent(q4hip* h) {
     return no("device allocation failed");
   }
   h->pers_grid = G;
+  for (int sp = 1; sp <= 2; sp++) {
+    const std::vector<int> map = persistent_wgmap(G, h->D / 16, h->H, h->KVH, sp);
+    if (map.empty()) continue;
+    if (hipMalloc(&h->pers_wgmap[sp - 1], (size_t)G * sizeof(int)) != hipSuccess ||
+        hipMemcpy(h->pers_wgmap[sp - 1], map.data(), (size_t)G * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) {
+      (void)hipGetLastError();
+      if (h->pers_wgmap[sp - 1]) (void)hipFree(h->pers_wgmap[sp - 1]);
+      h->pers_wgmap[sp - 1] = nullptr;       // identity placement
+    }
+  }
   if (const char* e = getenv("Q4HIP_POLL_SLEEP")) h->pers_nap = std::max(0, std::min(64, atoi(e)));
   // long contexts: two attention workgroups per head when the roles still fit one per CU
   if (pi->nRoles + h->H <= G && h->pers_ring > 0) {
@@ -1875,6 +1913,7 @@ hipError_t launch_persistent(q4hip* h, int pos0, int steps, unsigned long long* 
   a.ring = h->pers_ring;
   a.nap = h->pers_nap;
   a.prof = prof;
+  a.wgmap = h->pers_wgmap[a.asplit - 1];
   for (int i = 0; i < 4; i++) a.pf[i] = h->pers_pf[i];
   h->pers_last_steps = steps;
   if (h->pers_test_abort > 0) {          // Q4HIP_TEST_ABORT: the launch finds the flag raised
@@ -1963,7 +2002,7 @@ void q4hip_destroy(q4hip* h) {
   mat_free(h->head);
   void* bufs[] = {h->embd, h->out_norm, h->rope, h->x, h->qkv, h->att, h->gu, h->logits, h->kc, h->vc,
                   h->xq, h->am_v, h->am_i, h->tokens, h->st, h->d_layers, h->ll, h->ascr, h->xh, h->xh2, h->tpos,
-                  h->lsc};
+                  h->lsc, h->pers_wgmap[0], h->pers_wgmap[1]};
   for (void* p : bufs) if (p) (void)hipFree(p);
   if (h->pin_ids) (void)hipHostFree(h->pin_ids);
   if (h->pin_next) (void)hipHostFree(h->pin_next);
