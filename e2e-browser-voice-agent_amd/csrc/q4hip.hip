@@ -1556,6 +1556,213 @@ void launch_head(hipStream_t s, const Mat& W, const uint4* xq, float* logits) {
     launch_matvec<OP_STORE>(s, W, xq, 0, 1, logits, W.N, nullptr);
 }
 
+// Attention of a prompt pass (every row reads one shared cache), in three launches: the scores as
+// above; k_softmax_rows turns each (row, head)'s scores into p_t = e_t / sum in place (the
+// reference's max, e_t = fast_exp(s_t - max), sum in position order, division; kernels.c:367-371);
+// k_pv_tiles forms out[c] = sum_t p_t * v_t[c] in position order (kernels.c:372-375) for QT
+// consecutive rows at once, so each V chunk staged in shared memory serves QT rows.
+// k_softmax_rows: grid (KVH, rows), 256 threads, dynamic shared memory softmax_lds(H, KVH, ctx).
+__global__ __launch_bounds__(256) void k_softmax_rows(float* __restrict__ sc, int H, int KVH, int ctx,
+                                                      const int* __restrict__ pos) {
+  extern __shared__ __attribute__((aligned(16))) float lsm[];
+  const int g = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, G = H / KVH;
+  const int T = pos[b] + 1, TS = pv_row_stride(ctx), CS = score_stride(ctx), T4 = (T + 3) >> 2;
+  float* e = lsm;                         // [G][TS] exponentials
+  float* red = e + G * TS;                // [4 waves][kMaxGroup], then max [kMaxGroup], sum [kMaxGroup]
+  float* rmax = red + 4 * kMaxGroup;
+  float* rsum = rmax + kMaxGroup;
+  float* sb = sc + ((size_t)b * H + g * G) * CS;
+  float mxh[kMaxGroup];
+#pragma unroll
+  for (int gh = 0; gh < kMaxGroup; gh++) mxh[gh] = -1e30f;
+  for (int q = tid; q < T4; q += 256) {                    // maxima (order-free)
+#pragma unroll
+    for (int gh = 0; gh < kMaxGroup; gh++) {
+      if (gh < G) {
+        const float4 v = *reinterpret_cast<const float4*>(sb + (size_t)gh * CS + 4 * q);
+        const int t = 4 * q;
+        float m = mxh[gh];
+        m = __builtin_fmaxf(m, v.x);
+        m = __builtin_fmaxf(m, t + 1 < T ? v.y : -1e30f);
+        m = __builtin_fmaxf(m, t + 2 < T ? v.z : -1e30f);
+        m = __builtin_fmaxf(m, t + 3 < T ? v.w : -1e30f);
+        mxh[gh] = m;
+      }
+    }
+  }
+#pragma unroll
+  for (int gh = 0; gh < kMaxGroup; gh++) {
+    float m = mxh[gh];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0) red[wave * kMaxGroup + gh] = m;
+  }
+  __syncthreads();
+  if (tid < G)
+    rmax[tid] = __builtin_fmaxf(__builtin_fmaxf(red[tid], red[kMaxGroup + tid]),
+                                __builtin_fmaxf(red[2 * kMaxGroup + tid], red[3 * kMaxGroup + tid]));
+  __syncthreads();
+  for (int q = tid; q < T4; q += 256) {                    // e_t = fast_exp(s_t - max)
+#pragma unroll
+    for (int gh = 0; gh < kMaxGroup; gh++) {
+      if (gh < G) {
+        const float4 v = *reinterpret_cast<const float4*>(sb + (size_t)gh * CS + 4 * q);
+        const float mx = rmax[gh];
+        float4 x;
+        x.x = fast_exp(v.x - mx);
+        x.y = fast_exp(v.y - mx);
+        x.z = fast_exp(v.z - mx);
+        x.w = fast_exp(v.w - mx);
+        *reinterpret_cast<float4*>(&e[gh * TS + 4 * q]) = x;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < G) {                          // the sum in position order; the next 32 values load ahead
+    const float* er = e + tid * TS;
+    const int T32 = T & ~31;
+    float sum = 0.0f;
+    float4 a[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) a[u] = *reinterpret_cast<const float4*>(er + 4 * u);
+    for (int t = 0; t < T32; t += 32) {
+      float4 nx[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) nx[u] = *reinterpret_cast<const float4*>(er + t + 32 + 4 * u);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        sum = sum + a[u].x;
+        sum = sum + a[u].y;
+        sum = sum + a[u].z;
+        sum = sum + a[u].w;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 8; u++) a[u] = nx[u];
+    }
+    for (int t = T32; t < T; t++) sum = sum + er[t];
+    rsum[tid] = sum;
+  }
+  __syncthreads();
+  for (int q = tid; q < T4; q += 256) {                    // p_t = e_t / sum, over the scores
+#pragma unroll
+    for (int gh = 0; gh < kMaxGroup; gh++) {
+      if (gh < G) {
+        const float sum = rsum[gh];
+        float4 x = *reinterpret_cast<const float4*>(&e[gh * TS + 4 * q]);
+        x.x = x.x / sum;
+        x.y = x.y / sum;
+        x.z = x.z / sum;
+        x.w = x.w / sum;
+        *reinterpret_cast<float4*>(sb + (size_t)gh * CS + 4 * q) = x;
+      }
+    }
+  }
+}
+
+// Q4HIP_PV_TILES=0 keeps prompt passes on k_attn_pv_list (same bits; for comparison).
+bool pv_tiles_off() {
+  static const bool off = [] { const char* e = getenv("Q4HIP_PV_TILES"); return e && e[0] == '0'; }();
+  return off;
+}
+
+size_t softmax_lds(int H, int KVH, int ctx) {
+  return (size_t)((H / KVH) * pv_row_stride(ctx) + 6 * kMaxGroup) * sizeof(float);
+}
+
+// k_pv_tiles: grid (HD / 32, KVH, ceil(B / QT)), QT * G * 32 threads: thread (row q of the tile, head
+// h of the kv group, column c of the slice) runs its own chain over positions 0 .. pos[b] in order,
+// p and V read in chunks of 64 positions staged in shared memory (V column-major, 68 floats per
+// column: a 16-byte read of 16 columns hits distinct banks).  With xq, each (row, head)'s 32 outputs
+// are quantized as one quantize_row block, as in k_attn_pv_list.
+constexpr int kPvTileRows = 4;          // QT
+constexpr int kPvChunk = 64;
+template <int HD, class KT>
+__global__ __launch_bounds__(1024) void k_pv_tiles(const float* __restrict__ sc, int H, int KVH,
+                                                   const KT* __restrict__ vc, int ctx, int layer,
+                                                   float* __restrict__ att, int D, const int* __restrict__ pos, int B,
+                                                   uint4* __restrict__ xq, int xstride, uint4* __restrict__ xh) {
+  constexpr int CHS = kPvChunk + 4;
+  __shared__ __attribute__((aligned(16))) float vs[kPvCols * CHS];
+  __shared__ __attribute__((aligned(16))) float ps[kPvTileRows * kMaxGroup * CHS];
+  const int c0 = blockIdx.x * kPvCols, g = blockIdx.y, b0 = blockIdx.z * kPvTileRows, tid = threadIdx.x;
+  const int G = H / KVH, nthr = kPvTileRows * G * kPvCols, CS = score_stride(ctx);
+  const int q = tid / (G * kPvCols), h = (tid / kPvCols) % G, c = tid % kPvCols;
+  const int b = b0 + q;
+  const bool active = tid < nthr && b < B;
+  const int T = active ? pos[b] + 1 : 0;
+  int tmax = 0;                                            // the tile's longest row
+  for (int k = 0; k < kPvTileRows; k++)
+    if (b0 + k < B) tmax = max(tmax, pos[b0 + k] + 1);
+  const KT* vb = vc + ((size_t)layer * KVH + g) * ctx * HD + c0;
+  // staging: V float4 i (row i / 8, columns 4 (i % 8) ..), p float4 i (row r = i / 16 of the tile's
+  // (q, h) rows, positions 4 (i % 16) ..)
+  auto stage = [&](int t0) {
+    for (int i = tid; i < kPvChunk * kPvCols / 4; i += blockDim.x) {
+      const int row = i >> 3, c4 = (i & 7) * 4;
+      const int t = min(t0 + row, tmax - 1);               // rows from tmax on are never used
+      const float4 v = kv_ld4<KT>(vb + (size_t)t * HD + c4);
+      vs[(c4 + 0) * CHS + row] = v.x;
+      vs[(c4 + 1) * CHS + row] = v.y;
+      vs[(c4 + 2) * CHS + row] = v.z;
+      vs[(c4 + 3) * CHS + row] = v.w;
+    }
+    for (int i = tid; i < kPvTileRows * G * (kPvChunk / 4); i += blockDim.x) {
+      const int r = i / (kPvChunk / 4), u4 = (i % (kPvChunk / 4)) * 4;
+      const int qq = r / G, hh = r - qq * G, bb = b0 + qq;
+      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (bb < B && t0 + u4 < tmax)
+        v = *reinterpret_cast<const float4*>(sc + ((size_t)bb * H + g * G + hh) * CS + t0 + u4);
+      *reinterpret_cast<float4*>(&ps[r * CHS + u4]) = v;
+    }
+  };
+  const float* pr = ps + (q * G + h) * CHS;
+  const float* vr = vs + c * CHS;
+  float acc = 0.0f;
+  for (int t0 = 0; t0 < tmax; t0 += kPvChunk) {
+    __syncthreads();                                       // the previous chunk is read
+    stage(t0);
+    __syncthreads();
+    if (active) {
+      if (t0 + kPvChunk <= T) {                            // a whole chunk: no select on the chain
+#pragma unroll
+        for (int u = 0; u < kPvChunk; u += 4) {
+          const float4 p4 = *reinterpret_cast<const float4*>(pr + u);
+          const float4 v4 = *reinterpret_cast<const float4*>(vr + u);
+          acc = acc + p4.x * v4.x;
+          acc = acc + p4.y * v4.y;
+          acc = acc + p4.z * v4.z;
+          acc = acc + p4.w * v4.w;
+        }
+      } else {
+        const int n = T - t0;
+        for (int u = 0; u < kPvChunk; u++) {
+          const float x = acc + pr[u] * vr[u];
+          acc = u < n ? x : acc;
+        }
+      }
+    }
+  }
+  if (active) att[(size_t)b * D + (g * G + h) * HD + c0 + c] = acc;
+  if (xq) {
+    __syncthreads();
+    float* o = vs;                                          // [q][h][32] outputs of this slice
+    if (active) o[(q * G + h) * kPvCols + c] = acc;
+    __syncthreads();
+    if (tid < 4 * G * kPvTileRows) {
+      const int qq = tid / (4 * G), hh = (tid / 4) % G, j = tid & 3, bb = b0 + qq;
+      if (bb < B) {
+        const int base = (qq * G + hh) * kPvCols + 2 * j;
+        const float v[8] = {o[base], o[base + 1], o[base + 8], o[base + 9],
+                            o[base + 16], o[base + 17], o[base + 24], o[base + 25]};
+        const int blk = ((g * G + hh) * HD + c0) >> 5;
+        quantize_item(v, blk, j, xq + (size_t)bb * xstride * 4, xh ? xh + xh_tile(bb, xstride) : nullptr, bb & 15);
+      }
+    }
+  }
+}
+
 template <int MODE>
 void launch_quant(hipStream_t s, int rows, const float* in, int ld_in, int n, const float* w, float eps,
                   uint4* xq, int xstride, int m_first, uint4* xh = nullptr) {
@@ -1580,6 +1787,20 @@ void launch_attn_list_t(hipStream_t s, int HD, int B, int H, int KVH, const floa
   const unsigned units = (unsigned)KVH * (unsigned)B, pg = units * (unsigned)(HD / kPvCols);
   const bool xcd_group = units % kXcds == 0;
   const size_t lds = attn_pv_lds(H, KVH, ctx);
+  if (seq_stride == 0 && B > 1 && !pv_tiles_off()) {   // a prompt pass: rows share one cache
+    const dim3 tg((unsigned)(HD / kPvCols), (unsigned)KVH, (unsigned)((B + kPvTileRows - 1) / kPvTileRows));
+    const unsigned nthr = (unsigned)(kPvTileRows * (H / KVH) * kPvCols);
+    if (HD == 64) {
+      k_attn_scores_list<64, KT><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, 0);
+      k_softmax_rows<<<dim3((unsigned)KVH, (unsigned)B), 256, softmax_lds(H, KVH, ctx), s>>>(sc, H, KVH, ctx, pos);
+      k_pv_tiles<64, KT><<<tg, nthr, 0, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, B, xq, xstride, xh);
+    } else {
+      k_attn_scores_list<128, KT><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, 0);
+      k_softmax_rows<<<dim3((unsigned)KVH, (unsigned)B), 256, softmax_lds(H, KVH, ctx), s>>>(sc, H, KVH, ctx, pos);
+      k_pv_tiles<128, KT><<<tg, nthr, 0, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, B, xq, xstride, xh);
+    }
+    return;
+  }
   if (HD == 64) {
     k_attn_scores_list<64, KT><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, seq_stride);
     k_attn_pv_list<64, kPvRows, KT><<<pg, 256, lds, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, seq_stride, xq, xstride, xh,
@@ -1607,8 +1828,13 @@ void launch_attn_list(hipStream_t s, int HD, int B, int H, int KVH, const float*
 // limit raised where needed.  Checked once per shape.
 bool attn_list_ok(int H, int KVH, int HD, int ctx) {
   if (H / KVH > kMaxGroup) return false;
-  const size_t lds = attn_pv_lds(H, KVH, ctx);
+  const size_t lds = attn_pv_lds(H, KVH, ctx), slds = softmax_lds(H, KVH, ctx);
   if (lds > 160 * 1024) return false;
+  if (slds > 64 * 1024 &&
+      hipFuncSetAttribute((const void*)k_softmax_rows, hipFuncAttributeMaxDynamicSharedMemorySize, (int)slds) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
   if (lds > 64 * 1024) {
     const void* fns[2] = {HD == 64 ? (const void*)k_attn_pv_list<64, kPvRows, float> : (const void*)k_attn_pv_list<128, kPvRows, float>,
                           HD == 64 ? (const void*)k_attn_pv_list<64, kPvRows, kvhalf> : (const void*)k_attn_pv_list<128, kPvRows, kvhalf>};
