@@ -108,6 +108,7 @@ def _short(name: str) -> str:
             n = int(m.group(1))
             base = name[m.end():m.end() + n]
             name = base + ("<..., _Float16>" if "DF16_" in name else "<...>")
+    name = name.replace("(anonymous namespace)::", "")
     return name.split("(")[0].replace("void ", "")
 
 
