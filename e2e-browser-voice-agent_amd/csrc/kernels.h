@@ -199,14 +199,9 @@ __device__ __forceinline__ uint32_t pack_f16x2(int a, int b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
 }
 
-// Stage a row of n floats into shared memory "by lane": value i goes to xl[(i & 3) * st + (i >> 2)],
+// A row of n floats staged in shared memory "by lane" (sq_stage): value i at xl[(i & 3) * st + (i >> 2)],
 // st = n/4 + 1, so reference lane j (the values i = j mod 4, kernels.c:81-82) is one contiguous run
 // and the four runs start in different banks.
-__device__ __forceinline__ void stage_row_by_lane(const float* __restrict__ x, int n, float* xl, int st,
-                                                  int tid, int nthreads) {
-  for (int i = tid; i < n; i += nthreads) xl[(i & 3) * st + (i >> 2)] = x[i];
-}
-
 __device__ __forceinline__ float lane_staged(const float* xl, int st, int i) {
   return xl[(i & 3) * st + (i >> 2)];
 }
@@ -322,26 +317,69 @@ __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, c
   }
 }
 
-// 1 / sqrt(mean(x^2) + eps) with the reference's four lane sums (lane j takes i = j mod 4, in
-// order) and ((l0+l1)+l2)+l3 (kernels.c:81-84), over a row staged by stage_row_by_lane.  Threads
-// 0..3 run the four lanes from shared memory; the result is broadcast through `red` (>= 5 floats).
-__device__ __forceinline__ float rms_scale_staged(const float* xl, int n, int st, float eps, float* red) {
-  const int tid = threadIdx.x;
-  if (tid < 4) {
-    const float* p = xl + tid * st;
-    const int cnt = n >> 2;
-    float s = 0.0f;
-    int k = 0;
-    for (; k + 8 <= cnt; k += 8) {
-      float v[8];
+// e[0] + e[1] + ... + e[T - 1] in order (the serial sums of RMSNorm and softmax, kernels.c:81-84,
+// 372-375) from shared memory with room for ((T + 31) & ~31) + 32 floats (the values past T are
+// read, never added): 32 values are added while the next 32 load, the two register sets
+// alternating (no copies between them).
+__device__ __forceinline__ float ordered_sum(const float* e, int T) {
+  const int T32 = T & ~31;
+  float sum = 0.0f;
+  float4 a[8], b[8];
+  auto load = [&](float4* r, int t) {
 #pragma unroll
-      for (int u = 0; u < 8; u++) v[u] = p[k + u];
+    for (int u = 0; u < 8; u++) r[u] = *reinterpret_cast<const float4*>(e + t + 4 * u);
+  };
+  auto add = [&](const float4* r) {
 #pragma unroll
-      for (int u = 0; u < 8; u++) s = s + v[u] * v[u];
+    for (int u = 0; u < 8; u++) {
+      sum = sum + r[u].x;
+      sum = sum + r[u].y;
+      sum = sum + r[u].z;
+      sum = sum + r[u].w;
     }
-    for (; k < cnt; k++) { const float v = p[k]; s = s + v * v; }
-    red[tid] = s;
+  };
+  load(a, 0);
+  int t = 0;
+  for (; t + 64 <= T32; t += 64) {        // reads reach t + 95 <= T32 + 31
+    load(b, t + 32);
+    __builtin_amdgcn_sched_barrier(0);
+    add(a);
+    __builtin_amdgcn_sched_barrier(0);
+    load(a, t + 64);
+    __builtin_amdgcn_sched_barrier(0);
+    add(b);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  if (t < T32) {                          // one block of 32 left, loaded already
+    add(a);
+    t += 32;
+  }
+  for (; t < T; t++) sum = sum + e[t];
+  return sum;
+}
+
+// Floats per lane row of the squares staged for RMSNorm's sum (sq_stage): n/4 values and
+// ordered_sum's read room.
+__host__ __device__ inline int sq_stride(int n) { return (((n >> 2) + 31) & ~31) + 32; }
+
+// The row by reference lane (xl[(i & 3) * st + i / 4], read back by lane_staged) and the squares
+// x_i * x_i the same way (sq[(i & 3) * sst + i / 4], sst = sq_stride(n)); every product rounds once, as in the
+// reference's sum of v * v.
+__device__ __forceinline__ void sq_stage(const float* __restrict__ x, int n, float* sq, int sst, float* xl,
+                                         int st, int tid, int nthreads) {
+  for (int i = tid; i < n; i += nthreads) {
+    const float v = x[i];
+    sq[(i & 3) * sst + (i >> 2)] = v * v;
+    xl[(i & 3) * st + (i >> 2)] = v;
+  }
+}
+
+// 1 / sqrt(mean(x^2) + eps) with the reference's four lane sums (lane j adds the squares of i = j
+// mod 4 in order) and ((l0+l1)+l2)+l3 (kernels.c:81-84), over the squares staged by sq_stage.
+// Threads 0..3 run the four lanes; the result is broadcast through `red` (>= 5 floats).
+__device__ __forceinline__ float rms_scale_sq(const float* sq, int n, int sst, float eps, float* red) {
+  const int tid = threadIdx.x;
+  if (tid < 4) red[tid] = ordered_sum(sq + tid * sst, n >> 2);
   __syncthreads();
   if (tid == 0) {
     const float ss = red[0] + red[1] + red[2] + red[3];

@@ -91,8 +91,8 @@ __global__ void k_embed(const uint8_t* __restrict__ emb, int D, const int* __res
 }
 
 // Quantize rows m_first .. m_first+gridDim.x-1 of `in` into xq rows 0.. (kernels.c:328-331,
-// 379, 385-388, 393-397, 405-407).  QM_NORM stages the row in shared memory ((n/4+1)*4 floats of
-// dynamic shared memory) for the serial sum of squares.
+// 379, 385-388, 393-397, 405-407).  QM_NORM stages the row's squares for the serial sums and the
+// row itself by lane in shared memory (quant_lds: 4 sq_stride(n) + 4 (n/4 + 1) floats).
 template <int MODE>
 __global__ __launch_bounds__(256) void k_quant(const float* __restrict__ in, int ld_in, int n,
                                                const float* __restrict__ w, float eps,
@@ -103,12 +103,14 @@ __global__ __launch_bounds__(256) void k_quant(const float* __restrict__ in, int
   const float* xr = in + (size_t)(m_first + blockIdx.x) * ld_in;
   const int st = (n >> 2) + 1;
   float rs = 0.0f;
+  const int sst = sq_stride(n);
+  float* const xs = xl + 4 * sst;         // the row by lane, after the squares
   if (MODE == QM_NORM) {
-    stage_row_by_lane(xr, n, xl, st, threadIdx.x, blockDim.x);
+    sq_stage(xr, n, xl, sst, xs, st, threadIdx.x, blockDim.x);
     __syncthreads();
-    rs = rms_scale_staged(xl, n, st, eps, red);
+    rs = rms_scale_sq(xl, n, sst, eps, red);
   }
-  quantize_row_dev<MODE>(xr, xl, st, n, w, rs, xq + (size_t)blockIdx.x * xstride * 4, threadIdx.x, blockDim.x,
+  quantize_row_dev<MODE>(xr, xs, st, n, w, rs, xq + (size_t)blockIdx.x * xstride * 4, threadIdx.x, blockDim.x,
                          xh ? xh + xh_tile(blockIdx.x, xstride) : nullptr, blockIdx.x & 15);
 }
 
@@ -870,6 +872,53 @@ __host__ __device__ inline int pv_row_stride(int ctx) { return ((ctx + 31) & ~31
 // Floats per head row of the scores array (rows start 16-byte aligned).
 __host__ __device__ inline int score_stride(int ctx) { return (ctx + 3) & ~3; }
 
+// P.V products with p_t taken from a neighbouring lane: within each 16-lane row of a wave, lane K
+// holds p of position t0 + K and `row_newbcast:K` (DPP) hands it to every lane of the row as the
+// first operand of the product.  pv_step adds one product to the column's sum and then forms the
+// next one, so that the product issues while the add's result is pending.  (The product is inline
+// assembly and the add plain code: an add in assembly gets a wait state before it from the
+// compiler's hazard check, which takes any assembly statement for a possible DPP read of the sum
+// written just before.)
+template <int K>
+__device__ __forceinline__ float pv_mul(float p, float v) {
+  float n;
+  if constexpr (K == 0)   // the first broadcast of a fresh p register: two wait states after any write
+    asm volatile("s_nop 1\n\tv_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                 : "=v"(n) : "v"(p), "v"(v), "n"(K));
+  else
+    asm volatile("v_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                 : "=v"(n) : "v"(p), "v"(v), "n"(K));
+  return n;
+}
+template <int K>
+__device__ __forceinline__ void pv_step(float& acc, float d, float p, float v, float& n) {
+  acc = acc + d;
+  n = pv_mul<K>(p, v);
+}
+template <int K>
+__device__ __forceinline__ float f4_at(const float4& v) {
+  return (K & 3) == 0 ? v.x : (K & 3) == 1 ? v.y : (K & 3) == 2 ? v.z : v.w;
+}
+// One batch of 16 positions: the products of the batch (pv_row::mul) or the previous batch's
+// products d added while this batch's are formed (pv_row::step); v holds the column's 16 values.
+template <int K>
+struct pv_row {
+  static __device__ __forceinline__ void mul(float p, const float4* v, float* n) {
+    pv_row<K - 1>::mul(p, v, n);
+    n[K - 1] = pv_mul<(K - 1) & 15>(p, f4_at<K - 1>(v[(K - 1) >> 2]));
+  }
+  static __device__ __forceinline__ void step(float& acc, const float* d, float p, const float4* v, float* n) {
+    pv_row<K - 1>::step(acc, d, p, v, n);
+    pv_step<K - 1>(acc, d[K - 1], p, f4_at<K - 1>(v[(K - 1) >> 2]), n[K - 1]);
+  }
+};
+template <>
+struct pv_row<0> {
+  static __device__ __forceinline__ void mul(float, const float4*, float*) {}
+  static __device__ __forceinline__ void step(float&, const float*, float, const float4*, float*) {}
+};
+
+
 template <int HD, class KT>
 __global__ __launch_bounds__(64) void k_attn_scores_list(const float* __restrict__ qkv, int QKV, int H, int KVH,
                                                          const KT* __restrict__ kc, int ctx, int layer,
@@ -1056,32 +1105,7 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
     }
   }
   __syncthreads();
-  if (tid < G) {                          // the sum in position order; the next 32 values load ahead
-    const float* e = p + tid * TS;
-    const int T32 = T & ~31;
-    float sum = 0.0f;
-    float4 a[8];
-#pragma unroll
-    for (int u = 0; u < 8; u++) a[u] = *reinterpret_cast<const float4*>(e + 4 * u);
-    for (int t = 0; t < T32; t += 32) {
-      float4 nx[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++) nx[u] = *reinterpret_cast<const float4*>(e + t + 32 + 4 * u);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        sum = sum + a[u].x;
-        sum = sum + a[u].y;
-        sum = sum + a[u].z;
-        sum = sum + a[u].w;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < 8; u++) a[u] = nx[u];
-    }
-    for (int t = T32; t < T; t++) sum = sum + e[t];
-    rsum[tid] = sum;
-  }
+  if (tid < G) rsum[tid] = ordered_sum(p + tid * TS, T);   // the sum in position order
   __syncthreads();
   if (one_pass) {
 #pragma unroll
@@ -1123,58 +1147,49 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
   const bool active = gh < G;
   const float* pr = p + (active ? gh : 0) * TS;
   float acc = 0.0f;
+  // Products of the last batch of a whole chunk are added at the start of the next chunk (while its
+  // first shared-memory reads are in flight) or after the last one.
+  float pc[16];
+  bool carry = false;
+  const int rl = tid & 15;                // this lane's position in a batch (its 16-lane row)
+  auto add_carry = [&]() {
+#pragma unroll
+    for (int k = 0; k < 16; k++) acc = acc + pc[k];
+    carry = false;
+  };
   auto pv_chunk = [&](int ch) {           // acc += p[t] * V[t][c] over chunk ch, positions in order
     const int t0 = ch * CR, m = min(CR, T - t0);
     const float* vcol = vs + ((ch & 1) * kPvCols + c) * CRS;            // vcol[r]: row r, column c
-    if (active) {
-      if (m == CR) {
-        // products of the next 16 positions are formed while the current 16 are added; the
-        // shared-memory reads run one batch further ahead
-        float4 pa[4];
-        float va[16], pd[16];
+    if (!active) return;
+    if (m == CR) {
+      // batch j: positions t0 + 16 j .. t0 + 16 j + 15; register set j & 1 holds its p (one per
+      // lane: position rl) and the column's 16 V values; the reads run two batches ahead of the adds
+      float pb[2];
+      float4 va[2][4];
+      auto load = [&](int j, int st) {
+        pb[st] = pr[t0 + 16 * j + rl];
 #pragma unroll
-        for (int u = 0; u < 4; u++) pa[u] = *reinterpret_cast<const float4*>(pr + t0 + 4 * u);
+        for (int u = 0; u < 4; u++) va[st][u] = *reinterpret_cast<const float4*>(vcol + 16 * j + 4 * u);
+      };
+      load(0, 0);
+      load(1, 1);
+      if (carry) add_carry();
+      float d[16];
+      pv_row<16>::mul(pb[0], va[0], d);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const float4 w = *reinterpret_cast<const float4*>(vcol + 4 * u);
-          va[4 * u] = w.x; va[4 * u + 1] = w.y; va[4 * u + 2] = w.z; va[4 * u + 3] = w.w;
-        }
+      for (int j = 0; j + 1 < CR / 16; j++) {
+        if (j + 2 < CR / 16) load(j + 2, j & 1);
+        float n[16];
+        pv_row<16>::step(acc, d, pb[(j + 1) & 1], va[(j + 1) & 1], n);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          pd[4 * u] = pa[u].x * va[4 * u];
-          pd[4 * u + 1] = pa[u].y * va[4 * u + 1];
-          pd[4 * u + 2] = pa[u].z * va[4 * u + 2];
-          pd[4 * u + 3] = pa[u].w * va[4 * u + 3];
-        }
-        for (int r0 = 0; r0 < CR; r0 += 16) {
-          const int r1 = r0 + 16 < CR ? r0 + 16 : r0;
-#pragma unroll
-          for (int u = 0; u < 4; u++) pa[u] = *reinterpret_cast<const float4*>(pr + t0 + r1 + 4 * u);
-#pragma unroll
-          for (int u = 0; u < 4; u++) {
-            const float4 w = *reinterpret_cast<const float4*>(vcol + r1 + 4 * u);
-            va[4 * u] = w.x; va[4 * u + 1] = w.y; va[4 * u + 2] = w.z; va[4 * u + 3] = w.w;
-          }
-          __builtin_amdgcn_sched_barrier(0);
-          float pn[16];
-#pragma unroll
-          for (int u = 0; u < 4; u++) {
-            acc = acc + pd[4 * u];
-            pn[4 * u] = pa[u].x * va[4 * u];
-            acc = acc + pd[4 * u + 1];
-            pn[4 * u + 1] = pa[u].y * va[4 * u + 1];
-            acc = acc + pd[4 * u + 2];
-            pn[4 * u + 2] = pa[u].z * va[4 * u + 2];
-            acc = acc + pd[4 * u + 3];
-            pn[4 * u + 3] = pa[u].w * va[4 * u + 3];
-          }
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int u = 0; u < 16; u++) pd[u] = pn[u];
-        }
-      } else {
-        for (int r = 0; r < m; r++) acc = acc + pr[t0 + r] * vcol[r];
+        for (int k = 0; k < 16; k++) d[k] = n[k];
       }
+#pragma unroll
+      for (int k = 0; k < 16; k++) pc[k] = d[k];
+      carry = true;
+    } else {
+      if (carry) add_carry();
+      for (int r = 0; r < m; r++) acc = acc + pr[t0 + r] * vcol[r];
     }
   };
   // Full triples: after chunk ch, chunk ch + 1 goes into the other buffer (read last in chunk ch - 1,
@@ -1198,6 +1213,7 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
       if (c3 + k + 1 < nch) vstore((c3 + k + 1) & 1, vr[(k + 1) % 3]);
     }
   }
+  if (active && carry) add_carry();
   if (active) att[(size_t)b * D + (g * G + gh) * HD + c0 + c] = acc;
   if (xq) {
     // the o projection's activation: each head's 32 outputs are one quantize_row block of row b
@@ -1618,32 +1634,7 @@ __global__ __launch_bounds__(256) void k_softmax_rows(float* __restrict__ sc, in
     }
   }
   __syncthreads();
-  if (tid < G) {                          // the sum in position order; the next 32 values load ahead
-    const float* er = e + tid * TS;
-    const int T32 = T & ~31;
-    float sum = 0.0f;
-    float4 a[8];
-#pragma unroll
-    for (int u = 0; u < 8; u++) a[u] = *reinterpret_cast<const float4*>(er + 4 * u);
-    for (int t = 0; t < T32; t += 32) {
-      float4 nx[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++) nx[u] = *reinterpret_cast<const float4*>(er + t + 32 + 4 * u);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        sum = sum + a[u].x;
-        sum = sum + a[u].y;
-        sum = sum + a[u].z;
-        sum = sum + a[u].w;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < 8; u++) a[u] = nx[u];
-    }
-    for (int t = T32; t < T; t++) sum = sum + er[t];
-    rsum[tid] = sum;
-  }
+  if (tid < G) rsum[tid] = ordered_sum(e + tid * TS, T);   // the sum in position order
   __syncthreads();
   for (int q = tid; q < T4; q += 256) {                    // p_t = e_t / sum, over the scores
 #pragma unroll
@@ -1766,12 +1757,13 @@ __global__ __launch_bounds__(1024) void k_pv_tiles(const float* __restrict__ sc,
 template <int MODE>
 void launch_quant(hipStream_t s, int rows, const float* in, int ld_in, int n, const float* w, float eps,
                   uint4* xq, int xstride, int m_first, uint4* xh = nullptr) {
-  const size_t lds = MODE == QM_NORM ? (size_t)((n >> 2) + 1) * 4 * sizeof(float) : 0;
+  const size_t lds = MODE == QM_NORM ? (size_t)(sq_stride(n) + (n >> 2) + 1) * 4 * sizeof(float) : 0;
   k_quant<MODE><<<rows, 256, lds, s>>>(in, ld_in, n, w, eps, xq, xstride, m_first, xh);
 }
 
-// V rows per chunk of k_attn_pv_list: 64 keeps a workgroup at about 48 KB of LDS (three per CU).
-constexpr int kPvRows = 64;
+// V rows per chunk of k_attn_pv_list: 128 (34 KB of LDS for the two chunk buffers) halves the
+// chunk steps of 64 rows; 256 was slower again.
+constexpr int kPvRows = 128;
 
 size_t attn_pv_lds(int H, int KVH, int ctx) {
   const int G = H / KVH;
