@@ -17,8 +17,11 @@
 // tiled operand layout), their block scales dx, the weight words and the fp16 weight scales of the
 // workgroup's rows -- streams through an R-slot ring in shared memory by asynchronous
 // global -> LDS loads, R - 1 groups ahead of the group being computed.  Every wave issues the same
-// five load instructions per group, so the wait for the oldest slot is a single vmcnt; one barrier
-// per group.  Loads past the last group or block are clamped to it (valid memory, never used).
+// five load instructions per group, so the wait for the oldest slot is a single vmcnt.  JS = 1
+// shares each slot among the waves (one barrier per group); with JS = 4 the waves share nothing but
+// the scales, so each wave streams its own chain's operands, the dx and the scales through a ring
+// of its own and runs without barriers.  Loads past the last group or block are clamped to it
+// (valid memory, never used).
 #pragma once
 #include "kernels.h"
 
@@ -28,14 +31,16 @@ typedef __attribute__((address_space(3))) void SkLds;
 typedef _Float16 sk_h4 __attribute__((ext_vector_type(4)));
 typedef float sk_f4 __attribute__((ext_vector_type(4)));
 
-// Bytes of one ring slot.
+// Bytes of one ring slot: JS = 1 one shared part; JS = 4 one part (WAVE bytes) per wave, holding
+// that wave's chain only.
 template <int JS>
 struct SkSlot {
-  static constexpr int ACT = 8192;                 // [block 4][chain 4][quarter 4][token 16][8 B]
-  static constexpr int DX = 256;                   // [block 4][token 16] f32
-  static constexpr int QS = JS == 4 ? 1024 : 4096; // [chain 4][row 16 or 64] uint4
-  static constexpr int SC = JS == 4 ? 128 : 512;   // [row][2 dwords]: the 4 fp16 scales of the group
-  static constexpr int oDX = ACT, oQS = ACT + DX, oSC = ACT + DX + QS, BYTES = ACT + DX + QS + SC;
+  static constexpr int ACT = JS == 4 ? 2048 : 8192; // [block 4]([chain 4] for JS 1)[quarter 4][token 16][8 B]
+  static constexpr int DX = 256;                    // [block 4][token 16] f32
+  static constexpr int QS = JS == 4 ? 256 : 4096;   // JS 4: [row 16] uint4; JS 1: [chain 4][row 64] uint4
+  static constexpr int SC = JS == 4 ? 128 : 512;    // [row][2 dwords]: the 4 fp16 scales of the group
+  static constexpr int oDX = ACT, oQS = ACT + DX, oSC = ACT + DX + QS, WAVE = ACT + DX + QS + SC;
+  static constexpr int BYTES = JS == 4 ? 4 * WAVE : WAVE;
 };
 
 // Wait until at most n of this wave's load instructions are outstanding, and this wave's LDS
@@ -45,6 +50,13 @@ template <int N>
 __device__ __forceinline__ void sk_sync() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// The same wait without meeting the other waves (a ring of the wave's own).
+template <int N>
+__device__ __forceinline__ void sk_wait() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
 }
 
 // Asynchronous global -> LDS loads (global_load_lds): lane l's 16 (or 4) bytes from `src` land at
@@ -71,15 +83,17 @@ __device__ __forceinline__ void sk_dma4(const void* src, const void* lds) {
 #endif
 
 // Per-lane sources of a workgroup's loads, computed once; group g adds g times a stride.
-//   act  this wave's block (4g + wave) of the 16-token tile: 2 KB, two instructions of 1 KB
-//   dx   the same block's 16 block scales (lanes 0..15)
+//   act  JS 1: this wave's block (4g + wave) of the 16-token tile, 2 KB, two instructions of 1 KB;
+//        JS 4: chain `wave` of the group's 4 blocks (512 bytes each), two blocks per instruction
+//   dx   JS 1: the same block's 16 block scales (lanes 0..15); JS 4: the 4 blocks' (all lanes)
 //   qs   JS 4: row lane (0..15) of the workgroup, chain `wave`; JS 1: row lane (0..63), chain `wave`
-//   sc   the 8 bytes of the group's 4 fp16 scales of one row, as two dwords (JS 4: lanes 0..7 take
-//        rows 4 wave .. 4 wave + 3; JS 1: lanes 0..31 take rows 16 wave .. 16 wave + 15)
+//   sc   the 8 bytes of the group's 4 fp16 scales of one row, as two dwords (JS 4: lanes 0..31 take
+//        the 16 rows; JS 1: lanes 0..31 take rows 16 wave .. 16 wave + 15)
 // Blocks past nb and groups past ng are clamped to the last ones.
 template <int JS>
 struct SkSrc {
-  const uint4* act;      // block `wave` of group 0 of the tile
+  const uint4* act;      // JS 1: block `wave` of group 0 of the tile; JS 4: the lane's uint4 of chain `wave` of block 0
+  const float* dx;       // JS 4: the lane's token scale in block 0
   const uint4* qs;       // group 0
   const uint32_t* sc;    // group 0 (dword 0 of the row's 4-scale half of a uint4)
   int nb, ng, wave, lane;
@@ -102,14 +116,16 @@ struct SkSrc {
     nb = W.nb;
     ng = W.ng;
     act = xt + (size_t)T * xstride * kXhBlock;
+    dx = reinterpret_cast<const float*>(act + 128) + (lane & 15);
     const int tile = R0 >> 6, rr0 = R0 & 63;
+    if (JS == 4) act += wave * 32 + (lane & 31);
     if (JS == 4 && hd > 0) {
-      const int rq = rope_row(R0 >> 4, hd, lane & 15), rs = rope_row(R0 >> 4, hd, 4 * wave + ((lane >> 1) & 3));
+      const int rq = rope_row(R0 >> 4, hd, lane & 15), rs = rope_row(R0 >> 4, hd, (lane >> 1) & 15);
       qs = W.qs + ((size_t)(rq >> 6) * ng * 64 + (rq & 63)) * 4 + wave;
       sc = reinterpret_cast<const uint32_t*>(W.d + (size_t)(rs >> 6) * W.nb8 * 64 + (rs & 63)) + (lane & 1);
     } else if (JS == 4) {
       qs = W.qs + ((size_t)tile * ng * 64 + rr0 + (lane & 15)) * 4 + wave;
-      sc = reinterpret_cast<const uint32_t*>(W.d + (size_t)tile * W.nb8 * 64 + rr0 + 4 * wave + ((lane >> 1) & 3)) +
+      sc = reinterpret_cast<const uint32_t*>(W.d + (size_t)tile * W.nb8 * 64 + rr0 + ((lane >> 1) & 15)) +
            (lane & 1);
     } else {
       const int rq = row_of(R0, ffn, lane), rs = row_of(R0, ffn, 16 * wave + ((lane >> 1) & 15));
@@ -125,17 +141,28 @@ __device__ __forceinline__ void sk_issue(const unsigned char* slot, const SkSrc<
   using S = SkSlot<JS>;
   const int lane = src.lane, wave = src.wave;
   g = g < src.ng ? g : src.ng - 1;
+  const uint32_t* scg = src.sc + (size_t)(g >> 1) * 256 + ((g & 1) << 1);   // 64 rows x 4 dwords per uint4 group
+  if (JS == 4) {
+    // this wave's part of the slot: blocks 4g .. 4g + 3 of chain `wave` (lanes 0..31 and 32..63
+    // take one block each per instruction), the 4 blocks' dx, the rows' words and scales
+    unsigned char* const w = const_cast<unsigned char*>(slot) + wave * S::WAVE;
+    const int last = src.nb - 1;
+    const int b0 = min(4 * g + (lane >> 5), last), b1 = min(4 * g + 2 + (lane >> 5), last);
+    const int bd = min(4 * g + (lane >> 4), last);
+    sk_dma16(src.act + (size_t)b0 * kXhBlock, w);
+    sk_dma16(src.act + (size_t)b1 * kXhBlock, w + 1024);
+    sk_dma4(src.dx + (size_t)bd * kXhBlock * 4, w + S::oDX);
+    if (lane < 16) sk_dma16(src.qs + (size_t)g * 256, w + S::oQS);
+    if (lane < 32) sk_dma4(scg, w + S::oSC);
+    return;
+  }
   int b = 4 * g + wave;
   b = b < src.nb ? b : src.nb - 1;
   const uint4* a = src.act + (size_t)b * kXhBlock;
   sk_dma16(a + lane, slot + wave * 2048);
   sk_dma16(a + 64 + lane, slot + wave * 2048 + 1024);
   if (lane < 16) sk_dma4(reinterpret_cast<const float*>(a + 128) + lane, slot + S::oDX + wave * 64);
-  const uint32_t* scg = src.sc + (size_t)(g >> 1) * 256 + ((g & 1) << 1);   // 64 rows x 4 dwords per uint4 group
-  if (JS == 4) {
-    if (lane < 16) sk_dma16(src.qs + (size_t)g * 256, slot + S::oQS + wave * 256);
-    if (lane < 8) sk_dma4(scg, slot + S::oSC + wave * 32);
-  } else {
+  {
     sk_dma16(src.qs + (size_t)g * 256, slot + S::oQS + wave * 1024);
     if (lane < 32) sk_dma4(scg, slot + S::oSC + wave * 128);
   }
@@ -273,12 +300,13 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
     float4 dx[4];          // the 4 tokens' block scales, per block
   };
   auto read = [&](const unsigned char* slot, Regs& G) {
+    if (JS == 4) slot += wave * S::WAVE;                     // this wave's own part
     const uint2* acts = reinterpret_cast<const uint2*>(slot);
     const float4* dxs = reinterpret_cast<const float4*>(slot + S::oDX);
     const uint4* qss = reinterpret_cast<const uint4*>(slot + S::oQS);
     const uint2* scs = reinterpret_cast<const uint2*>(slot + S::oSC);
     G.sc = scs[wrow];
-    if (JS == 4) G.wq[0] = qss[wave * 16 + li];
+    if (JS == 4) G.wq[0] = qss[li];
     else {
 #pragma unroll
       for (int c = 0; c < 4; c++) G.wq[c] = qss[c * 64 + wrow];
@@ -287,7 +315,8 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
     for (int k = 0; k < 4; k++) {
       G.dx[k] = dxs[k * 4 + kg];
 #pragma unroll
-      for (int c = 0; c < NJ; c++) G.aw[k][c] = acts[((k * 4 + (JS == 4 ? wave : c)) * 4 + kg) * 16 + li];
+      for (int c = 0; c < NJ; c++)
+        G.aw[k][c] = acts[JS == 4 ? (k * 4 + kg) * 16 + li : ((k * 4 + c) * 4 + kg) * 16 + li];
     }
   };
   // The 4 NJ matrix-core products of group g, then the chain updates in block order.
@@ -334,12 +363,13 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
   for (int p = 0; p < R - 1; p++) sk_issue<JS>(ring[p], src, p);
   if (JS == 4) {
     // Software pipeline over groups (JS 4; the 64-row layout has no registers to spare for it):
-    // after the barrier that frees group g's slot, a wave reads group g + 1's operands from shared
-    // memory, then computes group g from registers read one step earlier.  R is even, so group g
-    // uses register set g & 1 in every pass of the unrolled loop.
+    // once group g's slot is free (its reads done), a wave reads group g + 1's operands from
+    // shared memory, then computes group g from registers read one step earlier.  R is even, so
+    // group g uses register set g & 1 in every pass of the unrolled loop.  The ring is the wave's
+    // own: its waits cover its own loads and reads, with no barrier.
     static_assert(R % 2 == 0, "register sets alternate with the group parity");
     Regs G[2];
-    sk_sync<5 * (R - 2)>();                                  // group 0 has landed
+    sk_wait<5 * (R - 2)>();                                  // group 0 has landed
     sk_issue<JS>(ring[R - 1], src, R - 1);
     read(ring[0], G[0]);
     for (int g0 = 0; g0 < ng; g0 += R) {
@@ -347,9 +377,9 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
       for (int u = 0; u < R; u++) {
         const int g = g0 + u;
         if (g < ng) {
-          // groups g + 1 .. g + R - 1 are in flight: wait for g + 1; after the barrier every wave
-          // has read group g's slot, which then takes group g + R
-          sk_sync<5 * (R - 2)>();
+          // groups g + 1 .. g + R - 1 are in flight: wait for g + 1; group g's slot has been read
+          // (into registers, one step earlier) and takes group g + R
+          sk_wait<5 * (R - 2)>();
           // the same wait in a form the compiler's wait tracking sees: the registers read in the
           // previous step are ready, so computing from them does not wait for the reads below
           __builtin_amdgcn_s_waitcnt(0xC07F);                // lgkmcnt(0)
