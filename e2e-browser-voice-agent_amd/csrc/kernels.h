@@ -178,6 +178,21 @@ __device__ __forceinline__ float4 kv_ld4<kvhalf>(const kvhalf* p) {
                      half_bits_to_float(u.y & 0xffffu), half_bits_to_float(u.y >> 16));
 }
 
+// Eight consecutive cache values as two float4 (one 16-byte load for fp16, two for fp32).
+template <class KT>
+__device__ __forceinline__ void kv_ld8(const KT* p, float4& a, float4& b) {
+  a = kv_ld4<KT>(p);
+  b = kv_ld4<KT>(p + 4);
+}
+template <>
+__device__ __forceinline__ void kv_ld8<kvhalf>(const kvhalf* p, float4& a, float4& b) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  a = make_float4(half_bits_to_float(u.x & 0xffffu), half_bits_to_float(u.x >> 16),
+                  half_bits_to_float(u.y & 0xffffu), half_bits_to_float(u.y >> 16));
+  b = make_float4(half_bits_to_float(u.z & 0xffffu), half_bits_to_float(u.z >> 16),
+                  half_bits_to_float(u.w & 0xffffu), half_bits_to_float(u.w >> 16));
+}
+
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }

@@ -855,8 +855,8 @@ __global__ void k_rope_kv_list(float* __restrict__ qkv, int QKV, int D, int H, i
 // Attention of token b over positions [0, pos[b]] of sequence b's cache (kernels.c:355-377), in
 // two launches that keep the reference's per-head operation order:
 //   k_attn_scores_list  scores s_t = (q . k_t) * 1/sqrt(head_dim) of the G = H/KVH heads of kv
-//                       head g, 64 positions per workgroup: grid (ctx/64, KVH, B), 64*G threads
-//                       (thread = head, position); K rows staged once in shared memory.
+//                       head g, 64 positions per workgroup, each thread one position and all G
+//                       heads (its K row in registers): grid (ctx/64, KVH, B).
 //   k_attn_pv_list      per (column slice, kv head, sequence): max, e_t = fast_exp(s_t - max), the
 //                       sum in position order, p_t = e_t / sum, then out[c] = sum_t p_t * v_t[c] in
 //                       position order, one thread per (head, column).  Every workgroup of a
@@ -943,9 +943,9 @@ __global__ __launch_bounds__(64) void k_attn_scores_list(const float* __restrict
   const int t = t0 + tid;
   if (t >= T) return;
   const KT* kr = kc + (size_t)b * seq_stride + (((size_t)layer * KVH + g) * ctx + t) * HD;
-  float4 kv[HD / 4];                     // the whole K row: one round trip to memory
+  float4 kv[HD / 4];                     // the whole K row: one round trip to memory, 16-byte loads
 #pragma unroll
-  for (int u = 0; u < HD / 4; u++) kv[u] = kv_ld4<KT>(kr + 4 * u);
+  for (int u = 0; u < HD / 8; u++) kv_ld8<KT>(kr + 8 * u, kv[2 * u], kv[2 * u + 1]);
   float s[kMaxGroup][4];
 #pragma unroll
   for (int gh = 0; gh < kMaxGroup; gh++) {
@@ -1473,7 +1473,7 @@ int check_ready(q4hip* h) {
 // Q4HIP_GEMM=valu keeps the matrix cores out (k_gemm_rows up to 64 tokens, else k_gemm_q4).
 enum { GK_ROWS2, GK_ROWS1, GK_TILED, GK_SK4, GK_SK1 };
 
-constexpr int kSkR4 = 4, kSkR1 = 4;    // ring slots of k_gemm_sk (JS 4: 38.4 KB, JS 1: 52.2 KB)
+constexpr int kSkR4 = 4, kSkR1 = 4;    // ring slots of k_gemm_sk (JS 4: 43 KB, JS 1: 52.2 KB; 6 or 8 were slower)
 
 // Whether multi-token projections use the matrix cores (not under Q4HIP_GEMM=valu).
 bool sk_enabled() {
