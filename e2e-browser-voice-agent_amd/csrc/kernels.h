@@ -178,6 +178,21 @@ __device__ __forceinline__ float4 kv_ld4<kvhalf>(const kvhalf* p) {
                      half_bits_to_float(u.y & 0xffffu), half_bits_to_float(u.y >> 16));
 }
 
+// Four consecutive cache values as loaded (kv_raw4) and widened to fp32 (kv_wide4): a register that
+// carries cache values across a loop holds them in the loaded form, so that the loop does not wait
+// for the load in flight to widen it before the values are used.
+template <class KT> struct KvRaw { typedef float4 T; };
+template <> struct KvRaw<kvhalf> { typedef uint2 T; };
+template <class KT>
+__device__ __forceinline__ typename KvRaw<KT>::T kv_raw4(const KT* p) {
+  return *reinterpret_cast<const typename KvRaw<KT>::T*>(p);
+}
+__device__ __forceinline__ float4 kv_wide4(float4 r) { return r; }
+__device__ __forceinline__ float4 kv_wide4(uint2 u) {
+  return make_float4(half_bits_to_float(u.x & 0xffffu), half_bits_to_float(u.x >> 16),
+                     half_bits_to_float(u.y & 0xffffu), half_bits_to_float(u.y >> 16));
+}
+
 // Eight consecutive cache values as two float4 (one 16-byte load for fp16, two for fp32).
 template <class KT>
 __device__ __forceinline__ void kv_ld8(const KT* p, float4& a, float4& b) {

@@ -1004,24 +1004,27 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
   // V chunks reach shared memory through registers: register set k holds the chunks ch = k mod 3;
   // chunk ch + 1 is stored at the end of chunk ch, and its set then loads chunk ch + 4 (the last
   // chunk again near the end, so that loads and stores stay unconditional)
-  auto vload = [&](int ch, float4* r) {
+  // the register sets hold V as loaded (fp16 stays fp16 until it is stored to shared memory)
+  typedef typename KvRaw<KT>::T VRaw;
+  auto vload = [&](int ch, VRaw* r) {
 #pragma unroll
     for (int u = 0; u < NV; u++) {
       // rows from T on are never read: they repeat row T - 1, so the loads carry no condition
       const int i = tid + 256 * u, row = i / (kPvCols / 4), c4 = i - row * (kPvCols / 4);
       const int t = min(ch * CR + row, T - 1);
-      r[u] = kv_ld4<KT>(vb + (size_t)t * HD + 4 * c4);
+      r[u] = kv_raw4<KT>(vb + (size_t)t * HD + 4 * c4);
     }
   };
-  auto vstore = [&](int buf, const float4* r) {
+  auto vstore = [&](int buf, const VRaw* r) {
 #pragma unroll
     for (int u = 0; u < NV; u++) {
       const int i = tid + 256 * u, row = i / (kPvCols / 4), c4 = i - row * (kPvCols / 4);
       float* d = vs + (buf * kPvCols + 4 * c4) * CRS + row;
-      d[0] = r[u].x;
-      d[CRS] = r[u].y;
-      d[2 * CRS] = r[u].z;
-      d[3 * CRS] = r[u].w;
+      const float4 w = kv_wide4(r[u]);
+      d[0] = w.x;
+      d[CRS] = w.y;
+      d[2 * CRS] = w.z;
+      d[3 * CRS] = w.w;
     }
   };
   auto head_max = [&](float* mxh) {       // block-wide maximum of each head (order-free)
@@ -1038,12 +1041,17 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
                                   __builtin_fmaxf(red[2 * kMaxGroup + tid], red[3 * kMaxGroup + tid]));
     __syncthreads();
   };
+  // float4 k of head gh in a pass from q0: thread tid takes q0 + tid for k = 0; for k >= 1 the
+  // threads are rotated by 64 (gh mod 4), so that the float4s past the first 256 of each head (a
+  // context just past a multiple of 1024 leaves one per head) fall to different waves instead of
+  // all to wave 0, whose exponentials and divisions the whole workgroup waits for
+  auto qof = [&](int q0, int gh, int k) { return q0 + 256 * k + (k == 0 ? tid : ((tid - 64 * (gh & 3)) & 255)); };
   auto load_scores = [&](int q0, float4 (*v)[PB]) {
 #pragma unroll
     for (int gh = 0; gh < kMaxGroup; gh++)
 #pragma unroll
       for (int k = 0; k < PB; k++) {
-        const int q = q0 + tid + 256 * k;
+        const int q = qof(q0, gh, k);
         v[gh][k] = (gh < G && q < T4) ? *reinterpret_cast<const float4*>(sb + (size_t)gh * CS + 4 * q)
                                       : make_float4(-1e30f, -1e30f, -1e30f, -1e30f);
       }
@@ -1053,7 +1061,7 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
     for (int gh = 0; gh < kMaxGroup; gh++)
 #pragma unroll
       for (int k = 0; k < PB; k++) {
-        const int t = 4 * (q0 + tid + 256 * k);
+        const int t = 4 * qof(q0, gh, k);
         float m = mxh[gh];
         m = __builtin_fmaxf(m, t < T ? v[gh][k].x : -1e30f);
         m = __builtin_fmaxf(m, t + 1 < T ? v[gh][k].y : -1e30f);
@@ -1067,7 +1075,7 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
     for (int gh = 0; gh < kMaxGroup; gh++)
 #pragma unroll
       for (int k = 0; k < PB; k++) {
-        const int q = q0 + tid + 256 * k;
+        const int q = qof(q0, gh, k);
         if (gh < G && q < T4) {
           const float mx = rmax[gh];
           float4 e;
@@ -1081,7 +1089,7 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
       }
   };
   // the first V chunk loads while the softmax runs (the score registers leave no room for more)
-  float4 vr[3][NV];
+  VRaw vr[3][NV];
   vload(0, vr[0]);
   float mxh[kMaxGroup];
 #pragma unroll
@@ -1112,7 +1120,7 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
     for (int gh = 0; gh < kMaxGroup; gh++)
 #pragma unroll
       for (int k = 0; k < PB; k++) {
-        const int q = tid + 256 * k;
+        const int q = qof(0, gh, k);
         if (gh < G && q < T4) {
           const float sum = rsum[gh];
           float4 e = v[gh][k];
