@@ -313,11 +313,22 @@ __device__ __forceinline__ void quantize_item(const float (&v)[8], int b, int j,
   }
 }
 
+// The norm weights of work item t (block t / 4, lane t % 4: the elements quantize_row_dev reads).
+__device__ __forceinline__ void norm_weights_item(const float* __restrict__ w, int t, float (&wv)[8]) {
+  const int base = ((t >> 2) << 5) + ((t & 3) << 1);
+  const int e[8] = {base, base + 1, base + 8, base + 9, base + 16, base + 17, base + 24, base + 25};
+#pragma unroll
+  for (int k = 0; k < 8; k++) wv[k] = w[e[k]];
+}
+
+// With pre (QM_NORM, at most one work item per thread), wpre holds the item's norm weights, loaded
+// by the caller before the row's sum of squares; otherwise they are read here.
 template <int MODE>
 __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, const float* xl, int st, int n,
                                                  const float* __restrict__ w, float rs,
                                                  uint4* __restrict__ out, int tid, int nthreads,
-                                                 uint4* __restrict__ outh = nullptr, int tok = 0) {
+                                                 uint4* __restrict__ outh, int tok,
+                                                 const float (&wpre)[8], bool pre) {
   const int nb = n >> 5;
   for (int t = tid; t < (nb << 2); t += nthreads) {
     const int b = t >> 2, j = t & 3;
@@ -337,7 +348,7 @@ __device__ __forceinline__ void quantize_row_dev(const float* __restrict__ xr, c
       for (int k = 0; k < 8; k++) {
         const int i = e[k];
         if (MODE == QM_NORM) {
-          v[k] = (lane_staged(xl, st, i) * rs) * w[i];
+          v[k] = (lane_staged(xl, st, i) * rs) * (pre ? wpre[k] : w[i]);
         } else {
           v[k] = xr[i];
         }
@@ -395,12 +406,25 @@ __host__ __device__ inline int sq_stride(int n) { return (((n >> 2) + 31) & ~31)
 // The row by reference lane (xl[(i & 3) * st + i / 4], read back by lane_staged) and the squares
 // x_i * x_i the same way (sq[(i & 3) * sst + i / 4], sst = sq_stride(n)); every product rounds once, as in the
 // reference's sum of v * v.
+// The loads of a thread's values are all issued before the first store (eight per pass), so the
+// staging waits for one memory round trip per pass, not one per value.
 __device__ __forceinline__ void sq_stage(const float* __restrict__ x, int n, float* sq, int sst, float* xl,
                                          int st, int tid, int nthreads) {
-  for (int i = tid; i < n; i += nthreads) {
-    const float v = x[i];
-    sq[(i & 3) * sst + (i >> 2)] = v * v;
-    xl[(i & 3) * st + (i >> 2)] = v;
+  for (int i0 = tid; i0 < n; i0 += 8 * nthreads) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int i = i0 + k * nthreads;
+      v[k] = i < n ? x[i] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int i = i0 + k * nthreads;
+      if (i < n) {
+        sq[(i & 3) * sst + (i >> 2)] = v[k] * v[k];
+        xl[(i & 3) * st + (i >> 2)] = v[k];
+      }
+    }
   }
 }
 

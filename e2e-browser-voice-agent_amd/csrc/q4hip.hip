@@ -105,13 +105,17 @@ __global__ __launch_bounds__(256) void k_quant(const float* __restrict__ in, int
   float rs = 0.0f;
   const int sst = sq_stride(n);
   float* const xs = xl + 4 * sst;         // the row by lane, after the squares
+  // with one work item per thread, its norm weights load with the row, ahead of the sum
+  const bool one = MODE == QM_NORM && (n >> 3) <= (int)blockDim.x;
+  float wv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  if (one && (int)threadIdx.x < (n >> 3)) norm_weights_item(w, threadIdx.x, wv);
   if (MODE == QM_NORM) {
     sq_stage(xr, n, xl, sst, xs, st, threadIdx.x, blockDim.x);
     __syncthreads();
     rs = rms_scale_sq(xl, n, sst, eps, red);
   }
   quantize_row_dev<MODE>(xr, xs, st, n, w, rs, xq + (size_t)blockIdx.x * xstride * 4, threadIdx.x, blockDim.x,
-                         xh ? xh + xh_tile(blockIdx.x, xstride) : nullptr, blockIdx.x & 15);
+                         xh ? xh + xh_tile(blockIdx.x, xstride) : nullptr, blockIdx.x & 15, wv, one);
 }
 
 enum { OP_STORE = 0, OP_BIAS = 1, OP_ADD = 2 };   // put() of kernels.c:190-194
