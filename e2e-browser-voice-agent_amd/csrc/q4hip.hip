@@ -639,6 +639,22 @@ __device__ __forceinline__ void amax_merge(float& bv, int& bi, float v, int i) {
   if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) { bv = v; bi = i; }
 }
 
+// This thread's (max, first index) over entries lo + tid + 256 k < hi of a 4096-entry slice: the
+// 16 values load together, then merge in index order.
+__device__ __forceinline__ void slice_amax(const float* __restrict__ row, int lo, int hi, int tid, float& bv, int& bi) {
+  float v[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    const int i = lo + tid + 256 * k;
+    v[k] = i < hi ? row[i] : 0.0f;
+  }
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    const int i = lo + tid + 256 * k;
+    if (i < hi) amax_merge(bv, bi, v[k], i);
+  }
+}
+
 __global__ __launch_bounds__(256) void k_argmax1(const float* __restrict__ lg, int V, float* __restrict__ pv,
                                                  int* __restrict__ pi) {
   __shared__ float sv[256];
@@ -647,7 +663,7 @@ __global__ __launch_bounds__(256) void k_argmax1(const float* __restrict__ lg, i
   const int lo = blockIdx.x * 4096, hi = min(V, lo + 4096);
   float bv = 0.0f;
   int bi = -1;
-  for (int i = lo + tid; i < hi; i += 256) amax_merge(bv, bi, lg[i], i);
+  slice_amax(lg, lo, hi, tid, bv, bi);
   sv[tid] = bv;
   si[tid] = bi;
   __syncthreads();
@@ -821,13 +837,25 @@ __global__ void k_embed_list(const uint8_t* __restrict__ emb, int D, const int* 
   const int m = blockIdx.x;
   const uint8_t* row = emb + (size_t)tok[m] * (D / 32) * 18;
   float* xr = x + (size_t)m * D;
-  for (int idx = threadIdx.x; idx < D / 2; idx += blockDim.x) {
-    const int blk = idx >> 4, j = idx & 15;
-    const uint8_t* bp = row + blk * 18;
-    const float d = half_bits_to_float((uint32_t)bp[0] | ((uint32_t)bp[1] << 8));
-    const int q = bp[2 + j];
-    xr[32 * blk + j] = (float)((q & 15) - 8) * d;
-    xr[32 * blk + 16 + j] = (float)((q >> 4) - 8) * d;
+  // four byte pairs per thread load together, then dequantize
+  for (int i0 = threadIdx.x; i0 < D / 2; i0 += 4 * blockDim.x) {
+    uint32_t dh[4], q[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int idx = i0 + k * blockDim.x;
+      const uint8_t* bp = row + (idx >> 4) * 18;
+      dh[k] = idx < D / 2 ? (uint32_t)bp[0] | ((uint32_t)bp[1] << 8) : 0u;
+      q[k] = idx < D / 2 ? bp[2 + (idx & 15)] : 0u;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int idx = i0 + k * blockDim.x, blk = idx >> 4, j = idx & 15;
+      if (idx < D / 2) {
+        const float d = half_bits_to_float(dh[k]);
+        xr[32 * blk + j] = (float)((int)(q[k] & 15) - 8) * d;
+        xr[32 * blk + 16 + j] = (float)((int)(q[k] >> 4) - 8) * d;
+      }
+    }
   }
 }
 
@@ -1254,7 +1282,7 @@ __global__ __launch_bounds__(256) void k_argmax_rows1(const float* __restrict__ 
   const int lo = blockIdx.x * 4096, hi = min(V, lo + 4096);
   float bv = 0.0f;
   int bi = -1;
-  for (int i = lo + tid; i < hi; i += 256) amax_merge(bv, bi, row[i], i);
+  slice_amax(row, lo, hi, tid, bv, bi);
   sv[tid] = bv;
   si[tid] = bi;
   __syncthreads();
