@@ -14,6 +14,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "gemm_sk.h"
@@ -1709,7 +1710,7 @@ size_t softmax_lds(int H, int KVH, int ctx) {
 // are quantized as one quantize_row block, as in k_attn_pv_list.
 constexpr int kPvTileRows = 4;          // QT
 constexpr int kPvChunk = 64;
-template <int HD, class KT>
+template <int HD, class KT, int NVT>
 __global__ __launch_bounds__(1024) void k_pv_tiles(const float* __restrict__ sc, int H, int KVH,
                                                    const KT* __restrict__ vc, int ctx, int layer,
                                                    float* __restrict__ att, int D, const int* __restrict__ pos, int B,
@@ -1727,34 +1728,51 @@ __global__ __launch_bounds__(1024) void k_pv_tiles(const float* __restrict__ sc,
   for (int k = 0; k < kPvTileRows; k++)
     if (b0 + k < B) tmax = max(tmax, pos[b0 + k] + 1);
   const KT* vb = vc + ((size_t)layer * KVH + g) * ctx * HD + c0;
-  // staging: V float4 i (row i / 8, columns 4 (i % 8) ..), p float4 i (row r = i / 16 of the tile's
-  // (q, h) rows, positions 4 (i % 16) ..)
-  auto stage = [&](int t0) {
-    for (int i = tid; i < kPvChunk * kPvCols / 4; i += blockDim.x) {
-      const int row = i >> 3, c4 = (i & 7) * 4;
-      const int t = min(t0 + row, tmax - 1);               // rows from tmax on are never used
-      const float4 v = kv_ld4<KT>(vb + (size_t)t * HD + c4);
-      vs[(c4 + 0) * CHS + row] = v.x;
-      vs[(c4 + 1) * CHS + row] = v.y;
-      vs[(c4 + 2) * CHS + row] = v.z;
-      vs[(c4 + 3) * CHS + row] = v.w;
+  // staging: V float4 i (row i / 8, columns 4 (i % 8) ..) for i = tid + k blockDim (k < NVT, with
+  // NVT blockDim >= 512: blockDim = 128 G) and p float4 tid (row r = tid / 16 of the tile's (q, h) rows,
+  // positions 4 (tid % 16) ..; 64 G of them).  A chunk's values come through one of two register
+  // sets, loaded two chunks ahead (V as loaded: fp16 stays fp16 until it is stored), so the loads
+  // of the next chunks are in flight while one is added; the loop runs in whole pairs, the sets'
+  // roles fixed in each pass.
+  typedef typename KvRaw<KT>::T VRaw;
+  constexpr int NVI = kPvChunk * kPvCols / 4;              // V float4 per chunk
+  const bool pth = tid < kPvTileRows * G * (kPvChunk / 4);
+  const int pr_ = tid / (kPvChunk / 4), pu4 = (tid % (kPvChunk / 4)) * 4;
+  const int pq = pr_ / G, ph = pr_ - pq * G, pb = b0 + pq;
+  const int nch = (tmax + kPvChunk - 1) / kPvChunk;
+  struct Set {
+    VRaw v[NVT];
+    float4 p;
+  };
+  auto load = [&](int ch, Set& st) {
+    const int t0 = min(ch, nch - 1) * kPvChunk;
+#pragma unroll
+    for (int k = 0; k < NVT; k++) {
+      const int i = tid + k * (int)blockDim.x;
+      if (i < NVI) st.v[k] = kv_raw4<KT>(vb + (size_t)min(t0 + (i >> 3), tmax - 1) * HD + (i & 7) * 4);   // rows from tmax on are never used
     }
-    for (int i = tid; i < kPvTileRows * G * (kPvChunk / 4); i += blockDim.x) {
-      const int r = i / (kPvChunk / 4), u4 = (i % (kPvChunk / 4)) * 4;
-      const int qq = r / G, hh = r - qq * G, bb = b0 + qq;
-      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (bb < B && t0 + u4 < tmax)
-        v = *reinterpret_cast<const float4*>(sc + ((size_t)bb * H + g * G + hh) * CS + t0 + u4);
-      *reinterpret_cast<float4*>(&ps[r * CHS + u4]) = v;
+    st.p = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (pth && pb < B && t0 + pu4 < tmax)
+      st.p = *reinterpret_cast<const float4*>(sc + ((size_t)pb * H + g * G + ph) * CS + t0 + pu4);
+  };
+  auto store = [&](const Set& st) {
+#pragma unroll
+    for (int k = 0; k < NVT; k++) {
+      const int i = tid + k * (int)blockDim.x, row = i >> 3, c4 = (i & 7) * 4;
+      if (i < NVI) {
+        const float4 w = kv_wide4(st.v[k]);
+        vs[(c4 + 0) * CHS + row] = w.x;
+        vs[(c4 + 1) * CHS + row] = w.y;
+        vs[(c4 + 2) * CHS + row] = w.z;
+        vs[(c4 + 3) * CHS + row] = w.w;
+      }
     }
+    if (pth) *reinterpret_cast<float4*>(&ps[pr_ * CHS + pu4]) = st.p;
   };
   const float* pr = ps + (q * G + h) * CHS;
   const float* vr = vs + c * CHS;
   float acc = 0.0f;
-  for (int t0 = 0; t0 < tmax; t0 += kPvChunk) {
-    __syncthreads();                                       // the previous chunk is read
-    stage(t0);
-    __syncthreads();
+  auto chunk = [&](int t0) {
     if (active) {
       if (t0 + kPvChunk <= T) {                            // a whole chunk: no select on the chain
 #pragma unroll
@@ -1766,13 +1784,36 @@ __global__ __launch_bounds__(1024) void k_pv_tiles(const float* __restrict__ sc,
           acc = acc + p4.z * v4.z;
           acc = acc + p4.w * v4.w;
         }
-      } else {
+      } else if (t0 < T) {
         const int n = T - t0;
         for (int u = 0; u < kPvChunk; u++) {
           const float x = acc + pr[u] * vr[u];
           acc = u < n ? x : acc;
         }
       }
+    }
+  };
+  constexpr int NS = 2;                                    // register sets
+  Set sets[NS];
+#pragma unroll
+  for (int k = 0; k < NS; k++) load(k, sets[k]);
+  int cs = 0;
+  for (; cs + NS < nch; cs += NS)
+#pragma unroll
+    for (int k = 0; k < NS; k++) {
+      __syncthreads();                                     // the previous chunk is read
+      store(sets[k]);
+      load(cs + k + NS, sets[k]);
+      __syncthreads();
+      chunk((cs + k) * kPvChunk);
+    }
+#pragma unroll
+  for (int k = 0; k < NS; k++) {                           // the last chunks, loaded already
+    if (cs + k < nch) {
+      __syncthreads();
+      store(sets[k]);
+      __syncthreads();
+      chunk((cs + k) * kPvChunk);
     }
   }
   if (active) att[(size_t)b * D + (g * G + h) * HD + c0 + c] = acc;
@@ -1821,15 +1862,25 @@ void launch_attn_list_t(hipStream_t s, int HD, int B, int H, int KVH, const floa
   const size_t lds = attn_pv_lds(H, KVH, ctx);
   if (seq_stride == 0 && B > 1 && !pv_tiles_off()) {   // a prompt pass: rows share one cache
     const dim3 tg((unsigned)(HD / kPvCols), (unsigned)KVH, (unsigned)((B + kPvTileRows - 1) / kPvTileRows));
-    const unsigned nthr = (unsigned)(kPvTileRows * (H / KVH) * kPvCols);
+    const int G = H / KVH;
+    const unsigned nthr = (unsigned)(kPvTileRows * G * kPvCols);
+    // V float4 per thread and chunk: 512 over 128 G threads
+    auto tiles = [&](auto hd, auto nvt) {
+      k_pv_tiles<decltype(hd)::value, KT, decltype(nvt)::value><<<tg, nthr, 0, s>>>(sc, H, KVH, vc, ctx, layer, att, D,
+                                                                                    pos, B, xq, xstride, xh);
+    };
+    if (HD == 64) k_attn_scores_list<64, KT><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, 0);
+    else k_attn_scores_list<128, KT><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, 0);
+    k_softmax_rows<<<dim3((unsigned)KVH, (unsigned)B), 256, softmax_lds(H, KVH, ctx), s>>>(sc, H, KVH, ctx, pos);
+    using I64 = std::integral_constant<int, 64>;
+    using I128 = std::integral_constant<int, 128>;
+    using N1 = std::integral_constant<int, 1>;
+    using N2 = std::integral_constant<int, 2>;
+    using N4 = std::integral_constant<int, 4>;
     if (HD == 64) {
-      k_attn_scores_list<64, KT><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, 0);
-      k_softmax_rows<<<dim3((unsigned)KVH, (unsigned)B), 256, softmax_lds(H, KVH, ctx), s>>>(sc, H, KVH, ctx, pos);
-      k_pv_tiles<64, KT><<<tg, nthr, 0, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, B, xq, xstride, xh);
+      if (G >= 4) tiles(I64(), N1()); else if (G >= 2) tiles(I64(), N2()); else tiles(I64(), N4());
     } else {
-      k_attn_scores_list<128, KT><<<sg, 64, 0, s>>>(qkv, QKV, H, KVH, kc, ctx, layer, sc, pos, 0);
-      k_softmax_rows<<<dim3((unsigned)KVH, (unsigned)B), 256, softmax_lds(H, KVH, ctx), s>>>(sc, H, KVH, ctx, pos);
-      k_pv_tiles<128, KT><<<tg, nthr, 0, s>>>(sc, H, KVH, vc, ctx, layer, att, D, pos, B, xq, xstride, xh);
+      if (G >= 4) tiles(I128(), N1()); else if (G >= 2) tiles(I128(), N2()); else tiles(I128(), N4());
     }
     return;
   }
