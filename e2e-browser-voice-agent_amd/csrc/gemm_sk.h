@@ -4,10 +4,11 @@
 // matmul_q4 does (engine/kernels.c:200-229): four lane chains acc_j += f32(p_j) * (dw * dx) over
 // the blocks in order, then ((a0 + a1) + a2) + a3.  p_j, the integer dot of reference lane j's 8
 // nibbles (as n - 8) with its 8 int8 activations, is one v_mfma_f32_16x16x16_f16 per 16 rows x 16
-// tokens: k = 0..7 carry x_k * (1024 + n_k) (the nibble becomes fp16 0x6400 | n by a byte
-// permute), k = 8 carries (-sum x) * 1032, k = 9..15 are zero; every product and partial sum is an
-// integer below 2^22, so the fp32 result is exactly p_j.  The chain updates stay on the vector
-// ALUs in block order.
+// tokens: k = 0..3 carry x_k * (1024 + n_k) (a low nibble becomes fp16 0x6400 | n by a byte
+// permute), k = 4..7 carry (x_k / 16) * (1024 + 16 n_k) (a high nibble masked in place, 0x6400 |
+// n << 4) = 64 x_k + n_k x_k, k = 8 carries (-sum of x_0..3) * 1032 and k = 9 (-sum of x_4..7) * 72,
+// k = 10..15 are zero; every product and partial sum is an integer below 2^21, so the fp32 result
+// is exactly p_j.  The chain updates stay on the vector ALUs in block order.
 //
 // Layout of a workgroup (16 tokens, 256 threads):
 //   JS = 4  16 weight rows; wave w runs lane chain w of all 16 rows (for matrices with few rows:
@@ -169,18 +170,18 @@ __device__ __forceinline__ void sk_issue(const unsigned char* slot, const SkSrc<
 }
 
 // The B operand of lane quarter kg for one weight word (4 nibble pairs of one block and chain):
-// kg 0 low nibbles, kg 1 high nibbles, each as fp16 1024 + n; kg 2 (1032, 0, 0, 0); kg 3 zero.
+// kg 0 the low nibbles as fp16 1024 + n, kg 1 the high nibbles masked in place (no shift) as
+// 1024 + 16 n, kg 2 (1032, 72, 0, 0), kg 3 zero: one and-or and two byte permutes per operand.
 struct SkB {
-  uint32_t sh, mask, orv, sel0, sel1;
+  uint32_t mask, orv, sel0, sel1;
   __device__ __forceinline__ explicit SkB(int kg) {
-    sh = (kg & 1) << 2;
-    mask = kg < 2 ? 0x0F0F0F0Fu : 0u;
-    orv = kg < 2 ? 0u : 0x08080808u;
-    sel0 = kg < 2 ? 0x04010400u : kg == 2 ? 0x0C0C0400u : 0x0C0C0C0Cu;
+    mask = kg == 0 ? 0x0F0F0F0Fu : kg == 1 ? 0xF0F0F0F0u : 0u;
+    orv = kg == 2 ? 0x54800008u : 0u;                        // bytes of fp16 1032 (0x6408) and 72 (0x5480)
+    sel0 = kg < 2 ? 0x04010400u : kg == 2 ? 0x03020400u : 0x0C0C0C0Cu;
     sel1 = kg < 2 ? 0x04030402u : 0x0C0C0C0Cu;
   }
   __device__ __forceinline__ sk_h4 operator()(uint32_t wv) const {
-    const uint32_t v = ((wv >> sh) & mask) | orv;
+    const uint32_t v = (wv & mask) | orv;
     return __builtin_bit_cast(sk_h4, make_uint2(__builtin_amdgcn_perm(0x64646464u, v, sel0),
                                                 __builtin_amdgcn_perm(0x64646464u, v, sel1)));
   }

@@ -228,6 +228,11 @@ __device__ __forceinline__ int quant_one(float v) {
 __device__ __forceinline__ uint32_t pack_f16x2(int a, int b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
 }
+// a / 16 and b / 16 as fp16 (exact for |a|, |b| <= 2048)
+__device__ __forceinline__ uint32_t pack_f16x2_16th(int a, int b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)((float)a * 0.0625f)) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)((float)b * 0.0625f)) << 16);
+}
 
 // A row of n floats staged in shared memory "by lane" (sq_stage): value i at xl[(i & 3) * st + (i >> 2)],
 // st = n/4 + 1, so reference lane j (the values i = j mod 4, kernels.c:81-82) is one contiguous run
@@ -287,7 +292,9 @@ __host__ __device__ inline size_t xh_bytes(int tokens, int xstride) {
 
 // Quantize the 8 values of reference lane j of block b (quantize_row, kernels.c:90-114) into
 // out[4b + j] = {A_j, B_j, -8 sum q, d}; with outh (the token's tile, xh_tile) also the fp16
-// operand of token t = m % 16 and, for j = 0, its block scale.
+// operand of token t = m % 16 and, for j = 0, its block scale.  The operand's four quarters (the
+// k = 0..15 of the matrix-core product against the weight encoding of gemm_sk.h): q0..q3;
+// q4..q7 / 16; -(q0 + .. + q3), -(q4 + .. + q7), 0, 0; zero.
 __device__ __forceinline__ void quantize_item(const float (&v)[8], int b, int j, uint4* __restrict__ out,
                                               uint4* __restrict__ outh, int t = 0) {
   float am = 0.0f;
@@ -306,8 +313,8 @@ __device__ __forceinline__ void quantize_item(const float (&v)[8], int b, int j,
     uint4* o = outh + (size_t)b * kXhBlock;
     uint2* oq = reinterpret_cast<uint2*>(o) + j * 64 + t;       // quarter q of (chain j, token t): oq[16 q]
     oq[0] = make_uint2(pack_f16x2(q[0], q[1]), pack_f16x2(q[2], q[3]));
-    oq[16] = make_uint2(pack_f16x2(q[4], q[5]), pack_f16x2(q[6], q[7]));
-    oq[32] = make_uint2(pack_f16x2(-sum, 0), 0u);
+    oq[16] = make_uint2(pack_f16x2_16th(q[4], q[5]), pack_f16x2_16th(q[6], q[7]));
+    oq[32] = make_uint2(pack_f16x2(-(q[0] + q[1] + q[2] + q[3]), -(q[4] + q[5] + q[6] + q[7])), 0u);
     oq[48] = make_uint2(0u, 0u);
     if (j == 0) reinterpret_cast<float*>(o + 128)[t] = dd;
   }
