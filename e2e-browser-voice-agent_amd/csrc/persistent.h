@@ -247,6 +247,16 @@ __device__ __forceinline__ void ll_wait1(const uint64_t* p, uint64_t& w, uint32_
 // fence of __syncthreads would.  The "memory" clobber keeps loads and stores on their side.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// The workgroup-uniform "give up" decision after a wait: a thread whose wait gave up raises the
+// shared flag before the barrier, every thread reads it after.  One barrier and one shared-memory
+// read, where __syncthreads_or takes three of each.  The flag is cleared once per launch and never
+// lowered: a raised flag ends the launch.
+__device__ __forceinline__ bool wg_bad(int* flag, bool bad) {
+  if (bad) *(volatile int*)flag = 1;
+  lds_barrier();
+  return *(volatile int*)flag != 0;
+}
+
 // ---------------------------------------------------------------- register-resident weights
 
 // CNT groups of one 16-row group, lane (r = lane/4, j = lane%4): word j of 4 blocks per group and
@@ -676,6 +686,7 @@ struct PSmem {
   float* argv;    // 8
   int* argi;      // 8
   uint32_t* raw;  // RAW words: exchange entries
+  int* flag;      // the give-up flag of wg_bad (word 7 of red)
   float* terms;   // last: 64 * NBM per-block terms (OD); for the attention role its ctx + 2 kRingRows
                   // scores, then its K/V ring and staged tile
 };
@@ -740,6 +751,7 @@ __device__ __forceinline__ PSmem psmem(unsigned char* base) {
   m.argv = (float*)(base + off);    off += 8 * 4;
   m.argi = (int*)(base + off);      off += 8 * 4;
   m.raw = (uint32_t*)(base + off);  off += (size_t)S::RAW * 4;
+  m.flag = (int*)(m.red + 7);
   m.terms = (float*)(base + off);
   return m;
 }
@@ -808,31 +820,38 @@ __device__ __forceinline__ void normw_load(const float* w, float (&nw)[4]) {
   }
 }
 
-// RMSNorm + quantize of the staged x into m.xq (kernels.c:80-86, 328-331): lanes 0..3 of wave 0
-// run the four lane sums of x*x in order, then thread t < NBD*4 quantizes block lane t.
-// The caller has synchronised after staging; returns after a barrier.
+// RMSNorm + quantize of the staged x into m.xq (kernels.c:80-86, 328-331): lanes 0..3 of every
+// wave run the four lane sums of x*x in order and the wave forms the scale from them itself (the
+// same operations on the same values in every wave, so the same bits), then thread t < NBD*8
+// quantizes half a block lane.  No shared-memory round trip and no barrier between the sums and
+// the quantize; the values a thread quantizes are read before the sums.  The caller has
+// synchronised after staging; returns after a barrier.
 template <class S>
 __device__ __forceinline__ void norm_quant(const PSmem& m, const float (&nw)[4], float eps, unsigned long long* mark = nullptr) {
-  const int tid = threadIdx.x;
-  if (tid < 64) {
-    float s = 0.0f;
-    if (tid < 4) s = run_sum<S::D / 4>(m.sq + tid * S::STV);
-    if (mark && tid == 0) {
-      asm volatile("" ::"v"(s));
-      *mark = wall_clock64();
-    }
-    const float s0 = __shfl(s, 0), s1 = __shfl(s, 1), s2 = __shfl(s, 2), s3 = __shfl(s, 3);
-    if (tid == 0) m.red[4] = recip(__builtin_sqrtf(div_const<S::D>(((s0 + s1) + s2) + s3) + eps));
-  }
-  __syncthreads();
-  const float rs = m.red[4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  float xv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (tid < S::NBD * 8) {
-    float v[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const int i = lane_elem(tid >> 1, 4 * (tid & 1) + k);
-      v[k] = (m.xl[(i & 3) * S::STV + (i >> 2)] * rs) * nw[k];
+      xv[k] = m.xl[(i & 3) * S::STV + (i >> 2)];
     }
+  }
+  float s = 0.0f;
+  if (lane < 4) s = run_sum<S::D / 4>(m.sq + lane * S::STV);
+  if (mark && tid == 0) {
+    asm volatile("" ::"v"(s));
+    *mark = wall_clock64();
+  }
+  const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+  const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 1));
+  const float s2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 2));
+  const float s3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 3));
+  const float rs = recip(__builtin_sqrtf(div_const<S::D>(((s0 + s1) + s2) + s3) + eps));
+  if (tid < S::NBD * 8) {
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] = (xv[k] * rs) * nw[k];
     const uint4 q = quant_half(v);
     if ((tid & 1) == 0) m.xq[tid >> 1] = q;
   }
@@ -873,7 +892,7 @@ __device__ __forceinline__ bool head_scan_q4(const PArgs& a, const PSmem& m, uin
   if (rgi < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi, lane, R0[0]);
   if (rgi + stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + stride, lane, R1[0]);
   recv_x<S>(a.ll + S::oXH, epx, a.st, m, bad, a.nap);
-  if (__syncthreads_or(bad)) return false;
+  if (wg_bad(m.flag, bad)) return false;
   prof_mark(a, s, a.NL * 16 + 0);
   norm_quant<S>(m, nw, a.eps);
   while (rgi < nRG) {
@@ -979,7 +998,7 @@ __device__ __forceinline__ bool head_scan_q8(const PArgs& a, const PSmem& m, uin
   WR8<NG8, S::NB8D> R0, R1;
   if (rgi < nRG) wr8_load<NG8, S::NB8D>(a.head, rgi, lane, R0);
   recv_x<S>(a.ll + S::oXH, epx, a.st, m, bad, a.nap);
-  if (__syncthreads_or(bad)) return false;
+  if (wg_bad(m.flag, bad)) return false;
   prof_mark(a, s, a.NL * 16 + 0);
   norm_quant<S>(m, nw, a.eps);
   while (rgi < nRG) {
@@ -1028,7 +1047,7 @@ __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32
     m.raw[tid] = v[0];
     if (tid + kPThreads < 2 * G) m.raw[tid + kPThreads] = v[1];
   }
-  if (__syncthreads_or(bad)) return -1;
+  if (wg_bad(m.flag, bad)) return -1;
   bv = 0.0f;
   bi = -1;
   for (int g = tid; g < G; g += kPThreads) arg_merge(bv, bi, __uint_as_float(m.raw[2 * g]), (int)m.raw[2 * g + 1]);
@@ -1235,7 +1254,7 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
       for (int k = 0; k < S::KD; k++)
         if (tid + kPThreads * k < S::D) m.xl[tid + kPThreads * k] = __uint_as_float(v[k]);
     }
-    if (__syncthreads_or(bad)) return false;
+    if (wg_bad(m.flag, bad)) return false;
     if (wg == 0) prof_mark(a, s, l * 16 + 0);
     prof_wg(a, s, l, 0);
     if (tid < S::NBD * 8) {
@@ -1270,7 +1289,7 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
       for (int k = 0; k < S::KACT; k++)
         if (tid + kPThreads * k < S::NACT) m.raw[tid + kPThreads * k] = v[k];
     }
-    if (__syncthreads_or(bad)) return false;
+    if (wg_bad(m.flag, bad)) return false;
     for (int b = tid; b < S::NBF; b += kPThreads) {
       uint32_t e[9];
 #pragma unroll
@@ -1400,7 +1419,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     } else {
       recv_x<S>(a.ll + S::oX2, phase_epoch(ep0, s, E, 4 * (l - 1) + 3), a.st, m, bad, a.nap);
     }
-    if (__syncthreads_or(bad)) return false;
+    if (wg_bad(m.flag, bad)) return false;
     if (mark) prof_mark(a, s, l * 16 + 4);
     prof_wg(a, s, l, 0);
     norm_quant<S>(m, nw, a.eps);
@@ -1550,7 +1569,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
           if (t < oend) sc[t] = __uint_as_float((uint32_t)w[k]);
         }
       }
-      if (__syncthreads_or(bad)) return false;
+      if (wg_bad(m.flag, bad)) return false;
       prof_wg(a, s, l, 3);
       for (int t = obeg + tid; t < oend; t += kPThreads) lmax = __builtin_fmaxf(lmax, sc[t]);
     }
@@ -1578,7 +1597,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       ll_wait1(ksrc, kw, ekv, a.st, bad, a.nap);
       kv[tid - 64] = __uint_as_float((uint32_t)kw);    // kv and vv are adjacent: 0..63 K, 64..127 V
     }
-    if (__syncthreads_or(bad)) return false;
+    if (wg_bad(m.flag, bad)) return false;
     if (mark) prof_mark(a, s, l * 16 + 15);
     prof_wg(a, s, l, 4);
     if (tid < kHD) {
@@ -1701,7 +1720,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
         }
       }
       ring_drain();
-      if (__syncthreads_or(bad)) {
+      if (wg_bad(m.flag, bad)) {
         if (tid == 0) __hip_atomic_store(&a.st->abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return false;
       }
@@ -1802,7 +1821,7 @@ __device__ __forceinline__ bool kv_step(const PArgs& a, const PSmem& m, uint32_t
     } else {
       recv_x<S>(a.ll + S::oX2, phase_epoch(ep0, s, E, 4 * (l - 1) + 3), a.st, m, bad, a.nap);
     }
-    if (__syncthreads_or(bad)) return false;
+    if (wg_bad(m.flag, bad)) return false;
     prof_wg(a, s, l, 0);
     norm_quant<S>(m, nw, a.eps, prof_slot(a, s, l, 7));
     prof_wg(a, s, l, 2);
@@ -1842,7 +1861,7 @@ __device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t
     float nw[4];
     normw_load<S>(L.ffn_norm, nw);
     recv_x<S>(a.ll + S::oX1, phase_epoch(ep0, s, E, 4 * l + 1), a.st, m, bad, a.nap);
-    if (__syncthreads_or(bad)) return false;
+    if (wg_bad(m.flag, bad)) return false;
     if (u == 0) prof_mark(a, s, l * 16 + 7);
     prof_wg(a, s, l, 0);
     norm_quant<S>(m, nw, a.eps, prof_slot(a, s, l, 7));
@@ -1884,6 +1903,8 @@ __global__ __launch_bounds__(kPThreads, 1) void k_decode_persistent(PArgs a) {
   int pos = a.st->pos0;
   int tok = a.tokens[pos];
   const int wg = lwg(a), wave = wave_id();
+  if (threadIdx.x == 0) *m.flag = 0;
+  __syncthreads();
   if (wg == 0) prof_mark(a, 0, a.NL * 16 + 3);
   if (a.prof && wg == 0 && threadIdx.x == 0) a.prof[a.NL * 16 + 4] = clock64();
   bool bad = false;
