@@ -527,9 +527,16 @@ __device__ __forceinline__ void matvec_rows16(const Q4Mat& W, int tile, int rr, 
 
 // ((acc_0 + acc_1) + acc_2) + acc_3 over the four lanes of a row (hsum, kernels.c:116-118);
 // valid in lane j == 0.
-__device__ __forceinline__ float hsum4(float a0) {
-  const float a1 = __shfl_down(a0, 1, 4), a2 = __shfl_down(a0, 2, 4), a3 = __shfl_down(a0, 3, 4);
-  return a0 + a1 + a2 + a3;
+// Lane k (0..3) of this lane's quad, by a DPP quad broadcast (no shared-memory round trip).
+template <int K>
+__device__ __forceinline__ float quad_lane(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), K * 0x55, 0xF, 0xF, false));
+}
+
+// ((l0 + l1) + l2) + l3 over the four lanes of a quad (hsum, kernels.c:116-118), in every lane.
+__device__ __forceinline__ float hsum4(float v) {
+  const float a0 = quad_lane<0>(v), a1 = quad_lane<1>(v), a2 = quad_lane<2>(v), a3 = quad_lane<3>(v);
+  return ((a0 + a1) + a2) + a3;
 }
 
 }  // namespace q4

@@ -124,9 +124,10 @@ struct PShape {
   // exchange area, in 8-byte entries: x after o, x after down, x into the head, attention
   // output, quantized activation, the new K and V rows of each kv group ([group][k, v][64]), then
   // two (value, index) argmax buffers used by step parity.
-  // Every producer's entries start a 128-byte line; the 9 activation entries of a GU workgroup
-  // get a line of their own (kActStride entries), since lines shared by producers on different
-  // XCDs reach the readers later.
+  // Every producer writes whole 128-byte lines (16 entries), each with one store instruction: a
+  // line written piecewise (by several waves or workgroups) reaches its readers ~0.3-0.7 us later.
+  // The 9 activation entries of a GU workgroup fill a line with padding (kActStride entries), and
+  // each K/V workgroup's 16 rows form one line.
   static constexpr int oX1 = 0, oX2 = D, oXH = 2 * D, oATT = 3 * D, oACT = 4 * D;
   static constexpr int oKV = oACT + kActStride * nGU, oARG = oKV + 2 * KVH * kHD;
   static constexpr size_t ll_entries(int G) { return (size_t)oARG + 2 * (size_t)kArgStride * G; }
@@ -1035,10 +1036,12 @@ __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32
   }
   if (lane == 0) { m.argv[wave] = bv; m.argi[wave] = bi; }
   __syncthreads();
-  if (tid == 0) {
+  if (tid < kArgStride) {
+    // every lane of the line merges the four waves' pairs; one store writes the whole line
+    bv = m.argv[0];
+    bi = m.argi[0];
     for (int w = 1; w < 4; w++) arg_merge(bv, bi, m.argv[w], m.argi[w]);
-    ll_put(LARG + kArgStride * wg, __float_as_uint(bv), eph);
-    ll_put(LARG + kArgStride * wg + 1, (uint32_t)bi, eph);
+    ll_put(LARG + kArgStride * wg + tid, tid == 0 ? __float_as_uint(bv) : (uint32_t)bi, eph);
   }
   prof_mark(a, s, a.NL * 16 + 1);
   {
@@ -1232,21 +1235,153 @@ __device__ __forceinline__ bool lds_wait_ge3(volatile LdsInt* c, int v) {
 
 // ---------------------------------------------------------------- roles (one step each)
 
-// o and down rows 16w..16w+15 for wave W's share of the blocks; the residual x of those rows lives
-// in m.own.  Wave 0 runs the serial passes and the stores.
-template <class S, int W>
+// Quad-chain rows (o and down of the OD role).  Wave w owns rows 4w..4w+3 of the workgroup's 16;
+// lane l is (row l >> 4, reference lane j = (l >> 2) & 3, phase p = l & 3).  Phase p holds the
+// groups g = 4k + p of four blocks and forms their terms f32(p_j) * (dw * dx) (kernels.c:137); the
+// four lanes of the quad all run the same chain acc = acc + term over the blocks in order
+// (kernels.c:217-218), taking each term from the lane that formed it by a DPP quad broadcast.  The
+// chain runs while the terms of later groups are formed, with no shared-memory terms and no barrier
+// between the waves.
+template <int NG>
+struct QR {
+  static constexpr int NK = (NG + 3) / 4;   // groups per phase
+  uint4 w[NK];                              // word j of the group's 4 blocks
+  uint2 s[NK];                              // the group's 4 fp16 scales
+};
+
+__device__ __forceinline__ uint2 gld2u(const void* p) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(1))) const u32x2 GU2;
+  const u32x2 v = *(GU2*)p;
+  return make_uint2(v.x, v.y);
+}
+
+// Groups 4k + p (the last group where 4k + p is past NG: never used) of row `row`.
+template <int NG, int NB8>
+__device__ __forceinline__ void qr_load(const Q4Mat& W, int row, int lane, QR<NG>& R) {
+  const int j = (lane >> 2) & 3, p = lane & 3, tile = row >> 6, rr = row & 63;
+  const uint4* wq = W.qs + ((size_t)tile * NG * 64 + rr) * 4 + j;
+  const uint4* wd = W.d + (size_t)tile * NB8 * 64 + rr;
+#pragma unroll
+  for (int k = 0; k < QR<NG>::NK; k++) {
+    const int g = 4 * k + p < NG ? 4 * k + p : NG - 1;
+    R.w[k] = gld(wq + (size_t)g * 256);
+    R.s[k] = gld2u(reinterpret_cast<const uint2*>(wd + (size_t)(g >> 1) * 64) + (g & 1));
+  }
+}
+
+// Activation blocks 4g .. 4g+3 of lane j (g clamped like the weights).
+template <int NG>
+__device__ __forceinline__ void qr_xload(const uint4* xq, int k, int p, int j, uint4 (&xv)[4]) {
+  const int g = 4 * k + p < NG ? 4 * k + p : NG - 1;
+#pragma unroll
+  for (int i = 0; i < 4; i++) xv[i] = xq[(4 * g + i) * 4 + j];
+}
+
+template <int Q>
+__device__ __forceinline__ float quad_add(float acc, float t) {
+  return acc + quad_lane<Q>(t);
+}
+
+// Terms of this lane's group of round k (four blocks).
+template <int NG>
+__device__ __forceinline__ void qr_terms(const QR<NG>& R, int k, const uint4 (&xv)[4], float (&t)[4]) {
+  const uint4 w = R.w[k];
+  const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+  const uint32_t sw[2] = {R.s[k].x, R.s[k].y};
+  int pp[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) pp[i] = sdot4(wv[i] & 0x0F0F0F0Fu, xv[i].x, (int)xv[i].z);
+#pragma unroll
+  for (int i = 0; i < 4; i++) pp[i] = sdot4((wv[i] >> 4) & 0x0F0F0F0Fu, xv[i].y, pp[i]);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float dw = half_bits_to_float((i & 1) ? (sw[i >> 1] >> 16) : (sw[i >> 1] & 0xffffu));
+    t[i] = (float)pp[i] * (dw * __uint_as_float(xv[i].w));
+  }
+}
+
+// The chain steps of round k: the terms of groups 4k .. 4k+3 in order, each from its phase lane.
+template <int NB, int NG>
+__device__ __forceinline__ float qr_steps(float acc, int k, const float (&t)[4]) {
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    if (4 * k + q < NG) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        if (4 * (4 * k + q) + i < NB) {
+          if (q == 0) acc = quad_add<0>(acc, t[i]);
+          else if (q == 1) acc = quad_add<1>(acc, t[i]);
+          else if (q == 2) acc = quad_add<2>(acc, t[i]);
+          else acc = quad_add<3>(acc, t[i]);
+        }
+      }
+    }
+  }
+  return acc;
+}
+
+// The chain ((0 + t_0) + t_1) + ... + t_{NB-1} of reference lane j of this lane's row, software
+// pipelined: the scheduling region of round k holds the activation reads and terms of round k + 1
+// and the (dependent) chain steps of round k, so the adds fill the latency of the next terms.
+template <int NB, int NG>
+__device__ __forceinline__ float qr_chain(const QR<NG>& R, const uint4* xq, int lane) {
+  constexpr int NK = QR<NG>::NK;
+  const int j = (lane >> 2) & 3, p = lane & 3;
+  float acc = 0.0f;
+  float t[2][4];
+  {
+    uint4 xv[4];
+    qr_xload<NG>(xq, 0, p, j, xv);
+    qr_terms<NG>(R, 0, xv, t[0]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) pin(t[0][i]);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < NK; k++) {
+    if (k + 1 < NK) {
+      uint4 xv[4];
+      qr_xload<NG>(xq, k + 1, p, j, xv);
+      qr_terms<NG>(R, k + 1, xv, t[(k + 1) & 1]);
+    }
+    acc = qr_steps<NB, NG>(acc, k, t[k & 1]);
+    pin(acc);
+    if (k + 1 < NK) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) pin(t[(k + 1) & 1][i]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  return acc;
+}
+
+// ((a_0 + a_1) + a_2) + a_3 over the reference lanes of this lane's row: lane 4j of the 16-lane row
+// holds chain j (DPP row broadcasts), in every lane of the row.
+template <int K>
+__device__ __forceinline__ float row_lane(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + K, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_hsum(float acc) {
+  const float a0 = row_lane<0>(acc), a1 = row_lane<4>(acc), a2 = row_lane<8>(acc), a3 = row_lane<12>(acc);
+  return ((a0 + a1) + a2) + a3;
+}
+
+// o and down rows 16w..16w+15: wave v takes rows 16w + 4v .. 16w + 4v + 3 as quad chains; every lane
+// of a row keeps that row's residual x in a register.  The 16 results meet in shared memory and
+// wave 0 stores them as one line.
+template <class S>
 __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int tok, bool& bad) {
-  constexpr int G0o = split_g0(S::NGD, W), Co = split_cnt(S::NGD, W);
-  constexpr int G0d = split_g0(S::NGF, W), Cd = split_cnt(S::NGF, W);
-  const int tid = threadIdx.x, lane = tid & 63, r = lane >> 2, j = lane & 3;
-  const int wg = lwg(a), row = wg * 16 + r, E = 4 * a.NL + 1;
-  if (tid < 16) m.own[tid] = embed_value(a.embd, S::D, tok, wg * 16 + tid);
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int wg = lwg(a), row = wg * 16 + 4 * wave + (lane >> 4), E = 4 * a.NL + 1;
+  const bool writer = (lane & 15) == 0;
+  float own = embed_value(a.embd, S::D, tok, row);   // the residual x of this lane's row
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
     // ---- o: x1 = x + W_o . quantize(att)
     if (l > 0) pf_delay(a.pf[0]);
-    WR<Co> ro;
-    wr_load<S::NGD, S::NB8D, G0o, Co>(L.o, wg, lane, ro);
+    QR<S::NGD> ro;
+    qr_load<S::NGD, S::NB8D>(L.o, row, lane, ro);
     {
       uint32_t v[S::KD];
       ll_recv<S::KD>(a.ll + S::oATT, S::D, phase_epoch(ep0, s, E, 4 * l + 0), a.st, bad, v, a.nap);
@@ -1265,23 +1400,20 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
       if ((tid & 1) == 0) m.xq[tid >> 1] = q;
     }
     __syncthreads();
-    wr_terms<S::NBD, G0o, Co>(ro, m.xq, lane, m.terms);
-    prof_wg(a, s, l, 4);
-    __syncthreads();
-    if constexpr (W == 0) {
-      const float v = hsum4(serial_sum<S::NBD>(m.terms, lane));
-      if (j == 0) {
-        const float x1 = m.own[r] + v;
-        m.own[r] = x1;
-        ll_put(a.ll + S::oX1 + row, __float_as_uint(x1), phase_epoch(ep0, s, E, 4 * l + 1));
-      }
-      if (wg == 0) prof_mark(a, s, l * 16 + 1);
-      prof_wg(a, s, l, 1);
+    {
+      const float v = row_hsum(qr_chain<S::NBD, S::NGD>(ro, m.xq, lane));
+      own = own + v;
+      if (writer) m.own[row - wg * 16] = own;
+      lds_barrier();
+      // the workgroup's 16 rows as one 128-byte line (lines written piecewise reach readers later)
+      if (tid < 16) ll_put(a.ll + S::oX1 + wg * 16 + tid, __float_as_uint(m.own[tid]), phase_epoch(ep0, s, E, 4 * l + 1));
     }
+    if (wg == 0) prof_mark(a, s, l * 16 + 1);
+    prof_wg(a, s, l, 1);
     // ---- down: x2 = x1 + W_down . act (act arrives quantized)
     pf_delay(a.pf[1]);
-    WR<Cd> rd;
-    wr_load<S::NGF, S::NB8F, G0d, Cd>(L.down, wg, lane, rd);
+    QR<S::NGF> rd;
+    qr_load<S::NGF, S::NB8F>(L.down, row, lane, rd);
     {
       uint32_t v[S::KACT];
       ll_recv<S::KACT>(a.ll + S::oACT, S::NACT, phase_epoch(ep0, s, E, 4 * l + 2), a.st, bad, v, a.nap, ActEntry());
@@ -1303,20 +1435,17 @@ __device__ __forceinline__ bool od_step(const PArgs& a, const PSmem& m, uint32_t
     __syncthreads();
     if (wg == 0) prof_mark(a, s, l * 16 + 2);
     prof_wg(a, s, l, 2);
-    wr_terms<S::NBF, G0d, Cd>(rd, m.xq, lane, m.terms);
-    prof_wg(a, s, l, 5);
-    __syncthreads();
-    prof_wg(a, s, l, 6);
-    if constexpr (W == 0) {
-      const float v = hsum4(serial_sum<S::NBF>(m.terms, lane));
-      if (j == 0) {
-        const float x2 = m.own[r] + v;
-        m.own[r] = x2;
-        ll_put(a.ll + (l == a.NL - 1 ? S::oXH : S::oX2) + row, __float_as_uint(x2), phase_epoch(ep0, s, E, 4 * l + 3));
-      }
-      if (wg == 0) prof_mark(a, s, l * 16 + 3);
-      prof_wg(a, s, l, 3);
+    {
+      const float v = row_hsum(qr_chain<S::NBF, S::NGF>(rd, m.xq, lane));
+      own = own + v;
+      if (writer) m.own[row - wg * 16] = own;
+      lds_barrier();
+      if (tid < 16)
+        ll_put(a.ll + (l == a.NL - 1 ? S::oXH : S::oX2) + wg * 16 + tid, __float_as_uint(m.own[tid]),
+               phase_epoch(ep0, s, E, 4 * l + 3));
     }
+    if (wg == 0) prof_mark(a, s, l * 16 + 3);
+    prof_wg(a, s, l, 3);
   }
   return true;
 }
@@ -1580,7 +1709,11 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     // Waves 1 and 2 poll for the group's new K and V rows (issued first, so the loads are in
     // flight during the softmax); the barriers in between wait for shared memory only.
     const bool kpoll = tid >= 64 && tid < 64 + 2 * kHD;
-    const uint64_t* ksrc = a.ll + S::oKV + 2 * kh * kHD + (tid - 64);
+    // entry of row li of k (or v): the K/V role's workgroup p = (li & 31) >> 3 writes its 16 rows
+    // {8p..8p+7, 32+8p..32+8p+7} as one line, slot (li >> 5) * 8 + (li & 7)
+    const int kvt = (tid - 64) & 127, kvli = kvt & 63;
+    const uint64_t* ksrc = a.ll + S::oKV + 2 * kh * kHD + (kvt >> 6) * kHD + ((kvli & 31) >> 3) * 16 +
+                           (kvli >> 5) * 8 + (kvli & 7);
     const uint32_t ekv = phase_epoch(ep0, s, E, 4 * l + 0);
     uint64_t kw = (uint64_t)ekv << 32;
     if (kpoll) kw = ll_peek(ksrc);
@@ -1839,7 +1972,8 @@ __device__ __forceinline__ bool kv_step(const PArgs& a, const PSmem& m, uint32_t
       if (j == 0) {
         const size_t cbase = ((size_t)l * S::KVH + kh) * a.ctx * kHD;
         st_coherent((KT*)(isv ? a.vc : a.kc) + cbase + (size_t)pos * kHD + li, y);
-        ll_put(a.ll + S::oKV + (2 * kh + isv) * kHD + li, __float_as_uint(y), phase_epoch(ep0, s, E, 4 * l + 0));
+        // the workgroup's 16 rows as one line (slot r: row li), written by one instruction
+        ll_put(a.ll + S::oKV + (2 * kh + isv) * kHD + p * 16 + r, __float_as_uint(y), phase_epoch(ep0, s, E, 4 * l + 0));
       }
       prof_wg(a, s, l, 1);
     }
@@ -1886,8 +2020,9 @@ __device__ __forceinline__ bool gu_step(const PArgs& a, const PSmem& m, uint32_t
       const int w = tid & 7, e0 = ((w >> 2) << 4) + ((w & 3) << 1);
       const int q0 = __shfl(q, e0), q1 = __shfl(q, e0 + 1), q2 = __shfl(q, e0 + 8), q3 = __shfl(q, e0 + 9);
       const uint32_t ep = phase_epoch(ep0, s, E, 4 * l + 2);
+      // the whole 16-entry line (entries 9..15 are padding), written by one instruction
       if (tid < 8) ll_put(a.ll + S::oACT + u * kActStride + tid, pack4(q0, q1, q2, q3), ep);
-      else if (tid == 8) ll_put(a.ll + S::oACT + u * kActStride + 8, __float_as_uint(dd), ep);
+      else if (tid < kActStride) ll_put(a.ll + S::oACT + u * kActStride + tid, __float_as_uint(dd), ep);
     }
     if (u == 0) prof_mark(a, s, l * 16 + 8);
     prof_wg(a, s, l, 1);
@@ -1911,12 +2046,7 @@ __global__ __launch_bounds__(kPThreads, 1) void k_decode_persistent(PArgs a) {
   for (int s = 0; s < a.steps; s++, pos++) {
     bool ok = true;
     if (wg < S::nOD) {
-      switch (wave) {
-        case 0: ok = od_step<S, 0>(a, m, ep0, s, tok, bad); break;
-        case 1: ok = od_step<S, 1>(a, m, ep0, s, tok, bad); break;
-        case 2: ok = od_step<S, 2>(a, m, ep0, s, tok, bad); break;
-        default: ok = od_step<S, 3>(a, m, ep0, s, tok, bad); break;
-      }
+      ok = od_step<S>(a, m, ep0, s, tok, bad);
     } else if (wg < S::nOD + S::H * a.asplit) {
       ok = attn_step<S, KT>(a, m, ep0, s, pos, tok, bad);
     } else if (wg < S::nOD + S::H * a.asplit + S::nKV) {
