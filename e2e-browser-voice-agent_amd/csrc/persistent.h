@@ -437,25 +437,32 @@ __device__ __forceinline__ float run_sum(const float* run) {
   static_assert(N % 16 == 0, "run length");
   constexpr int NC = N / 16;
   const float4* p = reinterpret_cast<const float4*>(run);
-  float4 buf[2][4];
+  // chunks stream through three register sets, two chunks ahead of the additions; the scheduling
+  // fences keep each chunk's reads in place (issued all at once, the reads of the whole run would
+  // delay the first addition by ~0.4 us), and pinning s keeps each chunk's additions in place
+  float4 buf[3][4];
+#pragma unroll
+  for (int c = 0; c < 2 && c < NC; c++) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) buf[c][u] = p[c * 4 + u];
+    __builtin_amdgcn_sched_barrier(0);
+  }
   float s = 0.0f;
 #pragma unroll
-  for (int u = 0; u < 4; u++) buf[0][u] = p[u];
-#pragma unroll
   for (int c = 0; c < NC; c++) {
-    if (c + 1 < NC) {
+    if (c + 2 < NC) {
 #pragma unroll
-      for (int u = 0; u < 4; u++) buf[(c + 1) & 1][u] = p[(c + 1) * 4 + u];
+      for (int u = 0; u < 4; u++) buf[(c + 2) % 3][u] = p[(c + 2) * 4 + u];
     }
-#pragma unroll
-    for (int u = 0; u < 4; u++) pin(buf[c & 1][u]);
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      s = s + buf[c & 1][u].x;
-      s = s + buf[c & 1][u].y;
-      s = s + buf[c & 1][u].z;
-      s = s + buf[c & 1][u].w;
+      s = s + buf[c % 3][u].x;
+      s = s + buf[c % 3][u].y;
+      s = s + buf[c % 3][u].z;
+      s = s + buf[c % 3][u].w;
     }
+    pin(s);
+    __builtin_amdgcn_sched_barrier(0);
   }
   return s;
 }
