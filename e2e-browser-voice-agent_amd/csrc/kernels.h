@@ -527,10 +527,12 @@ __device__ __forceinline__ void matvec_rows16(const Q4Mat& W, int tile, int rr, 
 
 // ((acc_0 + acc_1) + acc_2) + acc_3 over the four lanes of a row (hsum, kernels.c:116-118);
 // valid in lane j == 0.
-// Lane k (0..3) of this lane's quad, by a DPP quad broadcast (no shared-memory round trip).
+// Lane k (0..3) of this lane's quad, by a DPP quad broadcast (no shared-memory round trip).  Every
+// source lane is valid, so bound_ctrl changes nothing; it lets the compiler fold the broadcast into
+// the instruction that uses it (v_add_f32_dpp).
 template <int K>
 __device__ __forceinline__ float quad_lane(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), K * 0x55, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), K * 0x55, 0xF, 0xF, true));
 }
 
 // ((l0 + l1) + l2) + l3 over the four lanes of a quad (hsum, kernels.c:116-118), in every lane.

@@ -1290,74 +1290,65 @@ __device__ __forceinline__ float quad_add(float acc, float t) {
   return acc + quad_lane<Q>(t);
 }
 
-// Terms of this lane's group of round k (four blocks).
+// The term of block i (0..3) of this lane's group of round k.
 template <int NG>
-__device__ __forceinline__ void qr_terms(const QR<NG>& R, int k, const uint4 (&xv)[4], float (&t)[4]) {
+__device__ __forceinline__ float qr_term(const QR<NG>& R, int k, int i, const uint4& xv) {
   const uint4 w = R.w[k];
-  const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-  const uint32_t sw[2] = {R.s[k].x, R.s[k].y};
-  int pp[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) pp[i] = sdot4(wv[i] & 0x0F0F0F0Fu, xv[i].x, (int)xv[i].z);
-#pragma unroll
-  for (int i = 0; i < 4; i++) pp[i] = sdot4((wv[i] >> 4) & 0x0F0F0F0Fu, xv[i].y, pp[i]);
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float dw = half_bits_to_float((i & 1) ? (sw[i >> 1] >> 16) : (sw[i >> 1] & 0xffffu));
-    t[i] = (float)pp[i] * (dw * __uint_as_float(xv[i].w));
-  }
+  const uint32_t wv = i == 0 ? w.x : i == 1 ? w.y : i == 2 ? w.z : w.w;
+  const uint32_t sw = i < 2 ? R.s[k].x : R.s[k].y;
+  int pp = sdot4(wv & 0x0F0F0F0Fu, xv.x, (int)xv.z);
+  pp = sdot4((wv >> 4) & 0x0F0F0F0Fu, xv.y, pp);
+  const float dw = half_bits_to_float((i & 1) ? (sw >> 16) : (sw & 0xffffu));
+  return (float)pp * (dw * __uint_as_float(xv.w));
 }
 
-// The chain steps of round k: the terms of groups 4k .. 4k+3 in order, each from its phase lane.
-template <int NB, int NG>
-__device__ __forceinline__ float qr_steps(float acc, int k, const float (&t)[4]) {
+// The chain steps of phase q of round k: the terms of group 4k + q in order, from that phase's lane.
+template <int NB, int NG, int Q>
+__device__ __forceinline__ float qr_phase(float acc, int k, const float (&t)[4]) {
+  if (4 * k + Q < NG) {
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
-    if (4 * k + q < NG) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        if (4 * (4 * k + q) + i < NB) {
-          if (q == 0) acc = quad_add<0>(acc, t[i]);
-          else if (q == 1) acc = quad_add<1>(acc, t[i]);
-          else if (q == 2) acc = quad_add<2>(acc, t[i]);
-          else acc = quad_add<3>(acc, t[i]);
-        }
-      }
-    }
+    for (int i = 0; i < 4; i++)
+      if (4 * (4 * k + Q) + i < NB) acc = quad_add<Q>(acc, t[i]);
   }
   return acc;
 }
 
 // The chain ((0 + t_0) + t_1) + ... + t_{NB-1} of reference lane j of this lane's row, software
-// pipelined: the scheduling region of round k holds the activation reads and terms of round k + 1
-// and the (dependent) chain steps of round k, so the adds fill the latency of the next terms.
+// pipelined by hand: in round k the four phases' chain steps (dependent adds) alternate with the
+// terms of round k + 1, one block after each phase, and the activation reads run two rounds
+// ahead.  The pins fix that order (the scheduler would otherwise place every add after the terms).
 template <int NB, int NG>
 __device__ __forceinline__ float qr_chain(const QR<NG>& R, const uint4* xq, int lane) {
   constexpr int NK = QR<NG>::NK;
   const int j = (lane >> 2) & 3, p = lane & 3;
   float acc = 0.0f;
   float t[2][4];
-  {
-    uint4 xv[4];
-    qr_xload<NG>(xq, 0, p, j, xv);
-    qr_terms<NG>(R, 0, xv, t[0]);
-  }
+  uint4 xv[2][4];
+  qr_xload<NG>(xq, 0, p, j, xv[0]);
+  if (NK > 1) qr_xload<NG>(xq, 1, p, j, xv[1]);
 #pragma unroll
-  for (int i = 0; i < 4; i++) pin(t[0][i]);
+  for (int i = 0; i < 4; i++) {
+    t[0][i] = qr_term<NG>(R, 0, i, xv[0][i]);
+    pin(t[0][i]);
+  }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int k = 0; k < NK; k++) {
-    if (k + 1 < NK) {
-      uint4 xv[4];
-      qr_xload<NG>(xq, k + 1, p, j, xv);
-      qr_terms<NG>(R, k + 1, xv, t[(k + 1) & 1]);
+    // xv[(k + 1) & 1] holds round k + 1's activations; round k + 2's go into xv[k & 1]
+    if (k + 2 < NK) qr_xload<NG>(xq, k + 2, p, j, xv[k & 1]);
+    const int n = (k + 1) & 1;
+#define Q4_PHASE(Q)                                                          \
+    acc = qr_phase<NB, NG, Q>(acc, k, t[k & 1]);                             \
+    pin(acc);                                                                \
+    if (k + 1 < NK) {                                                        \
+      t[n][Q] = qr_term<NG>(R, k + 1, Q, xv[n][Q]);                          \
+      pin(t[n][Q]);                                                          \
     }
-    acc = qr_steps<NB, NG>(acc, k, t[k & 1]);
-    pin(acc);
-    if (k + 1 < NK) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) pin(t[(k + 1) & 1][i]);
-    }
+    Q4_PHASE(0)
+    Q4_PHASE(1)
+    Q4_PHASE(2)
+    Q4_PHASE(3)
+#undef Q4_PHASE
     __builtin_amdgcn_sched_barrier(0);
   }
   return acc;
@@ -1367,7 +1358,7 @@ __device__ __forceinline__ float qr_chain(const QR<NG>& R, const uint4* xq, int 
 // holds chain j (DPP row broadcasts), in every lane of the row.
 template <int K>
 __device__ __forceinline__ float row_lane(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + K, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + K, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float row_hsum(float acc) {
   const float a0 = row_lane<0>(acc), a1 = row_lane<4>(acc), a2 = row_lane<8>(acc), a3 = row_lane<12>(acc);
@@ -1735,42 +1726,44 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       prof_after(a, s, l, 6, m.red[8]);
     } else if (kpoll) {
       ll_wait1(ksrc, kw, ekv, a.st, bad, a.nap);
-      kv[tid - 64] = __uint_as_float((uint32_t)kw);    // kv and vv are adjacent: 0..63 K, 64..127 V
+      const float kval = __uint_as_float((uint32_t)kw);
+      kv[tid - 64] = kval;    // kv and vv are adjacent: 0..63 K, 64..127 V
+      if (wave == 1 && !bad) {
+        // wave 1 holds the new K row: the current position's score while wave 0 sums the past
+        // ones.  Lane i forms q_i * k_i; lane j < 4 adds the products j, j+4, ... in order, and the
+        // four lane sums combine in hsum order (kernels.c:362-366).
+        float* pq = m.gu;
+        pq[lane] = qv[lane] * kval;
+        float pj[kHD / 4];
+#pragma unroll
+        for (int i = 0; i < kHD / 4; i++) pj[i] = pq[4 * i + (lane & 3)];
+        float sj = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kHD / 4; i++) sj = sj + pj[i];
+        const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), 0));
+        const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), 1));
+        const float s2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), 2));
+        const float s3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), 3));
+        if (lane == 0) {
+          const float sv = (s0 + s1 + s2 + s3) * scale;
+          sc[pos] = sv;
+          if (sv > mpast) {
+            m.red[9] = 1.0f;               // the new score is the maximum: redo below
+          } else {
+            // e_pos stays out of ee[] until the barrier: wave 0's chain reads the zero padding
+            // past pos in whole 32-value chunks
+            m.red[10] = fast_exp(sv - mpast);
+            m.red[9] = 0.0f;
+          }
+        }
+      }
     }
     if (wg_bad(m.flag, bad)) return false;
     if (mark) prof_mark(a, s, l * 16 + 15);
     prof_wg(a, s, l, 4);
-    if (tid < kHD) {
-      // wave 0 forms the 64 products; lane j < 4 then adds products j, j+4, ... in order (one
-      // read of its 16 products), and the four lane sums combine in hsum order
-      float* pq = m.gu;
-      pq[tid] = qv[tid] * kv[tid];
-      float pj[kHD / 4];
-#pragma unroll
-      for (int i = 0; i < kHD / 4; i++) pj[i] = pq[4 * i + (tid & 3)];
-      float sj = 0.0f;
-#pragma unroll
-      for (int i = 0; i < kHD / 4; i++) sj = sj + pj[i];
-      const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), 0));
-      const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), 1));
-      const float s2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), 2));
-      const float s3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), 3));
-      if (tid == 0) {
-        const float sv = (s0 + s1 + s2 + s3) * scale;
-        sc[pos] = sv;
-        if (sv > mpast) {
-          m.red[9] = 1.0f;               // the new score is the maximum: redo below
-        } else {
-          const float en = fast_exp(sv - mpast);
-          ee[pos] = en;
-          m.red[8] = m.red[8] + en;
-          m.red[9] = 0.0f;
-        }
-      }
-    }
-    __syncthreads();
     if (mark) prof_mark(a, s, l * 16 + 12);
-    if (m.red[9] != 0.0f) {
+    const bool redo = m.red[9] != 0.0f;
+    if (redo) {
       const float mx = sc[pos];
       for (int t = tid; t < ((T + 31) & ~31); t += kPThreads) ee[t] = t < T ? fast_exp(sc[t] - mx) : 0.0f;
       __syncthreads();
@@ -1778,8 +1771,9 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       __syncthreads();
     }
     if (mark) prof_mark(a, s, l * 16 + 13);
-    const float sum = m.red[8];
-    for (int t = tid; t < T; t += kPThreads) sc[t] = ee[t] / sum;
+    // the running sum over every position: the past positions' chain, then the new one's term last
+    const float sum = redo ? m.red[8] : m.red[8] + m.red[10];
+    for (int t = tid; t < T; t += kPThreads) sc[t] = (t == pos && !redo ? m.red[10] : ee[t]) / sum;
     volatile LdsInt* cnt = (volatile LdsInt*)(m.red + 12);   // split P.V hand-offs (below)
     if (tid < 4) cnt[tid] = 0;
     __syncthreads();
