@@ -1083,31 +1083,73 @@ __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32
 
 // ---------------------------------------------------------------- the K/V ring of the attention role
 
+// The rows the attention role's ring loads read (host and device code: q4hip_attn_ring_rows runs the
+// same arithmetic on the host so a CPU test can check it).  The role streams the past positions of
+// its (layer, kv head) through the ring: rows [kbeg, kend) for its scores in 16-row chunks and, for
+// P.V, rows [nt, pos) in slots of vr rows (or, split, rows [0, pos) in half-width slots).  A load of
+// a row at or past the end of its stream reads the stream's last row instead, so no load touches the
+// current position or a later one: those rows are written during this step by the K/V role, possibly
+// on another XCD, and a stale copy could stay in this XCD's L2.
+__host__ __device__ constexpr int ring_row(int t, int limit) { return t < limit ? t : limit - 1; }
+constexpr int kVRows = 96;   // rows of a half-width P.V slot (split attention)
+struct AttnRing {
+  int nt;            // staged past positions [0, nt)
+  int kbeg, kend;    // K rows scored from the ring
+  int obeg, oend;    // split: the pair's other half, whose scores arrive through the exchange
+  int vr;            // rows of an unsplit P.V slot
+  int nstream, nck, nkc, nckv;
+};
+__host__ __device__ inline AttnRing attn_ring(int pos, int kv_tile, bool split, int half, bool f16) {
+  AttnRing r;
+  r.nt = split ? 0 : (pos < kv_tile ? pos : kv_tile);
+  const int nall = (pos + kRingRows - 1) / kRingRows;
+  r.kbeg = split ? (half == 0 ? 0 : (nall / 2) * kRingRows) : r.nt;
+  r.kend = split ? (half == 0 ? (nall / 2) * kRingRows : pos) : pos;
+  r.obeg = split ? (half == 0 ? (nall / 2) * kRingRows : 0) : 0;
+  r.oend = split ? (half == 0 ? pos : (nall / 2) * kRingRows) : 0;
+  r.vr = f16 ? 2 * kRingRows : kRingRows;
+  r.nstream = r.kend - r.kbeg;
+  r.nck = (r.nstream + r.vr - 1) / r.vr;
+  r.nkc = (r.nstream + 15) / 16;
+  r.nckv = split ? (pos + kVRows - 1) / kVRows : 0;
+  return r;
+}
+// K chunks of wave w: chunks w, w + 4, ... of the stream; issue j loads chunk min(j, nloc - 1).
+__host__ __device__ constexpr int attn_nloc(int nkc, int wave) { return nkc > wave ? (nkc - wave + 3) / 4 : 0; }
+__host__ __device__ constexpr int kchunk_t0(int kbeg, int j, int nloc, int wave) {
+  return kbeg + 16 * (4 * (j < nloc ? j : nloc - 1) + wave);
+}
+// First row of P.V slot c (issues past the last slot repeat it): unsplit and split.
+__host__ __device__ constexpr int vslot_t0(int nt, int c, int nck, int vr) { return nt + (c < nck ? c : nck - 1) * vr; }
+__host__ __device__ constexpr int vpslot_t0(int c, int nckv) { return (c < nckv ? c : nckv - 1) * kVRows; }
+
+
 typedef __attribute__((address_space(3))) void LdsVoid;
 typedef __attribute__((address_space(1))) const void GlobalVoid;
 
 // Issue the asynchronous loads of rows [t0, t0 + kRingRows) of one (layer, kv head) V block into
 // `slot` as plain rows: wave w issues instructions w, w+4, w+8, each moving rows t0+4i .. t0+4i+3.
-// Rows at or past ctx are read from row ctx-1 (their values are never used).
-__device__ __forceinline__ void ring_issue(const float* src, int t0, int ctx, float* slot) {
+// Rows at or past `limit` (the end of the streamed past positions) are read from row limit - 1
+// (ring_row; their values are never used).
+__device__ __forceinline__ void ring_issue(const float* src, int t0, int limit, float* slot) {
   const int lane = threadIdx.x & 63, wave = wave_id();
 #pragma unroll
   for (int k = 0; k < 3; k++) {
     const int i = wave + 4 * k;
     const int t = t0 + 4 * i + (lane >> 4);
-    const float* g = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + 4 * (lane & 15);
+    const float* g = src + (size_t)ring_row(t, limit) * kHD + 4 * (lane & 15);
     __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + i * 256), 16, 0, 0);
   }
 }
 // fp16 rows: a slot holds 2 kRingRows rows (the same 12 instructions, 8 rows each), row r at
 // half 64 r of the slot.
-__device__ __forceinline__ void ring_issue(const kvhalf* src, int t0, int ctx, float* slot) {
+__device__ __forceinline__ void ring_issue(const kvhalf* src, int t0, int limit, float* slot) {
   const int lane = threadIdx.x & 63, wave = wave_id();
 #pragma unroll
   for (int k = 0; k < 3; k++) {
     const int i = wave + 4 * k;
     const int t = t0 + 8 * i + (lane >> 3);
-    const kvhalf* g = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + 8 * (lane & 7);
+    const kvhalf* g = src + (size_t)ring_row(t, limit) * kHD + 8 * (lane & 7);
     __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + i * 256), 16, 0, 0);
   }
 }
@@ -1120,13 +1162,13 @@ __host__ __device__ constexpr int vslot_rows() { return sizeof(KT) == 4 ? kRingR
 // lane l fetches elements 4c .. 4c+3 (c = l >> 2) of row l & 3: element 4c + e of group row r
 // lands at float 16 c + 4 r + e.  Four lanes per row then read elements 4i + j of their row at
 // immediate offsets 16 i, and with the 16-float padding the 16 rows of the wave cover all 64 banks.
-// Rows at or past ctx are read from row ctx-1 (their values are never used).
-__device__ __forceinline__ void ring_issue_kc(const float* src, int t0, int ctx, float* slot) {
+// Rows at or past `limit` are read from row limit - 1 (ring_row; their values are never used).
+__device__ __forceinline__ void ring_issue_kc(const float* src, int t0, int limit, float* slot) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int g = 0; g < 4; g++) {
     const int t = t0 + 4 * g + (lane & 3);
-    const float* p = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + 4 * (lane >> 2);
+    const float* p = src + (size_t)ring_row(t, limit) * kHD + 4 * (lane >> 2);
     __builtin_amdgcn_global_load_lds((GlobalVoid*)p, (LdsVoid*)(slot + g * kGrpFloats), 16, 0, 0);
   }
 }
@@ -1139,12 +1181,12 @@ __device__ __forceinline__ void ring_issue_kc(const float* src, int t0, int ctx,
 // conflicts.  2304 bytes of the chunk's kChunkFloats.
 constexpr int kChunk16Bytes = 2304;
 static_assert(kChunk16Bytes <= kChunkFloats * 4, "fp16 chunk exceeds the chunk slot");
-__device__ __forceinline__ void ring_issue_kc(const kvhalf* src, int t0, int ctx, float* slot) {
+__device__ __forceinline__ void ring_issue_kc(const kvhalf* src, int t0, int limit, float* slot) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int h = 0; h < 2; h++) {
     const int t = t0 + 8 * h + (lane & 7);
-    const kvhalf* p = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + 8 * (lane >> 3);
+    const kvhalf* p = src + (size_t)ring_row(t, limit) * kHD + 8 * (lane >> 3);
     __builtin_amdgcn_global_load_lds((GlobalVoid*)p, (LdsVoid*)((char*)slot + 1152 * h), 16, 0, 0);
   }
 }
@@ -1187,14 +1229,13 @@ __device__ __forceinline__ void ring_drain() { __builtin_amdgcn_s_waitcnt(0x0F70
 // Half-width slots for the split attention's P.V: kVRows rows x 32 of the 64 columns (from c0) as
 // plain rows of 32 floats, the footprint of a full slot.  Producer wave pw (waves 1..3) loads rows
 // 32 pw .. 32 pw + 31 of a slot with 4 instructions of 8 rows each and forms their products.
-constexpr int kVRows = 96;
-__device__ __forceinline__ void ring_issue_vp(const float* src, int t0, int ctx, int c0, int pw, float* slot) {
+__device__ __forceinline__ void ring_issue_vp(const float* src, int t0, int limit, int c0, int pw, float* slot) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     const int i = 4 * pw + k;
     const int t = t0 + 8 * i + (lane >> 3);
-    const float* g = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + c0 + 4 * (lane & 7);
+    const float* g = src + (size_t)ring_row(t, limit) * kHD + c0 + 4 * (lane & 7);
     __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + i * 256), 16, 0, 0);
   }
 }
@@ -1202,12 +1243,12 @@ __device__ __forceinline__ void ring_issue_vp(const float* src, int t0, int ctx,
 // fp16 rows: producer pw's 32 rows x 32 halves (2 KB) in 2 instructions of 16 rows, landing in
 // the upper half of its 4 KB part (byte 2048 + 64 r + 2 col); it reads them all before it writes
 // the fp32 products over the part.
-__device__ __forceinline__ void ring_issue_vp(const kvhalf* src, int t0, int ctx, int c0, int pw, float* slot) {
+__device__ __forceinline__ void ring_issue_vp(const kvhalf* src, int t0, int limit, int c0, int pw, float* slot) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int k = 0; k < 2; k++) {
     const int t = t0 + 32 * pw + 16 * k + (lane >> 2);
-    const kvhalf* g = src + (size_t)(t < ctx ? t : ctx - 1) * kHD + c0 + 8 * (lane & 3);
+    const kvhalf* g = src + (size_t)ring_row(t, limit) * kHD + c0 + 8 * (lane & 3);
     __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + pw * 1024 + 512 + k * 256), 16, 0, 0);
   }
 }
@@ -1478,14 +1519,10 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
   const int vstride = kv_vstride(a.kv_tile);
   float* kt = ring + (size_t)a.ring * kSlotFloats;        // [kv_tile][kKVRow] K
   float* vT = kt + (size_t)(a.kv_tile + 16) * kKVRow;      // [64][vstride] V transposed
-  const int nt = split ? 0 : (pos < a.kv_tile ? pos : a.kv_tile);   // staged past positions
   // K rows streamed for the scores: [kbeg, kend) in chunks of kRingRows -- positions [nt, pos), or
   // in split mode this workgroup's half of the chunks of [0, pos) (the other half: [obeg, oend))
-  const int nall = (pos + kRingRows - 1) / kRingRows;
-  const int kbeg = split ? (half == 0 ? 0 : (nall / 2) * kRingRows) : nt;
-  const int kend = split ? (half == 0 ? (nall / 2) * kRingRows : pos) : pos;
-  const int obeg = split ? (half == 0 ? (nall / 2) * kRingRows : 0) : 0;
-  const int oend = split ? (half == 0 ? pos : (nall / 2) * kRingRows) : 0;
+  const AttnRing ar = attn_ring(pos, a.kv_tile, split, half, kF16);
+  const int nt = ar.nt, kbeg = ar.kbeg, kend = ar.kend, obeg = ar.obeg, oend = ar.oend;
   for (int l = 0; l < a.NL; l++) {
     const LayerView& L = a.layers[l];
     if (l > 0) pf_delay(a.pf[2]);
@@ -1532,15 +1569,15 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     // past positions [kbeg, kend) stream through the ring: for the scores in 16-row chunks, wave w
     // taking chunks w, w + 4, ... through its own ring of cs slots (the first ones load during the
     // wait for x); for P.V in slots of kRingRows (or kVRows) rows
-    const int nstream = kend - kbeg, nck = (nstream + VR - 1) / VR;
-    const int nkc = (nstream + 15) / 16, nloc = nkc > wave ? (nkc - wave + 3) / 4 : 0;
+    const int nstream = ar.nstream, nck = ar.nck;
+    const int nkc = ar.nkc, nloc = attn_nloc(nkc, wave);
     const int cs = kchunk_slots(a.ring);
     float* wring = ring + (size_t)wave * cs * kChunkFloats;
     const KT* kgl = (const KT*)a.kc + cbase;
     const KT* vgl = (const KT*)a.vc + cbase;
     if (nloc > 0)
       for (int j = 0; j < cs - 1; j++)
-        ring_issue_kc(kgl, kbeg + 16 * (4 * (j < nloc ? j : nloc - 1) + wave), a.ctx, wring + (size_t)j * kChunkFloats);
+        ring_issue_kc(kgl, kchunk_t0(kbeg, j, nloc, wave), kend, wring + (size_t)j * kChunkFloats);
     if (l == 0) {
       for (int i = tid; i < S::D; i += kPThreads) stage_x<S>(m, i, embed_value(a.embd, S::D, tok, i));
     } else {
@@ -1643,7 +1680,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
             lmax = __builtin_fmaxf(lmax, sv);
           }
           const int jn = j + cs - 1;
-          ring_issue_kc(kgl, kbeg + 16 * (4 * (jn < nloc ? jn : nloc - 1) + wave), a.ctx, wring + (size_t)(jn % cs) * kChunkFloats);
+          ring_issue_kc(kgl, kchunk_t0(kbeg, jn, nloc, wave), kend, wring + (size_t)(jn % cs) * kChunkFloats);
         }
       }
       ring_drain();
@@ -1652,9 +1689,9 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       // the ring is free: the first V slots stream in while exp, sum and division run
       if (!split)
         for (int c = 0; c < R - 1; c++)
-          ring_issue(vgl, nt + (c < nck ? c : nck - 1) * VR, a.ctx, ring + (size_t)c * kSlotFloats);
+          ring_issue(vgl, vslot_t0(nt, c, nck, VR), pos, ring + (size_t)c * kSlotFloats);
     }
-    const int nckv = split ? (pos + kVRows - 1) / kVRows : 0;     // split P.V: half-width V slots
+    const int nckv = ar.nckv;     // split P.V: half-width V slots
     if (split) {
       // the pair exchanges its scores: publish [kbeg, kend), receive [obeg, oend) (8 entries in
       // flight per thread, missing ones polled again; bounded like every wait)
@@ -1663,7 +1700,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
       for (int t = kbeg + tid; t < kend; t += kPThreads) ll_put(ex + t, __float_as_uint(sc[t]), eps);
       if (nckv > 0 && wave != 0)
         for (int c = 0; c < a.ring - 2; c++)
-          ring_issue_vp(vgl, (c < nckv ? c : nckv - 1) * kVRows, a.ctx, 32 * half, wave - 1, ring + (size_t)c * kSlotFloats);
+          ring_issue_vp(vgl, vpslot_t0(c, nckv), pos, 32 * half, wave - 1, ring + (size_t)c * kSlotFloats);
       for (int b0 = obeg; b0 < oend; b0 += 8 * kPThreads) {
         uint64_t w[8];
 #pragma unroll
@@ -1814,7 +1851,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
             break;
           }
           asm volatile("" ::: "memory");
-          ring_issue_vp(vgl, (cn < nckv ? cn : nckv - 1) * kVRows, a.ctx, 32 * half, pw, ring + (size_t)(cn % R) * kSlotFloats);
+          ring_issue_vp(vgl, vpslot_t0(cn, nckv), pos, 32 * half, pw, ring + (size_t)(cn % R) * kSlotFloats);
         }
       } else {
         for (int c = 0; c < nckv; c++) {
@@ -1900,7 +1937,7 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
           }
         }
         const int cn = c + R - 1;
-        ring_issue(vgl, nt + (cn < nck ? cn : nck - 1) * VR, a.ctx, ring + (size_t)(cn % R) * kSlotFloats);
+        ring_issue(vgl, vslot_t0(nt, cn, nck, VR), pos, ring + (size_t)(cn % R) * kSlotFloats);
       }
       ring_drain();
     }

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -3214,6 +3215,42 @@ int q4hip_check_division(int device, unsigned long long* mismatches, int n) {
   if (e == hipSuccess) e = hipMemcpy(mismatches, d, (size_t)n * sizeof(unsigned long long), hipMemcpyDeviceToHost);
   (void)hipFree(d);
   if (e != hipSuccess) return fail(Q4HIP_EHIP, "division check: %s", hipGetErrorString(e));
+  return Q4HIP_OK;
+}
+
+int q4hip_attn_ring_rows(int pos, int kv_tile, int ring_slots, int split, int half, int kv_f16, int* lo, int* hi,
+                         int* loads) {
+  if (!lo || !hi || !loads) return fail(Q4HIP_EINVAL, "null argument");
+  if (pos < 0 || kv_tile < 0 || (ring_slots != 3 && ring_slots != 7) || (half != 0 && half != 1))
+    return fail(Q4HIP_EINVAL, "bad argument");
+  // the issues of attn_step, with the kernel's own row arithmetic (attn_ring, kchunk_t0, vslot_t0,
+  // vpslot_t0, ring_row): each issue reads `span` rows from its first row on
+  const AttnRing r = attn_ring(pos, kv_tile, split != 0, half, kv_f16 != 0);
+  const int cs = kchunk_slots(ring_slots);
+  int mn = INT_MAX, mx = -1, cnt = 0;
+  auto take = [&](int t0, int span, int limit) {
+    for (int i = 0; i < span; i++) {
+      const int row = ring_row(t0 + i, limit);
+      mn = std::min(mn, row);
+      mx = std::max(mx, row);
+    }
+    cnt++;
+  };
+  for (int wave = 0; wave < 4; wave++) {           // K chunks: cs - 1 ahead, then one per chunk
+    const int nloc = attn_nloc(r.nkc, wave);
+    if (nloc > 0)
+      for (int j = 0; j < nloc + cs - 1; j++) take(kchunk_t0(r.kbeg, j, nloc, wave), 16, r.kend);
+  }
+  if (!split) {                                    // P.V slots: ring - 1 ahead, then one per slot
+    if (r.nck > 0)
+      for (int c = 0; c < r.nck + ring_slots - 1; c++) take(vslot_t0(r.nt, c, r.nck, r.vr), r.vr, pos);
+  } else {                                         // split: ring - 2 ahead, then one per slot
+    if (r.nckv > 0)
+      for (int c = 0; c < r.nckv + ring_slots - 2; c++) take(vpslot_t0(c, r.nckv), kVRows, pos);
+  }
+  *lo = cnt ? mn : 0;
+  *hi = cnt ? mx : -1;
+  *loads = cnt;
   return Q4HIP_OK;
 }
 

@@ -32,6 +32,7 @@ EXPORTS = [
     "q4hip_set_kv", "q4hip_profile_pass", "q4hip_batch_create", "q4hip_batch_destroy",
     "q4hip_batch_prefill", "q4hip_batch_set_kv", "q4hip_batch_generate", "q4hip_batch_time_generate",
     "q4hip_batch_read_logits", "q4hip_mv_time_cold", "q4hip_check_division", "q4hip_mv_run_noalloc",
+    "q4hip_attn_ring_rows",
 ]
 
 _lib = None
@@ -83,6 +84,7 @@ def lib() -> ctypes.CDLL:
         "q4hip_batch_read_logits": (I, [P, P, I64]),
         "q4hip_mv_time_cold": (I, [P, I64, I, ctypes.POINTER(F), ctypes.POINTER(I)]),
         "q4hip_mv_run_noalloc": (I, [P, P, P, P]),
+        "q4hip_attn_ring_rows": (I, [I, I, I, I, I, I, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.POINTER(I)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -116,6 +118,15 @@ def check_division(device: int = 0) -> dict:
     out = np.zeros(len(DIVISION_FORMS), np.uint64)
     _check(lib().q4hip_check_division(device, _ptr(out), len(DIVISION_FORMS)))
     return dict(zip(DIVISION_FORMS, (int(v) for v in out)))
+
+
+def attn_ring_rows(pos: int, kv_tile: int, ring_slots: int, split: bool, half: int, kv_f16: bool) -> tuple:
+    """(lowest row, highest row, loads) the persistent kernel's attention ring reads at position
+    pos, from the kernel's row arithmetic run on the host (q4hip_attn_ring_rows; no GPU)."""
+    lo, hi, n = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+    _check(lib().q4hip_attn_ring_rows(pos, kv_tile, ring_slots, int(split), half, int(kv_f16), ctypes.byref(lo),
+                                      ctypes.byref(hi), ctypes.byref(n)))
+    return lo.value, hi.value, n.value
 
 
 class Model:

@@ -229,6 +229,18 @@ int q4hip_mv_run_noalloc(q4hip_mv* m, const float* x, float* y, void* stream);
  * [3] a / 896 (a >= 0), [4] 1 / d (d >= 0).  No counterpart in the reference (a diagnostic). */
 int q4hip_check_division(int device, unsigned long long* mismatches, int n);
 
+/* ---- self-check of the attention ring's row bounds (host only, no GPU) ----------------------
+ * The persistent decode kernel's attention workgroups stream past K/V rows through a ring in
+ * shared memory; loads past the end of a stream are redirected to its last row.  This runs the
+ * kernel's row arithmetic on the host for one step at position `pos` (staged tile of kv_tile
+ * positions, a ring of ring_slots = 3 or 7 slots, split = two workgroups per head and `half` the
+ * one asked for, kv_f16 = an fp16 cache) and writes the lowest and highest row any ring load
+ * reads (*lo = 0, *hi = -1 when there is none) and the number of loads.  Every row must be a past
+ * position, < pos (the reference reads exactly pos + 1 positions, engine/kernels.c:355-360, the
+ * last from the new row).  No counterpart in the reference (a diagnostic). */
+int q4hip_attn_ring_rows(int pos, int kv_tile, int ring_slots, int split, int half, int kv_f16, int* lo, int* hi,
+                         int* loads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -94,3 +94,32 @@ def test_synthetic_model_is_deterministic():
         assert np.array_equal(a[n].data, b[n].data)
     assert not np.array_equal(a["output.weight"].data, c["output.weight"].data)
     assert synth.prompt_ids(3, 64, 151936) == synth.prompt_ids(3, 64, 151936)
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+@pytest.mark.parametrize("ring_slots", [3, 7])
+@pytest.mark.parametrize("split,half", [(False, 0), (True, 0), (True, 1)])
+@pytest.mark.parametrize("kv_tile", [0, 140, 192])
+def test_attention_ring_reads_only_past_rows(kv_tile, split, half, ring_slots, kv_f16):
+    """Every row the attention role's ring loads read is a past position (< pos), at every position
+    of a 4200-position context: the loads past a stream's end are redirected to its last row, not to
+    ctx - 1 (rows at and past pos are written during the step by the K/V role, possibly on another
+    XCD; the reference reads exactly pos + 1 positions, engine/kernels.c:355-360)."""
+    if split and kv_tile:
+        pytest.skip("the split pair stages no tile")
+    for pos in range(0, 4201):
+        lo, hi, n = q4hip.attn_ring_rows(pos, kv_tile, ring_slots, split, half, kv_f16)
+        if n == 0:
+            continue
+        assert 0 <= lo <= hi < pos, (pos, lo, hi, n)
+
+
+def test_attention_ring_bound_is_tight():
+    """The clamp is exercised: near a stream's end the ring still loads (the last row read is
+    exactly pos - 1), and positions past the staged tile are all streamed."""
+    lo, hi, n = q4hip.attn_ring_rows(1000, 140, 7, False, 0, False)
+    assert n > 0 and hi == 999 and lo == 140
+    lo, hi, n = q4hip.attn_ring_rows(100, 140, 7, False, 0, False)
+    assert n == 0          # everything staged
+    lo, hi, n = q4hip.attn_ring_rows(4096, 0, 7, True, 1, True)
+    assert n > 0 and hi == 4095
