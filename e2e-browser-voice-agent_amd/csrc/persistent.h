@@ -356,26 +356,56 @@ __device__ __forceinline__ void xg_load(const uint4* xq, int g, int j, uint4 (&x
   }
 }
 
-// acc_n = acc_n + term over blocks [4 G0, min(NB, 4 (G0 + CNT))) in order (kernels.c:217-218), for N
-// row groups sharing each activation read; the next group's activation blocks are read ahead.
+// The term f32(p_j) * (dw * dx) (kernels.c:137) of block k (0..3) of local group g of one 16-row
+// group, xv = {A_j, B_j, c_j, dx} of the block: the arithmetic of wr_group_terms for one block.
+template <int CNT>
+__device__ __forceinline__ float wr_term(const WR<CNT>& R, int g, int k, const uint4& xv) {
+  const uint4 w = R.w[g];
+  const uint32_t wv = k == 0 ? w.x : k == 1 ? w.y : k == 2 ? w.z : w.w;
+  const uint4 sv = R.s[g >> 1];
+  const int hb = ((g & 1) << 2) + k;
+  const uint32_t sw = (hb >> 1) == 0 ? sv.x : (hb >> 1) == 1 ? sv.y : (hb >> 1) == 2 ? sv.z : sv.w;
+  int p = sdot4(wv & 0x0F0F0F0Fu, xv.x, (int)xv.z);
+  p = sdot4((wv >> 4) & 0x0F0F0F0Fu, xv.y, p);
+  const float dw = half_bits_to_float((hb & 1) ? (sw >> 16) : (sw & 0xffffu));
+  return (float)p * (dw * __uint_as_float(xv.w));
+}
+
+// acc = acc + term over blocks [4 G0, min(NB, 4 (G0 + CNT))) in order (kernels.c:217-218) for one
+// 16-row group, software pipelined by hand: the activation reads run two groups ahead, and each
+// addition of group g alternates with one block's term of group g + 1 (the pins fix that order;
+// the scheduler would otherwise put a group's dependent additions after the next group's terms).
 template <int NB, int G0, int CNT, int N>
 __device__ __forceinline__ void wr_dot(const WR<CNT> (&R)[N], const uint4* xq, int j, float (&acc)[N]) {
+  static_assert(N == 1, "one row group");
   if constexpr (CNT > 0) {
     uint4 xb[2][4];
+    float t[2][4];
     xg_load<NB, G0>(xq, 0, j, xb[0]);
+    if (CNT > 1) xg_load<NB, G0>(xq, 1, j, xb[1]);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (G0 * 4 + k < NB) {
+        t[0][k] = wr_term<CNT>(R[0], 0, k, xb[0][k]);
+        pin(t[0][k]);
+      }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int g = 0; g < CNT; g++) {
-      if (g + 1 < CNT) xg_load<NB, G0>(xq, g + 1, j, xb[(g + 1) & 1]);
+      if (g + 2 < CNT) xg_load<NB, G0>(xq, g + 2, j, xb[g & 1]);
+      const int n = (g + 1) & 1;
 #pragma unroll
-      for (int k = 0; k < 4; k++) pin(xb[g & 1][k]);
-      float t[N][4];
-      wr_group_terms<NB, G0, CNT, N>(R, g, xb[g & 1], t);
-#pragma unroll
-      for (int k = 0; k < 4; k++)
+      for (int k = 0; k < 4; k++) {
         if ((G0 + g) * 4 + k < NB) {
-#pragma unroll
-          for (int n = 0; n < N; n++) acc[n] = acc[n] + t[n][k];
+          acc[0] = acc[0] + t[g & 1][k];
+          pin(acc[0]);
         }
+        if (g + 1 < CNT && (G0 + g + 1) * 4 + k < NB) {
+          t[n][k] = wr_term<CNT>(R[0], g + 1, k, xb[n][k]);
+          pin(t[n][k]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
