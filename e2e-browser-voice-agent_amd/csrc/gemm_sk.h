@@ -65,14 +65,6 @@ __device__ __forceinline__ void sk_wait() {
 // that the compiler does not treat every later shared-memory read as dependent on every load in
 // flight (it would wait for all of them): the ring's own vmcnt waits order the reads.  The s_nop
 // covers the wait state the hardware needs between writing M0 and the load that reads it.
-#ifdef SK_EMULATE_DMA
-__device__ __forceinline__ void sk_dma16(const void* src, const void* lds) {
-  reinterpret_cast<uint4*>(const_cast<void*>(lds))[threadIdx.x & 63] = *reinterpret_cast<const uint4*>(src);
-}
-__device__ __forceinline__ void sk_dma4(const void* src, const void* lds) {
-  reinterpret_cast<uint32_t*>(const_cast<void*>(lds))[threadIdx.x & 63] = *reinterpret_cast<const uint32_t*>(src);
-}
-#else
 __device__ __forceinline__ void sk_dma16(const void* src, const void* lds) {
   const uint32_t a = (uint32_t)(uintptr_t)(SkLds*)lds;
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(a) : "memory");
@@ -81,7 +73,6 @@ __device__ __forceinline__ void sk_dma4(const void* src, const void* lds) {
   const uint32_t a = (uint32_t)(uintptr_t)(SkLds*)lds;
   asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "{m0}"(a) : "memory");
 }
-#endif
 
 // Per-lane sources of a workgroup's loads, computed once; group g adds g times a stride.
 //   act  JS 1: this wave's block (4g + wave) of the 16-token tile, 2 KB, two instructions of 1 KB;

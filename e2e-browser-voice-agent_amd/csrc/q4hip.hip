@@ -263,17 +263,25 @@ constexpr int kSplitMinBlocks = 64;
 constexpr int kSplitMaxBlocks = 480;
 inline size_t split_lds(int nb) { return (size_t)nb * 320; }
 
-// Raise k_matvec_split's shared-memory limit once per device, with that device current (before
-// any graph capture: the handle and matvec constructors call it).
+// The widest row of a one-token projection on k_matvec<1> (rows wider than k_matvec_split takes):
+// 2048 blocks (K = 65536, the no-allocation matvec's limit), 64 bytes of activation block each in
+// shared memory.
+constexpr int kMatvec1MaxBlocks = 2048;
+
+// Raise the shared-memory limits of k_matvec_split and k_matvec<1> once per device, with that device
+// current (before any graph capture: the handle and matvec constructors call it).
 void matvec_split_setup(int device) {
   static std::mutex mu;
   static uint64_t done = 0;
   std::lock_guard<std::mutex> lock(mu);
   if (device < 0 || device >= 64 || (done >> device) & 1) return;
-  const int lds = (int)split_lds(kSplitMaxBlocks);
+  const int lds = (int)split_lds(kSplitMaxBlocks), lds1 = kMatvec1MaxBlocks * 64;
   (void)hipFuncSetAttribute((const void*)k_matvec_split<0>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   (void)hipFuncSetAttribute((const void*)k_matvec_split<1>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   (void)hipFuncSetAttribute((const void*)k_matvec_split<2>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  (void)hipFuncSetAttribute((const void*)k_matvec<1, 0>, hipFuncAttributeMaxDynamicSharedMemorySize, lds1);
+  (void)hipFuncSetAttribute((const void*)k_matvec<1, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, lds1);
+  (void)hipFuncSetAttribute((const void*)k_matvec<1, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, lds1);
   (void)hipGetLastError();
   done |= (uint64_t)1 << device;
 }

@@ -58,8 +58,9 @@ int q4hip_device_count(int* count);
  *                 to the reference's arithmetic
  *   Q4HIP_KV_F16  half the cache bytes: K and V rounded to fp16 (nearest, ties to even) when appended
  *                 or written by q4hip_set_kv, and read back exactly; results bit-identical to the
- *                 reference's arithmetic over a cache holding those rounded values.  Decode steps use
- *                 the persistent kernel while the context fits its staged tile, else the graph path. */
+ *                 reference's arithmetic over a cache holding those rounded values.  Decode steps run
+ *                 on the persistent kernel at every context length with either type (past rows
+ *                 beyond its staged tile stream through a ring in shared memory). */
 #define Q4HIP_KV_F32 0
 #define Q4HIP_KV_F16 1
 
@@ -171,8 +172,8 @@ void q4hip_destroy(q4hip* h);
  * B independent sequences decoded together, one token each per step, with the context's weights.
  * The reference decodes one sequence per backend (engine/cpu.js:33-50, engine/llm.js:86-97); a
  * batch runs B such loops at once, and every sequence's tokens and logits are the ones its own
- * loop would give.  Each sequence has its own fp32 K/V cache of the context's ctx positions; the
- * context's activation buffers are shared, so B <= the context's pass size and calls on a batch and
+ * loop would give.  Each sequence has its own K/V cache of the context's ctx positions, of the
+ * context's kv_type (fp32 or fp16); the context's activation buffers are shared, so B <= the context's pass size and calls on a batch and
  * on its context are serialized by the caller.  Destroy batches before their context. */
 typedef struct q4hip_batch q4hip_batch;
 int q4hip_batch_create(q4hip_batch** out, q4hip* h, int B);

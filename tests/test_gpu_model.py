@@ -468,22 +468,24 @@ def test_fp16_kv_matches_oracle(name, seed, n_prompt, mode):
 
 
 def test_fp16_kv_long_context_qwen05b_4096():
-    """The long-context workload with the fp16 cache: Qwen2.5-0.5B shape, 4096 cached fp16 K/V
-    positions (seeded N(0, 1), written through q4hip_set_kv), then 16 decode steps on the persistent
-    kernel (two attention workgroups per head, fp16 rows streamed through the ring).  Tokens and
-    logits equal the fp16-cache oracle's at every step; the distance from the fp32-cache oracle
-    (whose new rows are not rounded) is printed, not asserted: a rounded row flips int8
-    activation roundings downstream, so it exceeds 1e-3 (oracle/reassoc_study.py measures it)."""
+    """The long-context workload with the fp16 cache, all of it: Qwen2.5-0.5B shape, 4096 cached fp16
+    K/V positions (seeded N(0, 1), written through q4hip_set_kv), then the 256 decode steps the
+    benchmark times, on the persistent kernel (two attention workgroups per head, fp16 rows streamed
+    through the ring).  Tokens and logits equal the fp16-cache oracle's at every step, and one
+    256-step launch from the same cache (the benchmark's q4hip_generate) gives the same tokens.  The
+    distance from the fp32-cache oracle (whose new rows are not rounded) over the first 16 steps is
+    printed, not asserted: a rounded row flips int8 activation roundings downstream, so it exceeds
+    1e-3 (oracle/reassoc_study.py measures it)."""
     import q4hip
-    print("qwen2.5-0.5b long context 4096 positions, fp16 cache", flush=True)
-    P, steps = 4096, 16
+    print("qwen2.5-0.5b long context 4096 positions, fp16 cache, 256 steps", flush=True)
+    P, steps, steps32 = 4096, 256, 16
     shape = synth.SHAPES["qwen2.5-0.5b"]
     t = _model("qwen2.5-0.5b", 41)
-    g = q4hip.Model(shape, ctx=P + 40, kv_type=q4hip.KV_F16)
+    g = q4hip.Model(shape, ctx=P + steps + 8, kv_type=q4hip.KV_F16)
     g.load(t)
-    o = oracle.Model(shape, t, ctx=P + 40, mt=16, threads=16)
+    o = oracle.Model(shape, t, ctx=P + steps + 8, mt=16, threads=16)
     o.set_variant(oracle.V_KV_F16)
-    o32 = oracle.Model(shape, t, ctx=P + 40, mt=16, threads=16)
+    o32 = oracle.Model(shape, t, ctx=P + steps + 8, mt=16, threads=16)
     try:
         k, v = _fill_kv(shape, P, 41)
         for m in (o, o32):
@@ -493,15 +495,20 @@ def test_fp16_kv_long_context_qwen05b_4096():
         for l in range(shape.layers):
             for kh in range(shape.kv_heads):
                 g.set_kv(l, kh, 0, k[l, kh], v[l, kh])
-        tok, worst = 7, 0.0
+        tok, worst, toks = 7, 0.0, []
         for i in range(steps):
             ng, no = g.forward([tok], P + i), o.forward([tok], P + i)
-            o32.forward([tok], P + i)
             assert ng == no, f"step {i}"
             _compare_logits(g, o, f"step {i}")
-            worst = max(worst, float(np.max(np.abs(g.read_logits() - o32.logits()))))
+            if i < steps32:
+                o32.forward([tok], P + i)
+                worst = max(worst, float(np.max(np.abs(g.read_logits() - o32.logits()))))
+            toks.append(ng)
             tok = ng
-        print(f"max-abs logit distance from the fp32-cache oracle over {steps} steps: {worst:.4g}", flush=True)
+        print(f"max-abs logit distance from the fp32-cache oracle over {steps32} steps: {worst:.4g}", flush=True)
+        assert g.decode_mode_used() == q4hip.DECODE_PERSISTENT
+        # the same 256 steps as one launch (the rows it appends are the ones the steps above wrote)
+        assert g.generate(7, P, steps) == toks
         assert g.decode_mode_used() == q4hip.DECODE_PERSISTENT
     finally:
         g.close()

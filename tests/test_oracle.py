@@ -301,33 +301,40 @@ def test_rmsnorm():
     assert np.allclose(oracle.rmsnorm(c, np.ones(64, f32), 0.0), 1.0, rtol=1e-7)
 
 
-def test_rope_head():
-    rng = np.random.default_rng(8)
-    v = rng.standard_normal(64).astype(f32)
-    table = oracle.rope_table(8, 64, 1e6)
+@pytest.mark.parametrize("hd", [64, 128])
+def test_rope_head(hd):
+    """NEOX pairs (i, i + hd/2) (kernels.c:340-344) at both head dims the configurations use."""
+    rng = np.random.default_rng(8 + hd)
+    v = rng.standard_normal(hd).astype(f32)
+    table = oracle.rope_table(8, hd, 1e6)
     assert np.array_equal(oracle.rope_head(v, table[0].reshape(-1)), v)          # pos 0: identity
     got = oracle.rope_head(v, table[5].reshape(-1))
     c, s = table[5, :, 0].astype(np.float64), table[5, :, 1].astype(np.float64)
-    x0, x1 = v[:32].astype(np.float64), v[32:].astype(np.float64)
+    x0, x1 = v[:hd // 2].astype(np.float64), v[hd // 2:].astype(np.float64)
     ref = np.concatenate([x0 * c - x1 * s, x1 * c + x0 * s])
     assert np.allclose(got, ref, rtol=1e-6, atol=1e-7)
-    assert np.allclose(got[:32] ** 2 + got[32:] ** 2, v[:32] ** 2 + v[32:] ** 2, rtol=1e-5)
+    assert np.allclose(got[:hd // 2] ** 2 + got[hd // 2:] ** 2, v[:hd // 2] ** 2 + v[hd // 2:] ** 2, rtol=1e-5)
 
 
-def test_rope_table_vs_float64():
-    t = oracle.rope_table(300, 64, 1e6)
+@pytest.mark.parametrize("hd", [64, 128])
+def test_rope_table_vs_float64(hd):
+    """cos/sin(pos / theta^(2i/hd)) (cpu-worker.js:130-135) within one fp32 ulp of float64."""
+    t = oracle.rope_table(300, hd, 1e6)
     pos = np.arange(300)[:, None].astype(np.float64)
-    a = pos / np.power(1e6, 2.0 * np.arange(32)[None, :] / 64)
+    a = pos / np.power(1e6, 2.0 * np.arange(hd // 2)[None, :] / hd)
     assert np.all(np.abs(t[:, :, 0] - np.cos(a)) <= np.spacing(np.float32(1.0)))
     assert np.all(np.abs(t[:, :, 1] - np.sin(a)) <= np.spacing(np.float32(1.0)))
     assert np.all(t[0, :, 0] == 1.0) and np.all(t[0, :, 1] == 0.0)
     # the Python host's table (synth.rope_table) is bit-identical to the oracle's
-    assert np.array_equal(_bits(synth.rope_table(300, 64, 1e6)), _bits(t))
+    assert np.array_equal(_bits(synth.rope_table(300, hd, 1e6)), _bits(t))
 
 
-def test_attention():
-    rng = np.random.default_rng(9)
-    hd = 64
+@pytest.mark.parametrize("hd", [64, 128])
+def test_attention(hd):
+    """Softmax attention of one head (kernels.c:354-378) against float64 at both head dims (scale
+    1/sqrt(hd), four lane sums of hd/4 products), with its two closed forms: one position gives
+    that position's V row exactly, q = 0 gives the mean of V."""
+    rng = np.random.default_rng(9 + hd)
     for T in (1, 2, 7, 65, 300):
         q = rng.standard_normal(hd).astype(f32)
         k = rng.standard_normal((T, hd)).astype(f32)
@@ -335,7 +342,7 @@ def test_attention():
         got = oracle.attend(q, k, v, T, hd)
         if T == 1:
             assert np.array_equal(got, v[0])                                      # softmax of one = 1
-        s = (k.astype(np.float64) @ q.astype(np.float64)) / 8.0
+        s = (k.astype(np.float64) @ q.astype(np.float64)) / math.sqrt(hd)
         p = np.exp(s - s.max())
         ref = (p / p.sum()) @ v.astype(np.float64)
         assert np.allclose(got, ref, rtol=2e-5, atol=2e-6)
@@ -343,6 +350,22 @@ def test_attention():
     v = rng.standard_normal((50, hd)).astype(f32)
     got = oracle.attend(np.zeros(hd, f32), rng.standard_normal((50, hd)).astype(f32), v, 50, hd)
     assert np.allclose(got, v.astype(np.float64).mean(0), rtol=1e-5, atol=1e-6)
+
+
+def test_attention_float64_bound_catches_a_wrong_scale():
+    """The float64 bound above is sharp enough to see the plausible head-dim mistakes: the hd = 64
+    scale (1/8) used at hd = 128, or only half of the dimensions in the scores."""
+    rng = np.random.default_rng(99)
+    hd, T = 128, 65
+    q = rng.standard_normal(hd).astype(f32)
+    k = rng.standard_normal((T, hd)).astype(f32)
+    v = rng.standard_normal((T, hd)).astype(f32)
+    got = oracle.attend(q, k, v, T, hd)
+    for s in ((k.astype(np.float64) @ q.astype(np.float64)) / 8.0,
+              (k[:, :64].astype(np.float64) @ q[:64].astype(np.float64)) / math.sqrt(hd)):
+        p = np.exp(s - s.max())
+        wrong = (p / p.sum()) @ v.astype(np.float64)
+        assert not np.allclose(got, wrong, rtol=2e-5, atol=2e-6)
 
 
 def test_swiglu():
@@ -388,15 +411,16 @@ def test_model_context_full():
     m.close()
 
 
-def test_model_logits_near_float64_reference():
-    """End to end on a tiny model: the oracle's logits against a float64 model that quantizes the
+@pytest.mark.parametrize("name,seed", [("tiny", 41), ("small128", 42)])
+def test_model_logits_near_float64_reference(name, seed):
+    """End to end on a tiny model (head_dim 64) and on small128 (head_dim 128, the 1.5B shape's): the oracle's logits against a float64 model that quantizes the
     activations at the same points (quantize_row) and computes everything else exactly, except
     RMSNorm, which it takes in fp32 from the oracle: embedding rows are multiples of their Q4
     scale, so after the norm many values sit exactly on a .5 tie of the int8 grid and a 1-ulp
     difference would flip them (each flip moves a logit by ~5e-4)."""
-    shape = synth.SHAPES["tiny"]
-    t = synth.make_model(shape, 41)
-    ids = synth.prompt_ids(41, 9, shape.vocab)
+    shape = synth.SHAPES[name]
+    t = synth.make_model(shape, seed)
+    ids = synth.prompt_ids(seed, 9, shape.vocab)
     m = oracle.Model(shape, t, ctx=32)
     m.forward(ids, 0)
     lg = m.logits()

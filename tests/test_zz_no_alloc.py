@@ -107,6 +107,30 @@ def test_noalloc_matches_run_twice_second_smaller():
             b.free()
 
 
+def test_noalloc_at_the_largest_k():
+    """K = Q4HIP_NOALLOC_MAX_K (65536: 2048 activation blocks, 128 KB of shared memory in the
+    one-token matvec), bit-equal to q4hip_mv_run and to the oracle's matmul_q4."""
+    import q4hip
+    hip = _hip()
+    assert hip.hipSetDevice(0) == 0
+    N, K = 64, q4hip.NOALLOC_MAX_K
+    print(f"no-alloc matvec {N}x{K}", flush=True)
+    raw = _weights(N, K, 11)
+    mv = q4hip.Matvec(raw, N, K)
+    xb, yb = DevBuf(hip, K * 4), DevBuf(hip, N * 4)
+    try:
+        x = np.random.default_rng(12).standard_normal(K, dtype=np.float32)
+        ref = mv.run(x)
+        xb.put(x)
+        mv.run_device(xb.p.value, yb.p.value)
+        assert np.array_equal(_bits(yb.get(N)), _bits(ref))
+        assert np.array_equal(_bits(ref), _bits(oracle.matvec_q4(raw, N, K, x)))
+    finally:
+        mv.close()
+        xb.free()
+        yb.free()
+
+
 def test_noalloc_rejects_bad_buffers_and_sizes():
     """Host pointers, short buffers and K above the limit are refused before any launch."""
     import q4hip
