@@ -916,8 +916,9 @@ __device__ __forceinline__ void head_rows(const PArgs& a, const PSmem& m, const 
   }
 }
 
-// Logits of this workgroup's Q4_0 row groups (three rotating register buffers: two row groups in
-// flight while one is computed); x is received and normalised after the first two are issued.
+// Logits of this workgroup's Q4_0 row groups (five rotating register buffers: four row groups in
+// flight while one is computed; with two, the head streamed ~5 us slower per step); x is received
+// and normalised after the first four are issued.
 template <class S>
 __device__ __forceinline__ bool head_scan_q4(const PArgs& a, const PSmem& m, uint32_t epx, int s, bool& bad,
                                              float& bv, int& bi) {
@@ -925,26 +926,27 @@ __device__ __forceinline__ bool head_scan_q4(const PArgs& a, const PSmem& m, uin
   const int G = gridDim.x, wg = lwg(a), nRG = a.head.Np / 16, stride = 4 * G;
   float nw[4];
   normw_load<S>(a.out_norm, nw);
-  int rgi = wg + G * wave;
-  WR<S::NGD> R0[1], R1[1], R2[1];
-  if (rgi < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi, lane, R0[0]);
-  if (rgi + stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + stride, lane, R1[0]);
+  // row groups round-robin over the waves, the o/down workgroups last: they come to the head
+  // last (their final down stores end the layers), so they take the fewest row groups
+  int rgi = (G - 1 - wg) + G * wave;
+  constexpr int NBUF = 5;
+  WR<S::NGD> R[NBUF][1];
+#pragma unroll
+  for (int k = 0; k < NBUF - 1; k++)
+    if (rgi + k * stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + k * stride, lane, R[k][0]);
   recv_x<S>(a.ll + S::oXH, epx, a.st, m, bad, a.nap);
   if (wg_bad(m.flag, bad)) return false;
   prof_mark(a, s, a.NL * 16 + 0);
   norm_quant<S>(m, nw, a.eps);
-  while (rgi < nRG) {
-    if (rgi + 2 * stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + 2 * stride, lane, R2[0]);
-    head_rows<S>(a, m, R0, rgi, lane, bv, bi);
-    rgi += stride;
-    if (rgi >= nRG) break;
-    if (rgi + 2 * stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + 2 * stride, lane, R0[0]);
-    head_rows<S>(a, m, R1, rgi, lane, bv, bi);
-    rgi += stride;
-    if (rgi >= nRG) break;
-    if (rgi + 2 * stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + 2 * stride, lane, R1[0]);
-    head_rows<S>(a, m, R2, rgi, lane, bv, bi);
-    rgi += stride;
+  for (;;) {
+#pragma unroll
+    for (int i = 0; i < NBUF; i++) {
+      if (rgi + (NBUF - 1) * stride < nRG)
+        wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + (NBUF - 1) * stride, lane, R[(i + NBUF - 1) % NBUF][0]);
+      head_rows<S>(a, m, R[i], rgi, lane, bv, bi);
+      rgi += stride;
+      if (rgi >= nRG) return true;
+    }
   }
   return true;
 }
