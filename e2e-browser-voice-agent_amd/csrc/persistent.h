@@ -901,6 +901,35 @@ __device__ __forceinline__ void arg_merge(float& bv, int& bi, float v, int i) {
   if (i >= 0 && (bi < 0 || v > bv || (v == bv && i < bi))) { bv = v; bi = i; }
 }
 
+// The merge over the whole wave (all lanes active), the result in every lane.  The merge is a
+// maximum under a total order (value, then the lower index), so any pairing gives the same result:
+// quad permutations and the mirrors within 8 and 16 lanes by DPP, lane ^ 16 by swizzle, then lanes
+// 0 and 32 (as max64), with no shared-memory round trip.
+template <int C>
+__device__ __forceinline__ void arg_dpp(float& bv, int& bi) {
+  const float ov = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(bv), C, 0xF, 0xF, true));
+  const int oi = __builtin_amdgcn_mov_dpp(bi, C, 0xF, 0xF, true);
+  arg_merge(bv, bi, ov, oi);
+}
+__device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
+  arg_dpp<0xB1>(bv, bi);
+  arg_dpp<0x4E>(bv, bi);
+  arg_dpp<0x141>(bv, bi);
+  arg_dpp<0x140>(bv, bi);
+  {
+    const float ov = __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(bv), 0x401F));
+    const int oi = __builtin_amdgcn_ds_swizzle(bi, 0x401F);
+    arg_merge(bv, bi, ov, oi);
+  }
+  const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 0));
+  const int i0 = __builtin_amdgcn_readlane(bi, 0);
+  const float v1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 32));
+  const int i1 = __builtin_amdgcn_readlane(bi, 32);
+  bv = v0;
+  bi = i0;
+  arg_merge(bv, bi, v1, i1);
+}
+
 // ---------------------------------------------------------------- the output head + argmax
 
 template <class S>
@@ -1067,12 +1096,7 @@ __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32
   int bi = -1;
   const bool ok = a.head_q8 ? head_scan_q8<S>(a, m, epx, s, bad, bv, bi) : head_scan_q4<S>(a, m, epx, s, bad, bv, bi);
   if (!ok) return -1;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o);
-    const int oi = __shfl_xor(bi, o);
-    arg_merge(bv, bi, ov, oi);
-  }
+  wave_argmax(bv, bi);
   if (lane == 0) { m.argv[wave] = bv; m.argi[wave] = bi; }
   __syncthreads();
   if (tid < kArgStride) {
@@ -1093,12 +1117,7 @@ __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32
   bv = 0.0f;
   bi = -1;
   for (int g = tid; g < G; g += kPThreads) arg_merge(bv, bi, __uint_as_float(m.raw[2 * g]), (int)m.raw[2 * g + 1]);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o);
-    const int oi = __shfl_xor(bi, o);
-    arg_merge(bv, bi, ov, oi);
-  }
+  wave_argmax(bv, bi);
   __syncthreads();
   if (lane == 0) { m.argv[wave] = bv; m.argi[wave] = bi; }
   __syncthreads();
