@@ -74,13 +74,35 @@ PROFILE = os.path.join(REPO, "profiles", "decode_persistent_qwen05b_prompt64_ste
 
 
 def profile_blob(name):
-    """The JSON block at the end of a committed rocprofv3 summary profiles/<name>, or None."""
+    """The JSON block at the end of a committed rocprofv3 summary profiles/<name>, or None when there
+    is none or it was measured on other kernels: the block records the hash of the device code's
+    sources it was made with (kernel_sources_sha), and a figure from a summary of other kernels is
+    not reported (profile_source says which)."""
     try:
         text = open(os.path.join(REPO, "profiles", name)).read()
         blob = text[text.index("```json") + 7:]
-        return json.loads(blob[:blob.index("```")])
+        data = json.loads(blob[:blob.index("```")])
     except (OSError, ValueError):
         return None
+    import q4hip
+    if not isinstance(data, dict) or data.get("kernel_sources_sha") != q4hip.sources_sha():
+        return None
+    return data
+
+
+def profile_source(name):
+    """Where a profile-derived figure comes from: the summary, the kernels it measured, and whether
+    those are the kernels this run uses (else the figure is null)."""
+    import q4hip
+    try:
+        text = open(os.path.join(REPO, "profiles", name)).read()
+        blob = text[text.index("```json") + 7:]
+        data = json.loads(blob[:blob.index("```")])
+        sha = data.get("kernel_sources_sha") if isinstance(data, dict) else None
+    except (OSError, ValueError):
+        sha = None
+    return {"profile": "profiles/" + name, "kernel_sources_sha": sha, "current_kernels": q4hip.sources_sha(),
+            "matches": sha is not None and sha == q4hip.sources_sha()}
 
 
 def profiled_traffic():
@@ -100,14 +122,15 @@ def mall_share(footprint_bytes):
     """Fraction of a weight stream of this footprint, read in the same order every pass, that the
     256 MB last-level cache serves: the committed rotation sweep's row of the smallest footprint
     at or above it (None without the summary)."""
-    rows = profile_blob(MALL_PROFILE)
+    data = profile_blob(MALL_PROFILE)
+    rows = data.get("rows") if data else None
     if not rows:
         return None
     above = [r for r in rows if r["footprint_mb"] * 1e6 >= footprint_bytes]
     row = min(above, key=lambda r: r["footprint_mb"]) if above else rows[-1]
     return {"served_fraction": row["served_fraction"], "footprint_mb": round(footprint_bytes / 1e6, 1),
             "measured_at_mb": row["footprint_mb"], "method": "weight-copy rotation of the head matvec",
-            "profile": "profiles/" + MALL_PROFILE}
+            "profile_source": profile_source(MALL_PROFILE)}
 
 
 def cpu_baseline(shape, tensors, ids, first_tokens):
@@ -241,7 +264,7 @@ def bench_decode(args):
                 "frac": round(achieved_gbps / HBM_PEAK_GBPS, 4),
                 "traffic": round(per_step_traffic * args.steps) if per_step_traffic and mode == 2 else None,
                 "bytes_per_launch": tot, "avg_launch_us": round(dev_ms * 1e3, 1), "steps_per_launch": args.steps,
-                "profile": os.path.relpath(PROFILE, REPO)}
+                "traffic_source": profile_source(os.path.basename(PROFILE))}
     # how much of the weight set the 256 MB last-level cache can serve when it is read once per token
     share = mall_share(repacked_weight_bytes(shape))
     if share:
@@ -434,7 +457,7 @@ def bench_prefill(args):
                      "frac": round(pass_tflops / 2500.0, 5),
                      "traffic": round(pf["traffic_bytes"] * args.steps) if pf and pf.get("traffic_bytes") else None,
                      "flops_per_pass": flops, "ops_per_launch": flops * args.steps,
-                     "avg_launch_us": round(ms * 1e3, 1), "profile": "profiles/prefill_qwen05b_1024.md"},
+                     "avg_launch_us": round(ms * 1e3, 1), "traffic_source": profile_source("prefill_qwen05b_1024.md")},
         "gate_up_int8_dot_tops": {"achieved": round(tops, 2), "peak": 5000.0, "frac": round(tops / 5000.0, 5),
                                   "us_per_layer": round(gu_us, 1)},
         "next_token": nxt,
@@ -488,7 +511,7 @@ def bench_matvec(args):
         "roofline": {"bound": "hbm", "kernel": "k_matvec<1> 151936x896", "achieved": head["gbps"],
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4),
                      "traffic": _matvec_head_traffic(), "avg_launch_us": head["us"],
-                     "profile": "profiles/matvec_sweep_qwen05b.md"},
+                     "traffic_source": profile_source("matvec_sweep_qwen05b.md")},
     }
     if not args.no_cpu:
         oracle = _oracle()
@@ -568,7 +591,7 @@ def bench_batched(args):
                      "frac": round(gbps / HBM_PEAK_GBPS, 4),
                      "traffic": round(pb["traffic_bytes"] * args.steps) if pb and kv16 else None,
                      "bytes_per_launch": tot, "avg_launch_us": round(dev_ms * 1e3, 1), "steps_per_launch": args.steps,
-                     "profile": "profiles/batched_decode_qwen15b_b32_ctx1024.md"},
+                     "traffic_source": profile_source("batched_decode_qwen15b_b32_ctx1024.md")},
         "first_tokens": toks[0, :4].tolist(),
     }
     bt.close()

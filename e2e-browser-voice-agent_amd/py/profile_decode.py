@@ -164,6 +164,8 @@ def summarize(a) -> None:
             f"counter bounds the DRAM reads from above and does not split them (the MALL share is measured by weight "
             f"rotation, `profiles/mall_weight_rotation_head.md`).",
         ]
+    import q4hip
+    traffic["kernel_sources_sha"] = q4hip.sources_sha()
     lines += ["", "```json", json.dumps(traffic, indent=1), "```", ""]
     with open(a.out, "w") as f:
         f.write("\n".join(lines))

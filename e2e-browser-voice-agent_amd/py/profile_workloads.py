@@ -274,6 +274,8 @@ def summarize(a) -> None:
             "write_calibration": w_cal}
     if not a.marker:
         blob["per_launch"] = per_launch
+    import q4hip
+    blob["kernel_sources_sha"] = q4hip.sources_sha()
     lines += ["```json", json.dumps(blob, indent=1), "```", ""]
     with open(a.out, "w") as f:
         f.write("\n".join(lines))
@@ -316,7 +318,8 @@ def mall(a) -> None:
              "| copies | footprint MB | us per launch | GB/s | served fraction |", "|---|---|---|---|---|"]
     for r in rows:
         lines.append(f"| {r['copies']} | {r['footprint_mb']} | {r['us']:.2f} | {r['gbps']} | {r['served_fraction']} |")
-    lines += ["", "```json", json.dumps(rows, indent=1), "```", ""]
+    import q4hip
+    lines += ["", "```json", json.dumps({"rows": rows, "kernel_sources_sha": q4hip.sources_sha()}, indent=1), "```", ""]
     with open(a.out, "w") as f:
         f.write("\n".join(lines))
     print("\n".join(lines))

@@ -103,6 +103,21 @@ def _ptr(a: np.ndarray) -> ctypes.c_void_p:
     return ctypes.c_void_p(a.ctypes.data)
 
 
+def sources_sha() -> str:
+    """First 16 hex digits of the SHA-256 of the device code's sources (csrc/*.h and csrc/*.hip, by
+    name): what a rocprofv3 summary records as the kernels it measured, so that a figure taken from a
+    summary can be dropped once the kernels have changed."""
+    import hashlib
+    d = os.path.join(os.path.dirname(_HERE), "csrc")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(d)):
+        if name.endswith((".h", ".hip")):
+            h.update(name.encode())
+            with open(os.path.join(d, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def device_count() -> int:
     n = ctypes.c_int(0)
     _check(lib().q4hip_device_count(ctypes.byref(n)))
