@@ -500,17 +500,23 @@ def bench_matvec(args):
                      "cold_us": round(cold_us, 2), "cold_gbps": round(nbytes / (cold_us * 1e-6) / 1e9, 1),
                      "cold_copies": copies})
     head = rows[-1]
+    # value: the head streamed from HBM (launches cycle through weight copies larger than the 256 MB
+    # last-level cache); the cache-hot rate, where repeated launches find the weights in that cache,
+    # is reported beside it
     out = {
         "metric": "isolated Q4_0 matvec achieved GB/s (Qwen2.5-0.5B shapes, fp32 x quantized per 32-block)",
-        "value": head["gbps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(head["us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+        "value": head["cold_gbps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(head["cold_us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "i8xq4/f32", "data": "synthetic",
-        "config": {"workload": "Q4_0 matvec sweep, value = the 151936x896 head shape, cache-hot (cold per shape)",
+        "config": {"workload": "Q4_0 matvec sweep, value = the 151936x896 head shape read from HBM "
+                               f"(launches rotate over {head['cold_copies']} weight copies)",
                    "shapes": [r["shape"] for r in rows], "parallelism": "single-gpu"},
         "per_shape": rows,
-        "roofline": {"bound": "hbm", "kernel": "k_matvec<1> 151936x896", "achieved": head["gbps"],
-                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(head["gbps"] / HBM_PEAK_GBPS, 4),
-                     "traffic": _matvec_head_traffic(), "avg_launch_us": head["us"],
+        "cache_hot": {"value": head["gbps"], "us": head["us"],
+                      "note": "the same weights every launch: served largely by the 256 MB last-level cache"},
+        "roofline": {"bound": "hbm", "kernel": "k_matvec_stream<28> 151936x896", "achieved": head["cold_gbps"],
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(head["cold_gbps"] / HBM_PEAK_GBPS, 4),
+                     "traffic": _matvec_head_traffic(), "avg_launch_us": head["cold_us"],
                      "traffic_source": profile_source("matvec_sweep_qwen05b.md")},
     }
     if not args.no_cpu:
@@ -534,8 +540,11 @@ def bench_matvec(args):
 def _matvec_head_traffic():
     """HBM bytes of one head-shape matvec launch from the committed sweep profile, or None."""
     pm = profile_blob("matvec_sweep_qwen05b.md")
+    groups = 151936 // 16                               # 16-row groups; k_matvec_stream's grid, in threads
+    per = -(-groups // 2048)
+    grid = str(-(-(-(-groups // per)) // 4) * 256)
     for r in (pm or {}).get("per_launch", []):
-        if r["grid"].split(",")[0] == "607744" and r.get("fetch_bytes") is not None:
+        if r["grid"].split(",")[0] == grid and r.get("fetch_bytes") is not None:
             return round(r["fetch_bytes"] + r["write_bytes"])
     return None
 

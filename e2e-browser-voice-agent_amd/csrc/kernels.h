@@ -455,6 +455,12 @@ __device__ __forceinline__ float rms_scale_sq(const float* sq, int n, int sst, f
 // Device view of one Q4 matrix in the tiled layout:
 //   qs: uint4 [N/64][ng][64 rows][4 lanes j]  -- word j of blocks 4g..4g+3 of that row
 //   d : uint4 [N/64][nb8][64 rows]            -- 8 fp16 scales (blocks 8c..8c+7) of that row
+// A workgroup barrier for shared memory only: this wave's LDS accesses are done, then the waves
+// meet.  Outstanding global loads (a poll in flight, ring slots, weights loaded ahead) are not
+// waited for, as the fence of __syncthreads would.  The "memory" clobber keeps loads and stores on
+// their side.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 struct Q4Mat {
   const uint4* qs;
   const uint4* d;

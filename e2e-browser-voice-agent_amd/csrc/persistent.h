@@ -243,11 +243,6 @@ __device__ __forceinline__ void ll_wait1(const uint64_t* p, uint64_t& w, uint32_
   }
 }
 
-// A workgroup barrier for shared memory only: this wave's LDS accesses are done, then the waves
-// meet.  Outstanding global loads (a poll in flight, ring slots) are not waited for, as the
-// fence of __syncthreads would.  The "memory" clobber keeps loads and stores on their side.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 // The workgroup-uniform "give up" decision after a wait: a thread whose wait gave up raises the
 // shared flag before the barrier, every thread reads it after.  One barrier and one shared-memory
 // read, where __syncthreads_or takes three of each.  The flag is cleared once per launch and never

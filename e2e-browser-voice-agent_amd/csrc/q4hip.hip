@@ -157,6 +157,99 @@ __global__ __launch_bounds__(64) void k_matvec(Q4Mat W, const uint4* __restrict_
   }
 }
 
+// y = W x for one token and rows of NB blocks (the 896- and 1536-wide projections and output
+// heads): a grid-stride stream over 16-row groups.  Wave w of workgroup b takes groups 4b + w,
+// 4b + w + 4G, ... (G workgroups).  Each group's weights are loaded while the previous group's sums
+// run, and a wave's first loads are issued before the activation blocks are staged in shared memory
+// (once per workgroup), so the two latencies overlap.  The sums are those of k_matvec<1>: lane
+// (r, j) adds its terms acc = acc + f32(p) * (dw * dx) in block order (kernels.c:200-229), then
+// hsum4 across the row's four lanes.
+template <int NB>
+struct StreamRegs {
+  static constexpr int NG = (NB + 3) / 4, NS = (NB + 7) / 8;
+  uint4 w[NG], s[NS];
+};
+
+template <int NB>
+__device__ __forceinline__ void stream_issue(const Q4Mat& W, int g16, int r, int j, StreamRegs<NB>& R) {
+  const int tile = g16 >> 2, rr = ((g16 & 3) << 4) + r;
+  const uint4* wq = W.qs + ((size_t)tile * StreamRegs<NB>::NG * 64 + rr) * 4 + j;
+  const uint4* wd = W.d + (size_t)tile * StreamRegs<NB>::NS * 64 + rr;
+#pragma unroll
+  for (int g = 0; g < StreamRegs<NB>::NG; g++) R.w[g] = wq[(size_t)g * 256];
+#pragma unroll
+  for (int c = 0; c < StreamRegs<NB>::NS; c++) R.s[c] = wd[(size_t)c * 64];
+}
+
+template <int NB, int OP>
+__device__ __forceinline__ void stream_rows(const Q4Mat& W, int g16, int r, int j, const uint4* xs,
+                                            const StreamRegs<NB>& R, float* __restrict__ y,
+                                            const float* __restrict__ bias) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int g = 0; g < StreamRegs<NB>::NG; g++) {
+    const uint32_t ww[4] = {R.w[g].x, R.w[g].y, R.w[g].z, R.w[g].w};
+    const uint4 sv = R.s[g >> 1];
+    const uint32_t sh[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int b = g * 4 + k;
+      if (b < NB) {
+        const int hb = ((g & 1) << 2) + k;
+        const uint32_t hbits = (hb & 1) ? (sh[hb >> 1] >> 16) : (sh[hb >> 1] & 0xffffu);
+        const float dw = half_bits_to_float(hbits);
+        const uint32_t lo = ww[k] & 0x0F0F0F0Fu, hi = (ww[k] >> 4) & 0x0F0F0F0Fu;
+        const uint4 xv = xs[b * 4 + j];
+        int p = sdot4(lo, xv.x, (int)xv.z);
+        p = sdot4(hi, xv.y, p);
+        acc = acc + (float)p * (dw * __uint_as_float(xv.w));
+      }
+    }
+  }
+  const float v = hsum4(acc);
+  const int row = ((g16 >> 2) << 6) + ((g16 & 3) << 4) + r;
+  if (j == 0 && row < W.N) {
+    float* o = y + row;
+    if (OP == OP_ADD) *o = *o + v;
+    else if (OP == OP_BIAS) *o = v + bias[row];
+    else *o = v;
+  }
+}
+
+template <int NB, int OP>
+__global__ __launch_bounds__(256) void k_matvec_stream(Q4Mat W, const uint4* __restrict__ xq, float* __restrict__ y,
+                                                      const float* __restrict__ bias) {
+  __shared__ uint4 xs[NB * 4];
+  const int tid = threadIdx.x, lane = tid & 63, r = lane >> 2, j = lane & 3;
+  const int groups = W.Np >> 4, step = (int)gridDim.x * 4;
+  int g16 = (int)blockIdx.x * 4 + (tid >> 6);
+  StreamRegs<NB> ra, rb;
+  if (g16 < groups) stream_issue<NB>(W, g16, r, j, ra);
+  for (int i = tid; i < NB * 4; i += 256) xs[i] = xq[i];
+  lds_barrier();
+  // two register sets, alternating, so that neither is indexed at run time
+  while (g16 < groups) {
+    const int g1 = g16 + step;
+    if (g1 < groups) stream_issue<NB>(W, g1, r, j, rb);
+    stream_rows<NB, OP>(W, g16, r, j, xs, ra, y, bias);
+    if (g1 >= groups) break;
+    const int g2 = g1 + step;
+    if (g2 < groups) stream_issue<NB>(W, g2, r, j, ra);
+    stream_rows<NB, OP>(W, g1, r, j, xs, rb, y, bias);
+    g16 = g2;
+  }
+}
+
+// Workgroups of a k_matvec_stream<NB> launch over `groups` 16-row groups: every wave takes the same
+// number of groups (the last waves one fewer), at most stream_waves(NB) waves in all -- as many as
+// are resident at once (two per SIMD for 28-block rows, one for the wider register sets of 48).
+constexpr int stream_waves(int nb) { return nb <= 32 ? 2048 : 1024; }
+inline unsigned stream_grid(int groups, int max_waves) {
+  const int per = (groups + max_waves - 1) / max_waves;
+  const int waves = (groups + per - 1) / per;
+  return (unsigned)((waves + 3) / 4);
+}
+
 // One token, matrices with many blocks per row (down: 896 x 4864): the same sums as k_matvec<1>,
 // with the blocks of a 16-row group spread over four waves.  Wave w forms the terms
 // f32(p_j) * (dw * dx) of block groups w, w + 4, ... (every term is independent of the others) into
@@ -1593,7 +1686,11 @@ void launch_matvec(hipStream_t s, const Mat& W, const uint4* xq, int xstride, in
                    const float* bias, const uint4* xh = nullptr) {
   const unsigned grid = (unsigned)(W.Np / 16);
   if (M == 1) {
-    if (W.nb >= kSplitMinBlocks && W.nb <= kSplitMaxBlocks)
+    if (W.nb == 28)
+      k_matvec_stream<28, OP><<<stream_grid(W.Np / 16, stream_waves(28)), 256, 0, s>>>(W.view(), xq, y, bias);
+    else if (W.nb == 48)
+      k_matvec_stream<48, OP><<<stream_grid(W.Np / 16, stream_waves(48)), 256, 0, s>>>(W.view(), xq, y, bias);
+    else if (W.nb >= kSplitMinBlocks && W.nb <= kSplitMaxBlocks)
       k_matvec_split<OP><<<grid, kSplitThreads, split_lds(W.nb), s>>>(W.view(), xq, y, bias);
     else
       k_matvec<1, OP><<<grid, 64, (size_t)W.nb * 64, s>>>(W.view(), xq, xstride, 1, y, ldy, bias);

@@ -1,7 +1,9 @@
 """Isolated Q4_0 matvec on the GPU against the oracle's matmul_q4 (engine/kernels.c:200-273).
 
 Sweep shapes are the model's projections: [896x896] o, [128x896] k/v, [4864x896] gate/up,
-[896x4864] down and [151936x896] output head.  The activation is quantized to int8 per 32-block
+[896x4864] down and [151936x896] output head; [1536x1536] and [8960x1536] are the 1.5B shape's (the
+second width the one-token stream kernel is built for), and [200x896] a row count that is not a
+multiple of the 64-row tile.  The activation is quantized to int8 per 32-block
 on the device exactly as quantize_row does, and each output is accumulated in the reference's lane
 order, so the bar is bit-exact equality.
 """
@@ -13,7 +15,8 @@ import synth
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(896, 896), (128, 896), (4864, 896), (896, 4864), (151936, 896)]
+SHAPES = [(896, 896), (128, 896), (4864, 896), (896, 4864), (151936, 896), (1536, 1536), (8960, 1536),
+          (200, 896)]
 
 
 def _weights(N, K, seed):
