@@ -585,6 +585,15 @@ def bench_batched(args):
     tot = sum(weights + logits + BATCH * per_pos * (BATCH_PROMPT + i + 1) for i in range(args.steps))
     gbps = tot / (dev_ms / 1e3) / 1e9
     pb = profile_blob("batched_decode_qwen15b_b32_ctx1024.md")   # measured with the fp16 cache
+    # matrix-core work of the step's projections: one v_mfma_f32_16x16x16_f16 (8192 flops) per
+    # 16 weight rows x 16-token tile x block x reference lane chain (k_gemm_sk), over qkv, o, gate|up,
+    # down and the head
+    D, F, L, V, QKV = shape.dim, shape.ffn, shape.layers, shape.vocab, shape.qkv
+    tiles = (BATCH + 15) // 16
+    pad16 = lambda n: (n + 63) // 64 * 64 // 16          # noqa: E731  16-row groups of a 64-row-padded matrix
+    mfmas = tiles * 4 * (L * (pad16(QKV) * (D // 32) + pad16(D) * (D // 32) + pad16(2 * F) * (D // 32)
+                              + pad16(D) * (F // 32)) + pad16(V) * (D // 32))
+    mfma_tflops = mfmas * 8192 * args.steps / (dev_ms / 1e3) / 1e12
     out = {
         "metric": "batched decode tokens/s, 32 sequences at 1024-token context (Qwen2.5-1.5B Q4_0 shape)",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -595,6 +604,12 @@ def bench_batched(args):
                    "kv_cache": "fp16" if kv16 else "fp32 (the reference's cache type)",
                    "parallelism": "single-gpu"},
         "achieved_gbps": round(gbps, 1),
+        "mfma": {"instructions_per_step": mfmas, "flops_per_step": mfmas * 8192,
+                 "achieved_tflops": round(mfma_tflops, 2), "peak_tflops": 2500.0,
+                 "frac": round(mfma_tflops / 2500.0, 5),
+                 "note": "v_mfma_f32_16x16x16_f16 issued by the step's projections over the whole step time, "
+                         "against the dense fp16 matrix peak; 10 of each instruction's 16 k-slots carry data "
+                         "(the exact integer encoding of the reference's lane dots)"},
         "roofline": {"bound": "hbm", "kernel": "batched decode step (all kernels)",
                      "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4),

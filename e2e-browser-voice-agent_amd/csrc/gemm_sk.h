@@ -186,10 +186,20 @@ struct SkB {
 // spread over the XCDs), which keeps a weight matrix larger than an L2 shared by the tiles in
 // flight.  Measured on the 1024-token prefill: o/down fetch 5.5 -> 1.4 GB per pass with it, but
 // gate/up (4.9 MB of weights) 0.85 -> 7.5 GB, at unchanged kernel times; the host chooses per
-// matrix.  Returns false for the padding workgroups of the second case (row group past the last).
+// matrix.  A batch step of 2 .. kSkPairTiles token tiles (without by_tile) runs the tiles of one row
+// group on one XCD, dispatched 8 workgroups apart: they read the group's weights at the same time
+// and the XCD's L2 serves the second reader, where row-group-fastest order with a row-group count
+// that is not a multiple of 8 (the output head: 2374 groups of 64 rows) put them on different XCDs
+// a whole pass apart.  Returns false for padding workgroups (row group past the last).
 constexpr int kXcds = 8;
+constexpr int kSkPairTiles = 4;
+
+__host__ __device__ inline bool sk_paired(int ntiles, bool by_tile) {
+  return !by_tile && ntiles > 1 && ntiles <= kSkPairTiles;
+}
 
 __host__ __device__ inline int sk_grid(int nrg, int ntiles, bool by_tile) {
+  if (sk_paired(ntiles, by_tile)) return (nrg + kXcds - 1) / kXcds * kXcds * ntiles;
   if (!by_tile || ntiles % kXcds == 0) return nrg * ntiles;
   if (kXcds % ntiles == 0) {
     const int per = kXcds / ntiles;                 // XCDs per tile
@@ -200,6 +210,11 @@ __host__ __device__ inline int sk_grid(int nrg, int ntiles, bool by_tile) {
 
 __device__ __forceinline__ bool sk_place(int L, int nrg, int ntiles, bool by_tile, int& rg, int& T) {
   const int x = L % kXcds, q = L / kXcds;
+  if (sk_paired(ntiles, by_tile)) {
+    T = q % ntiles;
+    rg = (q / ntiles) * kXcds + x;
+    return rg < nrg;
+  }
   if (!by_tile) {
     rg = L % nrg;
     T = L / nrg;
