@@ -1805,6 +1805,14 @@ bool pv_tiles_off() {
   return off;
 }
 
+// Q4HIP_ATTN_ROWS=0 keeps prompt passes on the three-launch path (scores, softmax, P.V tiles; same
+// bits): also the path where k_attn_rows does not apply (head_dim 128, or a context whose scores do
+// not fit shared memory).
+bool attn_rows_off() {
+  static const bool off = [] { const char* e = getenv("Q4HIP_ATTN_ROWS"); return e && e[0] == '0'; }();
+  return off;
+}
+
 size_t softmax_lds(int H, int KVH, int ctx) {
   return (size_t)((H / KVH) * pv_row_stride(ctx) + 6 * kMaxGroup) * sizeof(float);
 }
@@ -1941,6 +1949,231 @@ __global__ __launch_bounds__(1024) void k_pv_tiles(const float* __restrict__ sc,
   }
 }
 
+// Attention of a prompt pass in one launch (head_dim 64, kernels.c:355-377): workgroup (kv group g,
+// row b) keeps the G heads' scores over positions [0, pos[b]] in shared memory and runs there the
+// reference's steps in its order -- scores as k_attn_scores_list forms them, the maximum,
+// e_t = fast_exp(s_t - max), the sum in position order, p_t = e_t / sum, and out[c] = sum_t p_t *
+// v_t[c] in position order (one thread per head and column) -- then writes att and its quantized
+// blocks as k_pv_tiles does.  Scores and probabilities never go to memory: the three-launch path
+// writes and reads them back twice.  Rows run longest first (row B - 1 - blockIdx.y).
+// Grid (KVH, B), kAttnRowsThreads threads, dynamic shared memory attn_rows_lds(G, ctx).
+constexpr int kAttnRowsThreads = 512;       // 8 waves: one per head of a group of up to 8
+constexpr int kAttnRowsChunk = 64;          // V rows staged per step
+__host__ __device__ inline int attn_rows_vstride() { return kAttnRowsChunk + 4; }
+inline size_t attn_rows_lds(int G, int ctx) {
+  return (size_t)(G * pv_row_stride(ctx) + 2 * 64 * attn_rows_vstride() + 3 * kMaxGroup * 8) * sizeof(float);
+}
+
+template <class KT>
+__global__ __launch_bounds__(kAttnRowsThreads) void k_attn_rows(const float* __restrict__ qkv, int QKV, int H, int KVH,
+                                                               const KT* __restrict__ kc, const KT* __restrict__ vc,
+                                                               int ctx, int layer, const int* __restrict__ pos, int B,
+                                                               float* __restrict__ att, int D, uint4* __restrict__ xq,
+                                                               int xstride, uint4* __restrict__ xh) {
+  constexpr int HD = 64, CH = kAttnRowsChunk, NW = kAttnRowsThreads / 64;
+  const int CHS = attn_rows_vstride();
+  extern __shared__ __attribute__((aligned(16))) float lsm[];
+  const int g = blockIdx.x, b = B - 1 - (int)blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = H / KVH, T = pos[b] + 1, TS = pv_row_stride(ctx);
+  float* e = lsm;                           // [G][TS] scores, then exponentials, then probabilities
+  float* vs = e + G * TS;                   // [2][64 columns][CHS] V chunks, column-major, double-buffered
+  float* red = vs + 2 * HD * CHS;           // [NW][kMaxGroup] maxima, [kMaxGroup] max, [kMaxGroup] sum
+  float* rmax = red + NW * kMaxGroup;
+  float* rsum = rmax + kMaxGroup;
+  const size_t cb = ((size_t)layer * KVH + g) * ctx * HD;
+  // V: a chunk's 64 rows come through one of NS register sets, loaded NS chunks ahead; the first NS
+  // load while the scores and the softmax run (rows from T on repeat row T - 1, never added)
+  typedef typename KvRaw<KT>::T VRaw;
+  constexpr int NV = CH * HD / 4 / kAttnRowsThreads, NS = 4;  // float4 of a chunk per thread, sets
+  const int nch = (T + CH - 1) / CH;
+  // lane l of a wave loads row l of the chunk (4 columns), so that its column-major stores below
+  // fall on distinct banks
+  auto load = [&](int ch, VRaw* r) {
+    const int t0 = min(ch, nch - 1) * CH;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+      const int i = tid + k * kAttnRowsThreads, row = i & 63, c4 = (i >> 6) * 4;
+      r[k] = kv_raw4<KT>(vc + cb + (size_t)min(t0 + row, T - 1) * HD + c4);
+    }
+  };
+  VRaw vset[NS][NV];
+#pragma unroll
+  for (int k = 0; k < NS; k++) load(k, vset[k]);
+  // scores (k_attn_scores_list's order): four lane sums over i = j mod 4, summed, scaled; q is read
+  // at workgroup-uniform addresses (scalar loads), not through shared memory
+  const float* qg = qkv + (size_t)b * QKV + g * G * HD;
+  const float scale = 1.0f / __builtin_sqrtf((float)HD);
+  float mxh[kMaxGroup];
+#pragma unroll
+  for (int gh = 0; gh < kMaxGroup; gh++) mxh[gh] = -1e30f;
+  for (int t = tid; t < T; t += kAttnRowsThreads) {
+    const KT* kr = kc + cb + (size_t)t * HD;
+    float4 kv[HD / 4];
+#pragma unroll
+    for (int u = 0; u < HD / 8; u++) kv_ld8<KT>(kr + 8 * u, kv[2 * u], kv[2 * u + 1]);
+#pragma unroll
+    for (int gh = 0; gh < kMaxGroup; gh++) {
+      if (gh < G) {
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+        for (int u = 0; u < HD / 4; u++) {
+          const float4 q4 = *reinterpret_cast<const float4*>(qg + gh * HD + 4 * u);
+          s0 = s0 + q4.x * kv[u].x;
+          s1 = s1 + q4.y * kv[u].y;
+          s2 = s2 + q4.z * kv[u].z;
+          s3 = s3 + q4.w * kv[u].w;
+        }
+        const float sv = (s0 + s1 + s2 + s3) * scale;
+        e[gh * TS + t] = sv;
+        mxh[gh] = __builtin_fmaxf(mxh[gh], sv);
+      }
+    }
+  }
+  // the maximum of each head (order-free)
+#pragma unroll
+  for (int gh = 0; gh < kMaxGroup; gh++) {
+    float m = mxh[gh];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0) red[wave * kMaxGroup + gh] = m;
+  }
+  lds_barrier();
+  if (tid < G) {
+    float m = red[tid];
+    for (int w = 1; w < NW; w++) m = __builtin_fmaxf(m, red[w * kMaxGroup + tid]);
+    rmax[tid] = m;
+  }
+  lds_barrier();
+  for (int gh = 0; gh < G; gh++) {
+    const float mx = rmax[gh];
+    for (int t = tid; t < T; t += kAttnRowsThreads) e[gh * TS + t] = fast_exp(e[gh * TS + t] - mx);
+  }
+  lds_barrier();
+  if (tid < G) rsum[tid] = ordered_sum(e + tid * TS, T);   // the sum in position order
+  lds_barrier();
+  for (int gh = 0; gh < G; gh++) {
+    const float sum = rsum[gh];
+    for (int t = tid; t < T; t += kAttnRowsThreads) e[gh * TS + t] = e[gh * TS + t] / sum;
+  }
+  // P.V: thread (head = wave, column = lane) adds p_t * v_t[c] over the chunks in order (each
+  // product rounded, then added).  In a batch of 16 positions lane K of every 16-lane row holds p of
+  // position K and a DPP broadcast hands it to the whole row as the product's first operand
+  // (pv_row), so a wave reads its head's probabilities with one 4-byte read per batch; the
+  // products of a batch are formed while the previous batch's are added, and a whole chunk's last
+  // batch is added at the start of the next chunk.
+  auto store = [&](int buf, const VRaw* r) {
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+      const int i = tid + k * kAttnRowsThreads, row = i & 63, c4 = (i >> 6) * 4;
+      float* d = vs + (buf * HD + c4) * CHS + row;
+      const float4 w = kv_wide4(r[k]);
+      d[0] = w.x;
+      d[CHS] = w.y;
+      d[2 * CHS] = w.z;
+      d[3 * CHS] = w.w;
+    }
+  };
+  const bool active = wave < G;
+  const float* pr = e + (active ? wave : 0) * TS;
+  const int rl = lane & 15;
+  float acc = 0.0f;
+  float pc[16];
+  bool carry = false;
+  auto add_carry = [&]() {
+#pragma unroll
+    for (int k = 0; k < 16; k++) acc = acc + pc[k];
+    carry = false;
+  };
+  auto chunk = [&](int ch) {
+    const int t0 = ch * CH, m = min(CH, T - t0);
+    const float* vcol = vs + ((ch & 1) * HD + lane) * CHS;
+    if (!active) return;
+    if (m == CH) {
+      float pb[2];
+      float4 va[2][4];
+      auto rd = [&](int j, int st) {
+        pb[st] = pr[t0 + 16 * j + rl];
+#pragma unroll
+        for (int u = 0; u < 4; u++) va[st][u] = *reinterpret_cast<const float4*>(vcol + 16 * j + 4 * u);
+      };
+      rd(0, 0);
+      rd(1, 1);
+      if (carry) add_carry();
+      float d[16];
+      pv_row<16>::mul(pb[0], va[0], d);
+#pragma unroll
+      for (int j = 0; j + 1 < CH / 16; j++) {
+        if (j + 2 < CH / 16) rd(j + 2, j & 1);
+        float n[16];
+        pv_row<16>::step(acc, d, pb[(j + 1) & 1], va[(j + 1) & 1], n);
+#pragma unroll
+        for (int k = 0; k < 16; k++) d[k] = n[k];
+      }
+#pragma unroll
+      for (int k = 0; k < 16; k++) pc[k] = d[k];
+      carry = true;
+    } else {
+      if (carry) add_carry();
+      for (int r = 0; r < m; r++) acc = acc + pr[t0 + r] * vcol[r];
+    }
+  };
+  // chunk ch sits in buffer ch & 1; after the barrier that opens chunk ch, chunk ch + 1 goes into
+  // the other buffer (its last reader, chunk ch - 1, is done) and its register set loads chunk
+  // ch + 1 + NS
+  store(0, vset[0]);
+  load(NS, vset[0]);
+  for (int c = 0; c < nch; c += NS) {
+#pragma unroll
+    for (int k = 0; k < NS; k++) {
+      if (c + k < nch) {
+        lds_barrier();
+        if (c + k + 1 < nch) {
+          store((k + 1) & 1, vset[(k + 1) % NS]);
+          load(c + k + 1 + NS, vset[(k + 1) % NS]);
+        }
+        chunk(c + k);
+      }
+    }
+  }
+  if (active && carry) add_carry();
+  if (active) att[(size_t)b * D + (g * G + wave) * HD + lane] = acc;
+  if (xq) {
+    // each head's 64 outputs as two quantize_row blocks
+    lds_barrier();
+    float* o = vs;                                         // [head][64]
+    if (active) o[wave * HD + lane] = acc;
+    lds_barrier();
+    if (tid < 8 * G) {
+      const int hh = tid >> 3, blk = (tid >> 2) & 1, j = tid & 3;
+      const int base = hh * HD + 32 * blk + 2 * j;
+      const float v[8] = {o[base], o[base + 1], o[base + 8], o[base + 9],
+                          o[base + 16], o[base + 17], o[base + 24], o[base + 25]};
+      const int bi = (((g * G + hh) * HD) >> 5) + blk;
+      quantize_item(v, bi, j, xq + (size_t)b * xstride * 4, xh ? xh + xh_tile(b, xstride) : nullptr, b & 15);
+    }
+  }
+}
+
+// Raise k_attn_rows' shared-memory limit to the whole 160 KB once per device, with that device
+// current (before any graph capture; attn_list_ok calls it).
+constexpr int kAttnRowsMaxLds = 160 * 1024;
+bool attn_rows_setup(int device) {
+  static std::mutex mu;
+  static uint64_t done = 0, ok = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (device < 0 || device >= 64) return false;
+  if (!((done >> device) & 1)) {
+    const bool a = hipFuncSetAttribute((const void*)k_attn_rows<float>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       kAttnRowsMaxLds) == hipSuccess;
+    const bool b = hipFuncSetAttribute((const void*)k_attn_rows<kvhalf>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       kAttnRowsMaxLds) == hipSuccess;
+    (void)hipGetLastError();
+    done |= (uint64_t)1 << device;
+    if (a && b) ok |= (uint64_t)1 << device;
+  }
+  return (ok >> device) & 1;
+}
+
 template <int MODE>
 void launch_quant(hipStream_t s, int rows, const float* in, int ld_in, int n, const float* w, float eps,
                   uint4* xq, int xstride, int m_first, uint4* xh = nullptr) {
@@ -1966,6 +2199,16 @@ void launch_attn_list_t(hipStream_t s, int HD, int B, int H, int KVH, const floa
   const unsigned units = (unsigned)KVH * (unsigned)B, pg = units * (unsigned)(HD / kPvCols);
   const bool xcd_group = units % kXcds == 0;
   const size_t lds = attn_pv_lds(H, KVH, ctx);
+  const int Gq = H / KVH;
+  int dev = 0;
+  if (seq_stride == 0 && B > 1 && !pv_tiles_off() && !attn_rows_off() && HD == 64 && Gq <= kMaxGroup &&
+      attn_rows_lds(Gq, ctx) <= (size_t)kAttnRowsMaxLds &&
+      (attn_rows_lds(Gq, ctx) <= 64 * 1024 || (hipGetDevice(&dev) == hipSuccess && attn_rows_setup(dev)))) {
+    // a prompt pass in one launch: scores and probabilities stay in shared memory
+    k_attn_rows<KT><<<dim3((unsigned)KVH, (unsigned)B), kAttnRowsThreads, attn_rows_lds(Gq, ctx), s>>>(
+        qkv, QKV, H, KVH, kc, vc, ctx, layer, pos, B, att, D, xq, xstride, xh);
+    return;
+  }
   if (seq_stride == 0 && B > 1 && !pv_tiles_off()) {   // a prompt pass: rows share one cache
     const dim3 tg((unsigned)(HD / kPvCols), (unsigned)KVH, (unsigned)((B + kPvTileRows - 1) / kPvTileRows));
     const int G = H / KVH;
@@ -2017,6 +2260,8 @@ void launch_attn_list(hipStream_t s, int HD, int B, int H, int KVH, const float*
 // limit raised where needed.  Checked once per shape.
 bool attn_list_ok(int H, int KVH, int HD, int ctx) {
   if (H / KVH > kMaxGroup) return false;
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess) (void)attn_rows_setup(dev);
   const size_t lds = attn_pv_lds(H, KVH, ctx), slds = softmax_lds(H, KVH, ctx);
   if (lds > 160 * 1024) return false;
   if (slds > 64 * 1024 &&

@@ -1,8 +1,9 @@
 """Multi-token passes under a kernel-selection switch, against the oracle, in a process of their own.
 
 The switches are read once per process (Q4HIP_GEMM=valu keeps the matrix cores out: k_gemm_rows for
-passes of 9..64 tokens, k_gemm_q4 above, unfused SwiGLU and RoPE launches; Q4HIP_PV_TILES=0 runs a
-prompt's attention on k_attn_pv_list), so tests/test_gpu_fallbacks.py starts this script as a
+passes of 9..64 tokens, k_gemm_q4 above, unfused SwiGLU and RoPE launches; Q4HIP_ATTN_ROWS=0 runs a
+prompt's attention in three launches instead of k_attn_rows; Q4HIP_PV_TILES=0 on k_attn_pv_list), so
+tests/test_gpu_fallbacks.py starts this script as a
 child with the switch set.  Prompts of 12, 40 and 150 tokens on two shapes (head_dim 64 and 128),
 then decode steps; a ragged batch of 12 sequences for two steps.  Tokens equal and logits bit
 for bit, as in the other GPU tests.  Prints the first mismatch and exits 1 on failure.
@@ -82,7 +83,7 @@ def batch(name, seed):
 
 
 def main():
-    print("switches:", {k: os.environ.get(k) for k in ("Q4HIP_GEMM", "Q4HIP_PV_TILES")}, flush=True)
+    print("switches:", {k: os.environ.get(k) for k in ("Q4HIP_GEMM", "Q4HIP_ATTN_ROWS", "Q4HIP_PV_TILES")}, flush=True)
     try:
         prompts("small", 71)
         prompts("small128", 72)
