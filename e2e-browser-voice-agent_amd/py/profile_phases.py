@@ -82,6 +82,8 @@ def main() -> None:
             if np.count_nonzero(raw) < raw.size // 2:
                 continue                                 # slot not written in this mode
             off = np.stack([wg[l, roles[role], k] - base[l - 1] for l in mid])
+            if np.median(off) < 0:
+                continue                                 # slot not written by this kernel (no stamp)
             print(f"{role:>3} {name:<18} min {np.median(off.min(1)):7.2f}  median {np.median(np.median(off, 1)):7.2f}"
                   f"  max {np.median(off.max(1)):7.2f}")
     hb = base[L - 1]
