@@ -397,6 +397,30 @@ def test_prefill_qwen05b_1024():
         o.close()
 
 
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_prompt_passes_large_context(kv):
+    """Prompt passes in a 4096-position context: the one-launch prompt attention keeps 7 heads x 4160
+    scores per row in shared memory (151 KB, past the 64 KB default limit), and the second pass's rows
+    attend over the first pass's positions too.  Both passes and a decode step after them agree with
+    the oracle bit for bit."""
+    print(f"qwen2.5-0.5b prompt passes at ctx 4096, kv {kv}", flush=True)
+    shape, g, o = _pair("qwen2.5-0.5b", 43, ctx=4096, threads=16, mode="persistent", kv=kv)
+    try:
+        ids = synth.prompt_ids(43, 330, shape.vocab)
+        ng, no = g.forward(ids[:250], 0), o.forward(ids[:250], 0)
+        assert ng == no
+        _compare_logits(g, o, "first pass")
+        ng, no = g.forward(ids[250:], 250), o.forward(ids[250:], 250)
+        assert ng == no
+        _compare_logits(g, o, "second pass")
+        ng, no = g.forward([ng], 330), o.forward([no], 330)
+        assert ng == no
+        _compare_logits(g, o, "step after the prompt")
+    finally:
+        g.close()
+        o.close()
+
+
 def test_short_rope_table_rejected():
     """q4hip_set_rope takes the table's float count and rejects a table shorter than ctx x head_dim
     before reading it; the N-API addon passes the typed array's length, so a short Float32Array
