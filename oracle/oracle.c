@@ -16,6 +16,7 @@
  */
 #include "oracle.h"
 
+#include <emmintrin.h>
 #include <math.h>
 #include <omp.h>
 #include <stdlib.h>
@@ -103,41 +104,53 @@ void orc_block_lanes_q4(const uint8_t* qs, const int8_t* x, int32_t p[4]) {
   }
 }
 
-static inline void block_lanes_q8(const int8_t* w, const int8_t* x, int32_t p[4]) {
-  for (int j = 0; j < 4; j++) {
-    int32_t acc = 0;
-    const int idx[4] = {2 * j, 2 * j + 1, 8 + 2 * j, 9 + 2 * j};
-    for (int t = 0; t < 4; t++) {
-      int e = idx[t];
-      acc += w[e] * x[e];
-      acc += w[16 + e] * x[16 + e];
-    }
-    p[j] = acc;
-  }
+/* The same lane sums with SSE2 (x86-64's baseline): the 32 products as int16, adjacent pairs
+ * (e, e+1) summed by pmaddwd, so int32 lane j of the low half holds pair (2j, 2j+1) and of the high
+ * half pair (8+2j, 9+2j); lane j of the total is the lane dot above (for int8 weights the same
+ * elements of w).  Integer sums are exact in any order, so this equals orc_block_lanes_q4
+ * (tests/test_oracle.py compares the dots with a NumPy emulation of the reference's SIMD). */
+static inline __m128i sx_lo(__m128i v) { return _mm_unpacklo_epi8(v, _mm_cmpgt_epi8(_mm_setzero_si128(), v)); }
+static inline __m128i sx_hi(__m128i v) { return _mm_unpackhi_epi8(v, _mm_cmpgt_epi8(_mm_setzero_si128(), v)); }
+static inline __m128i lanes16(__m128i w, __m128i x) {   /* 16 int8 weights x 16 int8 activations */
+  return _mm_add_epi32(_mm_madd_epi16(sx_lo(w), sx_lo(x)), _mm_madd_epi16(sx_hi(w), sx_hi(x)));
+}
+static inline __m128i block_lanes_q4_sse2(const uint8_t* qs, const int8_t* x) {
+  const __m128i q = _mm_loadu_si128((const __m128i*)qs), m4 = _mm_set1_epi8(15), e8 = _mm_set1_epi8(8);
+  const __m128i lo = _mm_sub_epi8(_mm_and_si128(q, m4), e8);
+  const __m128i hi = _mm_sub_epi8(_mm_and_si128(_mm_srli_epi16(q, 4), m4), e8);
+  return _mm_add_epi32(lanes16(lo, _mm_loadu_si128((const __m128i*)x)),
+                       lanes16(hi, _mm_loadu_si128((const __m128i*)(x + 16))));
+}
+static inline __m128i block_lanes_q8_sse2(const int8_t* w, const int8_t* x) {
+  return _mm_add_epi32(lanes16(_mm_loadu_si128((const __m128i*)w), _mm_loadu_si128((const __m128i*)x)),
+                       lanes16(_mm_loadu_si128((const __m128i*)(w + 16)), _mm_loadu_si128((const __m128i*)(x + 16))));
 }
 
-/* kernels.c:121-139: acc_lane += f32(p_lane) * (wd*xd), block by block, then hsum (kernels.c:116-118). */
+/* kernels.c:121-139: acc_lane += f32(p_lane) * (wd*xd), block by block, then hsum (kernels.c:116-118).
+ * The four lanes as one SSE vector: cvtdq2ps is exact for these sums (|p| < 2^24), mulps and addps
+ * round each lane once, as the reference's f32x4 operations do. */
+static inline float lanes_hsum(__m128 acc) {
+  float a[4];
+  _mm_storeu_ps(a, acc);
+  return a[0] + a[1] + a[2] + a[3];
+}
 float orc_dot_q4_q8(const uint8_t* wq, const float* wd, const int8_t* xq, const float* xd, int nb) {
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  __m128 acc = _mm_setzero_ps();
   for (int b = 0; b < nb; b++) {
-    int32_t p[4];
-    orc_block_lanes_q4(wq + 16 * b, xq + 32 * b, p);
-    float sc = wd[b] * xd[b];
-    for (int j = 0; j < 4; j++) acc[j] = acc[j] + (float)p[j] * sc;
+    const __m128 p = _mm_cvtepi32_ps(block_lanes_q4_sse2(wq + 16 * b, xq + 32 * b));
+    acc = _mm_add_ps(acc, _mm_mul_ps(p, _mm_set1_ps(wd[b] * xd[b])));
   }
-  return acc[0] + acc[1] + acc[2] + acc[3];
+  return lanes_hsum(acc);
 }
 
 /* kernels.c:157-170: same lane partition with int8 weights. */
 float orc_dot_q8_q8(const int8_t* wq, const float* wd, const int8_t* xq, const float* xd, int nb) {
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  __m128 acc = _mm_setzero_ps();
   for (int b = 0; b < nb; b++) {
-    int32_t p[4];
-    block_lanes_q8(wq + 32 * b, xq + 32 * b, p);
-    float sc = wd[b] * xd[b];
-    for (int j = 0; j < 4; j++) acc[j] = acc[j] + (float)p[j] * sc;
+    const __m128 p = _mm_cvtepi32_ps(block_lanes_q8_sse2(wq + 32 * b, xq + 32 * b));
+    acc = _mm_add_ps(acc, _mm_mul_ps(p, _mm_set1_ps(wd[b] * xd[b])));
   }
-  return acc[0] + acc[1] + acc[2] + acc[3];
+  return lanes_hsum(acc);
 }
 
 /* kernels.c:190-194 */

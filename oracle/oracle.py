@@ -117,6 +117,12 @@ def dot_q8_q8(wq, wd, xq, xd) -> float:
 def matvec_q4(raw_q4: np.ndarray, N: int, K: int, x: np.ndarray) -> np.ndarray:
     """y = W x with x quantized by quantize_row: what the reference computes for one projection."""
     qs, d = synth.q4_0_blocks(raw_q4)
+    return matvec_q4_blocks(qs, d, N, K, x)
+
+
+def matvec_q4_blocks(qs: np.ndarray, d: np.ndarray, N: int, K: int, x: np.ndarray) -> np.ndarray:
+    """matvec_q4 on weights already split into nibbles and fp32 scales (synth.q4_0_blocks), as the
+    reference holds them after loading (cpu-worker.js:93-104); one thread."""
     xq, xd, _ = quantize_row(x)
     y = np.zeros(N, np.float32)
     lib().orc_matmul_q4(ptr(qs), ptr(d), K, N, 0, N, 1, ptr(xq), ptr(xd), ptr(y), 0, None)
