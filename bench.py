@@ -466,13 +466,14 @@ def bench_prefill(args):
         oracle = _oracle()
         cores = _cores()
         o = oracle.Model(shape, tensors, ctx=n + 2, threads=cores)
-        k = 256
+        k = n                                   # the whole prompt (a few seconds with the SSE2 block dots)
         t0 = time.perf_counter()
-        o.forward(ids[:k], 0)
+        cpu_next = o.forward(ids[:k], 0)
         sec = time.perf_counter() - t0
         o.close()
         out["cpu_baseline"] = {"value": round(k / sec, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-                               "sample": f"oracle prefill of the first {k} of the 1024 ids (16-token chunks), "
+                               "tokens_agree_with_gpu": cpu_next == nxt,
+                               "sample": f"oracle prefill of all {k} of the 1024 ids (16-token chunks), "
                                          f"{sec:.1f} s, {cores} threads"}
     m.close()
     print(json.dumps(out))
