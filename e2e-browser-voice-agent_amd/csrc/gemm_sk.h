@@ -290,7 +290,7 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
   int rgi, T;
   if (!sk_place(blockIdx.x, nrg, (M + 15) / 16, by_tile, rgi, T)) return;
   const int R0 = EPI == 1 ? rgi * 32 : JS == 4 ? rgi * 16 : rgi * 64;
-  const int ng = W.ng, nb = W.nb;
+  const int ng = W.ng;
   const SkB bop(kg);
   const SkSrc<JS> src(W, xt, xstride, T, R0, EPI == 1 ? ffn : 0, EPI == 2 ? rp.hd : 0);
   constexpr int NJ = JS == 4 ? 1 : 4;
@@ -348,22 +348,14 @@ __global__ __launch_bounds__(256) void k_gemm_sk(Q4Mat W, const uint4* __restric
                                                      (sk_f4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
       }
     };
-    const int nbk = nb - 4 * g;                              // blocks of this group that exist (uniform)
-    if (nbk >= 4) {                                          // straight-line code for whole groups
-      sk_f4 d[4][NJ];
+    // every group is whole (the host takes this kernel only for rows of a multiple of 4 blocks),
+    // so the loop is straight-line code with no branch the accumulators would be copied around
+    (void)g;
+    sk_f4 d[4][NJ];
 #pragma unroll
-      for (int k = 0; k < 4; k++) product(k, d[k]);
+    for (int k = 0; k < 4; k++) product(k, d[k]);
 #pragma unroll
-      for (int k = 0; k < 4; k++) update(k, d[k]);
-    } else {
-#pragma unroll
-      for (int k = 0; k < 3; k++)
-        if (k < nbk) {
-          sk_f4 d[NJ];
-          product(k, d);
-          update(k, d);
-        }
-    }
+    for (int k = 0; k < 4; k++) update(k, d[k]);
   };
 
 #pragma unroll

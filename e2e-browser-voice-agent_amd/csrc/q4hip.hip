@@ -1625,7 +1625,8 @@ bool sk_enabled() {
 }
 
 int pick_gemm(const Mat& W, int M, bool have_xh) {
-  if (have_xh && sk_enabled()) return (W.Np / 64) * ((M + 15) / 16) >= 512 ? GK_SK1 : GK_SK4;
+  if (have_xh && sk_enabled() && W.nb % 4 == 0)            // k_gemm_sk takes whole groups of 4 blocks
+    return (W.Np / 64) * ((M + 15) / 16) >= 512 ? GK_SK1 : GK_SK4;
   if (M <= 64) return M >= 16 ? GK_ROWS2 : GK_ROWS1;
   return GK_TILED;
 }
@@ -1654,7 +1655,7 @@ void launch_sk(hipStream_t s, const Mat& W, const uint4* xh, int xstride, int M,
 // launched) where that path does not apply; the caller then runs the two launches.
 bool launch_gu_swiglu(hipStream_t s, const Mat& W, const uint4* xh_in, int xstride, int M, uint4* xq_out,
                       uint4* xh_out, int F) {
-  if (!xh_in || F % 32 || !sk_enabled()) return false;
+  if (!xh_in || F % 32 || !sk_enabled() || W.nb % 4) return false;
   const int nt = (M + 15) / 16;
   const bool by_tile = sk_by_tile(W, nt);
   k_gemm_sk<OP_STORE, 1, kSkR1, 1><<<(unsigned)sk_grid(F / 32, nt, by_tile), 256, 0, s>>>(
