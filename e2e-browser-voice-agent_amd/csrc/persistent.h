@@ -1254,6 +1254,42 @@ __device__ __forceinline__ void kchunk_row16(const float* chunk, int pr, int pj,
 // Wait until this wave's loads of its oldest K chunk in flight have landed (`cs` - 2 newer chunks
 // of N instructions -- 4 for fp32 rows, 2 for fp16 -- may still be outstanding).  Only the
 // issuing wave reads a chunk: no barrier.
+// Wide K chunks for fp16 caches: 32 rows of 8 pieces (16 bytes each), one row per pair of lanes
+// of the scoring wave.  Instruction g (0..3) loads rows 8g .. 8g+7 whole (8 full 128-byte lines):
+// lane l fetches piece (l + rot(r)) & 7 of row r = 8g + (l >> 3), rot(r) = (r >> 1) & 7, and it
+// lands at byte 1024 g + 16 l, so piece p of row r sits at byte 128 r + 16 ((p - rot(r)) & 7).
+// Both lanes of row t read piece p there: over 16 consecutive lanes (8 rows) the 16-byte bank
+// groups 8 (t & 1) + ((p - rot(t)) & 7) are distinct, so the reads are free of bank conflicts.
+// Rows at or past `limit` are read from row limit - 1 (ring_row; their scores are never stored).
+constexpr int kWideRows = 32;
+constexpr int kWideFloats = kWideRows * kHD / 2;     // 4 KB of fp16 rows
+constexpr int kWideIssue = kWideRows / 8;            // load instructions per chunk
+__device__ __forceinline__ int kwide_rot(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ void ring_issue_kw(const kvhalf* src, int t0, int limit, float* slot) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int g = 0; g < kWideIssue; g++) {
+    const int r = 8 * g + (lane >> 3);
+    const int pc = ((lane & 7) + kwide_rot(r)) & 7;
+    const kvhalf* p = src + (size_t)ring_row(t0 + r, limit) * kHD + 8 * pc;
+    __builtin_amdgcn_global_load_lds((GlobalVoid*)p, (LdsVoid*)(slot + g * 256), 16, 0, 0);
+  }
+}
+// First row of wide chunk j of wave w (chunks w, w + 4, ... of the stream; j clamped to the last).
+__host__ __device__ constexpr int kwide_t0(int kbeg, int j, int nloc, int wave) {
+  return kbeg + kWideRows * (4 * (j < nloc ? j : nloc - 1) + wave);
+}
+// Wide chunk slots in a wave's share of the ring: 5 (7-slot ring) or 2 (3-slot ring).
+__host__ __device__ constexpr int kwide_slots(int cs) {
+  return cs * kChunkFloats / kWideFloats < 5 ? cs * kChunkFloats / kWideFloats : 5;
+}
+static_assert(kwide_slots(kchunk_slots(7)) == 5 && kwide_slots(kchunk_slots(3)) == 2, "wide chunk slots");
+// Wait for the oldest of the wave's wide chunks in flight (ws - 1 newer ones may stay in flight).
+__device__ __forceinline__ void kwide_wait(int ws) {
+  if (ws == 5) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kWideIssue) : "memory");
+  else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kWideIssue) : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void kchunk_wait(int cs) {
   if (cs == 5) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * N) : "memory");
@@ -1621,9 +1657,18 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     float* wring = ring + (size_t)wave * cs * kChunkFloats;
     const KT* kgl = (const KT*)a.kc + cbase;
     const KT* vgl = (const KT*)a.vc + cbase;
-    if (nloc > 0)
+    // fp16 K: wide chunks, one row per pair of lanes
+    const bool wide = kF16;
+    const int ws = kwide_slots(cs), nlw = attn_nloc((nstream + kWideRows - 1) / kWideRows, wave);
+    if (wide) {
+      if constexpr (kF16)
+        if (nlw > 0)
+          for (int j = 0; j < ws - 1; j++)
+            ring_issue_kw(kgl, kwide_t0(kbeg, j, nlw, wave), kend, wring + (size_t)j * kWideFloats);
+    } else if (nloc > 0) {
       for (int j = 0; j < cs - 1; j++)
         ring_issue_kc(kgl, kchunk_t0(kbeg, j, nloc, wave), kend, wring + (size_t)j * kChunkFloats);
+    }
     if (l == 0) {
       for (int i = tid; i < S::D; i += kPThreads) stage_x<S>(m, i, embed_value(a.embd, S::D, tok, i));
     } else {
@@ -1697,7 +1742,53 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
     if (nck > 0) {
       const int R = a.ring;
       const int pj = lane & 3, pr = lane >> 2;   // lane pj of row pr of the wave's chunk
-      if (nloc > 0) {
+      if constexpr (kF16) {
+        if (wide && nlw > 0) {
+          // lane pair (row t = lane >> 1, h = lane & 1): lane h runs the reference lanes 2h and
+          // 2h + 1 of row t's score (elements 4i + 2h and 4i + 2h + 1, each product rounded, then
+          // added, i in order); the pair's four lane sums then combine in hsum order
+          const int h = lane & 1, tr = lane >> 1;
+          float2 qh[kHD / 4];
+#pragma unroll
+          for (int i = 0; i < kHD / 4; i++) qh[i] = *reinterpret_cast<const float2*>(qv + 4 * i + 2 * h);
+#pragma unroll
+          for (int i = 0; i < kHD / 4; i++) asm volatile("" : "+v"(qh[i].x), "+v"(qh[i].y));
+          const int rot = kwide_rot(tr);
+          for (int j = 0; j < nlw; j++) {
+            // the chunk ws - 1 ahead into the slot read in the previous iteration, then wait for
+            // this one (loads complete in order)
+            const int jn = j + ws - 1;
+            ring_issue_kw(kgl, kwide_t0(kbeg, jn, nlw, wave), kend, wring + (size_t)(jn % ws) * kWideFloats);
+            kwide_wait(ws);
+            // dwords h and h + 2 of each piece: elements 8p + 2h, +1 and 8p + 4 + 2h, +1
+            const uint32_t* row = reinterpret_cast<const uint32_t*>(wring + (size_t)(j % ws) * kWideFloats) + 32 * tr + h;
+            uint32_t dl[8], dh[8];
+#pragma unroll
+            for (int p = 0; p < 8; p++) {
+              const int o = 4 * ((p - rot) & 7);
+              dl[p] = row[o];
+              dh[p] = row[o + 2];
+            }
+            float ca = 0.0f, cb = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kHD / 4; i++) {
+              const uint32_t d = (i & 1) ? dh[i >> 1] : dl[i >> 1];
+              ca = ca + qh[i].x * half_bits_to_float(d & 0xffffu);
+              cb = cb + qh[i].y * half_bits_to_float(d >> 16);
+            }
+            // lane 2t gets lane 2t + 1's sums (quad_perm [1, 1, 3, 3])
+            const float c2 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ca), 0xF5, 0xF, 0xF, true));
+            const float c3 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(cb), 0xF5, 0xF, 0xF, true));
+            const float sv = (((ca + cb) + c2) + c3) * scale;
+            const int t = kwide_t0(kbeg, j, nlw, wave) + tr;
+            if (h == 0 && t < kend) {
+              sc[t] = sv;
+              lmax = __builtin_fmaxf(lmax, sv);
+            }
+          }
+        }
+      }
+      if (!wide && nloc > 0) {
         float qj[kHD / 4];                        // this lane's reference lane of q
 #pragma unroll
         for (int i = 0; i < kHD / 4; i++) qj[i] = qv[4 * i + pj];
