@@ -25,6 +25,7 @@
 // Arithmetic per output is the one of kernels.h (the reference's lane order), so results are
 // bit-identical to the kernel-per-operation path.
 #pragma once
+#include "gemm_sk.h"
 #include "kernels.h"
 
 namespace q4 {
@@ -1324,14 +1325,16 @@ __device__ __forceinline__ void ring_issue_vp(const float* src, int t0, int limi
 
 // fp16 rows: producer pw's 32 rows x 32 halves (2 KB) in 2 instructions of 16 rows, landing in
 // the upper half of its 4 KB part (byte 2048 + 64 r + 2 col); it reads them all before it writes
-// the fp32 products over the part.
+// the fp32 products over the part.  Issued as inline assembly (sk_dma16): with the builtin the
+// compiler made the producer's every shared-memory read wait for all of its loads in flight;
+// vpart_wait orders the reads instead.
 __device__ __forceinline__ void ring_issue_vp(const kvhalf* src, int t0, int limit, int c0, int pw, float* slot) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int k = 0; k < 2; k++) {
     const int t = t0 + 32 * pw + 16 * k + (lane >> 2);
     const kvhalf* g = src + (size_t)ring_row(t, limit) * kHD + c0 + 8 * (lane & 3);
-    __builtin_amdgcn_global_load_lds((GlobalVoid*)g, (LdsVoid*)(slot + pw * 1024 + 512 + k * 256), 16, 0, 0);
+    sk_dma16(g, slot + pw * 1024 + 512 + k * 256);
   }
 }
 
@@ -1970,16 +1973,34 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
           vpart_wait<NVP>(D);
           float* part = ring + (size_t)(c % R) * kSlotFloats + pw * 1024;
           const float* pc = sc + c * kVRows + 32 * pw;
-          const unsigned short* ph = reinterpret_cast<const unsigned short*>(part + 512);   // fp16 rows
-          float pv[16], vx[16];
+          if constexpr (kF16) {
+            // lane (column pair cp = lane & 15, row group rg = lane >> 4): rows 8 rg .. 8 rg + 7 of the
+            // part, columns 2 cp and 2 cp + 1 -- p of its 8 rows in two 16-byte reads, one 4-byte read
+            // of V per row, the row's two products in one 8-byte store: 10 reads in flight together
+            const int cp = lane & 15, rg = lane >> 4;
+            const float4 pa = *reinterpret_cast<const float4*>(pc + 8 * rg);
+            const float4 pb = *reinterpret_cast<const float4*>(pc + 8 * rg + 4);
+            const uint32_t* vw = reinterpret_cast<const uint32_t*>(part + 512) + 8 * rg * 16 + cp;   // fp16 rows
+            uint32_t vv[8];
 #pragma unroll
-          for (int k = 0; k < 16; k++) {
-            pv[k] = pc[(lane + 64 * k) >> 5];
-            vx[k] = kF16 ? half_bits_to_float(ph[lane + 64 * k]) : part[lane + 64 * k];
+            for (int r = 0; r < 8; r++) vv[r] = vw[r * 16];
+            asm volatile("" ::: "memory");   // every read of the part (fp16 rows included) before any write
+            const float pr[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+            float2* out = reinterpret_cast<float2*>(part) + 8 * rg * 16 + cp;
+#pragma unroll
+            for (int r = 0; r < 8; r++)
+              out[r * 16] = make_float2(pr[r] * half_bits_to_float(vv[r] & 0xffffu), pr[r] * half_bits_to_float(vv[r] >> 16));
+          } else {
+            float pv[16], vx[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+              pv[k] = pc[(lane + 64 * k) >> 5];
+              vx[k] = part[lane + 64 * k];
+            }
+            asm volatile("" ::: "memory");   // every read of the part before any write
+#pragma unroll
+            for (int k = 0; k < 16; k++) part[lane + 64 * k] = pv[k] * vx[k];
           }
-          asm volatile("" ::: "memory");     // every read of the part (fp16 rows included) before any write
-#pragma unroll
-          for (int k = 0; k < 16; k++) part[lane + 64 * k] = pv[k] * vx[k];
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
           if (lane == 0) cnt[pw] = c + 1;
           const int cn = c + D;
