@@ -2022,22 +2022,34 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
           const float* slot = ring + (size_t)(c % R) * kSlotFloats + lane;
           const int n = pos - c * kVRows;
           float pr[kVRows];
+          if (n >= kVRows) {
+            // a full slot, no select on the chain, read in quarters of 24 positions: two quarters
+            // ahead at first, then each quarter's reads issued before the one before it is added
+            // (12 reads in flight, so every wait is exact)
+            constexpr int Q = kVRows / 4;
 #pragma unroll
-          for (int u = 0; u < kVRows; u++) pr[u] = slot[u * 32];
+            for (int u = 0; u < 2 * Q; u++) pr[u] = slot[u * 32];
 #pragma unroll
-          for (int u = 0; u < kVRows / 2; u++) pin(pr[u]);
-          if (n >= kVRows) {                   // a full slot: no select on the chain
+            for (int q = 0; q < 4; q++) {
 #pragma unroll
-            for (int u = 0; u < kVRows / 2; u++) accv = accv + pr[u];
+              for (int u = q * Q; u < (q + 1) * Q; u++) pin(pr[u]);
+              if (q + 2 < 4) {
 #pragma unroll
-            for (int u = kVRows / 2; u < kVRows; u++) pin(pr[u]);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (lane == 0) cnt[3] = c + 1;
+                for (int u = (q + 2) * Q; u < (q + 3) * Q; u++) pr[u] = slot[u * 32];
+              }
+              if (q == 3) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                if (lane == 0) cnt[3] = c + 1;
+              }
 #pragma unroll
-            for (int u = kVRows / 2; u < kVRows; u++) accv = accv + pr[u];
+              for (int u = q * Q; u < (q + 1) * Q; u++) accv = accv + pr[u];
+              __builtin_amdgcn_sched_barrier(0);
+            }
           } else {
 #pragma unroll
-            for (int u = kVRows / 2; u < kVRows; u++) pin(pr[u]);
+            for (int u = 0; u < kVRows; u++) pr[u] = slot[u * 32];
+#pragma unroll
+            for (int u = 0; u < kVRows; u++) pin(pr[u]);
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             if (lane == 0) cnt[3] = c + 1;
 #pragma unroll
