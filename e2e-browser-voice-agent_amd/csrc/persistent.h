@@ -67,6 +67,8 @@ struct PArgs {
   // hand-off they follow is polled for.
   int pf[4];
   const int* wgmap;   // physical workgroup -> logical one (the role order below); identity when null
+  int hres;           // row groups of the Q4_0 head each wave outside the attention role keeps in
+                      // shared memory for the whole launch (0: the head is streamed whole every step)
 };
 
 // This workgroup's logical index.  The host places the attention workgroups of one kv group on one
@@ -723,6 +725,7 @@ struct PSmem {
   int* flag;      // the give-up flag of wg_bad (word 7 of red)
   float* terms;   // last: 64 * NBM per-block terms (OD); for the attention role its ctx + 2 kRingRows
                   // scores, then its K/V ring and staged tile
+  uint4* hcache;  // the resident head row groups (every role but attention), inside terms' space
 };
 
 // Staged K/V of the attention role: K as rows [kv_tile][kKVRow], V transposed [64][kv_vstride]
@@ -770,6 +773,18 @@ constexpr size_t psmem_attn_bytes(int ctx, int ring_slots, int kv_tile) {
          kv_lds_bytes(kv_tile);
 }
 
+// Resident row groups of the output head, after the K/V role's term buffer (the last shared-memory
+// use of the roles outside attention).  One row group holds a wave's WR<NGD> registers: word j of
+// the 4 blocks of group g for lane l at uint4 g * 64 + l, then scale word c of row r at uint4
+// NGD * 64 + c * 16 + r (64 uint4, one load instruction's worth).  Wave w's k-th row group is
+// slot w * hres + k.
+template <class S>
+constexpr size_t head_cache_offset() {
+  return (psmem_terms_offset<S>() + (size_t)64 * S::NBD * 4 + 15) & ~(size_t)15;
+}
+template <class S>
+constexpr size_t head_rg_bytes() { return ((size_t)S::NGD * 64 + 64) * 16; }
+
 template <class S>
 __device__ __forceinline__ PSmem psmem(unsigned char* base) {
   PSmem m;
@@ -787,6 +802,7 @@ __device__ __forceinline__ PSmem psmem(unsigned char* base) {
   m.raw = (uint32_t*)(base + off);  off += (size_t)S::RAW * 4;
   m.flag = (int*)(m.red + 7);
   m.terms = (float*)(base + off);
+  m.hcache = (uint4*)(base + head_cache_offset<S>());
   return m;
 }
 
@@ -941,6 +957,49 @@ __device__ __forceinline__ void head_rows(const PArgs& a, const PSmem& m, const 
   }
 }
 
+// This workgroup's rank among the ones that keep head row groups in shared memory (every role
+// but attention), or -1.
+template <class S>
+__device__ __forceinline__ int head_cache_rank(const PArgs& a, int wg) {
+  if (wg < S::nOD) return wg;
+  if (wg < S::nOD + S::H * a.asplit) return -1;
+  return wg - S::H * a.asplit;
+}
+
+// Row group k (k < hres) kept by wave `wave` of the workgroup of rank `rank`: row groups
+// [0, ranks * 4 * hres) are the resident ones, the rest are streamed.
+__device__ __forceinline__ int head_cache_rg(int hres, int rank, int wave, int k) {
+  return (rank * 4 + wave) * hres + k;
+}
+
+// Issue the asynchronous loads of this wave's resident row groups into `cache` (in the first step's
+// head phase, before its wait for x, which drains them).
+template <class S>
+__device__ __forceinline__ void head_cache_fill(const PArgs& a, uint4* cache, int rank, int hres) {
+  const int lane = threadIdx.x & 63, wave = wave_id(), j = lane & 3;
+  for (int k = 0; k < hres; k++) {
+    const int rg = head_cache_rg(hres, rank, wave, k);
+    uint4* dst = cache + (size_t)(wave * hres + k) * (head_rg_bytes<S>() / 16);
+    const int rr = (rg & 3) * 16 + (lane >> 2);            // row of lane l within its 64-row tile
+    const uint4* wq = a.head.qs + ((size_t)(rg >> 2) * S::NGD * 64 + rr) * 4 + j;
+#pragma unroll
+    for (int g = 0; g < S::NGD; g++) sk_dma16(wq + (size_t)g * 256, dst + g * 64);
+    // lane l: scale word c = l >> 4 of row r = l & 15 (words past NB8D repeat the last one, unused)
+    const int c = (lane >> 4) < S::NB8D ? (lane >> 4) : S::NB8D - 1;
+    const uint4* wd = a.head.d + ((size_t)(rg >> 2) * S::NB8D + c) * 64 + (rg & 3) * 16 + (lane & 15);
+    sk_dma16(wd, dst + S::NGD * 64);
+  }
+}
+
+// A resident row group into the registers wr_load would have filled.
+template <class S>
+__device__ __forceinline__ void head_cache_read(const uint4* src, int lane, WR<S::NGD>& R) {
+#pragma unroll
+  for (int g = 0; g < S::NGD; g++) R.w[g] = src[g * 64 + lane];
+#pragma unroll
+  for (int c = 0; c < (S::NGD + 1) / 2; c++) R.s[c] = src[S::NGD * 64 + c * 16 + (lane >> 2)];
+}
+
 // Logits of this workgroup's Q4_0 row groups (five rotating register buffers: four row groups in
 // flight while one is computed; with two, the head streamed ~5 us slower per step); x is received
 // and normalised after the first four are issued.
@@ -963,6 +1022,63 @@ __device__ __forceinline__ bool head_scan_q4(const PArgs& a, const PSmem& m, uin
   if (wg_bad(m.flag, bad)) return false;
   prof_mark(a, s, a.NL * 16 + 0);
   norm_quant<S>(m, nw, a.eps);
+  for (;;) {
+#pragma unroll
+    for (int i = 0; i < NBUF; i++) {
+      if (rgi + (NBUF - 1) * stride < nRG)
+        wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + (NBUF - 1) * stride, lane, R[(i + NBUF - 1) % NBUF][0]);
+      head_rows<S>(a, m, R[i], rgi, lane, bv, bi);
+      rgi += stride;
+      if (rgi >= nRG) return true;
+    }
+  }
+  return true;
+}
+
+// The same with resident row groups: the resident ones from shared memory, then the streamed
+// ones through the five rotating register buffers.  Workgroups that finish their last
+// layer early issue the first four streamed row groups before they wait for x; the o/down
+// workgroups, whose down stores end the layers, wait for x first (loads issued before a wait
+// delay it: the wait's memory counter covers every earlier load) and work on their resident row
+// groups while the streamed ones arrive.
+template <class S>
+__device__ __forceinline__ bool head_scan_q4_cached(const PArgs& a, const PSmem& m, uint32_t epx, int s, bool& bad,
+                                                    float& bv, int& bi) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int G = gridDim.x, wg = lwg(a), nRG = a.head.Np / 16, stride = 4 * G;
+  const int rank = head_cache_rank<S>(a, wg), hres = a.hres;
+  const int nres = rank >= 0 ? hres : 0;
+  float nw[4];
+  normw_load<S>(a.out_norm, nw);
+  // streamed row groups round-robin over the waves, the o/down workgroups last: they come to the
+  // head last, so they take the fewest row groups
+  int rgi = (G - S::H * a.asplit) * 4 * hres + (G - 1 - wg) + G * wave;
+  const bool early = wg >= S::nOD || nres == 0;
+  if (s == 0 && nres > 0) head_cache_fill<S>(a, m.hcache, rank, nres);
+  constexpr int NBUF = 5;
+  WR<S::NGD> R[NBUF][1];
+  if (early) {
+#pragma unroll
+    for (int k = 0; k < NBUF - 1; k++)
+      if (rgi + k * stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + k * stride, lane, R[k][0]);
+  }
+  recv_x<S>(a.ll + S::oXH, epx, a.st, m, bad, a.nap);
+  // every earlier load has completed, the resident row groups' included
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (wg_bad(m.flag, bad)) return false;
+  prof_mark(a, s, a.NL * 16 + 0);
+  if (!early) {
+#pragma unroll
+    for (int k = 0; k < NBUF - 1; k++)
+      if (rgi + k * stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + k * stride, lane, R[k][0]);
+  }
+  norm_quant<S>(m, nw, a.eps);
+  for (int k = 0; k < nres; k++) {
+    WR<S::NGD> C[1];
+    head_cache_read<S>(m.hcache + (size_t)(wave * nres + k) * (head_rg_bytes<S>() / 16), lane, C[0]);
+    head_rows<S>(a, m, C, head_cache_rg(hres, rank, wave, k), lane, bv, bi);
+  }
+  if (rgi >= nRG) return true;
   for (;;) {
 #pragma unroll
     for (int i = 0; i < NBUF; i++) {
@@ -1080,7 +1196,8 @@ __device__ __forceinline__ bool head_scan_q8(const PArgs& a, const PSmem& m, uin
 
 // Final RMSNorm, logits of this workgroup's row groups, then every workgroup reduces every
 // workgroup's (value, index): the same token everywhere.  Returns the token, or -1 on abort.
-template <class S>
+// HC: this kernel keeps head row groups in shared memory (PArgs::hres).
+template <class S, bool HC>
 __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32_t ep0, int s, int pos, bool& bad) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int G = gridDim.x, wg = lwg(a), E = 4 * a.NL + 1;
@@ -1090,7 +1207,9 @@ __device__ __forceinline__ int head_phase(const PArgs& a, const PSmem& m, uint32
 
   float bv = 0.0f;
   int bi = -1;
-  const bool ok = a.head_q8 ? head_scan_q8<S>(a, m, epx, s, bad, bv, bi) : head_scan_q4<S>(a, m, epx, s, bad, bv, bi);
+  const bool ok = a.head_q8 ? head_scan_q8<S>(a, m, epx, s, bad, bv, bi)
+                            : HC ? head_scan_q4_cached<S>(a, m, epx, s, bad, bv, bi)
+                                 : head_scan_q4<S>(a, m, epx, s, bad, bv, bi);
   if (!ok) return -1;
   wave_argmax(bv, bi);
   if (lane == 0) { m.argv[wave] = bv; m.argi[wave] = bi; }
@@ -2268,7 +2387,9 @@ __global__ __launch_bounds__(kPThreads, 1) void k_decode_persistent(PArgs a) {
       ok = gu_step<S>(a, m, ep0, s, bad);
     }
     if (!ok) return;
-    tok = head_phase<S>(a, m, ep0, s, pos, bad);
+    // resident head row groups in the fp32-cache kernel only: in the fp16-cache kernel the added
+    // code slowed the long-context attention loops by 1.5% (code placement), for no gain there
+    tok = head_phase<S, sizeof(KT) == 4>(a, m, ep0, s, pos, bad);
     if (tok < 0) return;
   }
   if (wg == 0 && threadIdx.x == 0) {

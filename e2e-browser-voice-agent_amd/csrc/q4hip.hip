@@ -1570,6 +1570,8 @@ struct q4hip {
   const char* pers_why = "";
   int pers_kv_tile = 0;
   size_t pers_lds = 0;
+  size_t pers_hc_off = 0, pers_hc_rg = 0;   // resident head row groups: shared-memory offset, bytes each
+  bool pers_head_cache = true;              // Q4HIP_HEAD_CACHE=0: stream the whole head every step
   int pers_ring = 0;
   int pers_test_abort = 0;   // persistent launches still to start with the abort flag raised
   int pers_last_steps = 0;   // steps of the last persistent launch (the epochs it may have used)
@@ -2381,13 +2383,14 @@ struct PersInstance {
   size_t (*attn_bytes)(int ctx, int ring_slots, int kv_tile);
   size_t (*ll_entries)(int);
   int nRoles, nbm;
+  size_t head_cache_off, head_rg_bytes;
 };
 
 template <class S>
 PersInstance pers_instance() {
   return PersInstance{S::D, S::F, S::H, S::KVH, (const void*)k_decode_persistent<S, float>,
                       (const void*)k_decode_persistent<S, kvhalf>, psmem_base_bytes<S>(), &psmem_attn_bytes<S>,
-                      &S::ll_entries, S::nRoles, S::NBM};
+                      &S::ll_entries, S::nRoles, S::NBM, head_cache_offset<S>(), head_rg_bytes<S>()};
 }
 
 const PersInstance* find_pers_instance(int D, int F, int H, int KVH) {
@@ -2488,6 +2491,9 @@ void setup_persistent(q4hip* h) {
     return no("device allocation failed");
   }
   h->pers_grid = G;
+  h->pers_hc_off = pi->head_cache_off;
+  h->pers_hc_rg = pi->head_rg_bytes;
+  if (const char* e = getenv("Q4HIP_HEAD_CACHE")) h->pers_head_cache = atoi(e) != 0;
   for (int sp = 1; sp <= 2; sp++) {
     const std::vector<int> map = persistent_wgmap(G, h->D / 16, h->H, h->KVH, sp);
     if (map.empty()) continue;
@@ -2576,6 +2582,15 @@ hipError_t launch_persistent(q4hip* h, int pos0, int steps, unsigned long long* 
   a.prof = prof;
   a.wgmap = h->pers_wgmap[a.asplit - 1];
   for (int i = 0; i < 4; i++) a.pf[i] = h->pers_pf[i];
+  // Q4_0 head row groups per wave kept in the shared memory the roles outside attention leave
+  // free (fp32-cache kernel): as many as fit, while the resident ones stay within the head
+  a.hres = 0;
+  if (!a.head_q8 && !h->kv16 && h->pers_head_cache && h->pers_lds > h->pers_hc_off) {
+    const int ranks = h->pers_grid - h->H * a.asplit, nrg = a.head.Np / 16;
+    int n = (int)std::min<size_t>(8, (h->pers_lds - h->pers_hc_off) / (4 * h->pers_hc_rg));
+    while (n > 0 && (long)ranks * 4 * n > nrg) n--;
+    a.hres = n;
+  }
   h->pers_last_steps = steps;
   if (h->pers_test_abort > 0) {          // Q4HIP_TEST_ABORT: the launch finds the flag raised
     h->pers_test_abort--;

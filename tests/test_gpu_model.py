@@ -169,6 +169,38 @@ def test_qwen05b_prompt64_greedy64(mode):
         o.close()
 
 
+def test_head_cache_switch(monkeypatch):
+    """The persistent kernel keeps a third of the Q4_0 head's row groups in shared memory (fp32
+    cache, 0.5B shape).  With them (the default) and with the head streamed whole every step
+    (Q4HIP_HEAD_CACHE=0) the tokens and the last step's logits are the oracle's, bit for bit, over
+    one-step launches (each fills the resident rows anew) and one 24-step launch."""
+    for env in ("1", "0"):
+        monkeypatch.setenv("Q4HIP_HEAD_CACHE", env)
+        print(f"head cache {env}", flush=True)
+        shape, g, o = _pair("qwen2.5-0.5b", 5, ctx=256, threads=16, mode="persistent")
+        try:
+            ids = synth.prompt_ids(5, 40, shape.vocab)
+            ng, no = g.forward(ids, 0), o.forward(ids, 0)
+            assert ng == no
+            pos = 40
+            for step in range(4):
+                ng, no = g.forward([ng], pos), o.forward([no], pos)
+                assert ng == no, f"cache {env} step {step}"
+                _compare_logits(g, o, f"cache {env} step {step}")
+                pos += 1
+            dev = g.generate(ng, pos, 24)
+            want = [no]
+            for _ in range(24):
+                want.append(o.forward([want[-1]], pos))
+                pos += 1
+            assert dev == want[1:], f"cache {env}"
+            _compare_logits(g, o, f"cache {env} after the 24-step launch")
+            assert g.decode_mode_used() == 2
+        finally:
+            g.close()
+            o.close()
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_decode_rewrites_positions(mode):
     """Decoding again over positions that an earlier launch filled with other tokens gives the
