@@ -876,7 +876,7 @@ __device__ __forceinline__ void normw_load(const float* w, float (&nw)[4]) {
 // quantizes half a block lane.  No shared-memory round trip and no barrier between the sums and
 // the quantize; the values a thread quantizes are read before the sums.  The caller has
 // synchronised after staging; returns after a barrier.
-template <class S>
+template <class S, bool kLdsOnly = false>
 __device__ __forceinline__ void norm_quant(const PSmem& m, const float (&nw)[4], float eps, unsigned long long* mark = nullptr) {
   const int tid = threadIdx.x, lane = tid & 63;
   float xv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -905,7 +905,13 @@ __device__ __forceinline__ void norm_quant(const PSmem& m, const float (&nw)[4],
     const uint4 q = quant_half(v);
     if ((tid & 1) == 0) m.xq[tid >> 1] = q;
   }
-  __syncthreads();
+  if constexpr (kLdsOnly) {
+    // shared memory only: row groups still loading are waited for where their registers are
+    // first used, not here
+    lds_barrier();
+  } else {
+    __syncthreads();
+  }
 }
 
 // (value, index) merge with the first-maximum rule of cpu-worker.js:157.
@@ -1050,9 +1056,11 @@ __device__ __forceinline__ bool head_scan_q4_cached(const PArgs& a, const PSmem&
   const int nres = rank >= 0 ? hres : 0;
   float nw[4];
   normw_load<S>(a.out_norm, nw);
-  // streamed row groups round-robin over the waves, the o/down workgroups last: they come to the
-  // head last, so they take the fewest row groups
-  int rgi = (G - S::H * a.asplit) * 4 * hres + (G - 1 - wg) + G * wave;
+  // streamed row groups round-robin over the waves, the o/down workgroups' waves last in each
+  // round: they come to the head last, so the last, partial round leaves them out
+  const int ord = wg < S::nOD ? 4 * (G - S::nOD) + (S::nOD - 1 - wg) + S::nOD * wave
+                              : (G - 1 - wg) + (G - S::nOD) * wave;
+  int rgi = (G - S::H * a.asplit) * 4 * hres + ord;
   const bool early = wg >= S::nOD || nres == 0;
   if (s == 0 && nres > 0) head_cache_fill<S>(a, m.hcache, rank, nres);
   constexpr int NBUF = 5;
@@ -1072,7 +1080,8 @@ __device__ __forceinline__ bool head_scan_q4_cached(const PArgs& a, const PSmem&
     for (int k = 0; k < NBUF - 1; k++)
       if (rgi + k * stride < nRG) wr_load<S::NGD, S::NB8D, 0, S::NGD>(a.head, rgi + k * stride, lane, R[k][0]);
   }
-  norm_quant<S>(m, nw, a.eps);
+  // the o/down workgroups' first row groups load while x is normalised and the resident rows run
+  norm_quant<S, true>(m, nw, a.eps);
   for (int k = 0; k < nres; k++) {
     WR<S::NGD> C[1];
     head_cache_read<S>(m.hcache + (size_t)(wave * nres + k) * (head_rg_bytes<S>() / 16), lane, C[0]);
