@@ -2167,7 +2167,10 @@ __device__ __forceinline__ bool attn_step(const PArgs& a, const PSmem& m, uint32
               }
               if (q == 3) {
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                if (lane == 0) cnt[3] = c + 1;
+                // every lane stores the same count: a store under lane == 0 would end the basic
+                // block here, and the compiler then sinks all four quarters' additions after it
+                cnt[3] = c + 1;
+                __builtin_amdgcn_sched_barrier(0);
               }
 #pragma unroll
               for (int u = q * Q; u < (q + 1) * Q; u++) accv = accv + pr[u];
