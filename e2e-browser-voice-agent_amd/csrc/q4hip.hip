@@ -95,14 +95,24 @@ __global__ void k_embed(const uint8_t* __restrict__ emb, int D, const int* __res
 // Quantize rows m_first .. m_first+gridDim.x-1 of `in` into xq rows 0.. (kernels.c:328-331,
 // 379, 385-388, 393-397, 405-407).  QM_NORM stages the row's squares for the serial sums and the
 // row itself by lane in shared memory (quant_lds: 4 sq_stride(n) + 4 (n/4 + 1) floats).
+// With xh and at least 128 rows, workgroup w takes row (w % 8) * ceil(rows / 8) + w / 8 (none past
+// rows): workgroup w runs on XCD w % 8, so the 16 rows of an operand tile are quantized on one or
+// two XCDs and the tile's lines, 8 bytes of each from every row, are completed in their L2 instead
+// of being written back in pieces from all eight (a 1024-token prompt pass: 8.98 -> 8.87 ms; with
+// 32 rows the spread over four XCDs instead of eight measured slower, so fewer rows keep row w).
 template <int MODE>
 __global__ __launch_bounds__(256) void k_quant(const float* __restrict__ in, int ld_in, int n,
                                                const float* __restrict__ w, float eps,
                                                uint4* __restrict__ xq, int xstride, int m_first,
-                                               uint4* __restrict__ xh) {
+                                               uint4* __restrict__ xh, int rows) {
   extern __shared__ float xl[];
   __shared__ float red[8];
-  const float* xr = in + (size_t)(m_first + blockIdx.x) * ld_in;
+  int row = blockIdx.x;
+  if (xh && rows >= 128) {
+    row = (int)(blockIdx.x & 7) * ((rows + 7) >> 3) + (int)(blockIdx.x >> 3);
+    if (row >= rows) return;
+  }
+  const float* xr = in + (size_t)(m_first + row) * ld_in;
   const int st = (n >> 2) + 1;
   float rs = 0.0f;
   const int sst = sq_stride(n);
@@ -116,8 +126,8 @@ __global__ __launch_bounds__(256) void k_quant(const float* __restrict__ in, int
     __syncthreads();
     rs = rms_scale_sq(xl, n, sst, eps, red);
   }
-  quantize_row_dev<MODE>(xr, xs, st, n, w, rs, xq + (size_t)blockIdx.x * xstride * 4, threadIdx.x, blockDim.x,
-                         xh ? xh + xh_tile(blockIdx.x, xstride) : nullptr, blockIdx.x & 15, wv, one);
+  quantize_row_dev<MODE>(xr, xs, st, n, w, rs, xq + (size_t)row * xstride * 4, threadIdx.x, blockDim.x,
+                         xh ? xh + xh_tile(row, xstride) : nullptr, row & 15, wv, one);
 }
 
 enum { OP_STORE = 0, OP_BIAS = 1, OP_ADD = 2 };   // put() of kernels.c:190-194
@@ -2181,7 +2191,7 @@ template <int MODE>
 void launch_quant(hipStream_t s, int rows, const float* in, int ld_in, int n, const float* w, float eps,
                   uint4* xq, int xstride, int m_first, uint4* xh = nullptr) {
   const size_t lds = MODE == QM_NORM ? (size_t)(sq_stride(n) + (n >> 2) + 1) * 4 * sizeof(float) : 0;
-  k_quant<MODE><<<rows, 256, lds, s>>>(in, ld_in, n, w, eps, xq, xstride, m_first, xh);
+  k_quant<MODE><<<xh && rows >= 128 ? 8 * ((rows + 7) / 8) : rows, 256, lds, s>>>(in, ld_in, n, w, eps, xq, xstride, m_first, xh, rows);
 }
 
 // V rows per chunk of k_attn_pv_list: 128 (34 KB of LDS for the two chunk buffers) halves the
