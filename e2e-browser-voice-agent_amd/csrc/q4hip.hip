@@ -687,8 +687,7 @@ __global__ __launch_bounds__(64) void k_attn(const float* __restrict__ qkv, int 
     sc[t] = v;
     lmax = __builtin_fmaxf(lmax, v);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) lmax = __builtin_fmaxf(lmax, __shfl_xor(lmax, o));
+  lmax = max64(lmax);
   __syncthreads();
   for (int t = tid; t < T; t += 64) sc[t] = fast_exp(sc[t] - lmax);
   __syncthreads();
@@ -1175,9 +1174,7 @@ __global__ __launch_bounds__(256) void k_attn_pv_list(const float* __restrict__ 
   auto head_max = [&](float* mxh) {       // block-wide maximum of each head (order-free)
 #pragma unroll
     for (int gh = 0; gh < kMaxGroup; gh++) {
-      float m = mxh[gh];
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o));
+      const float m = max64(mxh[gh]);   // DPP and one swizzle, not six shared-memory shuffles
       if (lane == 0) red[wave * kMaxGroup + gh] = m;
     }
     __syncthreads();
@@ -1768,9 +1765,7 @@ __global__ __launch_bounds__(256) void k_softmax_rows(float* __restrict__ sc, in
   }
 #pragma unroll
   for (int gh = 0; gh < kMaxGroup; gh++) {
-    float m = mxh[gh];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o));
+    const float m = max64(mxh[gh]);
     if (lane == 0) red[wave * kMaxGroup + gh] = m;
   }
   __syncthreads();
@@ -2045,9 +2040,7 @@ __global__ __launch_bounds__(kAttnRowsThreads) void k_attn_rows(const float* __r
   // the maximum of each head (order-free)
 #pragma unroll
   for (int gh = 0; gh < kMaxGroup; gh++) {
-    float m = mxh[gh];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o));
+    const float m = max64(mxh[gh]);
     if (lane == 0) red[wave * kMaxGroup + gh] = m;
   }
   lds_barrier();
